@@ -1,0 +1,290 @@
+/*
+ * intfer_amd.h -- C-ABI of the MI355X-native mixed-batch M-row forward.
+ *
+ * The reference drives its device layer through a C++ virtual interface
+ * (`struct LinearBackend`, examples/intfer_cli/main.cpp:455-566) and the
+ * `intfer::Engine` below it (include/intfer/engine.hpp:37-562).  This header
+ * replaces both with plain-C entry points: POD arguments, opaque handles,
+ * int status codes, no exceptions, no torch or HIP types in any signature.
+ *
+ * Threading: a context is single-threaded, like the reference's one
+ * dispatcher thread (main.cpp:9394-9402).  All device work of a context runs
+ * in order on the context's one HIP stream.
+ *
+ * Errors: every entry point returns IFR_OK or a negative IFR_E* code;
+ * ifr_last_error() returns a message for the last failure on this thread.
+ * IFR_EDECLINE keeps the reference's "decline, caller runs its host path"
+ * meaning (engine.hpp:102-118): nothing was written.
+ */
+#ifndef INTFER_AMD_H
+#define INTFER_AMD_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum {
+  IFR_OK = 0,
+  IFR_EDECLINE = -1, /* shape/format not handled: caller keeps its own path */
+  IFR_EINVAL = -2,   /* bad argument */
+  IFR_ENOMEM = -3,   /* device or host allocation failed / pool exhausted */
+  IFR_EDEVICE = -4,  /* HIP runtime error, or no device */
+  IFR_ESTATE = -5    /* call not valid in the current context state */
+};
+
+/* ------------------------------------------------------------------------
+ * Model description (host side).
+ * ---------------------------------------------------------------------- */
+
+/* Decoder configuration.  Mirrors the fields of the reference ModelConfig
+ * that the full-attention layer reads (main.cpp:91-132).  The synthetic
+ * 0.8B-class model is hidden 1024, 28 layers, 16 q / 8 kv heads, head_dim
+ * 128, SwiGLU 3072, vocab 151936, eps 1e-6, theta 1e6, rotary_dim 128. */
+typedef struct ifr_model_cfg {
+  int32_t hidden;
+  int32_t layers;
+  int32_t n_heads;
+  int32_t n_kv;
+  int32_t head_dim;
+  int32_t inter;
+  int32_t vocab;
+  int32_t rotary_dim;
+  float rms_eps;
+  float rope_theta;
+  int32_t group_size; /* weight K-group (128) */
+  int32_t qk_norm;    /* 1: per-head RMSNorm(1+w) on q and k (main.cpp:7641-7650) */
+  int32_t rotate;     /* 1: online Hadamard at the QKV/O/FFN_IN/FFN_OUT sites */
+} ifr_model_cfg;
+
+/* One quantized linear y = W x, W is [N][K].  Logical (load) layout:
+ *   codes : row-major packed, least-significant bits first: code(n,k) is
+ *           bits [(i*b)%8, +b) of byte (i*b)/8 with i = n*K + k (the
+ *           reference packing, src/quant/dashq.cpp:387-402, applied row-major)
+ *   scale : fp16 [N][K/group]
+ *   zero  : fp16 [N][K/group]
+ * Dequantized weight: w(n,k) = scale(n,g) * (code(n,k) - zero(n,g)), g = k/group.
+ * The reference codebook (dashq.cpp:405-417, (2c-C)/C) is the special case
+ * zero = C/2, scale = 2*s_ref/C with C = 2^b - 1. */
+typedef struct ifr_linear {
+  int32_t N, K, bits, group;
+  const uint8_t* codes;
+  const uint16_t* scale;
+  const uint16_t* zero;
+} ifr_linear;
+
+typedef struct ifr_layer_w {
+  ifr_linear q, k, v, o, gate, up, down;
+  const float* in_ln;   /* [hidden]  RMSNorm(1+w) before attention */
+  const float* post_ln; /* [hidden]  RMSNorm(1+w) before the MLP */
+  const float* q_norm;  /* [head_dim] */
+  const float* k_norm;  /* [head_dim] */
+} ifr_layer_w;
+
+typedef struct ifr_host_model {
+  ifr_model_cfg cfg;
+  const float* embed;      /* [vocab][hidden] fp32, tied with lm_head */
+  const float* final_norm; /* [hidden] */
+  const ifr_layer_w* layers; /* [layers] */
+} ifr_host_model;
+
+/* Synthetic seeded model (portable splitmix64 + Box-Muller; see the
+ * generator source for distributions).  bits_mode 2 or 4 = every linear at
+ * that width; bits_mode 0 = seeded per-tensor 70 % INT2 / 30 % INT4 split.
+ * The returned model owns its buffers; free with ifr_synth_free. */
+ifr_host_model* ifr_synth_model(const ifr_model_cfg* cfg, uint64_t seed, int32_t bits_mode);
+void ifr_synth_free(ifr_host_model* m);
+
+/* Default 0.8B-class configuration. */
+void ifr_default_cfg(ifr_model_cfg* out);
+
+/* ------------------------------------------------------------------------
+ * Context, memory helpers.
+ * ---------------------------------------------------------------------- */
+typedef struct ifr_ctx ifr_ctx;
+
+const char* ifr_last_error(void);
+/* Replaces Engine::load + DeviceManager::discover (engine.cpp:552,
+ * device_manager.cpp:30).  One HIP stream per context. */
+int ifr_ctx_create(int32_t device, ifr_ctx** out);
+int ifr_ctx_destroy(ifr_ctx* ctx);
+int ifr_sync(ifr_ctx* ctx);
+
+/* Device buffers for tests and benches (no torch in the boundary). */
+int ifr_malloc(ifr_ctx* ctx, size_t bytes, void** dptr);
+int ifr_free(ifr_ctx* ctx, void* dptr);
+int ifr_h2d(ifr_ctx* ctx, void* dst, const void* src, size_t bytes);
+int ifr_d2h(ifr_ctx* ctx, void* dst, const void* src, size_t bytes);
+int ifr_memset(ifr_ctx* ctx, void* dst, int value, size_t bytes);
+
+/* ------------------------------------------------------------------------
+ * Kernel-level entry points (tests, benches, and the reference's
+ * free kernel functions, include/intfer/gemm/quant_gemm.hpp).
+ * All pointers named *_d are device pointers.
+ * ---------------------------------------------------------------------- */
+
+/* A quantized linear repacked to the device MFMA layout.  Replaces
+ * Engine::shard_weight + repack_dpas412 (engine.cpp:434-549,
+ * quant_gemm.cpp:3294-3322). */
+typedef struct ifr_dlinear ifr_dlinear;
+int ifr_linear_upload(ifr_ctx* ctx, const ifr_linear* w, ifr_dlinear** out);
+int ifr_linear_free(ifr_ctx* ctx, ifr_dlinear* w);
+/* Bytes of the device copy (codes + scale/zero), for roofline accounting. */
+size_t ifr_linear_bytes(const ifr_dlinear* w);
+
+/* Per-token int8 activation quantization with optional fused pre-ops.
+ * Replaces dashq::act_quant_ga64_batch / act_quant_ga64_dev
+ * (dashq.cpp:221-336, quant_gemm.cpp:3325-3392) for a per-row (GA = K)
+ * or GA = 64 slice.  x_d fp32 [M][K].  Outputs: q_d int8 [M][K],
+ * scale_d fp32 [M][K/ga], gsum_d fp32 [M][K/128] (sum of the int8 codes
+ * per 128-column group; may be NULL).
+ *   norm_w_d : if non-NULL, x is first replaced by RMSNorm(1+w)(x) (main.cpp:337-351)
+ *   rotate   : if 1, then x <- FWHT(x)/sqrt(K) (spinquant.cpp:586-604)
+ *   round    : 0 half-away-from-zero (trunk), 1 nearest-even (lm_head)
+ *   ga       : 0 = per row, else slice width (64) */
+int ifr_act_quant(ifr_ctx* ctx, const float* x_d, int32_t M, int32_t K,
+                  const float* norm_w_d, float eps, int32_t rotate, int32_t round,
+                  int32_t ga, int8_t* q_d, float* scale_d, float* gsum_d);
+
+/* W2A8 / W4A8 / W8A8 GEMM with int32 accumulation (replaces
+ * quant_gemm_dpas48 / dpas48_tiled, quant_gemm.cpp:3492-3791):
+ *   T(m,n,g) = sum_{k in g} a_q(m,k) * code(n,k)            (int32, exact)
+ *   S(m,g)   = sum_{k in g} a_q(m,k)                         (gsum_d)
+ *   acc(m,n) = fold over g ascending of
+ *                d = fma(-zero(n,g), S(m,g), T(m,n,g)); acc = fma(scale(n,g), d, acc)
+ *   y(m,n)   = fp16_rne(ascale(m) * acc(m,n))
+ * out_d fp16 [M][N].  tdump_d, if non-NULL, receives T as int32 [M][N][K/128]. */
+int ifr_quant_gemm(ifr_ctx* ctx, const ifr_dlinear* w, const int8_t* a_d,
+                   const float* ascale_d, const float* gsum_d, int32_t M,
+                   uint16_t* out_d, int32_t* tdump_d);
+
+/* Same GEMM over the interleaved [gate;up] pair with the SwiGLU epilogue
+ * mg = fp16(silu(g) * u), g,u the fp16 GEMM outputs (main.cpp:7754-7758,
+ * silumul_to_half quant_gemm.cpp:4209).  out_d fp16 [M][N_gate]. */
+int ifr_linear_upload_pair(ifr_ctx* ctx, const ifr_linear* gate, const ifr_linear* up,
+                           ifr_dlinear** out);
+int ifr_quant_gemm_swiglu(ifr_ctx* ctx, const ifr_dlinear* gate_up, const int8_t* a_d,
+                          const float* ascale_d, const float* gsum_d, int32_t M,
+                          uint16_t* out_d);
+
+/* ------------------------------------------------------------------------
+ * Engine: model load, paged KV, one mixed iteration.
+ * ---------------------------------------------------------------------- */
+typedef struct ifr_kv_cfg {
+  int32_t max_seqs;       /* sequence slots */
+  int32_t max_seq_tokens; /* per-sequence KV capacity (INTFER_KV_CAP analogue, main.cpp:4348-4361) */
+  int32_t pool_tokens;    /* total KV tokens in the page pool */
+  int32_t kv_int8;        /* 0 fp16 KV; 1 int8 KV with fp16 scale per (token, kv_head) */
+  int32_t max_rows;       /* largest M one ifr_forward call may carry */
+} ifr_kv_cfg;
+
+/* Upload + repack a model (replaces Engine::load, build_shards,
+ * preload_all, engine.cpp:552-743, :1071).  The host model may be freed
+ * afterwards. */
+int ifr_model_load(ifr_ctx* ctx, const ifr_host_model* m, const ifr_kv_cfg* kv);
+
+/* Sequence slots over the paged KV pool.  truncate = speculative rollback
+ * (main.cpp:11896-11915) and prefix reuse: KV beyond len is dropped. */
+int ifr_seq_open(ifr_ctx* ctx, int32_t* slot);
+int ifr_seq_close(ifr_ctx* ctx, int32_t slot);
+int ifr_seq_truncate(ifr_ctx* ctx, int32_t slot, int32_t len);
+int ifr_seq_len(ifr_ctx* ctx, int32_t slot, int32_t* len);
+/* Per-sequence KV capacity in tokens of the loaded model. */
+int ifr_kv_capacity(ifr_ctx* ctx, int32_t* tokens);
+/* Fill an open, empty sequence with len cached positions: k, v are fp32
+ * host arrays [layers][len][n_kv][head_dim]; values are stored exactly as
+ * the forward stores them (fp16 round, or int8 with an fp16 scale per
+ * (token, kv_head)).  Used for the configs' seeded cached contexts. */
+int ifr_seq_load_kv(ifr_ctx* ctx, int32_t slot, int32_t len, const float* k, const float* v);
+
+enum { IFR_ROW_DECODE = 0, IFR_ROW_PREFILL = 1, IFR_ROW_VERIFY = 2 };
+
+/* One row of the ragged batch (BatchItem, main.cpp:4831, extended with the
+ * verify kind).  Rows of one sequence must be contiguous with consecutive
+ * positions starting at that sequence's current KV length. */
+typedef struct ifr_row {
+  int32_t seq;   /* sequence slot */
+  int32_t pos;   /* absolute position of this row's token */
+  int32_t token; /* input token id */
+  int32_t kind;  /* IFR_ROW_* */
+  int32_t want;  /* 1: score this row (argmax, optional logits) */
+} ifr_row;
+
+/* One mixed iteration (replaces step_batch main.cpp:7519-8320 and the
+ * LinearBackend calls it makes).  best_out[M]: argmax (first max wins) for
+ * rows with want=1, -1 otherwise.  logits_out, if non-NULL, receives fp32
+ * [n_want][vocab] logits of the scored rows in row order.  The call appends
+ * every row's K/V to its sequence. */
+int ifr_forward(ifr_ctx* ctx, const ifr_row* rows, int32_t M, int32_t* best_out,
+                float* logits_out);
+
+/* Ragged joint attention alone over the resident KV of `layer` (kernel-level
+ * entry; replaces the host attention loop, main.cpp:7657-7701, and the
+ * demo flash kernels, src/attention/flash_attention.cpp:30-273).  Rows as in
+ * ifr_forward but their KV must already be present (pos < sequence length);
+ * nothing is appended.  q_h: fp16 bits [M][n_heads][head_dim]; out_h: fp32
+ * [M][n_heads*head_dim]. */
+int ifr_attention(ifr_ctx* ctx, int32_t layer, const ifr_row* rows, int32_t M,
+                  const uint16_t* q_h, float* out_h);
+
+/* Per-kernel device timing of the last ifr_forward (HIP events on the
+ * context stream), for the bench: names are "qgemm", "attention", ... */
+int ifr_set_timing(ifr_ctx* ctx, int32_t on);
+int ifr_get_timing(ifr_ctx* ctx, const char* kernel, double* total_ms, int64_t* launches,
+                   double* bytes);
+
+/* Test hook (no reference counterpart): copies the last forward's packing
+ * outputs to host buffers (any may be NULL).  units: 8 int32 per unit
+ * {seq, kv_head, row0, q_tokens, q_pos0, kv_lo, kv_hi, 0}. */
+int ifr_debug_pack(ifr_ctx* ctx, int32_t M, int32_t* cu_seqlens, int32_t* row_grp,
+                   int32_t* comb_base, int32_t* comb_nsplit, int32_t* comb_tok, int32_t* units,
+                   int32_t* n_units, int32_t* split);
+
+/* ------------------------------------------------------------------------
+ * Scheduler / serve (C++ host side above the ABI).
+ * ---------------------------------------------------------------------- */
+typedef struct ifr_sched ifr_sched;
+
+typedef struct ifr_sched_cfg {
+  int32_t chunk_m;    /* prefill rows per iteration (INTFER_PREFILL_CHUNK_M, default 128) */
+  int32_t live_cap;   /* live decode cap (serve_live_cap, <= 64) */
+  int32_t split_iter; /* 1: split path (chunk forward, then decode forward) */
+  int32_t round_robin;/* 1: rotate unfilled prefill heads (INTFER_PREFILL_RR) */
+  int32_t spec_k;     /* n-gram draft width for verify rows; 0 = off */
+} ifr_sched_cfg;
+
+int ifr_sched_create(ifr_ctx* ctx, const ifr_sched_cfg* cfg, ifr_sched** out);
+
+/* The scheduler talks to its model through this table, the counterpart of
+ * the reference scheduler calling step_batch over a LinearBackend
+ * (main.cpp:455-566).  ifr_sched_create fills it with the engine's own
+ * entry points; a test may pass another model (e.g. a CPU checker). */
+typedef struct ifr_sched_backend {
+  void* user;
+  int (*seq_open)(void* user, int32_t* slot);
+  int (*seq_close)(void* user, int32_t slot);
+  int (*seq_truncate)(void* user, int32_t slot, int32_t len);
+  int (*forward)(void* user, const ifr_row* rows, int32_t M, int32_t* best);
+  int32_t kv_capacity;
+} ifr_sched_backend;
+int ifr_sched_create_backend(const ifr_sched_backend* be, const ifr_sched_cfg* cfg,
+                             ifr_sched** out);
+int ifr_sched_destroy(ifr_sched* s);
+/* Admit a request (prompt token ids, max_new).  Returns its id. */
+int ifr_sched_submit(ifr_sched* s, const int32_t* prompt, int32_t n, int32_t max_new,
+                     int64_t* id);
+/* Run one serve iteration (serve_iteration, main.cpp:9203-9259).  Returns
+ * the number of rows in the forward(s) it ran, 0 when idle. */
+int ifr_sched_step(ifr_sched* s, int32_t* rows_run);
+/* Generated tokens of a request so far; *done=1 once finished. */
+int ifr_sched_result(ifr_sched* s, int64_t id, int32_t* out, int32_t cap, int32_t* n,
+                     int32_t* done);
+/* Row list of the last forward the scheduler ran (for replay parity). */
+int ifr_sched_last_rows(ifr_sched* s, ifr_row* out, int32_t cap, int32_t* n);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* INTFER_AMD_H */

@@ -1,0 +1,295 @@
+"""intfer_amd: MI355X-native mixed-batch M-row forward (continuous batching).
+
+Python is only the test/bench harness over the C-ABI in include/intfer_amd.h;
+the product is the gfx950 library intfer_amd/libintfer_amd.so (HIP kernels,
+the C++ engine and the C++ scheduler).  Names follow the reference engine:
+rows, sequences, pages, chunks, drafts.
+"""
+from __future__ import annotations
+
+import ctypes as C
+from dataclasses import dataclass
+from typing import Iterable, Sequence
+
+import numpy as np
+
+from . import _abi
+from ._abi import (KVCfg, Linear, ModelCfg, Row, SchedBackend, SchedCfg, ROW_DECODE, ROW_PREFILL,
+                   ROW_VERIFY, IfrError, check, lib)
+
+__all__ = ["Device", "Engine", "Scheduler", "SynthModel", "default_cfg", "make_linear", "rows_array",
+           "ROW_DECODE", "ROW_PREFILL", "ROW_VERIFY", "IfrError", "ModelCfg", "KVCfg", "SchedCfg",
+           "Row", "Linear", "lib"]
+
+
+def default_cfg(**over) -> ModelCfg:
+    c = ModelCfg()
+    lib().ifr_default_cfg(C.byref(c))
+    for k, v in over.items():
+        setattr(c, k, v)
+    return c
+
+
+class SynthModel:
+    """Seeded synthetic decoder (owned by the library)."""
+
+    def __init__(self, cfg: ModelCfg, seed: int, bits: int = 2):
+        self.cfg = cfg
+        self.ptr = lib().ifr_synth_model(C.byref(cfg), C.c_uint64(seed), bits)
+        if not self.ptr:
+            raise ValueError("ifr_synth_model rejected the configuration")
+
+    @property
+    def model(self):
+        return self.ptr.contents
+
+    def layer(self, l: int):
+        return self.ptr.contents.layers[l]
+
+    def embed(self) -> np.ndarray:
+        c = self.cfg
+        return np.ctypeslib.as_array(self.ptr.contents.embed, shape=(c.vocab, c.hidden))
+
+    def close(self):
+        if self.ptr:
+            lib().ifr_synth_free(self.ptr)
+            self.ptr = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+@dataclass
+class HostLinear:
+    """A logical quantized linear held in numpy arrays (keeps them alive)."""
+    N: int
+    K: int
+    bits: int
+    codes: np.ndarray   # packed uint8
+    scale: np.ndarray   # uint16 fp16 bits [N][K/128]
+    zero: np.ndarray    # uint16 fp16 bits [N][K/128]
+    values: np.ndarray  # unpacked uint8 [N][K]
+
+    @property
+    def struct(self) -> Linear:
+        s = Linear()
+        s.N, s.K, s.bits, s.group = self.N, self.K, self.bits, 128
+        s.codes = self.codes.ctypes.data_as(C.POINTER(C.c_uint8))
+        s.scale = self.scale.ctypes.data_as(C.POINTER(C.c_uint16))
+        s.zero = self.zero.ctypes.data_as(C.POINTER(C.c_uint16))
+        return s
+
+
+def pack_codes(vals: np.ndarray, bits: int) -> np.ndarray:
+    """Row-major LSB-first packing (reference dashq pack_codes applied row-major)."""
+    flat = vals.reshape(-1).astype(np.uint8)
+    if bits == 8:
+        return flat.copy()
+    per = 8 // bits
+    flat = flat.reshape(-1, per)
+    out = np.zeros(flat.shape[0], dtype=np.uint8)
+    for j in range(per):
+        out |= (flat[:, j] & ((1 << bits) - 1)) << (j * bits)
+    return out
+
+
+def make_linear(N: int, K: int, bits: int, rng: np.random.Generator, scale_sigma=0.02,
+                zero=None) -> HostLinear:
+    vals = rng.integers(0, 1 << bits, size=(N, K), dtype=np.uint8)
+    ng = K // 128
+    sc = np.abs(rng.normal(0.0, scale_sigma, size=(N, ng))).astype(np.float16).view(np.uint16)
+    z = ((1 << bits) - 1) / 2.0 if zero is None else zero
+    if np.isscalar(z):
+        zz = np.full((N, ng), z, dtype=np.float16).view(np.uint16)
+    else:
+        zz = np.asarray(z, dtype=np.float16).reshape(N, ng).view(np.uint16)
+    return HostLinear(N, K, bits, pack_codes(vals, bits), sc.copy(), zz.copy(), vals)
+
+
+def rows_array(rows: Iterable[Sequence[int]]):
+    rows = list(rows)
+    arr = (Row * len(rows))()
+    for i, r in enumerate(rows):
+        seq, pos, tok, kind, want = r
+        arr[i].seq, arr[i].pos, arr[i].token, arr[i].kind, arr[i].want = seq, pos, tok, kind, want
+    return arr
+
+
+class DevBuf:
+    def __init__(self, dev: "Device", nbytes: int):
+        self.dev = dev
+        self.nbytes = nbytes
+        self.ptr = C.c_void_p()
+        check(lib().ifr_malloc(dev.ctx, nbytes, C.byref(self.ptr)), "ifr_malloc")
+
+    @property
+    def p(self):
+        return self.ptr
+
+    def free(self):
+        if self.ptr:
+            lib().ifr_free(self.dev.ctx, self.ptr)
+            self.ptr = C.c_void_p()
+
+
+class Device:
+    """One HIP context (one stream) on one GPU."""
+
+    def __init__(self, device: int = 0):
+        self.ctx = C.c_void_p()
+        check(lib().ifr_ctx_create(device, C.byref(self.ctx)), "ifr_ctx_create")
+        self._bufs: list[DevBuf] = []
+
+    def alloc(self, nbytes: int) -> DevBuf:
+        b = DevBuf(self, nbytes)
+        self._bufs.append(b)
+        return b
+
+    def upload(self, arr: np.ndarray) -> DevBuf:
+        arr = np.ascontiguousarray(arr)
+        b = self.alloc(arr.nbytes)
+        check(lib().ifr_h2d(self.ctx, b.p, arr.ctypes.data_as(C.c_void_p), arr.nbytes), "ifr_h2d")
+        return b
+
+    def download(self, b: DevBuf, dtype, shape) -> np.ndarray:
+        out = np.empty(shape, dtype=dtype)
+        check(lib().ifr_d2h(self.ctx, out.ctypes.data_as(C.c_void_p), b.p, out.nbytes), "ifr_d2h")
+        return out
+
+    def zeros(self, nbytes: int) -> DevBuf:
+        b = self.alloc(nbytes)
+        check(lib().ifr_memset(self.ctx, b.p, 0, nbytes), "ifr_memset")
+        return b
+
+    def sync(self):
+        check(lib().ifr_sync(self.ctx), "ifr_sync")
+
+    def close(self):
+        if self.ctx:
+            for b in self._bufs:
+                b.free()
+            self._bufs.clear()
+            lib().ifr_ctx_destroy(self.ctx)
+            self.ctx = C.c_void_p()
+
+
+class Engine:
+    """The device forward over one loaded model."""
+
+    def __init__(self, dev: Device, model: SynthModel, max_seqs=8, max_seq_tokens=4096,
+                 pool_tokens=None, kv_int8=0, max_rows=640):
+        self.dev = dev
+        self.cfg = model.cfg
+        kv = KVCfg()
+        kv.max_seqs, kv.max_seq_tokens = max_seqs, max_seq_tokens
+        kv.pool_tokens = pool_tokens or max_seqs * max_seq_tokens
+        kv.kv_int8, kv.max_rows = kv_int8, max_rows
+        self.kv = kv
+        check(lib().ifr_model_load(dev.ctx, model.ptr, C.byref(kv)), "ifr_model_load")
+
+    def seq_open(self) -> int:
+        s = C.c_int32()
+        check(lib().ifr_seq_open(self.dev.ctx, C.byref(s)), "ifr_seq_open")
+        return s.value
+
+    def seq_close(self, s: int):
+        check(lib().ifr_seq_close(self.dev.ctx, s), "ifr_seq_close")
+
+    def seq_truncate(self, s: int, n: int):
+        check(lib().ifr_seq_truncate(self.dev.ctx, s, n), "ifr_seq_truncate")
+
+    def seq_len(self, s: int) -> int:
+        n = C.c_int32()
+        check(lib().ifr_seq_len(self.dev.ctx, s, C.byref(n)), "ifr_seq_len")
+        return n.value
+
+    def load_kv(self, s: int, k: np.ndarray, v: np.ndarray):
+        k = np.ascontiguousarray(k, dtype=np.float32)
+        v = np.ascontiguousarray(v, dtype=np.float32)
+        check(lib().ifr_seq_load_kv(self.dev.ctx, s, k.shape[1],
+                                     k.ctypes.data_as(_abi.pf32), v.ctypes.data_as(_abi.pf32)),
+              "ifr_seq_load_kv")
+
+    def forward(self, rows, logits: bool = False):
+        arr = rows if isinstance(rows, C.Array) else rows_array(rows)
+        M = len(arr)
+        best = np.full(M, -1, dtype=np.int32)
+        nwant = sum(1 for r in arr if r.want)
+        lg = np.empty((nwant, self.cfg.vocab), dtype=np.float32) if logits else None
+        check(lib().ifr_forward(self.dev.ctx, arr, M, best.ctypes.data_as(_abi.pi32),
+                                lg.ctypes.data_as(_abi.pf32) if logits else None), "ifr_forward")
+        return (best, lg) if logits else best
+
+    def attention(self, layer: int, rows, q_fp16: np.ndarray) -> np.ndarray:
+        """Joint ragged attention over resident KV; q_fp16 [M][nq][hd] float16."""
+        arr = rows if isinstance(rows, C.Array) else rows_array(rows)
+        M = len(arr)
+        q = np.ascontiguousarray(q_fp16, dtype=np.float16)
+        out = np.empty((M, self.cfg.n_heads * self.cfg.head_dim), np.float32)
+        check(lib().ifr_attention(self.dev.ctx, layer, arr, M, q.ctypes.data_as(C.c_void_p),
+                                  out.ctypes.data_as(_abi.pf32)), "ifr_attention")
+        return out
+
+    def set_timing(self, on: bool):
+        check(lib().ifr_set_timing(self.dev.ctx, 1 if on else 0), "ifr_set_timing")
+
+    def timing(self, kernel: str):
+        ms, n, b = C.c_double(), C.c_int64(), C.c_double()
+        check(lib().ifr_get_timing(self.dev.ctx, kernel.encode(), C.byref(ms), C.byref(n),
+                                   C.byref(b)), "ifr_get_timing")
+        return ms.value, n.value, b.value
+
+
+class Scheduler:
+    """The C++ continuous-batching scheduler over an Engine, or over a
+    backend table (SchedBackend) for CPU-side checks."""
+
+    def __init__(self, engine: Engine | None = None, chunk_m=128, live_cap=64, split_iter=0,
+                 round_robin=1, spec_k=0, backend: SchedBackend | None = None):
+        cfg = SchedCfg()
+        cfg.chunk_m, cfg.live_cap, cfg.split_iter = chunk_m, live_cap, split_iter
+        cfg.round_robin, cfg.spec_k = round_robin, spec_k
+        self.h = C.c_void_p()
+        self._keep = backend
+        if backend is not None:
+            check(lib().ifr_sched_create_backend(C.byref(backend), C.byref(cfg), C.byref(self.h)),
+                  "ifr_sched_create_backend")
+        else:
+            check(lib().ifr_sched_create(engine.dev.ctx, C.byref(cfg), C.byref(self.h)),
+                  "ifr_sched_create")
+
+    def submit(self, prompt: Sequence[int], max_new: int) -> int:
+        p = np.ascontiguousarray(prompt, dtype=np.int32)
+        rid = C.c_int64()
+        check(lib().ifr_sched_submit(self.h, p.ctypes.data_as(_abi.pi32), len(p), max_new,
+                                     C.byref(rid)), "ifr_sched_submit")
+        return rid.value
+
+    def step(self) -> int:
+        n = C.c_int32()
+        check(lib().ifr_sched_step(self.h, C.byref(n)), "ifr_sched_step")
+        return n.value
+
+    def result(self, rid: int):
+        n, done = C.c_int32(), C.c_int32()
+        check(lib().ifr_sched_result(self.h, rid, None, 0, C.byref(n), C.byref(done)),
+              "ifr_sched_result")
+        out = np.zeros(max(n.value, 1), dtype=np.int32)
+        check(lib().ifr_sched_result(self.h, rid, out.ctypes.data_as(_abi.pi32), n.value,
+                                     C.byref(n), C.byref(done)), "ifr_sched_result")
+        return out[:n.value].tolist(), bool(done.value)
+
+    def last_rows(self):
+        n = C.c_int32()
+        check(lib().ifr_sched_last_rows(self.h, None, 0, C.byref(n)), "ifr_sched_last_rows")
+        arr = (Row * max(n.value, 1))()
+        check(lib().ifr_sched_last_rows(self.h, arr, n.value, C.byref(n)), "ifr_sched_last_rows")
+        return [(r.seq, r.pos, r.token, r.kind, r.want) for r in arr[:n.value]]
+
+    def close(self):
+        if self.h:
+            lib().ifr_sched_destroy(self.h)
+            self.h = C.c_void_p()

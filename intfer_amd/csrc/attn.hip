@@ -1,0 +1,244 @@
+// Ragged joint prefill + decode GQA attention on gfx950 (fp16 or int8 KV).
+//
+// Semantics follow the reference host loop (examples/intfer_cli/main.cpp:
+// 7657-7701): per row and q head, s_t = (q . k_t) / sqrt(hd) over the
+// sequence's KV positions t <= pos, softmax, o = sum_t p_t v_t.  Prefill and
+// verify rows of a sequence see the rows before them in the same chunk,
+// because KV is appended for every row before attention runs.
+//
+// Work decomposition: the pack kernel emits units (sequence, kv head, q-block
+// of up to 8 tokens, KV split).  One wave runs one unit: the q-block's
+// tokens x the GQA group (2 heads) form the 16 columns of S^T = K Q^T and of
+// O^T = V^T P^T, so K is the MFMA A operand row-major and V is read from its
+// transposed page; each 32-token page is one step with wave-level online
+// softmax (base-2 exponent).  Partial (m, l, O) per unit are merged by the
+// combine kernel, which also emits the per-token int8 input of the O
+// projection.  Decode units use 2 of the 16 columns; the kernel is bound by
+// the KV stream, which is read exactly once per unit.
+#include "ifr_dev.h"
+#include "ifr_kernels.h"
+
+namespace ifrk {
+namespace {
+
+constexpr int kHD = 128;
+constexpr int kPage = 32;
+
+template <bool KV8>
+__global__ __launch_bounds__(256) void attn_kernel(AttnArgs p, KVLayout kv) {
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int u = blockIdx.x * 4 + w;
+  if (u >= p.n_units) return;
+  const AttnUnit un = p.units[u];
+  const int G = p.nq / kv.nkv;
+  const int rows = un.qn * G;
+  const int c = lane & 15, g = lane >> 4;
+  const bool colv = c < rows;
+  const int qtok = c / G, qj = c % G;
+  const int qpos = un.qpos0 + qtok;
+
+  // Q^T as the B operand: MFMA i covers dims 32i + 8g .. +8 for column c.
+  v8h qf[4];
+  if (colv) {
+    const _Float16* qp = reinterpret_cast<const _Float16*>(p.q) +
+                         ((size_t)(un.row0 + qtok) * p.nq + un.kvh * G + qj) * kHD + 8 * g;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) qf[i] = *reinterpret_cast<const v8h*>(qp + 32 * i);
+  } else {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) qf[i] = (v8h){0, 0, 0, 0, 0, 0, 0, 0};
+  }
+
+  float m_run = -INFINITY, l_run = 0.0f;
+  v4f o[8];
+#pragma unroll
+  for (int d = 0; d < 8; ++d) o[d] = (v4f){0.f, 0.f, 0.f, 0.f};
+
+  const int32_t* bt = kv.block_table + (size_t)un.seq * kv.max_pages;
+  for (int t0 = un.kv_lo; t0 < un.kv_hi; t0 += kPage) {
+    const size_t pb = (size_t)bt[t0 / kPage] * kv.nkv + un.kvh;
+    // ---- issue K and V loads for this page
+    v8h ka[2][4];
+    v8h va[8];
+    float ks[2][4], vs[8];
+    if constexpr (!KV8) {
+      const _Float16* kp = reinterpret_cast<const _Float16*>(kv.kpool) + pb * kPage * kHD;
+      const _Float16* vp = reinterpret_cast<const _Float16*>(kv.vpool) + pb * kHD * kPage;
+#pragma unroll
+      for (int h = 0; h < 2; ++h)
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          ka[h][i] = *reinterpret_cast<const v8h*>(kp + (2 * c + h) * kHD + 32 * i + 8 * g);
+#pragma unroll
+      for (int d = 0; d < 8; ++d)
+        va[d] = *reinterpret_cast<const v8h*>(vp + (16 * d + c) * kPage + 8 * g);
+    } else {
+      const int8_t* kp = reinterpret_cast<const int8_t*>(kv.kpool) + pb * kPage * kHD;
+      const int8_t* vp = reinterpret_cast<const int8_t*>(kv.vpool) + pb * kHD * kPage;
+#pragma unroll
+      for (int h = 0; h < 2; ++h)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const uint2 raw = *reinterpret_cast<const uint2*>(kp + (2 * c + h) * kHD + 32 * i + 8 * g);
+#pragma unroll
+          for (int b = 0; b < 8; ++b)
+            ka[h][i][b] = (_Float16)(int8_t)(((b < 4 ? raw.x : raw.y) >> (8 * (b & 3))) & 0xFF);
+        }
+#pragma unroll
+      for (int d = 0; d < 8; ++d) {
+        const uint2 raw = *reinterpret_cast<const uint2*>(vp + (16 * d + c) * kPage + 8 * g);
+#pragma unroll
+        for (int b = 0; b < 8; ++b)
+          va[d][b] = (_Float16)(int8_t)(((b < 4 ? raw.x : raw.y) >> (8 * (b & 3))) & 0xFF);
+      }
+      const uint16_t* ksc = kv.kscale + pb * kPage;
+      const uint16_t* vsc = kv.vscale + pb * kPage;
+#pragma unroll
+      for (int h = 0; h < 2; ++h)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) ks[h][r] = ifrd::h2f(ksc[8 * g + 2 * r + h]);
+#pragma unroll
+      for (int j = 0; j < 8; ++j) vs[j] = ifrd::h2f(vsc[8 * g + j]);
+    }
+    // ---- S^T: tile h covers tokens 2c' + h; lane (c, g) reg r -> token 8g + 2r + h.
+    v4f s[2];
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      s[h] = (v4f){0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int i = 0; i < 4; ++i) s[h] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ka[h][i], qf[i], s[h], 0, 0, 0);
+    }
+    float sv[8];
+    float mt = -INFINITY;
+#pragma unroll
+    for (int r = 0; r < 4; ++r)
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const int t = t0 + 8 * g + 2 * r + h;
+        float v = s[h][r];
+        if constexpr (KV8) v *= ks[h][r];
+        v *= p.scale_log2;
+        if (!colv || t > qpos || t >= un.kv_hi) v = -INFINITY;
+        sv[2 * r + h] = v;
+        mt = fmaxf(mt, v);
+      }
+    mt = fmaxf(mt, __shfl_xor(mt, 16, 64));
+    mt = fmaxf(mt, __shfl_xor(mt, 32, 64));
+    const float m_new = fmaxf(m_run, mt);
+    const float m_use = (m_new == -INFINITY) ? 0.0f : m_new;
+    const float alpha = exp2f(m_run - m_use);
+    v8h pb16;
+    float rs = 0.0f;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const _Float16 ph = (_Float16)exp2f(sv[j] - m_use);
+      rs += (float)ph;
+      if constexpr (KV8) pb16[j] = (_Float16)((float)ph * vs[j]);
+      else pb16[j] = ph;
+    }
+    rs += __shfl_xor(rs, 16, 64);
+    rs += __shfl_xor(rs, 32, 64);
+    l_run = l_run * alpha + rs;
+    m_run = m_new;
+#pragma unroll
+    for (int d = 0; d < 8; ++d) {
+      o[d] *= alpha;
+      o[d] = __builtin_amdgcn_mfma_f32_16x16x32_f16(va[d], pb16, o[d], 0, 0, 0);
+    }
+  }
+  // ---- partials: O^T lane (c, g) reg r -> dim 16d + 4g + r of column c.
+  if (colv) {
+    float* po = p.part_o + ((size_t)u * 16 + c) * kHD;
+#pragma unroll
+    for (int d = 0; d < 8; ++d)
+      *reinterpret_cast<v4f*>(po + 16 * d + 4 * g) = o[d];
+    if (g == 0) {
+      p.part_ml[((size_t)u * 16 + c) * 2 + 0] = m_run;
+      p.part_ml[((size_t)u * 16 + c) * 2 + 1] = l_run;
+    }
+  }
+}
+
+// Merge the KV-split partials of one row for all heads, then per-token int8
+// quantization (half-away) of the [nq*hd] attention row for the O projection.
+__global__ __launch_bounds__(256) void combine_kernel(CombineArgs a) {
+  extern __shared__ float sh[];
+  const int m = blockIdx.x;
+  const int N = a.nq * a.hd;       // 2048
+  const int per = N / 256;         // dims per thread (8)
+  const int G = a.nq / a.nkv;
+  const int e0 = threadIdx.x * per;
+  const int h = e0 / a.hd, d0 = e0 % a.hd;
+  const int kvh = h / G, j = h % G;
+  const int ns = a.comb_nsplit[m];
+  const int base = a.comb_base[m] + kvh * ns;
+  const int col = a.comb_tok[m] * G + j;
+  float mx = -INFINITY;
+  for (int s = 0; s < ns; ++s) mx = fmaxf(mx, a.part_ml[((size_t)(base + s) * 16 + col) * 2]);
+  float L = 0.0f;
+  float acc[16];
+  for (int i = 0; i < per; ++i) acc[i] = 0.0f;
+  for (int s = 0; s < ns; ++s) {
+    const size_t pi = (size_t)(base + s) * 16 + col;
+    const float ms = a.part_ml[pi * 2];
+    if (ms == -INFINITY) continue;
+    const float f = exp2f(ms - mx);
+    L += f * a.part_ml[pi * 2 + 1];
+    const float* po = a.part_o + pi * a.hd + d0;
+    for (int i = 0; i < per; ++i) acc[i] += f * po[i];
+  }
+  const float invL = 1.0f / L;
+  float* x = sh;
+  int* codes = reinterpret_cast<int*>(sh + N);
+  __shared__ float red[8];
+  float amax = 0.0f;
+  for (int i = 0; i < per; ++i) {
+    const float v = acc[i] * invL;
+    x[e0 + i] = v;
+    amax = fmaxf(amax, fabsf(v));
+    if (a.attn_out) a.attn_out[(size_t)m * N + e0 + i] = v;
+  }
+  amax = ifrd::wave_max(amax);
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = amax;
+  __syncthreads();
+  const float mxa = fmaxf(1e-6f, fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3])));
+  const float sc = mxa / 127.0f;
+  const float inv = 1.0f / sc;
+  if (threadIdx.x == 0) a.qscale[m] = sc;
+  for (int i = 0; i < per; ++i) {
+    const int c = ifrd::quant_half_away(x[e0 + i], inv);
+    a.q[(size_t)m * N + e0 + i] = (int8_t)c;
+    codes[e0 + i] = c;
+  }
+  __syncthreads();
+  for (int gg = threadIdx.x; gg < N / 128; gg += 256) {
+    int S = 0;
+    for (int k = gg * 128; k < gg * 128 + 128; ++k) S += codes[k];
+    a.gsum[(size_t)m * (N / 128) + gg] = (float)S;
+  }
+}
+
+}  // namespace
+
+hipError_t launch_attention(const AttnArgs& a, const KVLayout& kv, hipStream_t st) {
+  if (a.n_units <= 0) return hipSuccess;
+  if (kv.hd != kHD || kv.page != kPage || a.nq % kv.nkv != 0 || (a.nq / kv.nkv) > 16 ||
+      !a.units || !a.q || !a.part_o || !a.part_ml)
+    return hipErrorInvalidValue;
+  const dim3 grid((a.n_units + 3) / 4), block(256);
+  if (kv.kv_int8) hipLaunchKernelGGL(attn_kernel<true>, grid, block, 0, st, a, kv);
+  else hipLaunchKernelGGL(attn_kernel<false>, grid, block, 0, st, a, kv);
+  return hipGetLastError();
+}
+
+hipError_t launch_combine(const CombineArgs& a, hipStream_t st) {
+  if (a.M <= 0) return hipSuccess;
+  const int N = a.nq * a.hd;
+  if (N % 256 != 0 || N / 256 > 16 || N % 128 != 0 || a.hd != kHD || !a.q || !a.qscale || !a.gsum)
+    return hipErrorInvalidValue;
+  const size_t lds = (size_t)2 * N * sizeof(float);
+  hipLaunchKernelGGL(combine_kernel, dim3(a.M), dim3(256), lds, st, a);
+  return hipGetLastError();
+}
+
+}  // namespace ifrk

@@ -1,0 +1,1093 @@
+// Engine: the C-ABI of include/intfer_amd.h over HIP on one gfx950 GPU.
+//
+// Replaces the reference's Engine + GpuBackend + step_batch device traffic
+// (include/intfer/engine.hpp:37-562, examples/intfer_cli/main.cpp:1027-2866,
+// :7519-8320): weights, KV and every intermediate stay resident in HBM; one
+// ifr_forward enqueues the whole 28-layer mixed iteration on one stream and
+// reads back only the argmax ids (and logits when asked).
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cmath>
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <string>
+#include <vector>
+
+#include "ifr_half.h"
+#include "ifr_kernels.h"
+#include "intfer_amd.h"
+
+using ifrk::DLin;
+
+namespace {
+
+thread_local std::string g_err;
+
+int fail(int code, const char* fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof(buf), fmt, ap);
+  va_end(ap);
+  g_err = buf;
+  return code;
+}
+
+#define HIPCHK(expr)                                                                   \
+  do {                                                                                 \
+    hipError_t e_ = (expr);                                                            \
+    if (e_ != hipSuccess)                                                              \
+      return fail(e_ == hipErrorInvalidValue ? IFR_EINVAL : IFR_EDEVICE, "%s: %s (%s:%d)", \
+                  #expr, hipGetErrorString(e_), __FILE__, __LINE__);                   \
+  } while (0)
+
+constexpr int kPage = 32;
+
+constexpr int kSplit = 256;  // KV tokens per attention unit
+
+struct Layer {
+  DLin qkv[3];     // fused QKV in qkv[0] when all widths match (nqkv = 1)
+  int nqkv = 1;
+  int qkv_off[3] = {0, 0, 0};
+  DLin o, down;
+  DLin gu[2];      // paired gate/up in gu[0] (ngu = 1) or separate gate, up
+  int ngu = 1;
+  float *in_ln = nullptr, *post_ln = nullptr, *q_norm = nullptr, *k_norm = nullptr;
+};
+
+struct Timer {
+  std::string name;
+  hipEvent_t a, b;
+  double bytes;
+};
+
+struct Stat {
+  double ms = 0, bytes = 0;
+  int64_t n = 0;
+};
+
+struct Seq {
+  bool open = false;
+  int len = 0;
+  std::vector<int> pages;
+};
+
+}  // namespace
+
+struct ifr_dlinear {
+  DLin d;
+};
+
+struct ifr_ctx {
+  int device = 0;
+  hipStream_t st = nullptr;
+  // model
+  bool loaded = false;
+  ifr_model_cfg cfg{};
+  ifr_kv_cfg kv{};
+  std::vector<Layer> layers;
+  std::vector<void*> allocs;
+  float* embed = nullptr;
+  float* final_norm = nullptr;
+  uint32_t* lm_w = nullptr;
+  uint16_t* lm_s = nullptr;
+  float *rope_cos = nullptr, *rope_sin = nullptr;
+  // paged KV
+  int n_pages = 0, max_pages = 0;
+  std::vector<void*> kpool, vpool;
+  std::vector<uint16_t*> kscale, vscale;
+  int32_t* bt_d = nullptr;
+  int32_t* bt_h = nullptr;  // pinned
+  std::vector<int> free_pages;
+  std::vector<Seq> seqs;
+  // workspaces
+  int maxM = 0, max_units = 0;
+  int32_t* rows_d = nullptr;
+  int32_t* rows_h = nullptr;  // pinned
+  float* resid = nullptr;
+  int8_t* aq = nullptr;
+  float* as = nullptr;
+  float* gs = nullptr;
+  uint16_t* qkv = nullptr;
+  uint16_t* qbuf = nullptr;
+  uint16_t* y = nullptr;
+  uint16_t* mg = nullptr;
+  uint16_t* gu = nullptr;
+  ifrk::PackOut pk{};
+  int32_t* row_tok = nullptr;
+  float* part_o = nullptr;
+  float* part_ml = nullptr;
+  int8_t* lm_aq = nullptr;
+  float* lm_as = nullptr;
+  float* lm_pv = nullptr;
+  int32_t* lm_pi = nullptr;
+  int32_t* best_d = nullptr;
+  int32_t* best_h = nullptr;  // pinned
+  float* logits_d = nullptr;
+  size_t logits_cap = 0;
+  // timing
+  bool timing = false;
+  std::vector<Timer> timers;
+  std::vector<std::pair<std::string, Stat>> stats;
+  // last forward's split (for tests / bench notes)
+  int last_split = 0, last_units = 0;
+  int qb = 8;  // q-block tokens per attention unit: 16 MFMA columns / GQA group
+
+  void* dalloc(size_t bytes) {
+    void* p = nullptr;
+    if (hipMalloc(&p, bytes == 0 ? 16 : bytes) != hipSuccess) return nullptr;
+    allocs.push_back(p);
+    return p;
+  }
+};
+
+namespace {
+
+Stat& stat_of(ifr_ctx* c, const std::string& n) {
+  for (auto& s : c->stats)
+    if (s.first == n) return s.second;
+  c->stats.push_back({n, Stat()});
+  return c->stats.back().second;
+}
+
+// Bracket one launch with events when timing is on.
+struct Scope {
+  ifr_ctx* c;
+  Timer t;
+  bool on;
+  Scope(ifr_ctx* c_, const char* name, double bytes) : c(c_), on(c_->timing) {
+    if (!on) return;
+    t.name = name;
+    t.bytes = bytes;
+    hipEventCreate(&t.a);
+    hipEventCreate(&t.b);
+    hipEventRecord(t.a, c->st);
+  }
+  ~Scope() {
+    if (!on) return;
+    hipEventRecord(t.b, c->st);
+    c->timers.push_back(t);
+  }
+};
+
+void flush_timers(ifr_ctx* c) {
+  for (auto& t : c->timers) {
+    float ms = 0;
+    hipEventSynchronize(t.b);
+    hipEventElapsedTime(&ms, t.a, t.b);
+    Stat& s = stat_of(c, t.name);
+    s.ms += ms;
+    s.n += 1;
+    s.bytes += t.bytes;
+    hipEventDestroy(t.a);
+    hipEventDestroy(t.b);
+  }
+  c->timers.clear();
+}
+
+int check_linear(const ifr_linear* w) {
+  if (!w || !w->codes || !w->scale || !w->zero)
+    return fail(IFR_EINVAL, "linear: null buffer");
+  if (w->bits != 2 && w->bits != 4 && w->bits != 8)
+    return fail(IFR_EDECLINE, "linear: bits %d not in {2,4,8}", w->bits);
+  if (w->group != 128) return fail(IFR_EDECLINE, "linear: group %d != 128", w->group);
+  if (w->N <= 0 || w->K <= 0 || w->N % 16 || w->K % 128)
+    return fail(IFR_EDECLINE, "linear: N %d must be a multiple of 16, K %d of 128", w->N, w->K);
+  return IFR_OK;
+}
+
+size_t code_bytes(int N, int K, int bits) { return (size_t)N * K * bits / 8; }
+size_t sz_bytes(int N, int K) { return (size_t)N * (K / 128) * 4; }
+
+// Upload `count` linears with equal bits and K as one device linear.
+// pair=1: exactly two (gate, up) interleaved per 16-column tile.
+int upload_group(ifr_ctx* c, const ifr_linear* const* ws, int count, int pair, DLin& d,
+                 bool own_tracked) {
+  const int K = ws[0]->K, bits = ws[0]->bits;
+  int N = 0;
+  for (int i = 0; i < count; ++i) {
+    if (int r = check_linear(ws[i])) return r;
+    if (ws[i]->K != K || ws[i]->bits != bits) return fail(IFR_EINVAL, "group: K/bits mismatch");
+    N += ws[i]->N;
+  }
+  if (pair && (count != 2 || ws[0]->N != ws[1]->N)) return fail(IFR_EINVAL, "pair: shape mismatch");
+  d.N = N;
+  d.K = K;
+  d.bits = bits;
+  d.ng = K / 128;
+  d.nsteps = K / 64;
+  d.pair = pair;
+  const size_t cb = code_bytes(N, K, bits), sb = sz_bytes(N, K);
+  std::vector<uint32_t> hc(cb / 4), hs(sb / 4);
+  int tile_off = 0;
+  for (int i = 0; i < count; ++i) {
+    if (pair)
+      ifrk::pack_linear_host(ws[i]->codes, ws[i]->scale, ws[i]->zero, ws[i]->N, K, bits, hc.data(),
+                             hs.data(), 2, i);
+    else
+      ifrk::pack_linear_host(ws[i]->codes, ws[i]->scale, ws[i]->zero, ws[i]->N, K, bits, hc.data(),
+                             hs.data(), 1, tile_off);
+    tile_off += ws[i]->N / 16;
+  }
+  void* pc = nullptr;
+  void* ps = nullptr;
+  if (own_tracked) {
+    pc = c->dalloc(cb);
+    ps = c->dalloc(sb);
+    if (!pc || !ps) return fail(IFR_ENOMEM, "hipMalloc weights (%zu B)", cb + sb);
+  } else {
+    HIPCHK(hipMalloc(&pc, cb));
+    if (hipMalloc(&ps, sb) != hipSuccess) {
+      hipFree(pc);
+      return fail(IFR_ENOMEM, "hipMalloc scales");
+    }
+  }
+  HIPCHK(hipMemcpy(pc, hc.data(), cb, hipMemcpyHostToDevice));
+  HIPCHK(hipMemcpy(ps, hs.data(), sb, hipMemcpyHostToDevice));
+  d.codes = static_cast<uint32_t*>(pc);
+  d.sz = static_cast<uint32_t*>(ps);
+  d.bytes = cb + sb;
+  return IFR_OK;
+}
+
+template <typename T>
+int upload(ifr_ctx* c, T** dst, const T* src, size_t n) {
+  *dst = static_cast<T*>(c->dalloc(n * sizeof(T)));
+  if (!*dst) return fail(IFR_ENOMEM, "hipMalloc %zu B", n * sizeof(T));
+  HIPCHK(hipMemcpy(*dst, src, n * sizeof(T), hipMemcpyHostToDevice));
+  return IFR_OK;
+}
+
+template <typename T>
+int walloc(ifr_ctx* c, T** dst, size_t n) {
+  *dst = static_cast<T*>(c->dalloc(n * sizeof(T)));
+  if (!*dst) return fail(IFR_ENOMEM, "hipMalloc %zu B", n * sizeof(T));
+  return IFR_OK;
+}
+
+void release_model(ifr_ctx* c) {
+  if (c->st) hipStreamSynchronize(c->st);
+  for (void* p : c->allocs) hipFree(p);
+  c->allocs.clear();
+  if (c->bt_h) hipHostFree(c->bt_h);
+  if (c->rows_h) hipHostFree(c->rows_h);
+  if (c->best_h) hipHostFree(c->best_h);
+  c->bt_h = nullptr;
+  c->rows_h = nullptr;
+  c->best_h = nullptr;
+  c->layers.clear();
+  c->kpool.clear();
+  c->vpool.clear();
+  c->kscale.clear();
+  c->vscale.clear();
+  c->seqs.clear();
+  c->free_pages.clear();
+  c->logits_d = nullptr;
+  c->logits_cap = 0;
+  c->loaded = false;
+}
+
+// Units the pack kernel will emit for a given split (same formula).
+long count_units(const std::vector<int>& g_pos0, const std::vector<int>& g_len, int nkv, int split,
+                 int qb) {
+  long n = 0;
+  for (size_t g = 0; g < g_len.size(); ++g) {
+    const int nb = (g_len[g] + qb - 1) / qb;
+    for (int b = 0; b < nb; ++b) {
+      const int kvhi = g_pos0[g] + std::min((b + 1) * qb, g_len[g]);
+      n += (long)nkv * ((kvhi + split - 1) / split);
+    }
+  }
+  return n;
+}
+
+}  // namespace
+
+extern "C" {
+
+const char* ifr_last_error(void) { return g_err.c_str(); }
+
+int ifr_ctx_create(int32_t device, ifr_ctx** out) {
+  if (!out) return fail(IFR_EINVAL, "out is null");
+  *out = nullptr;
+  int n = 0;
+  if (hipGetDeviceCount(&n) != hipSuccess || n <= 0) return fail(IFR_EDEVICE, "no HIP device");
+  if (device < 0 || device >= n) return fail(IFR_EINVAL, "device %d of %d", device, n);
+  HIPCHK(hipSetDevice(device));
+  hipDeviceProp_t prop;
+  HIPCHK(hipGetDeviceProperties(&prop, device));
+  if (std::strncmp(prop.gcnArchName, "gfx950", 6) != 0)
+    return fail(IFR_EDEVICE, "device %d is %s; this build targets gfx950", device, prop.gcnArchName);
+  auto* c = new ifr_ctx();
+  c->device = device;
+  if (hipStreamCreateWithFlags(&c->st, hipStreamNonBlocking) != hipSuccess) {
+    delete c;
+    return fail(IFR_EDEVICE, "hipStreamCreate");
+  }
+  *out = c;
+  return IFR_OK;
+}
+
+int ifr_ctx_destroy(ifr_ctx* c) {
+  if (!c) return IFR_OK;
+  hipSetDevice(c->device);
+  release_model(c);
+  if (c->st) hipStreamDestroy(c->st);
+  delete c;
+  return IFR_OK;
+}
+
+int ifr_sync(ifr_ctx* c) {
+  if (!c) return fail(IFR_EINVAL, "ctx null");
+  HIPCHK(hipStreamSynchronize(c->st));
+  return IFR_OK;
+}
+
+int ifr_malloc(ifr_ctx* c, size_t bytes, void** p) {
+  if (!c || !p) return fail(IFR_EINVAL, "null arg");
+  if (hipMalloc(p, bytes == 0 ? 16 : bytes) != hipSuccess) return fail(IFR_ENOMEM, "hipMalloc %zu", bytes);
+  return IFR_OK;
+}
+int ifr_free(ifr_ctx* c, void* p) {
+  if (!c) return fail(IFR_EINVAL, "ctx null");
+  HIPCHK(hipStreamSynchronize(c->st));
+  HIPCHK(hipFree(p));
+  return IFR_OK;
+}
+int ifr_h2d(ifr_ctx* c, void* dst, const void* src, size_t bytes) {
+  if (!c) return fail(IFR_EINVAL, "ctx null");
+  HIPCHK(hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, c->st));
+  HIPCHK(hipStreamSynchronize(c->st));
+  return IFR_OK;
+}
+int ifr_d2h(ifr_ctx* c, void* dst, const void* src, size_t bytes) {
+  if (!c) return fail(IFR_EINVAL, "ctx null");
+  HIPCHK(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, c->st));
+  HIPCHK(hipStreamSynchronize(c->st));
+  return IFR_OK;
+}
+int ifr_memset(ifr_ctx* c, void* dst, int v, size_t bytes) {
+  if (!c) return fail(IFR_EINVAL, "ctx null");
+  HIPCHK(hipMemsetAsync(dst, v, bytes, c->st));
+  return IFR_OK;
+}
+
+// ---- kernel-level entry points ------------------------------------------------
+
+int ifr_linear_upload(ifr_ctx* c, const ifr_linear* w, ifr_dlinear** out) {
+  if (!c || !out) return fail(IFR_EINVAL, "null arg");
+  auto* d = new ifr_dlinear();
+  const ifr_linear* ws[1] = {w};
+  if (int r = upload_group(c, ws, 1, 0, d->d, false)) { delete d; return r; }
+  *out = d;
+  return IFR_OK;
+}
+
+int ifr_linear_upload_pair(ifr_ctx* c, const ifr_linear* gate, const ifr_linear* up,
+                           ifr_dlinear** out) {
+  if (!c || !out) return fail(IFR_EINVAL, "null arg");
+  auto* d = new ifr_dlinear();
+  const ifr_linear* ws[2] = {gate, up};
+  if (int r = upload_group(c, ws, 2, 1, d->d, false)) { delete d; return r; }
+  *out = d;
+  return IFR_OK;
+}
+
+int ifr_linear_free(ifr_ctx* c, ifr_dlinear* w) {
+  if (!w) return IFR_OK;
+  if (c) hipStreamSynchronize(c->st);
+  hipFree(w->d.codes);
+  hipFree(w->d.sz);
+  delete w;
+  return IFR_OK;
+}
+
+size_t ifr_linear_bytes(const ifr_dlinear* w) { return w ? w->d.bytes : 0; }
+
+int ifr_act_quant(ifr_ctx* c, const float* x_d, int32_t M, int32_t K, const float* norm_w_d,
+                  float eps, int32_t rotate, int32_t round, int32_t ga, int8_t* q_d,
+                  float* scale_d, float* gsum_d) {
+  if (!c) return fail(IFR_EINVAL, "ctx null");
+  ifrk::RowQuantArgs a{};
+  a.src = ifrk::SRC_X;
+  a.x = x_d;
+  a.norm_w = norm_w_d;
+  a.eps = eps;
+  a.rotate = rotate;
+  a.round = round;
+  a.ga = ga;
+  a.q = q_d;
+  a.qscale = scale_d;
+  a.gsum = gsum_d;
+  a.M = M;
+  a.K = K;
+  HIPCHK(ifrk::launch_row_quant(a, c->st));
+  return IFR_OK;
+}
+
+int ifr_quant_gemm(ifr_ctx* c, const ifr_dlinear* w, const int8_t* a_d, const float* ascale_d,
+                   const float* gsum_d, int32_t M, uint16_t* out_d, int32_t* tdump_d) {
+  if (!c || !w) return fail(IFR_EINVAL, "null arg");
+  if (w->d.pair) return fail(IFR_EINVAL, "paired linear: use ifr_quant_gemm_swiglu");
+  ifrk::QGemmArgs a{a_d, ascale_d, gsum_d, out_d, tdump_d, M, w->d.N};
+  HIPCHK(ifrk::launch_qgemm(w->d, a, c->st));
+  return IFR_OK;
+}
+
+int ifr_quant_gemm_swiglu(ifr_ctx* c, const ifr_dlinear* w, const int8_t* a_d,
+                          const float* ascale_d, const float* gsum_d, int32_t M, uint16_t* out_d) {
+  if (!c || !w) return fail(IFR_EINVAL, "null arg");
+  if (!w->d.pair) return fail(IFR_EINVAL, "linear is not a gate/up pair");
+  ifrk::QGemmArgs a{a_d, ascale_d, gsum_d, out_d, nullptr, M, w->d.N / 2};
+  HIPCHK(ifrk::launch_qgemm(w->d, a, c->st));
+  return IFR_OK;
+}
+
+// ---- model load ------------------------------------------------------------------
+
+int ifr_model_load(ifr_ctx* c, const ifr_host_model* m, const ifr_kv_cfg* kvc) {
+  if (!c || !m || !kvc) return fail(IFR_EINVAL, "null arg");
+  HIPCHK(hipSetDevice(c->device));
+  const ifr_model_cfg& cf = m->cfg;
+  if (cf.head_dim != 128) return fail(IFR_EDECLINE, "head_dim %d != 128", cf.head_dim);
+  if (cf.n_heads % cf.n_kv != 0 || cf.n_heads / cf.n_kv > 8)
+    return fail(IFR_EDECLINE, "GQA group %d/%d unsupported", cf.n_heads, cf.n_kv);
+  if (cf.hidden % 256 || cf.hidden > 8192 || (cf.n_heads * cf.head_dim) % 256 ||
+      cf.inter % 128 || cf.inter > 8192 || cf.vocab % 16)
+    return fail(IFR_EDECLINE, "model shape unsupported");
+  if (cf.rotary_dim <= 0 || cf.rotary_dim > cf.head_dim || cf.rotary_dim % 2)
+    return fail(IFR_EINVAL, "rotary_dim");
+  if (kvc->max_seqs <= 0 || kvc->max_seq_tokens <= 0 || kvc->pool_tokens < kPage ||
+      kvc->max_rows <= 0 || kvc->max_rows > 6144)
+    return fail(IFR_EINVAL, "kv cfg");
+  release_model(c);
+  c->cfg = cf;
+  c->kv = *kvc;
+  c->qb = std::min(8, 16 / (cf.n_heads / cf.n_kv));
+  const int H = cf.hidden, L = cf.layers, hd = cf.head_dim, nq = cf.n_heads, nkv = cf.n_kv;
+  const int qN = nq * hd, kvN = nkv * hd, F = cf.inter, V = cf.vocab;
+  c->layers.resize(L);
+  for (int l = 0; l < L; ++l) {
+    const ifr_layer_w& lw = m->layers[l];
+    Layer& ly = c->layers[l];
+    if (lw.q.N != qN || lw.k.N != kvN || lw.v.N != kvN || lw.o.N != H || lw.o.K != qN ||
+        lw.gate.N != F || lw.up.N != F || lw.down.N != H || lw.down.K != F || lw.q.K != H)
+      return fail(IFR_EINVAL, "layer %d: linear shapes do not match the config", l);
+    if (lw.q.bits == lw.k.bits && lw.q.bits == lw.v.bits) {
+      const ifr_linear* ws[3] = {&lw.q, &lw.k, &lw.v};
+      ly.nqkv = 1;
+      if (int r = upload_group(c, ws, 3, 0, ly.qkv[0], true)) return r;
+    } else {
+      ly.nqkv = 3;
+      const ifr_linear* ws[3] = {&lw.q, &lw.k, &lw.v};
+      int off = 0;
+      for (int j = 0; j < 3; ++j) {
+        if (int r = upload_group(c, &ws[j], 1, 0, ly.qkv[j], true)) return r;
+        ly.qkv_off[j] = off;
+        off += ws[j]->N;
+      }
+    }
+    {
+      const ifr_linear* ws[1] = {&lw.o};
+      if (int r = upload_group(c, ws, 1, 0, ly.o, true)) return r;
+      const ifr_linear* wd[1] = {&lw.down};
+      if (int r = upload_group(c, wd, 1, 0, ly.down, true)) return r;
+    }
+    if (lw.gate.bits == lw.up.bits) {
+      const ifr_linear* ws[2] = {&lw.gate, &lw.up};
+      ly.ngu = 1;
+      if (int r = upload_group(c, ws, 2, 1, ly.gu[0], true)) return r;
+    } else {
+      ly.ngu = 2;
+      const ifr_linear* g1[1] = {&lw.gate};
+      const ifr_linear* u1[1] = {&lw.up};
+      if (int r = upload_group(c, g1, 1, 0, ly.gu[0], true)) return r;
+      if (int r = upload_group(c, u1, 1, 0, ly.gu[1], true)) return r;
+    }
+    if (int r = upload(c, &ly.in_ln, lw.in_ln, H)) return r;
+    if (int r = upload(c, &ly.post_ln, lw.post_ln, H)) return r;
+    if (cf.qk_norm) {
+      if (int r = upload(c, &ly.q_norm, lw.q_norm, hd)) return r;
+      if (int r = upload(c, &ly.k_norm, lw.k_norm, hd)) return r;
+    }
+  }
+  if (int r = upload(c, &c->embed, m->embed, (size_t)V * H)) return r;
+  if (int r = upload(c, &c->final_norm, m->final_norm, H)) return r;
+  // lm_head: per-row symmetric int8 of the tied embedding (main.cpp:1745-1761).
+  {
+    std::vector<uint8_t> q((size_t)V * H);
+    std::vector<uint16_t> s(V);
+    for (int r = 0; r < V; ++r) {
+      const float* Wr = m->embed + (size_t)r * H;
+      float mx = 0;
+      for (int k = 0; k < H; ++k) mx = std::max(mx, std::fabs(Wr[k]));
+      const float sc = (mx > 0) ? mx / 127.0f : 1.0f;
+      s[r] = ifr::f2h(sc);
+      const float inv = 1.0f / sc;
+      for (int k = 0; k < H; ++k) q[(size_t)r * H + k] = (uint8_t)(int8_t)std::lrint(Wr[k] * inv);
+    }
+    std::vector<uint32_t> packed((size_t)V * H / 4);
+    ifrk::pack_linear_host(q.data(), nullptr, nullptr, V, H, 8, packed.data(), nullptr, 1, 0);
+    if (int r = upload(c, &c->lm_w, packed.data(), packed.size())) return r;
+    if (int r = upload(c, &c->lm_s, s.data(), s.size())) return r;
+  }
+  // RoPE tables: cos/sin(inv_freq[d] * pos) in fp32 (main.cpp:365-373, :10594-10596).
+  {
+    const int half = cf.rotary_dim / 2, P = kvc->max_seq_tokens;
+    std::vector<float> inv(half), cs((size_t)P * half), sn((size_t)P * half);
+    for (int d = 0; d < half; ++d)
+      inv[d] = 1.0f / std::pow(cf.rope_theta, (2.0f * d) / (float)cf.rotary_dim);
+    for (int p = 0; p < P; ++p)
+      for (int d = 0; d < half; ++d) {
+        const float f = inv[d] * (float)p;
+        cs[(size_t)p * half + d] = std::cos(f);
+        sn[(size_t)p * half + d] = std::sin(f);
+      }
+    if (int r = upload(c, &c->rope_cos, cs.data(), cs.size())) return r;
+    if (int r = upload(c, &c->rope_sin, sn.data(), sn.size())) return r;
+  }
+  // paged KV pool (zero-filled so unused page slots stay finite)
+  c->n_pages = kvc->pool_tokens / kPage;
+  c->max_pages = (kvc->max_seq_tokens + kPage - 1) / kPage;
+  const size_t esz = kvc->kv_int8 ? 1 : 2;
+  const size_t page_bytes = (size_t)nkv * kPage * hd * esz;
+  c->kpool.resize(L);
+  c->vpool.resize(L);
+  c->kscale.assign(L, nullptr);
+  c->vscale.assign(L, nullptr);
+  for (int l = 0; l < L; ++l) {
+    c->kpool[l] = c->dalloc(page_bytes * c->n_pages);
+    c->vpool[l] = c->dalloc(page_bytes * c->n_pages);
+    if (!c->kpool[l] || !c->vpool[l]) return fail(IFR_ENOMEM, "KV pool (%zu B/layer)", 2 * page_bytes * c->n_pages);
+    HIPCHK(hipMemsetAsync(c->kpool[l], 0, page_bytes * c->n_pages, c->st));
+    HIPCHK(hipMemsetAsync(c->vpool[l], 0, page_bytes * c->n_pages, c->st));
+    if (kvc->kv_int8) {
+      const size_t sb = (size_t)nkv * kPage * 2 * c->n_pages;
+      c->kscale[l] = static_cast<uint16_t*>(c->dalloc(sb));
+      c->vscale[l] = static_cast<uint16_t*>(c->dalloc(sb));
+      if (!c->kscale[l] || !c->vscale[l]) return fail(IFR_ENOMEM, "KV scales");
+      HIPCHK(hipMemsetAsync(c->kscale[l], 0, sb, c->st));
+      HIPCHK(hipMemsetAsync(c->vscale[l], 0, sb, c->st));
+    }
+  }
+  c->free_pages.clear();
+  for (int p = c->n_pages - 1; p >= 0; --p) c->free_pages.push_back(p);
+  c->seqs.assign(kvc->max_seqs, Seq());
+  const size_t btn = (size_t)kvc->max_seqs * c->max_pages;
+  HIPCHK(hipHostMalloc(reinterpret_cast<void**>(&c->bt_h), btn * sizeof(int32_t), hipHostMallocDefault));
+  std::memset(c->bt_h, 0, btn * sizeof(int32_t));
+  if (int r = walloc(c, &c->bt_d, btn)) return r;
+  HIPCHK(hipMemcpyAsync(c->bt_d, c->bt_h, btn * sizeof(int32_t), hipMemcpyHostToDevice, c->st));
+  // workspaces
+  const int Mx = kvc->max_rows;
+  c->maxM = Mx;
+  const int Kmax = std::max(std::max(H, qN), F);
+  HIPCHK(hipHostMalloc(reinterpret_cast<void**>(&c->rows_h), (size_t)Mx * 5 * sizeof(int32_t), hipHostMallocDefault));
+  HIPCHK(hipHostMalloc(reinterpret_cast<void**>(&c->best_h), (size_t)Mx * sizeof(int32_t), hipHostMallocDefault));
+  int r = 0;
+  if ((r = walloc(c, &c->rows_d, (size_t)Mx * 5)) || (r = walloc(c, &c->resid, (size_t)Mx * H)) ||
+      (r = walloc(c, &c->aq, (size_t)Mx * Kmax)) || (r = walloc(c, &c->as, (size_t)Mx)) ||
+      (r = walloc(c, &c->gs, (size_t)Mx * (Kmax / 128))) ||
+      (r = walloc(c, &c->qkv, (size_t)Mx * (qN + 2 * kvN))) ||
+      (r = walloc(c, &c->qbuf, (size_t)Mx * qN)) || (r = walloc(c, &c->y, (size_t)Mx * H)) ||
+      (r = walloc(c, &c->mg, (size_t)Mx * F)) || (r = walloc(c, &c->gu, (size_t)Mx * 2 * F)) ||
+      (r = walloc(c, &c->pk.cu_seqlens, (size_t)Mx + 1)) || (r = walloc(c, &c->pk.row_grp, Mx)) ||
+      (r = walloc(c, &c->pk.row_seq, Mx)) || (r = walloc(c, &c->pk.row_pos, Mx)) ||
+      (r = walloc(c, &c->pk.row_kind, Mx)) || (r = walloc(c, &c->pk.comb_base, Mx)) ||
+      (r = walloc(c, &c->pk.comb_nsplit, Mx)) || (r = walloc(c, &c->pk.comb_tok, Mx)) ||
+      (r = walloc(c, &c->pk.want_rows, Mx)) || (r = walloc(c, &c->row_tok, Mx)) ||
+      (r = walloc(c, &c->lm_aq, (size_t)Mx * H)) || (r = walloc(c, &c->lm_as, (size_t)Mx * (H / 64))) ||
+      (r = walloc(c, &c->best_d, Mx)))
+    return r;
+  const int nparts = ifrk::lmhead_nparts(V);
+  if ((r = walloc(c, &c->lm_pv, (size_t)nparts * Mx)) || (r = walloc(c, &c->lm_pi, (size_t)nparts * Mx)))
+    return r;
+  c->max_units = 32768;
+  if ((r = walloc(c, &c->pk.units, c->max_units)) ||
+      (r = walloc(c, &c->part_o, (size_t)c->max_units * 16 * hd)) ||
+      (r = walloc(c, &c->part_ml, (size_t)c->max_units * 16 * 2)))
+    return r;
+  HIPCHK(hipStreamSynchronize(c->st));
+  c->loaded = true;
+  return IFR_OK;
+}
+
+// ---- sequences ---------------------------------------------------------------------
+
+int ifr_seq_open(ifr_ctx* c, int32_t* slot) {
+  if (!c || !slot) return fail(IFR_EINVAL, "null arg");
+  if (!c->loaded) return fail(IFR_ESTATE, "no model loaded");
+  for (size_t i = 0; i < c->seqs.size(); ++i)
+    if (!c->seqs[i].open) {
+      c->seqs[i] = Seq();
+      c->seqs[i].open = true;
+      *slot = (int32_t)i;
+      return IFR_OK;
+    }
+  return fail(IFR_ENOMEM, "all %zu sequence slots in use", c->seqs.size());
+}
+
+int ifr_seq_truncate(ifr_ctx* c, int32_t slot, int32_t len) {
+  if (!c || !c->loaded) return fail(IFR_ESTATE, "no model loaded");
+  if (slot < 0 || slot >= (int)c->seqs.size() || !c->seqs[slot].open) return fail(IFR_EINVAL, "slot %d", slot);
+  Seq& s = c->seqs[slot];
+  if (len < 0 || len > s.len) return fail(IFR_EINVAL, "truncate %d > len %d", len, s.len);
+  const int keep = (len + kPage - 1) / kPage;
+  while ((int)s.pages.size() > keep) {
+    c->free_pages.push_back(s.pages.back());
+    s.pages.pop_back();
+  }
+  s.len = len;
+  return IFR_OK;
+}
+
+int ifr_seq_close(ifr_ctx* c, int32_t slot) {
+  if (int r = ifr_seq_truncate(c, slot, 0)) return r;
+  c->seqs[slot].open = false;
+  return IFR_OK;
+}
+
+int ifr_seq_len(ifr_ctx* c, int32_t slot, int32_t* len) {
+  if (!c || !c->loaded || !len) return fail(IFR_ESTATE, "no model loaded");
+  if (slot < 0 || slot >= (int)c->seqs.size() || !c->seqs[slot].open) return fail(IFR_EINVAL, "slot %d", slot);
+  *len = c->seqs[slot].len;
+  return IFR_OK;
+}
+
+int ifr_kv_capacity(ifr_ctx* c, int32_t* tokens) {
+  if (!c || !c->loaded || !tokens) return fail(IFR_ESTATE, "no model loaded");
+  *tokens = c->kv.max_seq_tokens;
+  return IFR_OK;
+}
+
+int ifr_seq_load_kv(ifr_ctx* c, int32_t slot, int32_t len, const float* k, const float* v) {
+  if (!c || !c->loaded) return fail(IFR_ESTATE, "no model loaded");
+  if (slot < 0 || slot >= (int)c->seqs.size() || !c->seqs[slot].open) return fail(IFR_EINVAL, "slot %d", slot);
+  Seq& s = c->seqs[slot];
+  if (s.len != 0) return fail(IFR_ESTATE, "sequence %d is not empty", slot);
+  if (len < 0 || len > c->kv.max_seq_tokens || !k || !v) return fail(IFR_EINVAL, "len %d", len);
+  const int need = (len + kPage - 1) / kPage;
+  if (need > (int)c->free_pages.size()) return fail(IFR_ENOMEM, "KV pool exhausted");
+  for (int i = 0; i < need; ++i) {
+    const int p = c->free_pages.back();
+    c->free_pages.pop_back();
+    c->bt_h[(size_t)slot * c->max_pages + i] = p;
+    s.pages.push_back(p);
+  }
+  HIPCHK(hipMemcpy(c->bt_d + (size_t)slot * c->max_pages, c->bt_h + (size_t)slot * c->max_pages,
+                   c->max_pages * sizeof(int32_t), hipMemcpyHostToDevice));
+  const int nkv = c->cfg.n_kv, hd = c->cfg.head_dim, L = c->cfg.layers;
+  const bool i8 = c->kv.kv_int8 != 0;
+  const size_t per_page = (size_t)nkv * kPage * hd;
+  std::vector<uint16_t> kh(per_page), vh(per_page), ksc((size_t)nkv * kPage), vsc((size_t)nkv * kPage);
+  std::vector<int8_t> kq(per_page), vq(per_page);
+  // One (token, head) vector: fp16 round, then optionally int8 (same rule as the kernel).
+  auto enc = [&](const float* x, uint16_t* h16, int8_t* q8, uint16_t* sc, size_t stride) {
+    float r[128];
+    float mx = 0;
+    for (int d = 0; d < hd; ++d) {
+      r[d] = ifr::h2f(ifr::f2h(x[d]));
+      mx = std::max(mx, std::fabs(r[d]));
+    }
+    if (!i8) {
+      for (int d = 0; d < hd; ++d) h16[d * stride] = ifr::f2h(r[d]);
+      return;
+    }
+    const uint16_t s16 = ifr::f2h(mx > 0 ? mx / 127.0f : 1.0f);
+    const float inv = 1.0f / ifr::h2f(s16);
+    for (int d = 0; d < hd; ++d) {
+      const float t = r[d] * inv;
+      int q = (int)(t >= 0.0f ? t + 0.5f : t - 0.5f);
+      q = std::min(127, std::max(-127, q));
+      q8[d * stride] = (int8_t)q;
+    }
+    *sc = s16;
+  };
+  for (int l = 0; l < L; ++l) {
+    for (int pi = 0; pi < need; ++pi) {
+      std::fill(kh.begin(), kh.end(), 0);
+      std::fill(vh.begin(), vh.end(), 0);
+      std::fill(kq.begin(), kq.end(), 0);
+      std::fill(vq.begin(), vq.end(), 0);
+      std::fill(ksc.begin(), ksc.end(), 0);
+      std::fill(vsc.begin(), vsc.end(), 0);
+      for (int tk = 0; tk < kPage; ++tk) {
+        const int t = pi * kPage + tk;
+        if (t >= len) break;
+        for (int h = 0; h < nkv; ++h) {
+          const size_t src = (((size_t)l * len + t) * nkv + h) * hd;
+          const size_t kdst = ((size_t)h * kPage + tk) * hd;        // [h][tok][d]
+          const size_t vdst = (size_t)h * hd * kPage + tk;          // [h][d][tok]
+          enc(k + src, &kh[kdst], &kq[kdst], &ksc[(size_t)h * kPage + tk], 1);
+          enc(v + src, &vh[vdst], &vq[vdst], &vsc[(size_t)h * kPage + tk], kPage);
+        }
+      }
+      const size_t page = (size_t)s.pages[pi];
+      if (!i8) {
+        HIPCHK(hipMemcpy(static_cast<uint16_t*>(c->kpool[l]) + page * per_page, kh.data(), per_page * 2, hipMemcpyHostToDevice));
+        HIPCHK(hipMemcpy(static_cast<uint16_t*>(c->vpool[l]) + page * per_page, vh.data(), per_page * 2, hipMemcpyHostToDevice));
+      } else {
+        HIPCHK(hipMemcpy(static_cast<int8_t*>(c->kpool[l]) + page * per_page, kq.data(), per_page, hipMemcpyHostToDevice));
+        HIPCHK(hipMemcpy(static_cast<int8_t*>(c->vpool[l]) + page * per_page, vq.data(), per_page, hipMemcpyHostToDevice));
+        HIPCHK(hipMemcpy(c->kscale[l] + page * nkv * kPage, ksc.data(), ksc.size() * 2, hipMemcpyHostToDevice));
+        HIPCHK(hipMemcpy(c->vscale[l] + page * nkv * kPage, vsc.data(), vsc.size() * 2, hipMemcpyHostToDevice));
+      }
+    }
+  }
+  s.len = len;
+  return IFR_OK;
+}
+
+// ---- forward ---------------------------------------------------------------------------
+
+int ifr_forward(ifr_ctx* c, const ifr_row* rows, int32_t M, int32_t* best_out, float* logits_out) {
+  if (!c || !rows || !best_out) return fail(IFR_EINVAL, "null arg");
+  if (!c->loaded) return fail(IFR_ESTATE, "no model loaded");
+  if (M <= 0 || M > c->maxM) return fail(IFR_EINVAL, "M=%d outside [1, %d]", M, c->maxM);
+  const ifr_model_cfg& cf = c->cfg;
+  const int H = cf.hidden, hd = cf.head_dim, nq = cf.n_heads, nkv = cf.n_kv;
+  const int qN = nq * hd, kvN = nkv * hd, F = cf.inter, V = cf.vocab;
+  // ---- validate rows (BatchItem rules: one contiguous run per sequence)
+  std::vector<int> g_start, g_len, g_pos0, g_seq;
+  std::vector<int> want;
+  for (int m = 0; m < M; ++m) {
+    const ifr_row& r = rows[m];
+    if (r.seq < 0 || r.seq >= (int)c->seqs.size() || !c->seqs[r.seq].open)
+      return fail(IFR_EINVAL, "row %d: sequence slot %d not open", m, r.seq);
+    if (r.token < 0 || r.token >= V) return fail(IFR_EINVAL, "row %d: token %d", m, r.token);
+    if (r.kind < IFR_ROW_DECODE || r.kind > IFR_ROW_VERIFY) return fail(IFR_EINVAL, "row %d: kind", m);
+    if (r.pos < 0 || r.pos >= c->kv.max_seq_tokens)
+      return fail(IFR_EINVAL, "row %d: pos %d >= KV capacity %d", m, r.pos, c->kv.max_seq_tokens);
+    const bool first = (m == 0 || rows[m - 1].seq != r.seq);
+    if (first) {
+      if (r.pos != c->seqs[r.seq].len)
+        return fail(IFR_EINVAL, "row %d: pos %d != sequence length %d", m, r.pos, c->seqs[r.seq].len);
+      for (int s : g_seq)
+        if (s == r.seq) return fail(IFR_EINVAL, "row %d: sequence %d appears twice", m, r.seq);
+      g_start.push_back(m);
+      g_len.push_back(1);
+      g_pos0.push_back(r.pos);
+      g_seq.push_back(r.seq);
+    } else {
+      if (r.pos != rows[m - 1].pos + 1) return fail(IFR_EINVAL, "row %d: positions not consecutive", m);
+      g_len.back() += 1;
+    }
+    if (r.want) want.push_back(m);
+  }
+  const int nwant = (int)want.size();
+  // ---- pages for every new position
+  for (size_t g = 0; g < g_seq.size(); ++g) {
+    Seq& s = c->seqs[g_seq[g]];
+    const int need = (g_pos0[g] + g_len[g] + kPage - 1) / kPage;
+    if (need - (int)s.pages.size() > (int)c->free_pages.size())
+      return fail(IFR_ENOMEM, "KV pool exhausted (%zu free pages)", c->free_pages.size());
+  }
+  for (size_t g = 0; g < g_seq.size(); ++g) {
+    Seq& s = c->seqs[g_seq[g]];
+    const int need = (g_pos0[g] + g_len[g] + kPage - 1) / kPage;
+    bool dirty = false;
+    while ((int)s.pages.size() < need) {
+      const int p = c->free_pages.back();
+      c->free_pages.pop_back();
+      c->bt_h[(size_t)g_seq[g] * c->max_pages + s.pages.size()] = p;
+      s.pages.push_back(p);
+      dirty = true;
+    }
+    if (dirty) {
+      const size_t off = (size_t)g_seq[g] * c->max_pages;
+      HIPCHK(hipMemcpyAsync(c->bt_d + off, c->bt_h + off, c->max_pages * sizeof(int32_t),
+                            hipMemcpyHostToDevice, c->st));
+    }
+  }
+  // ---- KV split: fixed, so each row's partial decomposition depends only on
+  // its own sequence (batch-invariant results: split == joint, solo == loaded)
+  int split = kSplit;
+  long nunits = count_units(g_pos0, g_len, nkv, split, c->qb);
+  while (nunits > c->max_units) {
+    split *= 2;
+    nunits = count_units(g_pos0, g_len, nkv, split, c->qb);
+  }
+  c->last_split = split;
+  c->last_units = (int)nunits;
+  // ---- upload rows, pack
+  std::memcpy(c->rows_h, rows, (size_t)M * sizeof(ifr_row));
+  HIPCHK(hipMemcpyAsync(c->rows_d, c->rows_h, (size_t)M * sizeof(ifr_row), hipMemcpyHostToDevice, c->st));
+  {
+    Scope sc(c, "pack", 0);
+    HIPCHK(ifrk::launch_pack(c->rows_d, M, nkv, c->qb, split, c->pk, c->st));
+  }
+  // tokens column of the rows (stride 5) for the embedding gather
+  std::vector<int32_t> tok(M);
+  for (int m = 0; m < M; ++m) tok[m] = rows[m].token;
+  HIPCHK(hipMemcpyAsync(c->row_tok, tok.data(), M * sizeof(int32_t), hipMemcpyHostToDevice, c->st));
+  // ---- bytes accounting for the attention roofline (K+V per sequence, Q, O)
+  double attn_bytes = 0;
+  {
+    const double e = c->kv.kv_int8 ? 1.0 : 2.0;
+    for (size_t g = 0; g < g_seq.size(); ++g) {
+      const double Ls = g_pos0[g] + g_len[g];
+      attn_bytes += Ls * kvN * 2 * e + (c->kv.kv_int8 ? Ls * nkv * 2 * 2 : 0);
+    }
+    attn_bytes += (double)M * qN * 2 * 2;
+  }
+  const int ng_h = H / 128;
+  for (int l = 0; l < cf.layers; ++l) {
+    Layer& ly = c->layers[l];
+    ifrk::KVLayout kv{nkv, hd, kPage, c->max_pages, c->kv.kv_int8, c->kpool[l], c->vpool[l],
+                      c->kscale[l], c->vscale[l], c->bt_d};
+    // (1) layer input: embed (l == 0) or residual += FWHT(down out); RMSNorm; FWHT; quant
+    {
+      ifrk::RowQuantArgs a{};
+      if (l == 0) {
+        a.src = ifrk::SRC_EMBED;
+        a.embed = c->embed;
+        a.tokens = c->row_tok;
+      } else {
+        a.src = ifrk::SRC_RESID;
+        a.y = c->y;
+        a.rot_y = cf.rotate;
+      }
+      a.resid = c->resid;
+      a.norm_w = ly.in_ln;
+      a.eps = cf.rms_eps;
+      a.rotate = cf.rotate;
+      a.round = 0;
+      a.ga = 0;
+      a.q = c->aq;
+      a.qscale = c->as;
+      a.gsum = c->gs;
+      a.M = M;
+      a.K = H;
+      Scope sc(c, "row_quant", (double)M * H * 4 * 2);
+      HIPCHK(ifrk::launch_row_quant(a, c->st));
+    }
+    // (2) QKV
+    for (int j = 0; j < ly.nqkv; ++j) {
+      ifrk::QGemmArgs a{c->aq, c->as, c->gs, c->qkv + ly.qkv_off[j], nullptr, M, qN + 2 * kvN};
+      Scope sc(c, "qgemm", (double)ly.qkv[j].bytes + (double)M * H + (double)M * ly.qkv[j].N * 2);
+      HIPCHK(ifrk::launch_qgemm(ly.qkv[j], a, c->st));
+    }
+    // (3) q/k norm + RoPE + KV append
+    {
+      ifrk::QKArgs a{c->qkv, c->pk.row_seq, c->pk.row_pos, ly.q_norm, ly.k_norm, c->rope_cos,
+                     c->rope_sin, cf.rotary_dim, cf.rms_eps, nq, c->qbuf, M};
+      Scope sc(c, "qk_rope_kv", (double)M * (qN + 2 * kvN) * 2 * 2);
+      HIPCHK(ifrk::launch_qk_rope_kv(a, kv, c->st));
+    }
+    // (4) attention + combine (emits the O-proj int8 input)
+    {
+      ifrk::AttnArgs a{c->pk.units, (int)nunits, c->qbuf, nq, 1.4426950408889634f / std::sqrt((float)hd),
+                       c->part_o, c->part_ml};
+      Scope sc(c, "attention", attn_bytes);
+      HIPCHK(ifrk::launch_attention(a, kv, c->st));
+    }
+    {
+      ifrk::CombineArgs a{c->part_o, c->part_ml, c->pk.comb_base, c->pk.comb_nsplit, c->pk.comb_tok,
+                          M, nq, nkv, hd, nullptr, c->aq, c->as, c->gs};
+      Scope sc(c, "combine", 0);
+      HIPCHK(ifrk::launch_combine(a, c->st));
+    }
+    // (5) O projection
+    {
+      ifrk::QGemmArgs a{c->aq, c->as, c->gs, c->y, nullptr, M, H};
+      Scope sc(c, "qgemm", (double)ly.o.bytes + (double)M * qN + (double)M * H * 2);
+      HIPCHK(ifrk::launch_qgemm(ly.o, a, c->st));
+    }
+    // (6) residual += FWHT(o); post norm; FWHT; quant
+    {
+      ifrk::RowQuantArgs a{};
+      a.src = ifrk::SRC_RESID;
+      a.y = c->y;
+      a.rot_y = cf.rotate;
+      a.resid = c->resid;
+      a.norm_w = ly.post_ln;
+      a.eps = cf.rms_eps;
+      a.rotate = cf.rotate;
+      a.q = c->aq;
+      a.qscale = c->as;
+      a.gsum = c->gs;
+      a.M = M;
+      a.K = H;
+      Scope sc(c, "row_quant", (double)M * H * 4 * 2);
+      HIPCHK(ifrk::launch_row_quant(a, c->st));
+    }
+    // (7) gate/up + SwiGLU
+    if (ly.ngu == 1) {
+      ifrk::QGemmArgs a{c->aq, c->as, c->gs, c->mg, nullptr, M, F};
+      Scope sc(c, "qgemm", (double)ly.gu[0].bytes + (double)M * H + (double)M * F * 2);
+      HIPCHK(ifrk::launch_qgemm(ly.gu[0], a, c->st));
+    } else {
+      for (int j = 0; j < 2; ++j) {
+        ifrk::QGemmArgs a{c->aq, c->as, c->gs, c->gu + j * F, nullptr, M, 2 * F};
+        Scope sc(c, "qgemm", (double)ly.gu[j].bytes + (double)M * H + (double)M * F * 2);
+        HIPCHK(ifrk::launch_qgemm(ly.gu[j], a, c->st));
+      }
+      HIPCHK(ifrk::launch_swiglu(c->gu, M, F, c->mg, c->st));
+    }
+    // (8) quantize mg, down projection
+    {
+      Scope sc(c, "quant_plain", (double)M * F * 3);
+      HIPCHK(ifrk::launch_quant_plain(nullptr, c->mg, M, F, c->aq, c->as, c->gs, c->st));
+    }
+    {
+      ifrk::QGemmArgs a{c->aq, c->as, c->gs, c->y, nullptr, M, H};
+      Scope sc(c, "qgemm", (double)ly.down.bytes + (double)M * F + (double)M * H * 2);
+      HIPCHK(ifrk::launch_qgemm(ly.down, a, c->st));
+    }
+  }
+  (void)ng_h;
+  // ---- final residual, norm, lm_head on the scored rows
+  for (int m = 0; m < M; ++m) best_out[m] = -1;
+  if (nwant > 0) {
+    {
+      ifrk::RowQuantArgs a{};
+      a.src = ifrk::SRC_RESID;
+      a.y = c->y;
+      a.rot_y = cf.rotate;
+      a.resid = c->resid;
+      a.rowmap = c->pk.want_rows;
+      a.norm_w = c->final_norm;
+      a.eps = cf.rms_eps;
+      a.rotate = 0;
+      a.round = 1;
+      a.ga = 64;
+      a.q = c->lm_aq;
+      a.qscale = c->lm_as;
+      a.gsum = nullptr;
+      a.M = nwant;
+      a.K = H;
+      Scope sc(c, "row_quant", (double)nwant * H * 4 * 2);
+      HIPCHK(ifrk::launch_row_quant(a, c->st));
+    }
+    if (logits_out && c->logits_cap < (size_t)nwant * V) {
+      if (c->logits_d) hipFree(c->logits_d);
+      c->logits_d = nullptr;
+      HIPCHK(hipMalloc(reinterpret_cast<void**>(&c->logits_d), (size_t)nwant * V * sizeof(float)));
+      c->logits_cap = (size_t)nwant * V;
+    }
+    ifrk::LmHeadArgs a{};
+    a.a = c->lm_aq;
+    a.as = c->lm_as;
+    a.wcodes = c->lm_w;
+    a.wscale = c->lm_s;
+    a.W = nwant;
+    a.V = V;
+    a.H = H;
+    a.logits = logits_out ? c->logits_d : nullptr;
+    a.part_val = c->lm_pv;
+    a.part_idx = c->lm_pi;
+    a.best = c->best_d;
+    {
+      Scope sc(c, "lmhead", (double)V * H + (double)V * 2 + (double)nwant * H);
+      HIPCHK(ifrk::launch_lmhead(a, c->st));
+    }
+    HIPCHK(hipMemcpyAsync(c->best_h, c->best_d, nwant * sizeof(int32_t), hipMemcpyDeviceToHost, c->st));
+    if (logits_out)
+      HIPCHK(hipMemcpyAsync(logits_out, c->logits_d, (size_t)nwant * V * sizeof(float),
+                            hipMemcpyDeviceToHost, c->st));
+  }
+  HIPCHK(hipStreamSynchronize(c->st));
+  for (int i = 0; i < nwant; ++i) best_out[want[i]] = c->best_h[i];
+  for (size_t g = 0; g < g_seq.size(); ++g) c->seqs[g_seq[g]].len = g_pos0[g] + g_len[g];
+  if (c->timing) flush_timers(c);
+  return IFR_OK;
+}
+
+int ifr_attention(ifr_ctx* c, int32_t layer, const ifr_row* rows, int32_t M, const uint16_t* q_h,
+                  float* out_h) {
+  if (!c || !rows || !q_h || !out_h) return fail(IFR_EINVAL, "null arg");
+  if (!c->loaded) return fail(IFR_ESTATE, "no model loaded");
+  if (M <= 0 || M > c->maxM) return fail(IFR_EINVAL, "M=%d outside [1, %d]", M, c->maxM);
+  if (layer < 0 || layer >= c->cfg.layers) return fail(IFR_EINVAL, "layer %d", layer);
+  const int nq = c->cfg.n_heads, nkv = c->cfg.n_kv, hd = c->cfg.head_dim;
+  std::vector<int> g_len, g_pos0, g_seq;
+  for (int m = 0; m < M; ++m) {
+    const ifr_row& r = rows[m];
+    if (r.seq < 0 || r.seq >= (int)c->seqs.size() || !c->seqs[r.seq].open)
+      return fail(IFR_EINVAL, "row %d: sequence slot %d not open", m, r.seq);
+    if (r.pos < 0 || r.pos >= c->seqs[r.seq].len)
+      return fail(IFR_EINVAL, "row %d: pos %d has no KV (len %d)", m, r.pos, c->seqs[r.seq].len);
+    const bool first = (m == 0 || rows[m - 1].seq != r.seq);
+    if (first) {
+      for (int s : g_seq)
+        if (s == r.seq) return fail(IFR_EINVAL, "row %d: sequence %d appears twice", m, r.seq);
+      g_len.push_back(1);
+      g_pos0.push_back(r.pos);
+      g_seq.push_back(r.seq);
+    } else {
+      if (r.pos != rows[m - 1].pos + 1) return fail(IFR_EINVAL, "row %d: positions not consecutive", m);
+      g_len.back() += 1;
+    }
+  }
+  int split = kSplit;
+  long nunits = count_units(g_pos0, g_len, nkv, split, c->qb);
+  while (nunits > c->max_units) {
+    split *= 2;
+    nunits = count_units(g_pos0, g_len, nkv, split, c->qb);
+  }
+  c->last_split = split;
+  c->last_units = (int)nunits;
+  std::memcpy(c->rows_h, rows, (size_t)M * sizeof(ifr_row));
+  HIPCHK(hipMemcpyAsync(c->rows_d, c->rows_h, (size_t)M * sizeof(ifr_row), hipMemcpyHostToDevice, c->st));
+  HIPCHK(ifrk::launch_pack(c->rows_d, M, nkv, c->qb, split, c->pk, c->st));
+  HIPCHK(hipMemcpyAsync(c->qbuf, q_h, (size_t)M * nq * hd * 2, hipMemcpyHostToDevice, c->st));
+  ifrk::KVLayout kv{nkv, hd, kPage, c->max_pages, c->kv.kv_int8, c->kpool[layer], c->vpool[layer],
+                    c->kscale[layer], c->vscale[layer], c->bt_d};
+  ifrk::AttnArgs a{c->pk.units, (int)nunits, c->qbuf, nq, 1.4426950408889634f / std::sqrt((float)hd),
+                   c->part_o, c->part_ml};
+  HIPCHK(ifrk::launch_attention(a, kv, c->st));
+  float* out_d = nullptr;
+  HIPCHK(hipMalloc(reinterpret_cast<void**>(&out_d), (size_t)M * nq * hd * sizeof(float)));
+  ifrk::CombineArgs cb{c->part_o, c->part_ml, c->pk.comb_base, c->pk.comb_nsplit, c->pk.comb_tok,
+                       M, nq, nkv, hd, out_d, c->aq, c->as, c->gs};
+  hipError_t e = ifrk::launch_combine(cb, c->st);
+  if (e == hipSuccess) e = hipMemcpyAsync(out_h, out_d, (size_t)M * nq * hd * sizeof(float), hipMemcpyDeviceToHost, c->st);
+  if (e == hipSuccess) e = hipStreamSynchronize(c->st);
+  hipFree(out_d);
+  HIPCHK(e);
+  return IFR_OK;
+}
+
+int ifr_set_timing(ifr_ctx* c, int32_t on) {
+  if (!c) return fail(IFR_EINVAL, "ctx null");
+  c->timing = on != 0;
+  c->stats.clear();
+  return IFR_OK;
+}
+
+int ifr_get_timing(ifr_ctx* c, const char* kernel, double* total_ms, int64_t* launches,
+                   double* bytes) {
+  if (!c || !kernel) return fail(IFR_EINVAL, "null arg");
+  for (auto& s : c->stats)
+    if (s.first == kernel) {
+      if (total_ms) *total_ms = s.second.ms;
+      if (launches) *launches = s.second.n;
+      if (bytes) *bytes = s.second.bytes;
+      return IFR_OK;
+    }
+  if (total_ms) *total_ms = 0;
+  if (launches) *launches = 0;
+  if (bytes) *bytes = 0;
+  return IFR_OK;
+}
+
+// Test hook: device pointers of the last forward's pack outputs.
+int ifr_debug_pack(ifr_ctx* c, int32_t M, int32_t* cu, int32_t* row_grp, int32_t* comb_base,
+                   int32_t* comb_nsplit, int32_t* comb_tok, int32_t* units, int32_t* n_units,
+                   int32_t* split) {
+  if (!c || !c->loaded) return fail(IFR_ESTATE, "no model loaded");
+  HIPCHK(hipStreamSynchronize(c->st));
+  if (cu) HIPCHK(hipMemcpy(cu, c->pk.cu_seqlens, (M + 1) * 4, hipMemcpyDeviceToHost));
+  if (row_grp) HIPCHK(hipMemcpy(row_grp, c->pk.row_grp, M * 4, hipMemcpyDeviceToHost));
+  if (comb_base) HIPCHK(hipMemcpy(comb_base, c->pk.comb_base, M * 4, hipMemcpyDeviceToHost));
+  if (comb_nsplit) HIPCHK(hipMemcpy(comb_nsplit, c->pk.comb_nsplit, M * 4, hipMemcpyDeviceToHost));
+  if (comb_tok) HIPCHK(hipMemcpy(comb_tok, c->pk.comb_tok, M * 4, hipMemcpyDeviceToHost));
+  if (units) HIPCHK(hipMemcpy(units, c->pk.units, (size_t)c->last_units * sizeof(ifrk::AttnUnit), hipMemcpyDeviceToHost));
+  if (n_units) *n_units = c->last_units;
+  if (split) *split = c->last_split;
+  return IFR_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,173 @@
+// Host-side launchers of the gfx950 kernels (one .hip file per family).
+// Every launcher checks the shapes its kernel assumes before launching and
+// returns a hipError_t (hipErrorInvalidValue for a shape it cannot run).
+#pragma once
+#include <hip/hip_runtime.h>
+#include <cstddef>
+#include <cstdint>
+
+namespace ifrk {
+
+// ---- quantized linear in the device MFMA layout ---------------------------
+// codes: fragment-major.  For column tile t (16 columns), 64-wide K step s and
+// lane l (column 16t + l%16, K range [64s + 16(l/16), +16)), the lane's
+// bits/2 dwords sit at ((t * nsteps + s) * 64 + l) * (bits/2).  Inside them
+// code j (j = 0..15) of the lane's 16 K values is stored so that a shift and
+// a mask yield the int8 operand dword d = j/4 with byte j%4 (see qgemm.hip).
+// sz: (scale, zero) fp16 pairs, [ntiles][ngroups][16].
+struct DLin {
+  int N = 0;       // device columns (2 * F for an interleaved gate/up pair)
+  int K = 0;
+  int bits = 0;
+  int ng = 0;      // K / 128
+  int nsteps = 0;  // K / 64
+  int pair = 0;    // 1: tiles alternate gate / up (SwiGLU epilogue)
+  uint32_t* codes = nullptr;
+  uint32_t* sz = nullptr;
+  size_t bytes = 0;
+};
+
+// Pack one logical linear (row-major LSB-first codes, fp16 scale/zero
+// [N][K/128]) into host buffers of the device layout.  For a gate/up pair
+// call with both; columns are interleaved per 16-column tile.
+void pack_linear_host(const uint8_t* codes, const uint16_t* scale, const uint16_t* zero, int N,
+                      int K, int bits, uint32_t* out_codes, uint32_t* out_sz, int tile_stride,
+                      int tile_offset);
+
+struct QGemmArgs {
+  const int8_t* a;      // [M][K]
+  const float* as;      // [M] per-row activation scale
+  const float* gs;      // [M][K/128] per-group code sums (float)
+  uint16_t* out;        // [M][ldo]
+  int32_t* tdump;       // optional [M][N][K/128]
+  int M;
+  int ldo;
+};
+hipError_t launch_qgemm(const DLin& w, const QGemmArgs& a, hipStream_t st);
+
+// ---- row kernels -----------------------------------------------------------
+enum { SRC_X = 0, SRC_EMBED = 1, SRC_RESID = 2 };
+struct RowQuantArgs {
+  int src;                 // SRC_*
+  const float* x;          // SRC_X: [M][K] fp32 input
+  const float* embed;      // SRC_EMBED: [V][K]; tokens: [M]
+  const int32_t* tokens;
+  float* resid;            // SRC_EMBED: written; SRC_RESID: resid += rot?(y)
+  const uint16_t* y;       // SRC_RESID: fp16 [M][K]
+  int rot_y;               // SRC_RESID: rotate y before the add (left site)
+  const int32_t* rowmap;   // optional: row m reads input row rowmap[m]
+  const float* norm_w;     // optional RMSNorm(1+w)
+  float eps;
+  int rotate;              // FWHT the normed row (right site)
+  int round;               // 0 half-away, 1 RNE
+  int ga;                  // 0 per row, else slice width (64)
+  int8_t* q;               // [M][K]
+  float* qscale;           // [M][K/ga or 1]
+  float* gsum;             // optional [M][K/128]
+  int M, K;
+};
+hipError_t launch_row_quant(const RowQuantArgs& a, hipStream_t st);
+
+// Plain per-token quantization of an fp32 or fp16 [M][K] buffer (no norm, no
+// rotation), K a multiple of 128 and <= 8192.
+hipError_t launch_quant_plain(const float* xf, const uint16_t* xh, int M, int K, int8_t* q,
+                              float* qscale, float* gsum, hipStream_t st);
+
+// ---- q/k norm + RoPE + KV append --------------------------------------------
+struct KVLayout {
+  int nkv, hd, page;          // page = tokens per page (32)
+  int max_pages;              // block-table row length
+  int kv_int8;
+  void* kpool;                // this layer: [pages][nkv][page][hd]   (fp16 or int8)
+  void* vpool;                // this layer: [pages][nkv][hd][page]   (transposed)
+  uint16_t* kscale;           // int8: [pages][nkv][page] fp16
+  uint16_t* vscale;
+  const int32_t* block_table; // [max_seqs][max_pages]
+};
+struct QKArgs {
+  const uint16_t* qkv;        // [M][nq*hd + 2*nkv*hd] fp16
+  const int32_t* row_seq;     // [M]
+  const int32_t* row_pos;     // [M]
+  const float* q_norm;        // [hd] or null
+  const float* k_norm;
+  const float* rope_cos;      // [max_pos][rotary/2]
+  const float* rope_sin;
+  int rotary;
+  float eps;
+  int nq;
+  uint16_t* qout;             // [M][nq][hd] fp16
+  int M;
+};
+hipError_t launch_qk_rope_kv(const QKArgs& a, const KVLayout& kv, hipStream_t st);
+
+// ---- ragged batch packing ---------------------------------------------------
+struct AttnUnit {
+  int seq, kvh, row0, qn, qpos0, kv_lo, kv_hi, pad;
+};
+struct PackOut {
+  int32_t* cu_seqlens;   // [ngroups + 1]
+  int32_t* row_grp;      // [M]
+  int32_t* row_seq;      // [M]
+  int32_t* row_pos;      // [M]
+  int32_t* row_kind;     // [M]
+  int32_t* comb_base;    // [M] unit index of (q-block, kvh 0, split 0)
+  int32_t* comb_nsplit;  // [M]
+  int32_t* comb_tok;     // [M] token index inside its q-block
+  AttnUnit* units;       // [n_units]
+  int32_t* want_rows;    // [n_want] rows to score, in row order
+};
+// rows: device copy of ifr_row[M] (5 int32 each).  qb = q-block tokens,
+// split = kv tokens per unit (multiple of the page size).
+hipError_t launch_pack(const int32_t* rows, int M, int nkv, int qb, int split, const PackOut& o,
+                       hipStream_t st);
+
+// ---- attention ------------------------------------------------------------------
+struct AttnArgs {
+  const AttnUnit* units;
+  int n_units;
+  const uint16_t* q;       // [M][nq][hd]
+  int nq;
+  float scale_log2;        // log2(e) / sqrt(hd)
+  float* part_o;           // [n_units][16][hd]
+  float* part_ml;          // [n_units][16][2]
+};
+hipError_t launch_attention(const AttnArgs& a, const KVLayout& kv, hipStream_t st);
+
+struct CombineArgs {
+  const float* part_o;
+  const float* part_ml;
+  const int32_t* comb_base;
+  const int32_t* comb_nsplit;
+  const int32_t* comb_tok;
+  int M, nq, nkv, hd;
+  float* attn_out;         // optional fp32 [M][nq*hd]
+  int8_t* q;               // [M][nq*hd] per-token int8 (half-away)
+  float* qscale;           // [M]
+  float* gsum;             // [M][nq*hd/128]
+};
+hipError_t launch_combine(const CombineArgs& a, hipStream_t st);
+
+// ---- lm_head + argmax ---------------------------------------------------------
+struct LmHeadArgs {
+  const int8_t* a;         // [W][H] GA64 RNE codes
+  const float* as;         // [W][H/64]
+  const uint32_t* wcodes;  // int8 weights in the bits=8 fragment layout
+  const uint16_t* wscale;  // [V] fp16 per-row scale
+  int W, V, H;
+  float* logits;           // optional [W][V]
+  float* part_val;         // [nparts][W]
+  int32_t* part_idx;
+  int32_t* best;           // [W]
+  int nparts;              // filled by the launcher
+};
+int lmhead_nparts(int V);
+hipError_t launch_lmhead(LmHeadArgs& a, hipStream_t st);
+
+// mg = fp16(silu(g) * u) over an unpaired [M][2F] gate|up fp16 buffer.
+hipError_t launch_swiglu(const uint16_t* gu, int M, int F, uint16_t* mg, hipStream_t st);
+
+// Gather rows for scoring: dst[i] = src[rows[i]] over H floats.
+hipError_t launch_gather_rows(const float* src, const int32_t* rows, int n, int H, float* dst,
+                              hipStream_t st);
+
+}  // namespace ifrk

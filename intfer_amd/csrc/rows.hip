@@ -1,0 +1,467 @@
+// Row-wise kernels of the mixed-batch forward on gfx950:
+//   row_quant   : [embed gather | residual += FWHT(y)/sqrt(K)] -> RMSNorm(1+w)
+//                 -> FWHT/sqrt(K) -> per-token (or GA64) int8 quantization
+//                 + per-128-group code sums (the S of the GEMM contract)
+//   quant_plain : per-token int8 quantization of an fp32/fp16 row
+//   qk_rope_kv  : per-head q/k RMSNorm(1+w) + rotate-half RoPE + fp16 round,
+//                 Q store, K/V append to the paged cache (fp16 or int8)
+//   pack        : ragged batch -> cu_seqlens, row maps, attention work units
+// One workgroup per row; the arithmetic follows the reference host helpers
+// operation for operation so the results are bit-identical to the CPU oracle
+// (RMSNorm in the reference's 8-lane fused order, main.cpp:306-351; FWHT in
+// the reference stage order, src/spinquant.cpp:303-312; act-quant with
+// correctly rounded division, dashq.cpp:221-336).
+#include "ifr_dev.h"
+#include "ifr_kernels.h"
+
+namespace ifrk {
+namespace {
+
+__device__ __forceinline__ float block_max(float v, float* red) {
+  v = ifrd::wave_max(v);
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  __syncthreads();
+  if (lane == 0) red[w] = v;
+  __syncthreads();
+  float r = red[0];
+  for (int i = 1; i < (int)(blockDim.x >> 6); ++i) r = fmaxf(r, red[i]);
+  return r;
+}
+
+// RMSNorm factor over x[0..n) (n a multiple of 8) in the reference AVX2 order:
+// eight fused lane accumulators, lanes folded (j, j+4), then two horizontal
+// adds.  Called by all threads; returns v = 1/sqrt(sum/n + eps) to all.
+__device__ float rms_factor(const float* x, int n, float eps, float* red) {
+  __syncthreads();
+  if (threadIdx.x < 8) {
+    float acc = 0.0f;
+    for (int i = threadIdx.x; i < n; i += 8) acc = fmaf(x[i], x[i], acc);
+    red[threadIdx.x] = acc;
+  }
+  __syncthreads();
+  const float s0 = red[0] + red[4], s1 = red[1] + red[5], s2 = red[2] + red[6], s3 = red[3] + red[7];
+  const float tot = (s0 + s1) + (s2 + s3);
+  const float v = 1.0f / sqrtf(tot / (float)n + eps);
+  __syncthreads();
+  return v;
+}
+
+// In-place FWHT of x[0..p) (p a power of two) in the reference stage order,
+// then x *= 1/sqrt(p).
+__device__ void fwht_lds(float* x, int p) {
+  for (int len = 2; len <= p; len <<= 1) {
+    const int half = len >> 1;
+    __syncthreads();
+    for (int b = threadIdx.x; b < (p >> 1); b += blockDim.x) {
+      const int i = (b / half) * len + (b % half);
+      const float u = x[i], v = x[i + half];
+      x[i] = u + v;
+      x[i + half] = u - v;
+    }
+  }
+  __syncthreads();
+  const float inv = 1.0f / sqrtf((float)p);
+  for (int i = threadIdx.x; i < p; i += blockDim.x) x[i] *= inv;
+  __syncthreads();
+}
+
+__device__ __forceinline__ int floor_pow2(int n) {
+  int p = 1;
+  while (p * 2 <= n) p *= 2;
+  return p;
+}
+
+// Quantize x[0..K) held in LDS.  Per row (ga == 0) or per ga-slice.
+__device__ void quant_lds(const float* x, int K, int ga, int round, int8_t* q, float* qs,
+                          float* gsum, float* red, int* codes_lds) {
+  if (ga == 0) {
+    float mx = 0.0f;
+    for (int i = threadIdx.x; i < K; i += blockDim.x) mx = fmaxf(mx, fabsf(x[i]));
+    mx = fmaxf(1e-6f, block_max(mx, red));
+    const float s = mx / 127.0f;
+    const float inv = 1.0f / s;
+    if (threadIdx.x == 0) qs[0] = s;
+    for (int i = threadIdx.x; i < K; i += blockDim.x) {
+      const int c = round == 0 ? ifrd::quant_half_away(x[i], inv) : ifrd::quant_rne(x[i], inv);
+      q[i] = (int8_t)c;
+      codes_lds[i] = c;
+    }
+  } else {
+    const int ns = K / ga;
+    __syncthreads();
+    for (int sl = threadIdx.x; sl < ns; sl += blockDim.x) {
+      float mx = 1e-6f;
+      for (int k = sl * ga; k < (sl + 1) * ga; ++k) mx = fmaxf(mx, fabsf(x[k]));
+      const float s = mx / 127.0f;
+      red[64 + sl] = 1.0f / s;
+      qs[sl] = s;
+    }
+    __syncthreads();
+    for (int i = threadIdx.x; i < K; i += blockDim.x) {
+      const float inv = red[64 + i / ga];
+      const int c = round == 0 ? ifrd::quant_half_away(x[i], inv) : ifrd::quant_rne(x[i], inv);
+      q[i] = (int8_t)c;
+      codes_lds[i] = c;
+    }
+  }
+  if (gsum) {
+    __syncthreads();
+    for (int g = threadIdx.x; g < K / 128; g += blockDim.x) {
+      int S = 0;
+      for (int k = g * 128; k < g * 128 + 128; ++k) S += codes_lds[k];
+      gsum[g] = (float)S;
+    }
+  }
+}
+
+__global__ __launch_bounds__(256) void row_quant_kernel(RowQuantArgs a) {
+  extern __shared__ float sh[];
+  float* x = sh;                                  // K floats
+  int* codes = reinterpret_cast<int*>(sh + a.K);  // K ints
+  float* red = sh + 2 * a.K;                      // 64 + K/64 floats
+  const int m = blockIdx.x, K = a.K;
+  const int src = a.rowmap ? a.rowmap[m] : m;
+  if (a.src == SRC_X) {
+    for (int i = threadIdx.x; i < K; i += blockDim.x) x[i] = a.x[(size_t)src * K + i];
+  } else if (a.src == SRC_EMBED) {
+    const float* e = a.embed + (size_t)a.tokens[src] * K;
+    for (int i = threadIdx.x; i < K; i += blockDim.x) {
+      const float v = e[i];
+      x[i] = v;
+      a.resid[(size_t)src * K + i] = v;
+    }
+  } else {
+    for (int i = threadIdx.x; i < K; i += blockDim.x) x[i] = ifrd::h2f(a.y[(size_t)src * K + i]);
+    if (a.rot_y) fwht_lds(x, floor_pow2(K));
+    __syncthreads();
+    for (int i = threadIdx.x; i < K; i += blockDim.x) {
+      const float v = a.resid[(size_t)src * K + i] + x[i];
+      a.resid[(size_t)src * K + i] = v;
+      x[i] = v;
+    }
+  }
+  __syncthreads();
+  if (a.norm_w) {
+    const float v = rms_factor(x, K, a.eps, red);
+    for (int i = threadIdx.x; i < K; i += blockDim.x) x[i] = (x[i] * v) * (1.0f + a.norm_w[i]);
+  }
+  if (a.rotate) fwht_lds(x, floor_pow2(K));
+  __syncthreads();
+  const int ns = a.ga ? K / a.ga : 1;
+  quant_lds(x, K, a.ga, a.round, a.q + (size_t)m * K, a.qscale + (size_t)m * ns,
+            a.gsum ? a.gsum + (size_t)m * (K / 128) : nullptr, red, codes);
+}
+
+__global__ __launch_bounds__(256) void quant_plain_kernel(const float* xf, const uint16_t* xh,
+                                                          int K, int8_t* q, float* qs,
+                                                          float* gsum) {
+  extern __shared__ float sh[];
+  float* x = sh;
+  int* codes = reinterpret_cast<int*>(sh + K);
+  float* red = sh + 2 * K;
+  const int m = blockIdx.x;
+  for (int i = threadIdx.x; i < K; i += blockDim.x)
+    x[i] = xf ? xf[(size_t)m * K + i] : ifrd::h2f(xh[(size_t)m * K + i]);
+  __syncthreads();
+  quant_lds(x, K, 0, 0, q + (size_t)m * K, qs + m, gsum ? gsum + (size_t)m * (K / 128) : nullptr,
+            red, codes);
+}
+
+// ---- q/k norm + RoPE + KV append --------------------------------------------
+// One workgroup per row, one wave per head vector (hd = 128, 2 dims per lane).
+__global__ __launch_bounds__(256) void qk_rope_kv_kernel(QKArgs a, KVLayout kv) {
+  __shared__ float hx[4][128];
+  __shared__ float red[4][16];
+  const int m = blockIdx.x, lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int hd = kv.hd, nq = a.nq, nkv = kv.nkv;
+  const int ncols = (nq + 2 * nkv) * hd;
+  const int pos = a.row_pos[m], seq = a.row_seq[m];
+  const int page = kv.block_table[(size_t)seq * kv.max_pages + pos / kv.page];
+  const int tok = pos % kv.page;
+  const int half = a.rotary / 2;
+  float* x = hx[w];
+  for (int h = w; h < nq + 2 * nkv; h += 4) {
+    const int kind = h < nq ? 0 : (h < nq + nkv ? 1 : 2);  // q, k, v
+    const int hh = kind == 0 ? h : (kind == 1 ? h - nq : h - nq - nkv);
+    const uint16_t* src = a.qkv + (size_t)m * ncols + (size_t)h * hd;
+    x[2 * lane] = ifrd::h2f(src[2 * lane]);
+    x[2 * lane + 1] = ifrd::h2f(src[2 * lane + 1]);
+    ifrd::wave_sync();
+    float v0 = x[2 * lane], v1 = x[2 * lane + 1];
+    if (kind < 2) {
+      const float* nw = kind == 0 ? a.q_norm : a.k_norm;
+      if (nw) {
+        // 8-lane fused partials (reference AVX2 order), as in rms_factor.
+        if (lane < 8) {
+          float acc = 0.0f;
+          for (int i = lane; i < hd; i += 8) acc = fmaf(x[i], x[i], acc);
+          red[w][lane] = acc;
+        }
+        ifrd::wave_sync();
+        const float s0 = red[w][0] + red[w][4], s1 = red[w][1] + red[w][5];
+        const float s2 = red[w][2] + red[w][6], s3 = red[w][3] + red[w][7];
+        const float tot = (s0 + s1) + (s2 + s3);
+        const float f = 1.0f / sqrtf(tot / (float)hd + a.eps);
+        v0 = (v0 * f) * (1.0f + nw[2 * lane]);
+        v1 = (v1 * f) * (1.0f + nw[2 * lane + 1]);
+        ifrd::wave_sync();
+        x[2 * lane] = v0;
+        x[2 * lane + 1] = v1;
+        ifrd::wave_sync();
+      }
+      // rotate-half RoPE on the first `rotary` dims (main.cpp:365-373)
+      const float* cs = a.rope_cos + (size_t)pos * half;
+      const float* sn = a.rope_sin + (size_t)pos * half;
+      float o[2] = {v0, v1};
+#pragma unroll
+      for (int e2 = 0; e2 < 2; ++e2) {
+        const int e = 2 * lane + e2;
+        if (e < half) {
+          const float p = x[e] * cs[e];
+          const float q = x[e + half] * sn[e];
+          o[e2] = p - q;
+        } else if (e < 2 * half) {
+          const int d = e - half;
+          const float p = x[d] * sn[d];
+          const float q = x[e] * cs[d];
+          o[e2] = p + q;
+        }
+      }
+      v0 = o[0];
+      v1 = o[1];
+      ifrd::wave_sync();
+    }
+    v0 = ifrd::fp16r(v0);
+    v1 = ifrd::fp16r(v1);
+    if (kind == 0) {
+      uint16_t* dst = a.qout + ((size_t)m * nq + hh) * hd;
+      dst[2 * lane] = ifrd::f2h(v0);
+      dst[2 * lane + 1] = ifrd::f2h(v1);
+    } else {
+      const size_t base = ((size_t)page * nkv + hh);
+      if (!kv.kv_int8) {
+        if (kind == 1) {
+          uint16_t* kp = reinterpret_cast<uint16_t*>(kv.kpool) + (base * kv.page + tok) * hd;
+          kp[2 * lane] = ifrd::f2h(v0);
+          kp[2 * lane + 1] = ifrd::f2h(v1);
+        } else {
+          uint16_t* vp = reinterpret_cast<uint16_t*>(kv.vpool) + base * hd * kv.page;
+          vp[(size_t)(2 * lane) * kv.page + tok] = ifrd::f2h(v0);
+          vp[(size_t)(2 * lane + 1) * kv.page + tok] = ifrd::f2h(v1);
+        }
+      } else {
+        const float mx = ifrd::wave_max(fmaxf(fabsf(v0), fabsf(v1)));
+        const uint16_t sh16 = ifrd::f2h(mx > 0.0f ? mx / 127.0f : 1.0f);
+        const float s = ifrd::h2f(sh16);
+        const float inv = 1.0f / s;
+        int q0, q1;
+        {
+          const float t0 = v0 * inv, t1 = v1 * inv;
+          q0 = (int)(t0 >= 0.0f ? t0 + 0.5f : t0 - 0.5f);
+          q1 = (int)(t1 >= 0.0f ? t1 + 0.5f : t1 - 0.5f);
+          q0 = min(127, max(-127, q0));
+          q1 = min(127, max(-127, q1));
+        }
+        if (kind == 1) {
+          int8_t* kp = reinterpret_cast<int8_t*>(kv.kpool) + (base * kv.page + tok) * hd;
+          kp[2 * lane] = (int8_t)q0;
+          kp[2 * lane + 1] = (int8_t)q1;
+          if (lane == 0) kv.kscale[base * kv.page + tok] = sh16;
+        } else {
+          int8_t* vp = reinterpret_cast<int8_t*>(kv.vpool) + base * hd * kv.page;
+          vp[(size_t)(2 * lane) * kv.page + tok] = (int8_t)q0;
+          vp[(size_t)(2 * lane + 1) * kv.page + tok] = (int8_t)q1;
+          if (lane == 0) kv.vscale[base * kv.page + tok] = sh16;
+        }
+      }
+    }
+    ifrd::wave_sync();
+  }
+}
+
+// ---- ragged batch packing ------------------------------------------------------
+// Block-wide exclusive scan of n ints in LDS (in place); returns the total.
+__device__ int block_exscan(int* v, int n, int* tmp) {
+  const int T = blockDim.x;
+  // per-thread contiguous chunk
+  const int per = (n + T - 1) / T;
+  const int b = threadIdx.x * per, e = min(n, b + per);
+  int s = 0;
+  for (int i = b; i < e; ++i) s += v[i];
+  tmp[threadIdx.x] = s;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    int run = 0;
+    for (int i = 0; i < T; ++i) { const int t = tmp[i]; tmp[i] = run; run += t; }
+    tmp[T] = run;
+  }
+  __syncthreads();
+  int run = tmp[threadIdx.x];
+  for (int i = b; i < e; ++i) { const int t = v[i]; v[i] = run; run += t; }
+  __syncthreads();
+  const int total = tmp[T];
+  __syncthreads();
+  return total;
+}
+
+__global__ __launch_bounds__(1024) void pack_kernel(const int32_t* rows, int M, int nkv, int qb,
+                                                    int split, PackOut o) {
+  extern __shared__ int sm[];
+  int* flag = sm;              // [M]   group start -> group index
+  int* grp_start = sm + M;     // [M+1] row offset of group g
+  int* nblk = sm + 2 * M + 1;  // [M+1] q-blocks per group -> block base
+  int* ucnt = sm + 3 * M + 2;  // [M]   units per q-block -> unit base
+  int* wnt = sm + 4 * M + 2;   // [M]   want flags -> want slot
+  int* tmp = sm + 5 * M + 2;   // [blockDim + 1]
+  for (int m = threadIdx.x; m < M; m += blockDim.x) {
+    const int32_t* r = rows + 5 * m;
+    flag[m] = (m == 0 || rows[5 * (m - 1)] != r[0]) ? 1 : 0;
+    wnt[m] = r[4] ? 1 : 0;
+    o.row_seq[m] = r[0];
+    o.row_pos[m] = r[1];
+    o.row_kind[m] = r[3];
+  }
+  __syncthreads();
+  // group index of each row: inclusive scan of the start flags - 1
+  for (int m = threadIdx.x; m < M; m += blockDim.x) grp_start[m] = flag[m];
+  __syncthreads();
+  const int ngroups = block_exscan(grp_start, M, tmp);  // grp_start[m] = #starts before m
+  for (int m = threadIdx.x; m < M; m += blockDim.x) {
+    const int g = grp_start[m] + flag[m] - 1;
+    o.row_grp[m] = g;
+    flag[m] = g;
+  }
+  __syncthreads();
+  for (int m = threadIdx.x; m < M; m += blockDim.x)
+    if (m == 0 || flag[m] != flag[m - 1]) grp_start[flag[m]] = m;
+  if (threadIdx.x == 0) grp_start[ngroups] = M;
+  __syncthreads();
+  for (int g = threadIdx.x; g <= ngroups; g += blockDim.x) o.cu_seqlens[g] = grp_start[g];
+  for (int g = threadIdx.x; g < ngroups; g += blockDim.x) {
+    const int len = grp_start[g + 1] - grp_start[g];
+    nblk[g] = (len + qb - 1) / qb;
+  }
+  __syncthreads();
+  const int nb = block_exscan(nblk, ngroups, tmp);  // nblk[g] = first block of group g
+  if (threadIdx.x == 0) nblk[ngroups] = nb;
+  __syncthreads();
+  // units per q-block
+  for (int g = threadIdx.x; g < ngroups; g += blockDim.x) {
+    const int r0 = grp_start[g], len = grp_start[g + 1] - r0;
+    const int pos0 = rows[5 * r0 + 1];
+    for (int b = 0; b < nblk[g + 1] - nblk[g]; ++b) {
+      const int kvhi = pos0 + min((b + 1) * qb, len);
+      ucnt[nblk[g] + b] = nkv * ((kvhi + split - 1) / split);
+    }
+  }
+  __syncthreads();
+  block_exscan(ucnt, nb, tmp);  // ucnt[b] = first unit of block b
+  for (int g = threadIdx.x; g < ngroups; g += blockDim.x) {
+    const int r0 = grp_start[g], len = grp_start[g + 1] - r0;
+    const int pos0 = rows[5 * r0 + 1], seq = rows[5 * r0];
+    for (int b = 0; b < nblk[g + 1] - nblk[g]; ++b) {
+      const int qn = min(qb, len - b * qb);
+      const int kvhi = pos0 + b * qb + qn;
+      const int ns = (kvhi + split - 1) / split;
+      const int base = ucnt[nblk[g] + b];
+      for (int kvh = 0; kvh < nkv; ++kvh)
+        for (int s = 0; s < ns; ++s) {
+          AttnUnit u;
+          u.seq = seq;
+          u.kvh = kvh;
+          u.row0 = r0 + b * qb;
+          u.qn = qn;
+          u.qpos0 = pos0 + b * qb;
+          u.kv_lo = s * split;
+          u.kv_hi = min((s + 1) * split, kvhi);
+          u.pad = 0;
+          o.units[base + kvh * ns + s] = u;
+        }
+      for (int i = 0; i < qn; ++i) {
+        const int m = r0 + b * qb + i;
+        o.comb_base[m] = base;
+        o.comb_nsplit[m] = ns;
+        o.comb_tok[m] = i;
+      }
+    }
+  }
+  __syncthreads();
+  block_exscan(wnt, M, tmp);
+  for (int m = threadIdx.x; m < M; m += blockDim.x)
+    if (rows[5 * m + 4]) o.want_rows[wnt[m]] = m;
+}
+
+// mg = fp16(silu(g) * u) over an unpaired [M][2F] gate|up buffer (used when
+// gate and up have different bit widths and cannot share one launch).
+__global__ void swiglu_kernel(const uint16_t* gu, int F, uint16_t* mg) {
+  const int m = blockIdx.y;
+  for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < F; i += gridDim.x * blockDim.x) {
+    const float g = ifrd::h2f(gu[(size_t)m * 2 * F + i]);
+    const float u = ifrd::h2f(gu[(size_t)m * 2 * F + F + i]);
+    mg[(size_t)m * F + i] = ifrd::f2h(g / (1.0f + expf(-g)) * u);
+  }
+}
+
+__global__ void gather_rows_kernel(const float* src, const int32_t* rows, int H, float* dst) {
+  const int i = blockIdx.x;
+  const float* s = src + (size_t)rows[i] * H;
+  for (int k = threadIdx.x; k < H; k += blockDim.x) dst[(size_t)i * H + k] = s[k];
+}
+
+}  // namespace
+
+hipError_t launch_row_quant(const RowQuantArgs& a, hipStream_t st) {
+  if (a.M <= 0) return hipSuccess;
+  if (a.K <= 0 || a.K % 128 != 0 || a.K > 8192 || !a.q || !a.qscale) return hipErrorInvalidValue;
+  if (a.ga != 0 && (a.ga != 64 || a.K / 64 > 192)) return hipErrorInvalidValue;
+  if (a.src == SRC_X && !a.x) return hipErrorInvalidValue;
+  if (a.src == SRC_EMBED && (!a.embed || !a.tokens || !a.resid)) return hipErrorInvalidValue;
+  if (a.src == SRC_RESID && (!a.y || !a.resid)) return hipErrorInvalidValue;
+  const size_t lds = (size_t)(2 * a.K + 64 + a.K / 64) * sizeof(float);
+  hipLaunchKernelGGL(row_quant_kernel, dim3(a.M), dim3(256), lds, st, a);
+  return hipGetLastError();
+}
+
+hipError_t launch_quant_plain(const float* xf, const uint16_t* xh, int M, int K, int8_t* q,
+                              float* qscale, float* gsum, hipStream_t st) {
+  if (M <= 0) return hipSuccess;
+  if (K <= 0 || K % 128 != 0 || K > 8192 || (!xf && !xh) || !q || !qscale)
+    return hipErrorInvalidValue;
+  const size_t lds = (size_t)(2 * K + 64) * sizeof(float);
+  hipLaunchKernelGGL(quant_plain_kernel, dim3(M), dim3(256), lds, st, xf, xh, K, q, qscale, gsum);
+  return hipGetLastError();
+}
+
+hipError_t launch_qk_rope_kv(const QKArgs& a, const KVLayout& kv, hipStream_t st) {
+  if (a.M <= 0) return hipSuccess;
+  if (kv.hd != 128 || a.rotary <= 0 || a.rotary > kv.hd || a.rotary % 2 != 0 || kv.page <= 0 ||
+      !a.qkv || !a.qout || !kv.kpool || !kv.vpool || !kv.block_table)
+    return hipErrorInvalidValue;
+  if (kv.kv_int8 && (!kv.kscale || !kv.vscale)) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(qk_rope_kv_kernel, dim3(a.M), dim3(256), 0, st, a, kv);
+  return hipGetLastError();
+}
+
+hipError_t launch_pack(const int32_t* rows, int M, int nkv, int qb, int split, const PackOut& o,
+                       hipStream_t st) {
+  if (M <= 0) return hipSuccess;
+  if (M > 8192 || qb <= 0 || split <= 0 || nkv <= 0) return hipErrorInvalidValue;
+  const size_t lds = (size_t)(5 * M + 2 + 1024 + 1) * sizeof(int);
+  hipLaunchKernelGGL(pack_kernel, dim3(1), dim3(1024), lds, st, rows, M, nkv, qb, split, o);
+  return hipGetLastError();
+}
+
+hipError_t launch_swiglu(const uint16_t* gu, int M, int F, uint16_t* mg, hipStream_t st) {
+  if (M <= 0) return hipSuccess;
+  hipLaunchKernelGGL(swiglu_kernel, dim3((F + 255) / 256, M), dim3(256), 0, st, gu, F, mg);
+  return hipGetLastError();
+}
+
+hipError_t launch_gather_rows(const float* src, const int32_t* rows, int n, int H, float* dst,
+                              hipStream_t st) {
+  if (n <= 0) return hipSuccess;
+  hipLaunchKernelGGL(gather_rows_kernel, dim3(n), dim3(256), 0, st, src, rows, H, dst);
+  return hipGetLastError();
+}
+
+}  // namespace ifrk

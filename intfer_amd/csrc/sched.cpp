@@ -1,0 +1,338 @@
+// Continuous-batching iteration scheduler over the C-ABI engine.
+//
+// Restates the reference serve loop's policy (examples/intfer_cli/main.cpp):
+//   sched_iteration_joint :8427-8542  one forward = [decode rows of live
+//                                     requests in live order | up to chunk_m
+//                                     prefill rows of the prefill-queue head]
+//   sched_iteration       :8382-8413  decode-only forward (split path)
+//   serve_iteration       :9203-9259  joint, or split (chunk forward, then
+//                                     decode forward) when split_iter is set
+//   serve_rotate_unfilled :9187-9195  round-robin rotation of unfilled heads
+//   run_serve admission   :9329-9342  FIFO admission while live < cap
+//   finish rule           :8409-8410  EOS 248044/248046 or max_new+1 ids
+// plus n-gram speculative verify rows (main.cpp:11522-11550 ngram_from,
+// :11842-11931 verify / accept / rollback) as a third row kind: a speculating
+// request contributes its token and K drafts as one causal verify group.
+#include <algorithm>
+#include <deque>
+#include <map>
+#include <memory>
+#include <string>
+#include <vector>
+
+#include "intfer_amd.h"
+
+namespace {
+
+constexpr int kEos0 = 248044, kEos1 = 248046;
+
+struct Req {
+  int64_t id = 0;
+  std::vector<int32_t> prompt, generated;
+  int token = -1, pos = 0, fill = 0, max_new = 0;
+  bool finished = false;
+  int slot = -1;
+};
+
+// Drafts: tokens following the last occurrence of `tok` in generated (stops
+// at its end), else in the prompt continuing into generated (main.cpp:
+// 11522-11550, restated exactly, including that a search hit at the end of
+// `gen` yields nothing and ends the generated search).
+std::vector<int32_t> ngram_from(const std::vector<int32_t>& gen, const std::vector<int32_t>& pr,
+                                int tok, int K) {
+  std::vector<int32_t> d;
+  for (int occ = (int)gen.size() - 1; occ >= 0 && (int)d.size() < K; --occ) {
+    if (gen[(size_t)occ] == tok) {
+      for (int j = occ + 1; j < (int)gen.size() && (int)d.size() < K; ++j) d.push_back(gen[(size_t)j]);
+      break;
+    }
+  }
+  if ((int)d.size() < K) {
+    for (int occ = (int)pr.size() - 1; occ >= 0 && (int)d.size() < K; --occ) {
+      if (pr[(size_t)occ] == tok) {
+        for (int j = occ + 1; j < (int)pr.size() && (int)d.size() < K; ++j) d.push_back(pr[(size_t)j]);
+        for (int j = 0; j < (int)gen.size() && (int)d.size() < K; ++j) d.push_back(gen[(size_t)j]);
+        break;
+      }
+    }
+  }
+  if ((int)d.size() > K) d.resize(K);
+  return d;
+}
+
+bool is_eos(int t) { return t == kEos0 || t == kEos1; }
+
+}  // namespace
+
+struct ifr_sched {
+  ifr_sched_backend be{};
+  ifr_sched_cfg cfg{};
+  int max_seq_tokens = 0;
+  std::map<int64_t, std::unique_ptr<Req>> pool;
+  std::deque<Req*> pending;
+  std::vector<Req*> live;
+  std::deque<Req*> prefill_q;
+  int64_t next_id = 1;
+  std::vector<ifr_row> last_rows;
+  std::vector<ifr_row> rows;
+  std::vector<int32_t> best;
+
+  struct DecodeItem {
+    Req* r;
+    int row0;
+    std::vector<int32_t> drafts;
+  };
+
+  int forward() {
+    best.assign(rows.size(), -1);
+    last_rows = rows;
+    return be.forward(be.user, rows.data(), (int32_t)rows.size(), best.data());
+  }
+
+  // Decode (or verify) rows for every live request (main.cpp:8438-8446).
+  void build_decode(std::vector<DecodeItem>& items) {
+    for (Req* q : live) {
+      if (q->finished) continue;
+      if ((int)q->generated.size() >= q->max_new + 1) { q->finished = true; continue; }
+      DecodeItem it{q, (int)rows.size(), {}};
+      if (cfg.spec_k > 0) {
+        it.drafts = ngram_from(q->generated, q->prompt, q->token, cfg.spec_k);
+        while (!it.drafts.empty() && q->pos + (int)it.drafts.size() >= max_seq_tokens) it.drafts.pop_back();
+      }
+      const int kind = it.drafts.empty() ? IFR_ROW_DECODE : IFR_ROW_VERIFY;
+      rows.push_back({q->slot, q->pos, q->token, kind, 1});
+      for (size_t i = 0; i < it.drafts.size(); ++i)
+        rows.push_back({q->slot, q->pos + 1 + (int)i, it.drafts[i], IFR_ROW_VERIFY, 1});
+      items.push_back(std::move(it));
+    }
+  }
+
+  // Advance decode / verify rows after the forward (main.cpp:8500-8515,
+  // :11867-11931).
+  int finish_decode(const std::vector<DecodeItem>& items) {
+    for (const DecodeItem& it : items) {
+      Req& q = *it.r;
+      if (it.drafts.empty()) {
+        const int next = best[(size_t)it.row0];
+        q.generated.push_back(next);
+        q.pos++;
+        q.token = next;
+        if (is_eos(next)) q.finished = true;
+        if ((int)q.generated.size() >= q.max_new + 1) q.finished = true;
+        continue;
+      }
+      const int K = (int)it.drafts.size();
+      int a = 0;
+      while (a < K && best[(size_t)it.row0 + a] == it.drafts[(size_t)a]) a++;
+      const int corr = best[(size_t)it.row0 + a];
+      std::vector<int32_t> emit;
+      for (int i = 0; i < a; ++i) {
+        emit.push_back(it.drafts[(size_t)i]);
+        if (is_eos(it.drafts[(size_t)i])) break;
+      }
+      bool stopped = !emit.empty() && is_eos(emit.back());
+      if (!stopped) emit.push_back(corr);
+      int budget = q.max_new + 1 - (int)q.generated.size();
+      if (budget < 1) budget = 1;
+      while ((int)emit.size() > budget) emit.pop_back();
+      stopped = !emit.empty() && is_eos(emit.back());
+      const int n_draft_emit = (int)emit.size() - (stopped ? 0 : 1);
+      const int pend = q.pos + n_draft_emit;
+      if (int r = be.seq_truncate(be.user, q.slot, pend + 1)) return r;
+      for (int t : emit) q.generated.push_back(t);
+      q.token = q.generated.back();
+      q.pos = pend + 1;
+      if (stopped) q.finished = true;
+      if ((int)q.generated.size() >= q.max_new + 1) q.finished = true;
+    }
+    return IFR_OK;
+  }
+
+  void prefill_done(Req* pq, int best_id) {
+    const int Sr = (int)pq->prompt.size();
+    pq->generated.push_back(best_id);
+    pq->token = best_id;
+    pq->pos = Sr;
+    live.push_back(pq);
+  }
+
+  int joint(int32_t* nrun) {
+    rows.clear();
+    std::vector<DecodeItem> items;
+    build_decode(items);
+    Req* pq = prefill_q.empty() ? nullptr : prefill_q.front();
+    int P = 0, p0 = (int)rows.size();
+    if (pq) {
+      const int Sr = (int)pq->prompt.size();
+      P = std::min(cfg.chunk_m, Sr - pq->fill);
+      for (int k = 0; k < P; ++k) {
+        const int pos = pq->fill + k;
+        rows.push_back({pq->slot, pos, pq->prompt[(size_t)pos], IFR_ROW_PREFILL,
+                        (pq->fill + P == Sr && k == P - 1) ? 1 : 0});
+      }
+    }
+    *nrun = (int32_t)rows.size();
+    if (rows.empty()) return IFR_OK;
+    if (int r = forward()) return r;
+    if (int r = finish_decode(items)) return r;
+    if (pq) {
+      const int Sr = (int)pq->prompt.size();
+      pq->fill += P;
+      if (pq->fill == Sr) {
+        prefill_q.pop_front();
+        prefill_done(pq, best[(size_t)p0 + P - 1]);
+      } else if (cfg.round_robin && prefill_q.size() > 1) {
+        prefill_q.pop_front();
+        prefill_q.push_back(pq);
+      }
+    }
+    return IFR_OK;
+  }
+
+  int split(int32_t* nrun) {
+    *nrun = 0;
+    if (!prefill_q.empty()) {
+      Req* q = prefill_q.front();
+      const int Sr = (int)q->prompt.size();
+      const int cm = std::min(cfg.chunk_m, Sr - q->fill);
+      rows.clear();
+      for (int k = 0; k < cm; ++k) {
+        const int pos = q->fill + k;
+        rows.push_back({q->slot, pos, q->prompt[(size_t)pos], IFR_ROW_PREFILL,
+                        (q->fill + cm == Sr && k == cm - 1) ? 1 : 0});
+      }
+      if (int r = forward()) return r;
+      *nrun += cm;
+      q->fill += cm;
+      if (q->fill == Sr) {
+        prefill_q.pop_front();
+        prefill_done(q, best[(size_t)cm - 1]);
+      } else if (cfg.round_robin && prefill_q.size() > 1 && prefill_q.front() == q) {
+        prefill_q.pop_front();
+        prefill_q.push_back(q);
+      }
+    }
+    if (!live.empty()) {
+      rows.clear();
+      std::vector<DecodeItem> items;
+      build_decode(items);
+      if (!rows.empty()) {
+        if (int r = forward()) return r;
+        *nrun += (int32_t)rows.size();
+        if (int r = finish_decode(items)) return r;
+      }
+    }
+    return IFR_OK;
+  }
+};
+
+extern "C" {
+
+namespace {
+int eng_open(void* u, int32_t* slot) { return ifr_seq_open(static_cast<ifr_ctx*>(u), slot); }
+int eng_close(void* u, int32_t slot) { return ifr_seq_close(static_cast<ifr_ctx*>(u), slot); }
+int eng_trunc(void* u, int32_t slot, int32_t len) {
+  return ifr_seq_truncate(static_cast<ifr_ctx*>(u), slot, len);
+}
+int eng_fwd(void* u, const ifr_row* rows, int32_t M, int32_t* best) {
+  return ifr_forward(static_cast<ifr_ctx*>(u), rows, M, best, nullptr);
+}
+}  // namespace
+
+int ifr_sched_create_backend(const ifr_sched_backend* be, const ifr_sched_cfg* cfg, ifr_sched** out) {
+  if (!be || !cfg || !out || !be->seq_open || !be->seq_close || !be->seq_truncate || !be->forward)
+    return IFR_EINVAL;
+  if (cfg->chunk_m < 1 || cfg->chunk_m > 4096 || cfg->live_cap < 1 || cfg->spec_k < 0 ||
+      cfg->spec_k > 15 || be->kv_capacity <= 0)
+    return IFR_EINVAL;
+  auto* s = new ifr_sched();
+  s->be = *be;
+  s->cfg = *cfg;
+  s->max_seq_tokens = be->kv_capacity;
+  *out = s;
+  return IFR_OK;
+}
+
+int ifr_sched_create(ifr_ctx* ctx, const ifr_sched_cfg* cfg, ifr_sched** out) {
+  if (!ctx) return IFR_EINVAL;
+  ifr_sched_backend be{};
+  be.user = ctx;
+  be.seq_open = eng_open;
+  be.seq_close = eng_close;
+  be.seq_truncate = eng_trunc;
+  be.forward = eng_fwd;
+  if (int r = ifr_kv_capacity(ctx, &be.kv_capacity)) return r;
+  return ifr_sched_create_backend(&be, cfg, out);
+}
+
+int ifr_sched_destroy(ifr_sched* s) {
+  if (!s) return IFR_OK;
+  for (auto& kv : s->pool)
+    if (kv.second->slot >= 0) s->be.seq_close(s->be.user, kv.second->slot);
+  delete s;
+  return IFR_OK;
+}
+
+int ifr_sched_submit(ifr_sched* s, const int32_t* prompt, int32_t n, int32_t max_new, int64_t* id) {
+  if (!s || !prompt || n <= 0 || max_new < 0) return IFR_EINVAL;
+  auto r = std::make_unique<Req>();
+  r->id = s->next_id++;
+  r->prompt.assign(prompt, prompt + n);
+  r->max_new = max_new;
+  if (id) *id = r->id;
+  s->pending.push_back(r.get());
+  s->pool[r->id] = std::move(r);
+  return IFR_OK;
+}
+
+int ifr_sched_step(ifr_sched* s, int32_t* rows_run) {
+  if (!s) return IFR_EINVAL;
+  int32_t dummy = 0;
+  if (!rows_run) rows_run = &dummy;
+  *rows_run = 0;
+  // admission: FIFO while live < cap and a KV slot is free
+  while (!s->pending.empty() && (int)s->live.size() < s->cfg.live_cap) {
+    Req* q = s->pending.front();
+    int32_t slot = -1;
+    if (s->be.seq_open(s->be.user, &slot) != IFR_OK) break;
+    q->slot = slot;
+    s->pending.pop_front();
+    s->prefill_q.push_back(q);
+  }
+  int r = s->cfg.split_iter ? s->split(rows_run) : s->joint(rows_run);
+  if (r) return r;
+  // live compaction; finished requests release their KV
+  std::vector<Req*> still;
+  for (Req* q : s->live) {
+    if (q->finished) {
+      if (q->slot >= 0) s->be.seq_close(s->be.user, q->slot);
+      q->slot = -1;
+    } else {
+      still.push_back(q);
+    }
+  }
+  s->live.swap(still);
+  return IFR_OK;
+}
+
+int ifr_sched_result(ifr_sched* s, int64_t id, int32_t* out, int32_t cap, int32_t* n, int32_t* done) {
+  if (!s) return IFR_EINVAL;
+  auto it = s->pool.find(id);
+  if (it == s->pool.end()) return IFR_EINVAL;
+  const Req& q = *it->second;
+  const int k = std::min<int>(cap, (int)q.generated.size());
+  for (int i = 0; i < k && out; ++i) out[i] = q.generated[(size_t)i];
+  if (n) *n = (int32_t)q.generated.size();
+  if (done) *done = q.finished ? 1 : 0;
+  return IFR_OK;
+}
+
+int ifr_sched_last_rows(ifr_sched* s, ifr_row* out, int32_t cap, int32_t* n) {
+  if (!s) return IFR_EINVAL;
+  const int k = std::min<int>(cap, (int)s->last_rows.size());
+  for (int i = 0; i < k && out; ++i) out[i] = s->last_rows[(size_t)i];
+  if (n) *n = (int32_t)s->last_rows.size();
+  return IFR_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,361 @@
+"""Pins of the CPU oracle (oracle/oracle.cpp) before it is trusted as the checker.
+
+Each oracle function is checked against something other than itself:
+  or_f2h / or_h2f        reference dashq float_to_half / half_to_float (all 65536
+                         halves + 2M float patterns) and numpy's IEEE conversion
+  or_act_quant (GA64)    reference dashq::act_quant_ga64_batch, both roundings,
+                         random rows and .5-tie-adversarial rows
+  or_act_quant (per row) numpy float32 closed form of the same rule
+  or_rot                 reference make_hadamard + apply_rotation_fwht (bit-exact,
+                         pow2 and blockdiag(H_p, I)); dense H in float64
+  or_dequant             reference QuantResult::dequant (canonical codebook)
+  or_rmsnorm             float64 formula (1+w form, eps) -- order is checked
+                         bit-exactly against the GPU kernel, not here
+  or_qgemm_ts            int64 brute force
+  or_qgemm (fold)        float64 dequant GEMM
+  or_lmhead_quant        numpy float32 closed form of main.cpp:1745-1761
+  or_lmhead / or_argmax  float64 logits; first-max-wins on planted ties
+  or_attention_row       float64 softmax attention
+  or_rope                float64 cos/sin of the float32 angle
+  forward (a8 / f32)     chunk invariance (M=1 == M=8 rows), f32 ~ a8 agreement
+Parity unpinned: none of the oracle functions above; the composition of the
+forward is pinned by its parts plus the invariants in the last tests.
+"""
+import ctypes as C
+
+import numpy as np
+import pytest
+
+import intfer_amd as ia
+from oracle import pyoracle as po
+from oracle.pyoracle import ptr
+
+REF = po.ref()
+needs_ref = pytest.mark.skipif(REF is None, reason="oracle/_ref not built (no reference tree)")
+
+
+@pytest.fixture(scope="module")
+def O():
+    return po.oracle()
+
+
+# ---- fp16 --------------------------------------------------------------------------
+
+def test_h2f_all_halves_match_reference_and_numpy(O):
+    h = np.arange(65536, dtype=np.uint16)
+    ours = np.empty(65536, np.float32)
+    O.or_h2f_batch(ptr(h), ptr(ours), 65536)
+    npv = h.view(np.float16).astype(np.float32)
+    fin = np.isfinite(npv)
+    assert np.array_equal(ours.view(np.uint32)[fin], npv.view(np.uint32)[fin])
+    assert np.all(np.isnan(ours[np.isnan(npv)]))
+    if REF is not None:
+        ref = np.array([REF.ref_half_to_float(int(x)) for x in h[::7]], np.float32)
+        f7 = fin[::7]  # NaN payloads do not survive a Python float round trip
+        assert np.array_equal(ours[::7].view(np.uint32)[f7], ref.view(np.uint32)[f7])
+
+
+def test_f2h_matches_reference_and_numpy(O):
+    rng = np.random.default_rng(1)
+    bits = rng.integers(0, 2**32, size=2_000_000, dtype=np.uint64).astype(np.uint32)
+    # plus every half-way point between consecutive halves (RNE ties)
+    h = np.arange(0, 0x7C00, dtype=np.uint32)
+    lo = h.astype(np.uint16).view(np.float16).astype(np.float64)
+    hi = (h + 1).astype(np.uint16).view(np.float16).astype(np.float64)
+    mids = ((lo + hi) / 2).astype(np.float32)
+    x = np.concatenate([bits.view(np.float32), mids, -mids]).astype(np.float32)
+    x = x[np.isfinite(x)]
+    ours = np.empty(x.size, np.uint16)
+    O.or_f2h_batch(ptr(x), ptr(ours), x.size)
+    with np.errstate(over="ignore"):
+        npv = x.astype(np.float16).view(np.uint16)
+    assert np.array_equal(ours, npv)
+    if REF is not None:
+        sub = x[::997]
+        ref = np.array([REF.ref_float_to_half(float(v)) for v in sub], np.uint16)
+        assert np.array_equal(ours[::997], ref)
+
+
+# ---- act-quant ---------------------------------------------------------------------
+
+def _tie_rows(rng, M, K):
+    """Rows where many x*inv land exactly on .5 (half-away vs RNE differ)."""
+    x = rng.normal(0, 1, size=(M, K)).astype(np.float32)
+    for m in range(M):
+        mx = np.float32(127.0)  # s = 1 -> inv = 1, x*inv = x
+        x[m, :] = (rng.integers(-126, 126, size=K) + 0.5).astype(np.float32)
+        x[m, 0] = mx
+    return x
+
+
+@needs_ref
+@pytest.mark.parametrize("rnd", [0, 1])
+def test_act_quant_ga64_matches_reference(O, rnd):
+    rng = np.random.default_rng(2)
+    K = 1024
+    x = np.concatenate([rng.normal(0, 1, size=(8, K)).astype(np.float32) * 3,
+                        _tie_rows(rng, 4, K),
+                        np.zeros((1, K), np.float32)])
+    q, s, _ = po.act_quant(x, round=rnd, ga=64)
+    for m in range(x.shape[0]):
+        qr = np.empty(K, np.int8)
+        sr = np.empty(K // 64, np.float32)
+        REF.ref_act_quant_ga64(ptr(x[m].copy()), ptr(qr), ptr(sr), K, rnd)
+        assert np.array_equal(q[m], qr), f"row {m}"
+        assert np.array_equal(s[m].view(np.uint32), sr.view(np.uint32))
+    # the tie rows really exercise both roundings
+    qa, _, _ = po.act_quant(x[8:12], round=0, ga=64)
+    qb, _, _ = po.act_quant(x[8:12], round=1, ga=64)
+    assert (qa != qb).sum() > 100
+
+
+def _np_quant_row(x, rnd):
+    x = x.astype(np.float32)
+    mx = np.float32(max(np.float32(1e-6), np.abs(x).max()))
+    s = np.float32(mx / np.float32(127.0))
+    inv = np.float32(np.float32(1.0) / s)
+    v = np.clip(x * inv, np.float32(-127), np.float32(127)).astype(np.float32)
+    if rnd == 0:
+        q = np.trunc((v + np.copysign(np.float32(0.5), v)).astype(np.float32))
+    else:
+        q = np.rint(v)
+    return q.astype(np.int8), s
+
+
+@pytest.mark.parametrize("rnd", [0, 1])
+def test_act_quant_per_token_closed_form(O, rnd):
+    rng = np.random.default_rng(3)
+    x = np.concatenate([rng.normal(0, 2, size=(6, 2048)).astype(np.float32),
+                        _tie_rows(rng, 2, 2048), np.zeros((1, 2048), np.float32)])
+    q, s, g = po.act_quant(x, round=rnd, ga=0)
+    for m in range(x.shape[0]):
+        qe, se = _np_quant_row(x[m], rnd)
+        assert np.array_equal(q[m], qe)
+        assert s[m, 0] == se
+        assert np.array_equal(g[m], q[m].astype(np.int64).reshape(-1, 128).sum(1).astype(np.float32))
+
+
+# ---- rotation ------------------------------------------------------------------------
+
+@pytest.mark.parametrize("dim", [128, 1024, 4096, 5120])
+def test_rotation_matches_reference_and_dense(O, dim):
+    rng = np.random.default_rng(4)
+    x = rng.normal(0, 1, size=dim).astype(np.float32)
+    out = np.empty(dim, np.float32)
+    O.or_rot(ptr(x), ptr(out), dim)
+    if REF is not None:
+        ro = np.empty(dim, np.float32)
+        mat = np.empty(dim * dim, np.float32) if dim <= 1024 else None
+        assert REF.ref_rotation_fwht(dim, ptr(x), ptr(ro), ptr(mat) if mat is not None else None) == 0
+        assert np.array_equal(out.view(np.uint32), ro.view(np.uint32))
+        if mat is not None:
+            R = mat.reshape(dim, dim).astype(np.float64)
+            assert np.allclose(R @ R.T, np.eye(dim), atol=1e-6)
+            assert np.allclose(x.astype(np.float64) @ R, out, atol=1e-5)
+    p = 1 << (dim.bit_length() - 1)
+    y = np.empty(dim, np.float32)
+    O.or_rot(ptr(out), ptr(y), dim)  # H is symmetric and orthogonal: self-inverse
+    assert np.allclose(y[:p], x[:p], atol=1e-5)
+    assert np.array_equal(out[p:], x[p:])
+
+
+# ---- dequant (canonical codebook equivalence) --------------------------------------------
+
+@needs_ref
+@pytest.mark.parametrize("bits", [2, 4])
+def test_dequant_equals_reference_codebook(O, bits):
+    rng = np.random.default_rng(5)
+    N, K, G = 32, 256, 128
+    C_ = (1 << bits) - 1
+    vals = rng.integers(0, C_ + 1, size=(N, K), dtype=np.uint8)
+    e = rng.integers(-8, -2, size=K // G)
+    s_ref = (C_ / 2.0) * np.exp2(e)                      # exact in fp16
+    s_ours = np.exp2(e)                                  # 2 * s_ref / C
+    # reference: group-major codes, one scale per group shared by all rows
+    gm = np.concatenate([vals[:, g * G:(g + 1) * G].reshape(-1) for g in range(K // G)])
+    gm_packed = ia.pack_codes(gm, bits)
+    ref_out = np.empty(N * K, np.float32)
+    REF.ref_dequant(bits, N, K, G, ptr(gm_packed), gm_packed.size,
+                    ptr(s_ref.astype(np.float16).view(np.uint16).copy()), K // G, ptr(ref_out))
+    lin = ia.HostLinear(N, K, bits, ia.pack_codes(vals, bits),
+                        np.tile(s_ours.astype(np.float16).view(np.uint16), (N, 1)).copy(),
+                        np.full((N, K // G), C_ / 2.0, np.float16).view(np.uint16).copy(), vals)
+    ours = np.empty((N, K), np.float32)
+    O.or_dequant(C.byref(lin.struct), ptr(ours))
+    assert np.allclose(ours.reshape(-1), ref_out, rtol=2 ** -21, atol=0)
+    cb = np.empty(C_ + 1, np.float32)
+    REF.ref_canonical_codebook(bits, ptr(cb))
+    assert np.allclose(cb, (2 * np.arange(C_ + 1) - C_) / C_, atol=1e-7)
+
+
+# ---- rmsnorm -------------------------------------------------------------------------------
+
+@pytest.mark.parametrize("dim", [128, 1024])
+def test_rmsnorm_formula(O, dim):
+    rng = np.random.default_rng(6)
+    x = rng.normal(0, 3, size=dim).astype(np.float32)
+    w = rng.normal(0, 0.1, size=dim).astype(np.float32)
+    out = np.empty(dim, np.float32)
+    O.or_rmsnorm(ptr(x), ptr(w), ptr(out), dim, np.float32(1e-6))
+    xd = x.astype(np.float64)
+    ref = xd / np.sqrt((xd * xd).mean() + 1e-6) * (1 + w.astype(np.float64))
+    assert np.allclose(out, ref, rtol=2e-6, atol=1e-6)
+
+
+# ---- quant GEMM -------------------------------------------------------------------------------
+
+@pytest.mark.parametrize("bits,N,K", [(2, 64, 1024), (4, 48, 2048), (8, 32, 384)])
+def test_qgemm_ts_brute_force(bits, N, K):
+    rng = np.random.default_rng(7)
+    lin = ia.make_linear(N, K, bits, rng)
+    a = rng.integers(-127, 128, size=(5, K), dtype=np.int8)
+    T, S = po.qgemm_ts(a, lin)
+    ng = K // 128
+    Te = np.einsum("mgk,ngk->mng", a.astype(np.int64).reshape(5, ng, 128),
+                   lin.values.astype(np.int64).reshape(N, ng, 128))
+    assert np.array_equal(T, Te.astype(np.int32))
+    assert np.array_equal(S, a.astype(np.int64).reshape(5, ng, 128).sum(-1))
+
+
+@pytest.mark.parametrize("bits", [2, 4])
+def test_qgemm_fold_matches_float64_dequant(bits):
+    rng = np.random.default_rng(8)
+    N, K, M = 96, 1024, 7
+    zero = rng.uniform(0, (1 << bits) - 1, size=(N, K // 128))  # general zeros too
+    lin = ia.make_linear(N, K, bits, rng, zero=zero)
+    x = rng.normal(0, 1, size=(M, K)).astype(np.float32)
+    q, s, _ = po.act_quant(x)
+    out = po.qgemm(q, s[:, 0], lin).view(np.float16).astype(np.float64)
+    sc = lin.scale.view(np.float16).astype(np.float64)
+    ze = lin.zero.view(np.float16).astype(np.float64)
+    W = sc.repeat(128, 1) * (lin.values.astype(np.float64) - ze.repeat(128, 1))
+    ref = s[:, :1].astype(np.float64) * (q.astype(np.float64) @ W.T)
+    assert np.allclose(out, ref, rtol=2e-3, atol=2e-3 * np.abs(ref).max())
+
+
+# ---- lm_head ----------------------------------------------------------------------------------
+
+def test_lmhead_quant_closed_form(O):
+    rng = np.random.default_rng(9)
+    V, H = 64, 256
+    W = rng.normal(0, 1, size=(V, H)).astype(np.float32)
+    W[3] = 0
+    q = np.empty((V, H), np.int8)
+    s = np.empty(V, np.uint16)
+    O.or_lmhead_quant(ptr(W), V, H, ptr(q), ptr(s))
+    for r in range(V):
+        mx = np.abs(W[r]).max()
+        sc = np.float32(mx / np.float32(127.0)) if mx > 0 else np.float32(1.0)
+        assert s[r] == np.float16(sc).view(np.uint16)
+        inv = np.float32(np.float32(1.0) / sc)
+        assert np.array_equal(q[r], np.rint(W[r] * inv).astype(np.int8))
+
+
+def test_lmhead_logits_and_first_max(O):
+    rng = np.random.default_rng(10)
+    V, H, M = 80, 256, 3
+    wq = rng.integers(-127, 128, size=(V, H), dtype=np.int8)
+    wq[17] = wq[5]  # identical rows -> tied logits, the lower index must win
+    ws = np.full(V, 0.01, np.float16).view(np.uint16)
+    x = rng.normal(0, 1, size=(M, H)).astype(np.float32)
+    x[1] = wq[5].astype(np.float32)  # row 1 prefers vocab 5 (and its tie 17)
+    aq, as_, _ = po.act_quant(x, round=1, ga=64)
+    logits = np.empty((M, V), np.float32)
+    best = np.empty(M, np.int32)
+    O.or_lmhead(ptr(aq), ptr(as_), M, ptr(wq), ptr(ws), V, H, ptr(logits), ptr(best))
+    ref = (aq.astype(np.float64).reshape(M, H // 64, 64) * as_[:, :, None]).reshape(M, H) @ \
+        wq.astype(np.float64).T * float(np.float16(0.01))
+    assert np.allclose(logits, ref, rtol=1e-5, atol=1e-4)
+    assert best[1] == 5 and logits[1, 5] == logits[1, 17]
+    assert all(best[m] == int(np.argmax(logits[m])) for m in range(M))
+
+
+# ---- attention / rope / kv int8 ------------------------------------------------------------------
+
+def test_attention_row_matches_float64(O):
+    rng = np.random.default_rng(11)
+    nq, nkv, hd, pos = 16, 8, 128, 77
+    q = rng.normal(0, 1, size=nq * hd).astype(np.float32)
+    k = rng.normal(0, 1, size=(pos + 1, nkv * hd)).astype(np.float32)
+    v = rng.normal(0, 1, size=(pos + 1, nkv * hd)).astype(np.float32)
+    out = np.empty(nq * hd, np.float32)
+    O.or_attention_row(ptr(q), ptr(k), ptr(v), pos, nq, nkv, hd, ptr(out))
+    G = nq // nkv
+    qd = q.astype(np.float64).reshape(nq, hd)
+    kd = k.astype(np.float64).reshape(pos + 1, nkv, hd)
+    vd = v.astype(np.float64).reshape(pos + 1, nkv, hd)
+    ref = np.empty((nq, hd))
+    for h in range(nq):
+        s = kd[:, h // G] @ qd[h] / np.sqrt(hd)
+        p = np.exp(s - s.max())
+        p /= p.sum()
+        ref[h] = p @ vd[:, h // G]
+    assert np.allclose(out.reshape(nq, hd), ref, atol=2e-5)
+
+
+def test_rope_matches_float64_of_f32_angle(O):
+    rng = np.random.default_rng(12)
+    hd, theta = 128, 1e6
+    for pos in (0, 1, 17, 999, 8191):
+        x = rng.normal(0, 1, size=hd).astype(np.float32)
+        y = x.copy()
+        O.or_rope(ptr(y), pos, hd, np.float32(theta))
+        half = hd // 2
+        d = np.arange(half)
+        # powf is correctly rounded here: float64 pow rounded once to float32
+        pw = np.array([np.float32(float(np.float32(theta)) ** (2.0 * dd / hd)) for dd in d], np.float32)
+        inv = (np.float32(1.0) / pw).astype(np.float32)
+        f = (inv * np.float32(pos)).astype(np.float32).astype(np.float64)
+        a, b = x[:half].astype(np.float64), x[half:].astype(np.float64)
+        ref = np.concatenate([a * np.cos(f) - b * np.sin(f), a * np.sin(f) + b * np.cos(f)])
+        assert np.allclose(y, ref, atol=3e-6), pos
+
+
+def test_kv_int8_round_closed_form(O):
+    rng = np.random.default_rng(13)
+    x = rng.normal(0, 1, size=128).astype(np.float32)
+    y = x.copy()
+    O.or_kv_int8_round(ptr(y), 128)
+    s = np.float32(np.float16(np.abs(x).max() / np.float32(127.0)))
+    inv = np.float32(np.float32(1.0) / s)
+    t = (x * inv).astype(np.float32)
+    q = np.clip(np.trunc(np.where(t >= 0, t + np.float32(0.5), t - np.float32(0.5))), -127, 127)
+    assert np.array_equal(y, (q.astype(np.float32) * s).astype(np.float32))
+
+
+# ---- forward invariants ---------------------------------------------------------------------------
+
+def tiny_cfg(**over):
+    return ia.default_cfg(hidden=256, layers=2, n_heads=4, n_kv=2, inter=384, vocab=512, **over)
+
+
+def test_forward_chunk_invariance():
+    """A prefill chunk of 8 rows equals 8 single-row forwards (test_cpu_parity.sh:65-74)."""
+    m = ia.SynthModel(tiny_cfg(), seed=21)
+    rng = np.random.default_rng(21)
+    toks = rng.integers(0, 512, size=12).tolist()
+    e1 = po.OracleEngine(m)
+    e2 = po.OracleEngine(m)
+    s1, s2 = e1.seq_open(), e2.seq_open()
+    b1, l1 = e1.forward([(s1, p, t, 1, 1) for p, t in enumerate(toks)], logits=True)
+    l2 = []
+    for p, t in enumerate(toks):
+        b, lg = e2.forward([(s2, p, t, 1, 1)], logits=True)
+        l2.append(lg[0])
+    assert np.array_equal(l1, np.stack(l2))
+
+
+def test_forward_f32_tracks_a8():
+    m = ia.SynthModel(tiny_cfg(), seed=22)
+    rng = np.random.default_rng(22)
+    toks = rng.integers(0, 512, size=10).tolist()
+    outs = []
+    for mode in (0, 1):
+        e = po.OracleEngine(m, mode=mode)
+        s = e.seq_open()
+        b, lg = e.forward([(s, p, t, 1, 1) for p, t in enumerate(toks)], logits=True)
+        outs.append(lg)
+    a8, f32 = outs
+    for r in range(len(toks)):
+        c = np.corrcoef(a8[r], f32[r])[0, 1]
+        assert c > 0.98, (r, c)
