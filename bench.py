@@ -1,0 +1,247 @@
+#!/usr/bin/env python3
+"""Headline benchmark: continuous-batching serve load on the 0.8B-class INT2
+engine at concurrency C=64, one MI355X.
+
+A step is one complete C=64 serve load: 64 synthetic requests (uniform
+token-id prompts of length U[64, 2048], max_new 64, greedy) are submitted at
+once and the C++ scheduler runs joint iterations (decode rows + a 512-row
+prefill chunk, round-robin) until every request is done.  value = output
+tokens (64 per request) / wall time of the timed steps.  Weights, KV and all
+intermediates are resident in HBM before the timed region starts.
+
+Extra objects on the JSON line:
+  roofline      dominant kernel of the load, from HIP events on the engine's
+                stream (achieved algorithmic GB/s vs 8 TB/s)
+  serve_roofline achieved decode tok/s vs the per-iteration roofline
+                t_roof(i) = max(HBM bytes / 8 TB/s, GEMM int8 ops / 5 POP/s +
+                attention flops / 2.5 PFLOP/s)
+  cpu_baseline  the reference CPU path (oracle f32 mode: CpuBackend FP32
+                dequant GEMM, host attention, serial tied lm_head), timed on a
+                bounded sample of the same workload
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+import numpy as np
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+HBM_PEAK = 8.0e12
+INT8_PEAK = 5.0e15
+FP16_PEAK = 2.5e15
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=2)
+    ap.add_argument("--warmup", type=int, default=1)
+    ap.add_argument("--concurrency", type=int, default=64)
+    ap.add_argument("--max-new", type=int, default=64)
+    ap.add_argument("--chunk", type=int, default=512)
+    ap.add_argument("--kv-int8", type=int, default=0)
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-roofline", action="store_true")
+    return ap.parse_args()
+
+
+def log(msg):
+    sys.stderr.write(f"[bench] {msg}\n")
+    sys.stderr.flush()
+
+
+def run_load(ia, eng, prompts, max_new, chunk, record=None):
+    sch = ia.Scheduler(eng, chunk_m=chunk, live_cap=64)
+    ids = [sch.submit(p, max_new) for p in prompts]
+    done_at = {}
+    iters = rows = 0
+    t0 = time.perf_counter()
+    while True:
+        n = sch.step()
+        iters += 1
+        rows += n
+        if record is not None:
+            record.append(sch.last_rows())
+        if n == 0:
+            fin = [sch.result(i)[1] for i in ids]
+            if all(fin):
+                break
+        if iters % 16 == 0 or n == 0:
+            now = time.perf_counter()
+            for i in ids:
+                if i not in done_at and sch.result(i)[1]:
+                    done_at[i] = now - t0
+    t1 = time.perf_counter()
+    for i in ids:
+        done_at.setdefault(i, t1 - t0)
+    toks = len(ids) * max_new
+    sch.close()
+    return t1 - t0, toks, iters, rows, sorted(done_at.values())
+
+
+def pct(xs, p):
+    s = sorted(xs)
+    k = (len(s) - 1) * p / 100.0
+    f, c = int(k), min(int(k) + 1, len(s) - 1)
+    return s[f] + (s[c] - s[f]) * (k - f)
+
+
+def serve_roofline(cfg, weight_bytes, lm_bytes, iters_rows, kv_elem):
+    """Sum of per-iteration roofline times and decode tokens (decode rows)."""
+    H, L, nq, nkv, hd = cfg.hidden, cfg.layers, cfg.n_heads, cfg.n_kv, cfg.head_dim
+    F, V = cfg.inter, cfg.vocab
+    macs_tok = L * (H * (nq * hd + 2 * nkv * hd) + nq * hd * H + H * 2 * F + F * H)
+    kv_tok = L * nkv * hd * 2 * kv_elem
+    t_roof = 0.0
+    dec = 0
+    for rows in iters_rows:
+        if not rows:
+            continue
+        M = len(rows)
+        want = sum(r[4] for r in rows)
+        dec += sum(1 for r in rows if r[3] == 0)
+        # KV read per sequence: its length after the iteration
+        seq_len = {}
+        for r in rows:
+            seq_len[r[0]] = max(seq_len.get(r[0], 0), r[1] + 1)
+        B = weight_bytes + (lm_bytes if want else 0) + sum(seq_len.values()) * kv_tok
+        ops = 2.0 * M * macs_tok + 2.0 * want * V * H
+        fl = sum(4.0 * nq * hd * (r[1] + 1) * L for r in rows)
+        t_roof += max(B / HBM_PEAK, ops / INT8_PEAK + fl / FP16_PEAK)
+    return t_roof, dec
+
+
+def cpu_baseline(ia, model, cfg):
+    """Reference CPU path on a bounded sample with the load's per-output-token
+    mix: 4 decode rows at the load's mean context (1088) + one 66-row prefill
+    chunk at offset 512 (each request of the load prefills ~16.5 tokens per
+    output token).  cpu tok/s = decode rows / iteration time."""
+    from oracle import pyoracle as po
+    threads = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
+    ora = po.OracleEngine(model, mode=1, max_seqs=8)
+    rng = np.random.default_rng(0)
+    ctx, D, P, off = 1088, 4, 66, 512
+    seqs = []
+    for _ in range(D):
+        s = ora.seq_open()
+        k = rng.standard_normal((cfg.layers, ctx, cfg.n_kv * cfg.head_dim), dtype=np.float32)
+        ora.set_kv(s, k, k)
+        seqs.append(s)
+    sp = ora.seq_open()
+    kp = rng.standard_normal((cfg.layers, off, cfg.n_kv * cfg.head_dim), dtype=np.float32)
+    ora.set_kv(sp, kp, kp)
+    rows = [(s, ctx, int(rng.integers(0, cfg.vocab)), 0, 1) for s in seqs]
+    rows += [(sp, off + i, int(rng.integers(0, cfg.vocab)), 1, 0) for i in range(P)]
+    t0 = time.perf_counter()
+    ora.forward(rows)
+    dt = time.perf_counter() - t0
+    ora.close()
+    return {"value": D / dt, "unit": "tok/s", "cores": threads, "kind": "port",
+            "sample": f"one mixed iteration of the 28-layer f32 CPU path: {D} decode rows at "
+                      f"context {ctx} + a {P}-row prefill chunk at offset {off} "
+                      f"(the load's ~16.5 prefill tokens per output token); {dt:.1f} s"}
+
+
+def main():
+    a = parse()
+    if a.gpus != 1:
+        print(f"bench.py: this build measures one GPU; --gpus {a.gpus} is not supported "
+              "(the path shards as independent data-parallel engines, see DESIGN.md)",
+              file=sys.stderr)
+        return 2
+    import intfer_amd as ia
+    from intfer_amd import workloads as wl
+
+    cfg = ia.default_cfg()
+    log("building the synthetic 0.8B-class INT2 model")
+    model = ia.SynthModel(cfg, seed=11, bits=2)
+    dev = ia.Device(0)
+    C, max_new, chunk = a.concurrency, a.max_new, a.chunk
+    cap = 2176
+    eng = ia.Engine(dev, model, max_seqs=C, max_seq_tokens=cap, pool_tokens=C * cap,
+                    kv_int8=a.kv_int8, max_rows=64 + chunk)
+    prompts = wl.cfg4_requests(C, seed=4, vocab=cfg.vocab)
+    log(f"C={C} prompts: mean {np.mean([len(p) for p in prompts]):.0f} tokens, max_new {max_new}")
+    for w in range(a.warmup):
+        dt, toks, iters, rows, _ = run_load(ia, eng, prompts, max_new, chunk)
+        log(f"warmup {w}: {dt:.3f} s, {iters} iterations, {toks / dt:.0f} tok/s")
+    dev.sync()
+    total_t = 0.0
+    total_tok = 0
+    lat = []
+    iters_total = 0
+    for s in range(a.steps):
+        dt, toks, iters, rows, done = run_load(ia, eng, prompts, max_new, chunk)
+        dev.sync()
+        total_t += dt
+        total_tok += toks
+        lat += done
+        iters_total += iters
+        log(f"step {s}: {dt:.3f} s, {iters} iterations, {rows} rows, {toks / dt:.0f} tok/s")
+    value = total_tok / total_t
+    out = {
+        "metric": "output tok/s @C=64 0.8B-INT2 (1 GPU); quant-GEMM HBM GB/s as % of peak",
+        "value": round(value, 2), "unit": "tok/s", "n_gpus": 1, "steps": a.steps,
+        "warmup": a.warmup, "ms_per_step": round(1e3 * total_t / a.steps, 3),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "int8xint2->int32 GEMM, fp16 KV" if not a.kv_int8 else "int8xint2->int32 GEMM, int8 KV",
+        "data": "synthetic (seeded random-init weights and uniform token-id prompts)",
+        "config": {"workload": "cfg4 serve load C=64: prompts U[64,2048], max_new 64, greedy, "
+                               "chunk 512, round-robin", "concurrency": C,
+                   "requests_per_step": C, "req_per_s": round(C * a.steps / total_t, 3),
+                   "p50_latency_s": round(pct(lat, 50), 4), "p99_latency_s": round(pct(lat, 99), 4),
+                   "iterations_per_step": iters_total // a.steps},
+    }
+    if not a.no_roofline:
+        rec = []
+        eng.set_timing(True)
+        dt, toks, iters, rows, _ = run_load(ia, eng, prompts, max_new, chunk, record=rec)
+        kernels = ["qgemm", "attention", "row_quant", "qk_rope_kv", "combine", "quant_plain",
+                   "lmhead", "pack"]
+        stats = {k: eng.timing(k) for k in kernels}
+        eng.set_timing(False)
+        busy = sum(v[0] for v in stats.values())
+        dom = max(kernels, key=lambda k: stats[k][0])
+        ms, n, b = stats[dom]
+        ach = (b / n) / (ms / n * 1e-3) if n else 0.0
+        out["roofline"] = {"bound": "hbm", "kernel": dom, "achieved": round(ach / 1e9, 1),
+                           "peak": 8000.0, "unit": "GB/s", "frac": round(ach / HBM_PEAK, 4),
+                           "traffic": None, "launches": n, "avg_us": round(1e3 * ms / n, 2),
+                           "bytes_per_launch": round(b / n)}
+        out["kernel_ms_per_step"] = {k: round(v[0], 2) for k, v in stats.items()}
+        out["gpu_busy_frac"] = round(busy / (dt * 1e3), 3)
+        qms, qn, qb = stats["qgemm"]
+        out["quant_gemm"] = {"achieved_GBps": round(qb / (qms * 1e-3) / 1e9, 1),
+                             "frac_of_hbm_peak": round(qb / (qms * 1e-3) / HBM_PEAK, 4),
+                             "launches": qn, "avg_us": round(1e3 * qms / qn, 2) if qn else None,
+                             "note": "in-load W2A8 GEMMs; the cache-cold sweep is in profiles/"}
+        wbytes = sum(0 for _ in ())
+        kv_elem = 1 if a.kv_int8 else 2
+        H, L = cfg.hidden, cfg.layers
+        per_layer = (H * (16 * 128 + 2 * 8 * 128) + 16 * 128 * H + H * 2 * cfg.inter + cfg.inter * H)
+        wbytes = L * per_layer * 2 / 8 + L * per_layer / 128 * 4
+        lm_bytes = cfg.vocab * H + cfg.vocab * 2
+        t_roof, dec = serve_roofline(cfg, wbytes, lm_bytes, rec, kv_elem)
+        roof_tok_s = C * max_new / t_roof
+        out["serve_roofline"] = {"roofline_tok_s": round(roof_tok_s, 1),
+                                 "achieved_tok_s": round(value, 1),
+                                 "frac": round(value / roof_tok_s, 4),
+                                 "decode_rows": dec, "iterations": len(rec)}
+        log(f"timing pass: {dt:.3f} s; dominant {dom} {ms:.1f} ms; roofline tok/s {roof_tok_s:.0f}")
+    if not a.no_cpu:
+        log("timing the reference CPU path on a bounded sample")
+        out["cpu_baseline"] = cpu_baseline(ia, model, cfg)
+    print(json.dumps(out))
+    dev.close()
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -127,14 +127,19 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs p, KVLayout kv) {
     const float m_new = fmaxf(m_run, mt);
     const float m_use = (m_new == -INFINITY) ? 0.0f : m_new;
     const float alpha = exp2f(m_run - m_use);
-    v8h pb16;
+    // P enters the PV product as an fp16 hi + lo pair (p ~ hi + lo to ~22
+    // bits): V is exact in fp16, so O carries fp32-level accuracy and the
+    // downstream per-token int8 codes match the fp32 reference loop.
+    v8h phi, plo;
     float rs = 0.0f;
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
-      const _Float16 ph = (_Float16)exp2f(sv[j] - m_use);
-      rs += (float)ph;
-      if constexpr (KV8) pb16[j] = (_Float16)((float)ph * vs[j]);
-      else pb16[j] = ph;
+      const float pf = exp2f(sv[j] - m_use);
+      rs += pf;
+      const float pv = KV8 ? pf * vs[j] : pf;
+      const _Float16 h = (_Float16)pv;
+      phi[j] = h;
+      plo[j] = (_Float16)(pv - (float)h);
     }
     rs += __shfl_xor(rs, 16, 64);
     rs += __shfl_xor(rs, 32, 64);
@@ -143,7 +148,8 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs p, KVLayout kv) {
 #pragma unroll
     for (int d = 0; d < 8; ++d) {
       o[d] *= alpha;
-      o[d] = __builtin_amdgcn_mfma_f32_16x16x32_f16(va[d], pb16, o[d], 0, 0, 0);
+      o[d] = __builtin_amdgcn_mfma_f32_16x16x32_f16(va[d], phi, o[d], 0, 0, 0);
+      o[d] = __builtin_amdgcn_mfma_f32_16x16x32_f16(va[d], plo, o[d], 0, 0, 0);
     }
   }
   // ---- partials: O^T lane (c, g) reg r -> dim 16d + 4g + r of column c.

@@ -225,10 +225,10 @@ int upload_group(ifr_ctx* c, const ifr_linear* const* ws, int count, int pair, D
   for (int i = 0; i < count; ++i) {
     if (pair)
       ifrk::pack_linear_host(ws[i]->codes, ws[i]->scale, ws[i]->zero, ws[i]->N, K, bits, hc.data(),
-                             hs.data(), 2, i);
+                             hs.data(), 2, i, 0x80u);
     else
       ifrk::pack_linear_host(ws[i]->codes, ws[i]->scale, ws[i]->zero, ws[i]->N, K, bits, hc.data(),
-                             hs.data(), 1, tile_off);
+                             hs.data(), 1, tile_off, 0x80u);
     tile_off += ws[i]->N / 16;
   }
   void* pc = nullptr;
@@ -529,7 +529,7 @@ int ifr_model_load(ifr_ctx* c, const ifr_host_model* m, const ifr_kv_cfg* kvc) {
       for (int k = 0; k < H; ++k) q[(size_t)r * H + k] = (uint8_t)(int8_t)std::lrint(Wr[k] * inv);
     }
     std::vector<uint32_t> packed((size_t)V * H / 4);
-    ifrk::pack_linear_host(q.data(), nullptr, nullptr, V, H, 8, packed.data(), nullptr, 1, 0);
+    ifrk::pack_linear_host(q.data(), nullptr, nullptr, V, H, 8, packed.data(), nullptr, 1, 0, 0u);
     if (int r = upload(c, &c->lm_w, packed.data(), packed.size())) return r;
     if (int r = upload(c, &c->lm_s, s.data(), s.size())) return r;
   }

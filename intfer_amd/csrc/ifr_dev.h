@@ -13,11 +13,19 @@ namespace ifrd {
 __device__ __forceinline__ float h2f(uint16_t h) {
   return (float)__builtin_bit_cast(_Float16, h);
 }
-// v_cvt_f16_f32 rounds to nearest even (IEEE default mode).
+// fp32 -> fp16 round-to-nearest-even of an fp32 VALUE.  The empty asm pins
+// the operand in a VGPR as a finished fp32 result: otherwise the compiler may
+// fold the producing multiply/add into a mixed-precision instruction that
+// rounds the exact result straight to fp16 (one rounding instead of the
+// contract's fp32-then-fp16), which differs in rare ulp cases.
 __device__ __forceinline__ uint16_t f2h(float f) {
+  asm volatile("" : "+v"(f));
   return __builtin_bit_cast(uint16_t, (_Float16)f);
 }
-__device__ __forceinline__ float fp16r(float f) { return (float)(_Float16)f; }
+__device__ __forceinline__ float fp16r(float f) {
+  asm volatile("" : "+v"(f));
+  return (float)(_Float16)f;
+}
 
 // Half-away-from-zero after clamping to +-127: trunc(v + copysign(0.5, v)),
 // the reference trunk rounding (dashq.cpp:243-246).

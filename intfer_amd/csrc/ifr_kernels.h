@@ -29,10 +29,11 @@ struct DLin {
 
 // Pack one logical linear (row-major LSB-first codes, fp16 scale/zero
 // [N][K/128]) into host buffers of the device layout.  For a gate/up pair
-// call with both; columns are interleaved per 16-column tile.
+// call with both; columns are interleaved per 16-column tile.  xor8 is
+// applied to 8-bit codes (0x80 for unsigned INT8 codes, 0 for signed int8).
 void pack_linear_host(const uint8_t* codes, const uint16_t* scale, const uint16_t* zero, int N,
                       int K, int bits, uint32_t* out_codes, uint32_t* out_sz, int tile_stride,
-                      int tile_offset);
+                      int tile_offset, uint32_t xor8);
 
 struct QGemmArgs {
   const int8_t* a;      // [M][K]

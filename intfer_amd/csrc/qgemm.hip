@@ -53,6 +53,14 @@ __device__ __forceinline__ v4i load_b(const uint32_t* __restrict__ codes, size_t
   return r;
 }
 
+// INT8 codes (0..255) are stored as c - 128 so the signed-int8 MFMA sees
+// them exactly; the true T is T' + 128 * S (exact in int32).
+template <int BITS>
+__device__ __forceinline__ int32_t true_t(int32_t t, float S) {
+  if constexpr (BITS == 8) return t + 128 * (int32_t)S;
+  return t;
+}
+
 struct KParams {
   const int8_t* a;
   const float* as;
@@ -148,10 +156,11 @@ __global__ __launch_bounds__(256) void qgemm_kernel(KParams p) {
             int row = row0 + 16 * i + 4 * lgrp + r;
             row = row < p.M ? row : p.M - 1;
             const float S = p.gs[(size_t)row * p.ng + g];
-            const float d = fmaf(-ze, S, (float)T[i][j][r]);
+            const int32_t Tv = true_t<BITS>(T[i][j][r], S);
+            const float d = fmaf(-ze, S, (float)Tv);
             acc[i][j][r] = fmaf(sc, d, acc[i][j][r]);
             if (p.tdump && row0 + 16 * i + 4 * lgrp + r < p.M && tile0 + j < ntiles)
-              p.tdump[((size_t)row * p.N + 16 * tl[j] + lrow) * p.ng + g] = T[i][j][r];
+              p.tdump[((size_t)row * p.N + 16 * tl[j] + lrow) * p.ng + g] = Tv;
           }
           T[i][j] = (v4i){0, 0, 0, 0};
         }
@@ -202,7 +211,7 @@ __global__ __launch_bounds__(256) void qgemm_kernel(KParams p) {
 #pragma unroll
         for (int q = 0; q < JS; ++q) {
           const int j = jj + q;
-          const int32_t Tv = lds[(((size_t)g * WM + i) * WN + j) * 256 + ln * 4 + r];
+          const int32_t Tv = true_t<BITS>(lds[(((size_t)g * WM + i) * WN + j) * 256 + ln * 4 + r], S);
           const uint32_t szw = p.sz[((size_t)tl[j] * p.ng + g) * 16 + c];
           const float sc = ifrd::h2f((uint16_t)(szw & 0xFFFFu));
           const float ze = ifrd::h2f((uint16_t)(szw >> 16));
@@ -259,7 +268,7 @@ hipError_t launch_bits(const KParams& p, hipStream_t st) {
 
 void pack_linear_host(const uint8_t* codes, const uint16_t* scale, const uint16_t* zero, int N,
                       int K, int bits, uint32_t* out_codes, uint32_t* out_sz, int tile_stride,
-                      int tile_offset) {
+                      int tile_offset, uint32_t xor8) {
   const int ntiles = N / 16, nsteps = K / 64, ng = K / kG, W = bits / 2;
   auto code_at = [&](size_t n, size_t k) -> uint32_t {
     const size_t i = n * (size_t)K + k;
@@ -280,7 +289,7 @@ void pack_linear_host(const uint8_t* codes, const uint16_t* scale, const uint16_
             const int d = j >> 2, b = j & 3;
             if (bits == 2) w[0] |= c << (8 * b + 2 * d);
             else if (bits == 4) w[d >> 1] |= c << (8 * b + 4 * (d & 1));
-            else w[d] |= c << (8 * b);
+            else w[d] |= (c ^ xor8) << (8 * b);
           }
           uint32_t* dst = out_codes + ((td * nsteps + s) * 64 + l) * W;
           for (int q = 0; q < W; ++q) dst[q] = w[q];

@@ -8,7 +8,9 @@
 //   codes          uniform over [0, 2^bits)
 //   scale(n,g)     fp16(|N(0, 0.02)|)
 //   zero(n,g)      fp16((2^bits - 1) / 2)       (the reference codebook centre)
-//   embed          N(0, 1)                       (tied with lm_head)
+//   embed          N(0, 0.02)                    (tied with lm_head; a small
+//                  embedding keeps the input token from dominating its own
+//                  logit, so greedy streams are not degenerate)
 //   norm weights   N(0, 0.1)   used as (1 + w)   (Qwen3.5 offset form)
 // bits_mode 0 draws each linear's width with P(INT2) = 0.7, else INT4
 // (a seeded stand-in for the reference's RCO budget split, src/quant/rco.cpp).
@@ -141,7 +143,7 @@ extern "C" ifr_host_model* ifr_synth_model(const ifr_model_cfg* cfg, uint64_t se
   const int H = cfg->hidden, L = cfg->layers, hd = cfg->head_dim;
   const int qN = cfg->n_heads * hd, kvN = cfg->n_kv * hd, F = cfg->inter, G = cfg->group_size;
   m->embed.resize((size_t)cfg->vocab * H);
-  fill_normal(m->embed.data(), m->embed.size(), 1.0f, seed, 1);
+  fill_normal(m->embed.data(), m->embed.size(), 0.02f, seed, 1);
   m->final_norm.resize(H);
   fill_normal(m->final_norm.data(), H, 0.1f, seed, 2);
   m->layers.resize(L);

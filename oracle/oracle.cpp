@@ -476,8 +476,15 @@ int forward(Engine& e, const ifr_row* rows, int M, int32_t* best, float* logits_
   }
   for (int m = 0; m < M; ++m) e.seqs[rows[m].seq].len = rows[m].pos + 1;
   // final norm + lm_head + argmax (main.cpp:8231-8317)
-  std::vector<int> want;
-  for (int m = 0; m < M; ++m) { best[m] = -1; if (rows[m].want) want.push_back(m); }
+  // The reference scores every row (main.cpp:8231-8232); the f32 mode keeps
+  // that cost and reports the requested rows.  The a8 mode scores requested
+  // rows only, like the device.
+  std::vector<int> want, report;
+  for (int m = 0; m < M; ++m) {
+    best[m] = -1;
+    if (rows[m].want || e.mode == 1) want.push_back(m);
+    if (rows[m].want) report.push_back(m);
+  }
   const int W = (int)want.size();
   if (W == 0) return IFR_OK;
   std::vector<float> fn((size_t)W * H), lg((size_t)W * c.vocab);
@@ -493,13 +500,25 @@ int forward(Engine& e, const ifr_row* rows, int M, int32_t* best, float* logits_
                         &as[(size_t)i * ng + gg]);
     lmhead_rows(aq.data(), as.data(), W, e.lm_q.data(), e.lm_s.data(), c.vocab, H, lg.data());
   } else {
-    gemm_f32(e.m->embed, fn.data(), lg.data(), W, c.vocab, H);
+    // tied-embedding lm_head, serial as in the reference (main.cpp:8302-8307)
+    for (int i = 0; i < W; ++i)
+      for (int v = 0; v < c.vocab; ++v) {
+        const float* er = e.m->embed + (size_t)v * H;
+        const float* f = &fn[(size_t)i * H];
+        float s = 0;
+        for (int k = 0; k < H; ++k) s += f[k] * er[k];
+        lg[(size_t)i * c.vocab + v] = s;
+      }
   }
+  int out_i = 0;
   for (int i = 0; i < W; ++i) {
+    if (!rows[want[i]].want) continue;
     best[want[i]] = argmax_first(&lg[(size_t)i * c.vocab], c.vocab);
     if (logits_out)
-      std::memcpy(logits_out + (size_t)i * c.vocab, &lg[(size_t)i * c.vocab], c.vocab * sizeof(float));
+      std::memcpy(logits_out + (size_t)out_i * c.vocab, &lg[(size_t)i * c.vocab], c.vocab * sizeof(float));
+    ++out_i;
   }
+  (void)report;
   return IFR_OK;
 }
 
