@@ -152,6 +152,183 @@ __global__ __launch_bounds__(256) void row_quant_kernel(RowQuantArgs a) {
             a.gsum ? a.gsum + (size_t)m * (K / 128) : nullptr, red, codes);
 }
 
+// ---- fast path: K = 1024 rows, 4 contiguous elements per thread --------------
+//
+// FWHT stages in the reference order (half = 1, 2, ..., 512): half 1-2 inside a
+// thread, half 4-128 across lanes of a wave (partner lane ^ half/4), half
+// 256-512 through one LDS exchange.  Every output is formed by the same adds
+// on the same operands as the sequential loop, so the result is bit-identical.
+__device__ __forceinline__ float bfly_lane(float x, int m, bool upper) {
+  const float o = __shfl_xor(x, m, 64);
+  return upper ? (o - x) : (x + o);
+}
+
+__device__ void fwht1024(float (&v)[4], float* xs) {
+  float a, b;
+  a = v[0]; b = v[1]; v[0] = a + b; v[1] = a - b;
+  a = v[2]; b = v[3]; v[2] = a + b; v[3] = a - b;
+  a = v[0]; b = v[2]; v[0] = a + b; v[2] = a - b;
+  a = v[1]; b = v[3]; v[1] = a + b; v[3] = a - b;
+  const int lane = threadIdx.x & 63;
+#pragma unroll
+  for (int m = 1; m <= 32; m <<= 1) {
+    const bool up = (lane & m) != 0;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) v[e] = bfly_lane(v[e], m, up);
+  }
+  __syncthreads();
+#pragma unroll
+  for (int e = 0; e < 4; ++e) xs[4 * threadIdx.x + e] = v[e];
+  __syncthreads();
+  const int q = threadIdx.x >> 6;  // quarter of the 1024 elements
+  const float inv = 1.0f / sqrtf(1024.0f);
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    const int base = (4 * threadIdx.x + e) & 255;
+    const float a0 = xs[base], a1 = xs[base + 256], a2 = xs[base + 512], a3 = xs[base + 768];
+    const float b0 = a0 + a1, b1 = a0 - a1, b2 = a2 + a3, b3 = a2 - a3;
+    const float c = q == 0 ? b0 + b2 : q == 1 ? b1 + b3 : q == 2 ? b0 - b2 : b1 - b3;
+    v[e] = c * inv;
+  }
+}
+
+// RMSNorm factor of the 1024 values held 4 per thread, reference order: eight
+// sequential fused chains over x[j + 8n], folded (j, j+4) then two horizontal
+// adds.  The chains read LDS in batches of 16 so loads overlap.
+__device__ float rms1024(const float (&v)[4], float* xs, float* red, float eps) {
+  __syncthreads();
+#pragma unroll
+  for (int e = 0; e < 4; ++e) xs[4 * threadIdx.x + e] = v[e];
+  __syncthreads();
+  if (threadIdx.x < 8) {
+    float acc = 0.0f;
+    for (int n0 = 0; n0 < 128; n0 += 16) {
+      float t[16];
+#pragma unroll
+      for (int i = 0; i < 16; ++i) t[i] = xs[threadIdx.x + 8 * (n0 + i)];
+#pragma unroll
+      for (int i = 0; i < 16; ++i) acc = fmaf(t[i], t[i], acc);
+    }
+    red[threadIdx.x] = acc;
+  }
+  __syncthreads();
+  const float s0 = red[0] + red[4], s1 = red[1] + red[5], s2 = red[2] + red[6], s3 = red[3] + red[7];
+  const float tot = (s0 + s1) + (s2 + s3);
+  return 1.0f / sqrtf(tot / 1024.0f + eps);
+}
+
+__global__ __launch_bounds__(256) void row_quant1024_kernel(RowQuantArgs a) {
+  __shared__ float xs[1024];
+  __shared__ float red[16];
+  const int m = blockIdx.x, t = threadIdx.x, lane = t & 63;
+  const int src = a.rowmap ? a.rowmap[m] : m;
+  float v[4];
+  if (a.src == SRC_X) {
+    const float4 x4 = *reinterpret_cast<const float4*>(a.x + (size_t)src * 1024 + 4 * t);
+    v[0] = x4.x; v[1] = x4.y; v[2] = x4.z; v[3] = x4.w;
+  } else if (a.src == SRC_EMBED) {
+    const float4 x4 = *reinterpret_cast<const float4*>(a.embed + (size_t)a.tokens[src] * 1024 + 4 * t);
+    v[0] = x4.x; v[1] = x4.y; v[2] = x4.z; v[3] = x4.w;
+    *reinterpret_cast<float4*>(a.resid + (size_t)src * 1024 + 4 * t) = x4;
+  } else {
+    const uint2 y2 = *reinterpret_cast<const uint2*>(a.y + (size_t)src * 1024 + 4 * t);
+    v[0] = ifrd::h2f((uint16_t)(y2.x & 0xFFFF));
+    v[1] = ifrd::h2f((uint16_t)(y2.x >> 16));
+    v[2] = ifrd::h2f((uint16_t)(y2.y & 0xFFFF));
+    v[3] = ifrd::h2f((uint16_t)(y2.y >> 16));
+    if (a.rot_y) fwht1024(v, xs);
+    float4* rp = reinterpret_cast<float4*>(a.resid + (size_t)src * 1024 + 4 * t);
+    float4 r4 = *rp;
+    r4.x = r4.x + v[0]; r4.y = r4.y + v[1]; r4.z = r4.z + v[2]; r4.w = r4.w + v[3];
+    *rp = r4;
+    v[0] = r4.x; v[1] = r4.y; v[2] = r4.z; v[3] = r4.w;
+  }
+  if (a.norm_w) {
+    const float f = rms1024(v, xs, red, a.eps);
+    const float4 w4 = *reinterpret_cast<const float4*>(a.norm_w + 4 * t);
+    v[0] = (v[0] * f) * (1.0f + w4.x);
+    v[1] = (v[1] * f) * (1.0f + w4.y);
+    v[2] = (v[2] * f) * (1.0f + w4.z);
+    v[3] = (v[3] * f) * (1.0f + w4.w);
+  }
+  if (a.rotate) fwht1024(v, xs);
+  int c[4];
+  if (a.ga == 0) {
+    float mx = fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3])));
+    mx = ifrd::wave_max(mx);
+    __syncthreads();
+    if (lane == 0) red[8 + (t >> 6)] = mx;
+    __syncthreads();
+    mx = fmaxf(1e-6f, fmaxf(fmaxf(red[8], red[9]), fmaxf(red[10], red[11])));
+    const float s = mx / 127.0f;
+    const float inv = 1.0f / s;
+    if (t == 0) a.qscale[m] = s;
+#pragma unroll
+    for (int e = 0; e < 4; ++e)
+      c[e] = a.round == 0 ? ifrd::quant_half_away(v[e], inv) : ifrd::quant_rne(v[e], inv);
+  } else {  // 64-wide slices = 16 lanes
+    float mx = fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3])));
+#pragma unroll
+    for (int o = 1; o < 16; o <<= 1) mx = fmaxf(mx, __shfl_xor(mx, o, 64));
+    mx = fmaxf(1e-6f, mx);
+    const float s = mx / 127.0f;
+    const float inv = 1.0f / s;
+    if ((lane & 15) == 0) a.qscale[(size_t)m * 16 + (t >> 4)] = s;
+#pragma unroll
+    for (int e = 0; e < 4; ++e)
+      c[e] = a.round == 0 ? ifrd::quant_half_away(v[e], inv) : ifrd::quant_rne(v[e], inv);
+  }
+  const uint32_t packed = (uint32_t)(c[0] & 0xFF) | ((uint32_t)(c[1] & 0xFF) << 8) |
+                          ((uint32_t)(c[2] & 0xFF) << 16) | ((uint32_t)(c[3] & 0xFF) << 24);
+  *reinterpret_cast<uint32_t*>(a.q + (size_t)m * 1024 + 4 * t) = packed;
+  if (a.gsum) {  // 128-wide groups = 32 lanes (integer sums: order-free)
+    int S = c[0] + c[1] + c[2] + c[3];
+#pragma unroll
+    for (int o = 1; o < 32; o <<= 1) S += __shfl_xor(S, o, 64);
+    if ((lane & 31) == 0) a.gsum[(size_t)m * 8 + (t >> 5)] = (float)S;
+  }
+}
+
+// Per-token int8 quantization of an fp32 / fp16 row of K = 256 * E values.
+template <int E>
+__global__ __launch_bounds__(256) void quant_plain_fast(const float* xf, const uint16_t* xh, int8_t* q,
+                                                        float* qs, float* gsum) {
+  constexpr int K = 256 * E;
+  __shared__ float red[4];
+  __shared__ int gl[K / 128];
+  const int m = blockIdx.x, t = threadIdx.x, lane = t & 63;
+  float v[E];
+#pragma unroll
+  for (int e = 0; e < E; ++e) {
+    const size_t i = (size_t)m * K + (size_t)e * 256 + t;  // coalesced: element e*256 + t
+    v[e] = xf ? xf[i] : ifrd::h2f(xh[i]);
+  }
+  if (t < K / 128) gl[t] = 0;
+  float mx = 0.0f;
+#pragma unroll
+  for (int e = 0; e < E; ++e) mx = fmaxf(mx, fabsf(v[e]));
+  mx = ifrd::wave_max(mx);
+  if (lane == 0) red[t >> 6] = mx;
+  __syncthreads();
+  mx = fmaxf(1e-6f, fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3])));
+  const float s = mx / 127.0f;
+  const float inv = 1.0f / s;
+  if (t == 0) qs[m] = s;
+#pragma unroll
+  for (int e = 0; e < E; ++e) {
+    const int c = ifrd::quant_half_away(v[e], inv);
+    q[(size_t)m * K + e * 256 + t] = (int8_t)c;
+    // element e*256 + t lies in group (e*256 + t) / 128 = 2e + (t >= 128); a wave of
+    // 64 lanes stays in one group: reduce in the wave, one LDS add per wave.
+    int S = c;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) S += __shfl_xor(S, o, 64);
+    if (lane == 0) atomicAdd(&gl[2 * e + (t >> 7)], S);
+  }
+  __syncthreads();
+  if (gsum && t < K / 128) gsum[(size_t)m * (K / 128) + t] = (float)gl[t];
+}
+
 __global__ __launch_bounds__(256) void quant_plain_kernel(const float* xf, const uint16_t* xh,
                                                           int K, int8_t* q, float* qs,
                                                           float* gsum) {
@@ -168,138 +345,141 @@ __global__ __launch_bounds__(256) void quant_plain_kernel(const float* xf, const
 }
 
 // ---- q/k norm + RoPE + KV append --------------------------------------------
-// One workgroup per row, one wave per head vector (hd = 128, 2 dims per lane).
+// grid (M, ceil(heads / 4)): one wave per head vector (hd = 128, 2 dims per lane).
 __global__ __launch_bounds__(256) void qk_rope_kv_kernel(QKArgs a, KVLayout kv) {
   __shared__ float hx[4][128];
-  __shared__ float red[4][16];
+  __shared__ float red[4][8];
   const int m = blockIdx.x, lane = threadIdx.x & 63, w = threadIdx.x >> 6;
   const int hd = kv.hd, nq = a.nq, nkv = kv.nkv;
+  const int h = blockIdx.y * 4 + w;
+  if (h >= nq + 2 * nkv) return;  // no block-wide barrier below
   const int ncols = (nq + 2 * nkv) * hd;
   const int pos = a.row_pos[m], seq = a.row_seq[m];
-  const int page = kv.block_table[(size_t)seq * kv.max_pages + pos / kv.page];
-  const int tok = pos % kv.page;
   const int half = a.rotary / 2;
   float* x = hx[w];
-  for (int h = w; h < nq + 2 * nkv; h += 4) {
-    const int kind = h < nq ? 0 : (h < nq + nkv ? 1 : 2);  // q, k, v
-    const int hh = kind == 0 ? h : (kind == 1 ? h - nq : h - nq - nkv);
-    const uint16_t* src = a.qkv + (size_t)m * ncols + (size_t)h * hd;
-    x[2 * lane] = ifrd::h2f(src[2 * lane]);
-    x[2 * lane + 1] = ifrd::h2f(src[2 * lane + 1]);
+  const int kind = h < nq ? 0 : (h < nq + nkv ? 1 : 2);  // q, k, v
+  const int hh = kind == 0 ? h : (kind == 1 ? h - nq : h - nq - nkv);
+  const uint32_t y2 = *reinterpret_cast<const uint32_t*>(a.qkv + (size_t)m * ncols + (size_t)h * hd + 2 * lane);
+  float v0 = ifrd::h2f((uint16_t)(y2 & 0xFFFF)), v1 = ifrd::h2f((uint16_t)(y2 >> 16));
+  if (kind < 2) {
+    x[2 * lane] = v0;
+    x[2 * lane + 1] = v1;
     ifrd::wave_sync();
-    float v0 = x[2 * lane], v1 = x[2 * lane + 1];
-    if (kind < 2) {
-      const float* nw = kind == 0 ? a.q_norm : a.k_norm;
-      if (nw) {
-        // 8-lane fused partials (reference AVX2 order), as in rms_factor.
-        if (lane < 8) {
-          float acc = 0.0f;
-          for (int i = lane; i < hd; i += 8) acc = fmaf(x[i], x[i], acc);
-          red[w][lane] = acc;
-        }
-        ifrd::wave_sync();
-        const float s0 = red[w][0] + red[w][4], s1 = red[w][1] + red[w][5];
-        const float s2 = red[w][2] + red[w][6], s3 = red[w][3] + red[w][7];
-        const float tot = (s0 + s1) + (s2 + s3);
-        const float f = 1.0f / sqrtf(tot / (float)hd + a.eps);
-        v0 = (v0 * f) * (1.0f + nw[2 * lane]);
-        v1 = (v1 * f) * (1.0f + nw[2 * lane + 1]);
-        ifrd::wave_sync();
-        x[2 * lane] = v0;
-        x[2 * lane + 1] = v1;
-        ifrd::wave_sync();
-      }
-      // rotate-half RoPE on the first `rotary` dims (main.cpp:365-373)
-      const float* cs = a.rope_cos + (size_t)pos * half;
-      const float* sn = a.rope_sin + (size_t)pos * half;
-      float o[2] = {v0, v1};
+    const float* nw = kind == 0 ? a.q_norm : a.k_norm;
+    if (nw) {
+      // eight sequential fused chains (reference AVX2 order, main.cpp:306-351)
+      if (lane < 8) {
+        float t[16];
 #pragma unroll
-      for (int e2 = 0; e2 < 2; ++e2) {
-        const int e = 2 * lane + e2;
-        if (e < half) {
-          const float p = x[e] * cs[e];
-          const float q = x[e + half] * sn[e];
-          o[e2] = p - q;
-        } else if (e < 2 * half) {
-          const int d = e - half;
-          const float p = x[d] * sn[d];
-          const float q = x[e] * cs[d];
-          o[e2] = p + q;
-        }
+        for (int i = 0; i < 16; ++i) t[i] = x[lane + 8 * i];
+        float acc = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) acc = fmaf(t[i], t[i], acc);
+        red[w][lane] = acc;
       }
-      v0 = o[0];
-      v1 = o[1];
+      ifrd::wave_sync();
+      const float s0 = red[w][0] + red[w][4], s1 = red[w][1] + red[w][5];
+      const float s2 = red[w][2] + red[w][6], s3 = red[w][3] + red[w][7];
+      const float tot = (s0 + s1) + (s2 + s3);
+      const float f = 1.0f / sqrtf(tot / (float)hd + a.eps);
+      v0 = (v0 * f) * (1.0f + nw[2 * lane]);
+      v1 = (v1 * f) * (1.0f + nw[2 * lane + 1]);
+      ifrd::wave_sync();
+      x[2 * lane] = v0;
+      x[2 * lane + 1] = v1;
       ifrd::wave_sync();
     }
-    v0 = ifrd::fp16r(v0);
-    v1 = ifrd::fp16r(v1);
-    if (kind == 0) {
-      uint16_t* dst = a.qout + ((size_t)m * nq + hh) * hd;
-      dst[2 * lane] = ifrd::f2h(v0);
-      dst[2 * lane + 1] = ifrd::f2h(v1);
-    } else {
-      const size_t base = ((size_t)page * nkv + hh);
-      if (!kv.kv_int8) {
-        if (kind == 1) {
-          uint16_t* kp = reinterpret_cast<uint16_t*>(kv.kpool) + (base * kv.page + tok) * hd;
-          kp[2 * lane] = ifrd::f2h(v0);
-          kp[2 * lane + 1] = ifrd::f2h(v1);
-        } else {
-          uint16_t* vp = reinterpret_cast<uint16_t*>(kv.vpool) + base * hd * kv.page;
-          vp[(size_t)(2 * lane) * kv.page + tok] = ifrd::f2h(v0);
-          vp[(size_t)(2 * lane + 1) * kv.page + tok] = ifrd::f2h(v1);
-        }
-      } else {
-        const float mx = ifrd::wave_max(fmaxf(fabsf(v0), fabsf(v1)));
-        const uint16_t sh16 = ifrd::f2h(mx > 0.0f ? mx / 127.0f : 1.0f);
-        const float s = ifrd::h2f(sh16);
-        const float inv = 1.0f / s;
-        int q0, q1;
-        {
-          const float t0 = v0 * inv, t1 = v1 * inv;
-          q0 = (int)(t0 >= 0.0f ? t0 + 0.5f : t0 - 0.5f);
-          q1 = (int)(t1 >= 0.0f ? t1 + 0.5f : t1 - 0.5f);
-          q0 = min(127, max(-127, q0));
-          q1 = min(127, max(-127, q1));
-        }
-        if (kind == 1) {
-          int8_t* kp = reinterpret_cast<int8_t*>(kv.kpool) + (base * kv.page + tok) * hd;
-          kp[2 * lane] = (int8_t)q0;
-          kp[2 * lane + 1] = (int8_t)q1;
-          if (lane == 0) kv.kscale[base * kv.page + tok] = sh16;
-        } else {
-          int8_t* vp = reinterpret_cast<int8_t*>(kv.vpool) + base * hd * kv.page;
-          vp[(size_t)(2 * lane) * kv.page + tok] = (int8_t)q0;
-          vp[(size_t)(2 * lane + 1) * kv.page + tok] = (int8_t)q1;
-          if (lane == 0) kv.vscale[base * kv.page + tok] = sh16;
-        }
+    // rotate-half RoPE on the first `rotary` dims (main.cpp:365-373)
+    const float* cs = a.rope_cos + (size_t)pos * half;
+    const float* sn = a.rope_sin + (size_t)pos * half;
+    float o[2] = {v0, v1};
+#pragma unroll
+    for (int e2 = 0; e2 < 2; ++e2) {
+      const int e = 2 * lane + e2;
+      if (e < half) {
+        const float p = x[e] * cs[e];
+        const float q = x[e + half] * sn[e];
+        o[e2] = p - q;
+      } else if (e < 2 * half) {
+        const int d = e - half;
+        const float p = x[d] * sn[d];
+        const float q = x[e] * cs[d];
+        o[e2] = p + q;
       }
     }
-    ifrd::wave_sync();
+    v0 = o[0];
+    v1 = o[1];
+  }
+  v0 = ifrd::fp16r(v0);
+  v1 = ifrd::fp16r(v1);
+  if (kind == 0) {
+    uint16_t* dst = a.qout + ((size_t)m * nq + hh) * hd;
+    *reinterpret_cast<uint32_t*>(dst + 2 * lane) = (uint32_t)ifrd::f2h(v0) | ((uint32_t)ifrd::f2h(v1) << 16);
+    return;
+  }
+  const int page = kv.block_table[(size_t)seq * kv.max_pages + pos / kv.page];
+  const int tok = pos % kv.page;
+  const size_t base = ((size_t)page * nkv + hh);
+  if (!kv.kv_int8) {
+    if (kind == 1) {
+      uint16_t* kp = reinterpret_cast<uint16_t*>(kv.kpool) + (base * kv.page + tok) * hd;
+      *reinterpret_cast<uint32_t*>(kp + 2 * lane) = (uint32_t)ifrd::f2h(v0) | ((uint32_t)ifrd::f2h(v1) << 16);
+    } else {
+      uint16_t* vp = reinterpret_cast<uint16_t*>(kv.vpool) + base * hd * kv.page;
+      vp[(size_t)(2 * lane) * kv.page + tok] = ifrd::f2h(v0);
+      vp[(size_t)(2 * lane + 1) * kv.page + tok] = ifrd::f2h(v1);
+    }
+  } else {
+    const float mx = ifrd::wave_max(fmaxf(fabsf(v0), fabsf(v1)));
+    const uint16_t sh16 = ifrd::f2h(mx > 0.0f ? mx / 127.0f : 1.0f);
+    const float s = ifrd::h2f(sh16);
+    const float inv = 1.0f / s;
+    const float t0 = v0 * inv, t1 = v1 * inv;
+    int q0 = (int)(t0 >= 0.0f ? t0 + 0.5f : t0 - 0.5f);
+    int q1 = (int)(t1 >= 0.0f ? t1 + 0.5f : t1 - 0.5f);
+    q0 = min(127, max(-127, q0));
+    q1 = min(127, max(-127, q1));
+    if (kind == 1) {
+      int8_t* kp = reinterpret_cast<int8_t*>(kv.kpool) + (base * kv.page + tok) * hd;
+      kp[2 * lane] = (int8_t)q0;
+      kp[2 * lane + 1] = (int8_t)q1;
+      if (lane == 0) kv.kscale[base * kv.page + tok] = sh16;
+    } else {
+      int8_t* vp = reinterpret_cast<int8_t*>(kv.vpool) + base * hd * kv.page;
+      vp[(size_t)(2 * lane) * kv.page + tok] = (int8_t)q0;
+      vp[(size_t)(2 * lane + 1) * kv.page + tok] = (int8_t)q1;
+      if (lane == 0) kv.vscale[base * kv.page + tok] = sh16;
+    }
   }
 }
 
 // ---- ragged batch packing ------------------------------------------------------
-// Block-wide exclusive scan of n ints in LDS (in place); returns the total.
+// Block-wide exclusive scan of v[0..n) in LDS (in place); returns the total.
+// Each thread scans a contiguous chunk; chunk totals are scanned with wave
+// shuffles and one LDS pass over the wave totals.
 __device__ int block_exscan(int* v, int n, int* tmp) {
-  const int T = blockDim.x;
-  // per-thread contiguous chunk
+  const int T = blockDim.x, lane = threadIdx.x & 63, w = threadIdx.x >> 6, nw = T >> 6;
   const int per = (n + T - 1) / T;
   const int b = threadIdx.x * per, e = min(n, b + per);
   int s = 0;
   for (int i = b; i < e; ++i) s += v[i];
-  tmp[threadIdx.x] = s;
+  int incl = s;
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const int y = __shfl_up(incl, o, 64);
+    if (lane >= o) incl += y;
+  }
+  if (lane == 63) tmp[w] = incl;
   __syncthreads();
   if (threadIdx.x == 0) {
     int run = 0;
-    for (int i = 0; i < T; ++i) { const int t = tmp[i]; tmp[i] = run; run += t; }
-    tmp[T] = run;
+    for (int i = 0; i < nw; ++i) { const int t = tmp[i]; tmp[i] = run; run += t; }
+    tmp[nw] = run;
   }
   __syncthreads();
-  int run = tmp[threadIdx.x];
+  int run = tmp[w] + incl - s;
   for (int i = b; i < e; ++i) { const int t = v[i]; v[i] = run; run += t; }
-  __syncthreads();
-  const int total = tmp[T];
+  const int total = tmp[nw];
   __syncthreads();
   return total;
 }
@@ -312,18 +492,17 @@ __global__ __launch_bounds__(1024) void pack_kernel(const int32_t* rows, int M, 
   int* nblk = sm + 2 * M + 1;  // [M+1] q-blocks per group -> block base
   int* ucnt = sm + 3 * M + 2;  // [M]   units per q-block -> unit base
   int* wnt = sm + 4 * M + 2;   // [M]   want flags -> want slot
-  int* tmp = sm + 5 * M + 2;   // [blockDim + 1]
+  int* bgrp = sm + 5 * M + 2;  // [M]   group of each q-block
+  int* tmp = sm + 6 * M + 2;   // [blockDim/64 + 1]
   for (int m = threadIdx.x; m < M; m += blockDim.x) {
     const int32_t* r = rows + 5 * m;
     flag[m] = (m == 0 || rows[5 * (m - 1)] != r[0]) ? 1 : 0;
+    grp_start[m] = flag[m];
     wnt[m] = r[4] ? 1 : 0;
     o.row_seq[m] = r[0];
     o.row_pos[m] = r[1];
     o.row_kind[m] = r[3];
   }
-  __syncthreads();
-  // group index of each row: inclusive scan of the start flags - 1
-  for (int m = threadIdx.x; m < M; m += blockDim.x) grp_start[m] = flag[m];
   __syncthreads();
   const int ngroups = block_exscan(grp_start, M, tmp);  // grp_start[m] = #starts before m
   for (int m = threadIdx.x; m < M; m += blockDim.x) {
@@ -345,44 +524,44 @@ __global__ __launch_bounds__(1024) void pack_kernel(const int32_t* rows, int M, 
   const int nb = block_exscan(nblk, ngroups, tmp);  // nblk[g] = first block of group g
   if (threadIdx.x == 0) nblk[ngroups] = nb;
   __syncthreads();
-  // units per q-block
   for (int g = threadIdx.x; g < ngroups; g += blockDim.x) {
     const int r0 = grp_start[g], len = grp_start[g + 1] - r0;
     const int pos0 = rows[5 * r0 + 1];
     for (int b = 0; b < nblk[g + 1] - nblk[g]; ++b) {
       const int kvhi = pos0 + min((b + 1) * qb, len);
       ucnt[nblk[g] + b] = nkv * ((kvhi + split - 1) / split);
+      bgrp[nblk[g] + b] = g;
     }
   }
   __syncthreads();
   block_exscan(ucnt, nb, tmp);  // ucnt[b] = first unit of block b
-  for (int g = threadIdx.x; g < ngroups; g += blockDim.x) {
+  // one thread per q-block: its units and its rows' combine map
+  for (int gb = threadIdx.x; gb < nb; gb += blockDim.x) {
+    const int g = bgrp[gb], b = gb - nblk[g];
     const int r0 = grp_start[g], len = grp_start[g + 1] - r0;
     const int pos0 = rows[5 * r0 + 1], seq = rows[5 * r0];
-    for (int b = 0; b < nblk[g + 1] - nblk[g]; ++b) {
-      const int qn = min(qb, len - b * qb);
-      const int kvhi = pos0 + b * qb + qn;
-      const int ns = (kvhi + split - 1) / split;
-      const int base = ucnt[nblk[g] + b];
-      for (int kvh = 0; kvh < nkv; ++kvh)
-        for (int s = 0; s < ns; ++s) {
-          AttnUnit u;
-          u.seq = seq;
-          u.kvh = kvh;
-          u.row0 = r0 + b * qb;
-          u.qn = qn;
-          u.qpos0 = pos0 + b * qb;
-          u.kv_lo = s * split;
-          u.kv_hi = min((s + 1) * split, kvhi);
-          u.pad = 0;
-          o.units[base + kvh * ns + s] = u;
-        }
-      for (int i = 0; i < qn; ++i) {
-        const int m = r0 + b * qb + i;
-        o.comb_base[m] = base;
-        o.comb_nsplit[m] = ns;
-        o.comb_tok[m] = i;
+    const int qn = min(qb, len - b * qb);
+    const int kvhi = pos0 + b * qb + qn;
+    const int ns = (kvhi + split - 1) / split;
+    const int base = ucnt[gb];
+    for (int kvh = 0; kvh < nkv; ++kvh)
+      for (int s = 0; s < ns; ++s) {
+        AttnUnit u;
+        u.seq = seq;
+        u.kvh = kvh;
+        u.row0 = r0 + b * qb;
+        u.qn = qn;
+        u.qpos0 = pos0 + b * qb;
+        u.kv_lo = s * split;
+        u.kv_hi = min((s + 1) * split, kvhi);
+        u.pad = 0;
+        o.units[base + kvh * ns + s] = u;
       }
+    for (int i = 0; i < qn; ++i) {
+      const int m = r0 + b * qb + i;
+      o.comb_base[m] = base;
+      o.comb_nsplit[m] = ns;
+      o.comb_tok[m] = i;
     }
   }
   __syncthreads();
@@ -417,6 +596,10 @@ hipError_t launch_row_quant(const RowQuantArgs& a, hipStream_t st) {
   if (a.src == SRC_X && !a.x) return hipErrorInvalidValue;
   if (a.src == SRC_EMBED && (!a.embed || !a.tokens || !a.resid)) return hipErrorInvalidValue;
   if (a.src == SRC_RESID && (!a.y || !a.resid)) return hipErrorInvalidValue;
+  if (a.K == 1024 && (a.ga == 0 || a.ga == 64)) {
+    hipLaunchKernelGGL(row_quant1024_kernel, dim3(a.M), dim3(256), 0, st, a);
+    return hipGetLastError();
+  }
   const size_t lds = (size_t)(2 * a.K + 64 + a.K / 64) * sizeof(float);
   hipLaunchKernelGGL(row_quant_kernel, dim3(a.M), dim3(256), lds, st, a);
   return hipGetLastError();
@@ -427,6 +610,14 @@ hipError_t launch_quant_plain(const float* xf, const uint16_t* xh, int M, int K,
   if (M <= 0) return hipSuccess;
   if (K <= 0 || K % 128 != 0 || K > 8192 || (!xf && !xh) || !q || !qscale)
     return hipErrorInvalidValue;
+  if (K == 2048) {
+    hipLaunchKernelGGL(quant_plain_fast<8>, dim3(M), dim3(256), 0, st, xf, xh, q, qscale, gsum);
+    return hipGetLastError();
+  }
+  if (K == 3072) {
+    hipLaunchKernelGGL(quant_plain_fast<12>, dim3(M), dim3(256), 0, st, xf, xh, q, qscale, gsum);
+    return hipGetLastError();
+  }
   const size_t lds = (size_t)(2 * K + 64) * sizeof(float);
   hipLaunchKernelGGL(quant_plain_kernel, dim3(M), dim3(256), lds, st, xf, xh, K, q, qscale, gsum);
   return hipGetLastError();
@@ -438,15 +629,23 @@ hipError_t launch_qk_rope_kv(const QKArgs& a, const KVLayout& kv, hipStream_t st
       !a.qkv || !a.qout || !kv.kpool || !kv.vpool || !kv.block_table)
     return hipErrorInvalidValue;
   if (kv.kv_int8 && (!kv.kscale || !kv.vscale)) return hipErrorInvalidValue;
-  hipLaunchKernelGGL(qk_rope_kv_kernel, dim3(a.M), dim3(256), 0, st, a, kv);
+  const int heads = a.nq + 2 * kv.nkv;
+  hipLaunchKernelGGL(qk_rope_kv_kernel, dim3(a.M, (heads + 3) / 4), dim3(256), 0, st, a, kv);
   return hipGetLastError();
 }
 
 hipError_t launch_pack(const int32_t* rows, int M, int nkv, int qb, int split, const PackOut& o,
                        hipStream_t st) {
   if (M <= 0) return hipSuccess;
-  if (M > 8192 || qb <= 0 || split <= 0 || nkv <= 0) return hipErrorInvalidValue;
-  const size_t lds = (size_t)(5 * M + 2 + 1024 + 1) * sizeof(int);
+  if (M > 6144 || qb <= 0 || split <= 0 || nkv <= 0) return hipErrorInvalidValue;
+  const size_t lds = (size_t)(6 * M + 2 + 16 + 1) * sizeof(int);
+  static bool attr = false;
+  if (!attr) {
+    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(pack_kernel),
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
+    if (e != hipSuccess) return e;
+    attr = true;
+  }
   hipLaunchKernelGGL(pack_kernel, dim3(1), dim3(1024), lds, st, rows, M, nkv, qb, split, o);
   return hipGetLastError();
 }
