@@ -134,10 +134,21 @@ int ifr_linear_free(ifr_ctx* ctx, ifr_dlinear* w);
 /* Bytes of the device copy (codes + scale/zero), for roofline accounting. */
 size_t ifr_linear_bytes(const ifr_dlinear* w);
 
+/* Int8 GEMM activations ("A tiles"): 16 rows x 64 columns per 1 KB tile,
+ * tiles ordered (row block, column block); inside a tile the 16 bytes one
+ * MFMA lane consumes are contiguous, so a wavefront reads a 16 x 64 operand
+ * with one coalesced 1 KB load.  Element (m, k) of an [M][K] matrix sits at
+ * byte IFR_ATILE_OFF(m, k, K); a buffer holds ceil(M/16)*16*K bytes (the
+ * padding rows are never read into an output). */
+#define IFR_ATILE_OFF(m, k, K)                                                   \
+  ((((size_t)(m) >> 4) * ((size_t)(K) >> 6) + ((size_t)(k) >> 6)) * 1024 +      \
+   ((((size_t)(k) & 63) >> 4) * 16 + ((size_t)(m) & 15)) * 16 + ((size_t)(k) & 15))
+
 /* Per-token int8 activation quantization with optional fused pre-ops.
  * Replaces dashq::act_quant_ga64_batch / act_quant_ga64_dev
  * (dashq.cpp:221-336, quant_gemm.cpp:3325-3392) for a per-row (GA = K)
- * or GA = 64 slice.  x_d fp32 [M][K].  Outputs: q_d int8 [M][K],
+ * or GA = 64 slice.  x_d fp32 [M][K].  Outputs: q_d int8 [M][K] in the
+ * A-tile layout (IFR_ATILE_OFF below; ceil(M/16)*16*K bytes),
  * scale_d fp32 [M][K/ga], gsum_d fp32 [M][K/128] (sum of the int8 codes
  * per 128-column group; may be NULL).
  *   norm_w_d : if non-NULL, x is first replaced by RMSNorm(1+w)(x) (main.cpp:337-351)
@@ -155,7 +166,9 @@ int ifr_act_quant(ifr_ctx* ctx, const float* x_d, int32_t M, int32_t K,
  *   acc(m,n) = fold over g ascending of
  *                d = fma(-zero(n,g), S(m,g), T(m,n,g)); acc = fma(scale(n,g), d, acc)
  *   y(m,n)   = fp16_rne(ascale(m) * acc(m,n))
- * out_d fp16 [M][N].  tdump_d, if non-NULL, receives T as int32 [M][N][K/128]. */
+ * a_d holds the int8 activations in the A-tile layout (IFR_ATILE_OFF), as
+ * ifr_act_quant writes them.  out_d fp16 [M][N].  tdump_d, if non-NULL,
+ * receives T as int32 [M][N][K/128]. */
 int ifr_quant_gemm(ifr_ctx* ctx, const ifr_dlinear* w, const int8_t* a_d,
                    const float* ascale_d, const float* gsum_d, int32_t M,
                    uint16_t* out_d, int32_t* tdump_d);
@@ -168,6 +181,16 @@ int ifr_linear_upload_pair(ifr_ctx* ctx, const ifr_linear* gate, const ifr_linea
 int ifr_quant_gemm_swiglu(ifr_ctx* ctx, const ifr_dlinear* gate_up, const int8_t* a_d,
                           const float* ascale_d, const float* gsum_d, int32_t M,
                           uint16_t* out_d);
+
+/* No counterpart in the reference (its DPAS kernels have one fixed shape):
+ * run ifr_quant_gemm / ifr_quant_gemm_swiglu with launch shape `variant`
+ * (0 .. ifr_quant_gemm_variants()-1) instead of the size heuristic, for
+ * parity tests and tuning.  Every shape yields identical bits; IFR_EDECLINE
+ * where a shape does not apply to (M, N, K). */
+int ifr_quant_gemm_variants(void);
+int ifr_quant_gemm_variant(ifr_ctx* ctx, const ifr_dlinear* w, const int8_t* a_d,
+                           const float* ascale_d, const float* gsum_d, int32_t M,
+                           uint16_t* out_d, int32_t variant);
 
 /* ------------------------------------------------------------------------
  * Engine: model load, paged KV, one mixed iteration.

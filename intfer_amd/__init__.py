@@ -15,9 +15,11 @@ import numpy as np
 
 from . import _abi
 from ._abi import (KVCfg, Linear, ModelCfg, Row, SchedBackend, SchedCfg, ROW_DECODE, ROW_PREFILL,
-                   ROW_VERIFY, IfrError, check, lib)
+                   ROW_VERIFY, IFR_OK, IFR_EDECLINE, IFR_EINVAL, IFR_ENOMEM, IFR_EDEVICE, IFR_ESTATE,
+                   IfrError, check, lib)
 
 __all__ = ["Device", "Engine", "Scheduler", "SynthModel", "default_cfg", "make_linear", "rows_array",
+           "atile", "untile",
            "ROW_DECODE", "ROW_PREFILL", "ROW_VERIFY", "IfrError", "ModelCfg", "KVCfg", "SchedCfg",
            "Row", "Linear", "lib"]
 
@@ -107,6 +109,25 @@ def make_linear(N: int, K: int, bits: int, rng: np.random.Generator, scale_sigma
     else:
         zz = np.asarray(z, dtype=np.float16).reshape(N, ng).view(np.uint16)
     return HostLinear(N, K, bits, pack_codes(vals, bits), sc.copy(), zz.copy(), vals)
+
+
+def atile(q: np.ndarray) -> np.ndarray:
+    """Row-major int8 [M][K] -> the A-tile byte layout the GEMM entry points
+    read (IFR_ATILE_OFF in intfer_amd.h), padded to a multiple of 16 rows."""
+    M, K = q.shape
+    Mp = (M + 15) // 16 * 16
+    p = np.zeros((Mp, K), dtype=np.int8)
+    p[:M] = q
+    # [mb][m16][kb][kc][k16] -> [mb][kb][kc][m16][k16]
+    t = p.reshape(Mp // 16, 16, K // 64, 4, 16).transpose(0, 2, 3, 1, 4)
+    return np.ascontiguousarray(t).reshape(-1)
+
+
+def untile(buf: np.ndarray, M: int, K: int) -> np.ndarray:
+    """Inverse of atile: the first M rows as a row-major int8 [M][K]."""
+    Mp = (M + 15) // 16 * 16
+    t = np.asarray(buf, dtype=np.int8)[:Mp * K].reshape(Mp // 16, K // 64, 4, 16, 16)
+    return np.ascontiguousarray(t.transpose(0, 3, 1, 2, 4)).reshape(Mp, K)[:M]
 
 
 def rows_array(rows: Iterable[Sequence[int]]):

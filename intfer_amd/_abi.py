@@ -93,6 +93,8 @@ _PROTOS = {
     "ifr_act_quant": (C.c_int, [P, P, i32, i32, P, f32, i32, i32, i32, P, P, P]),
     "ifr_quant_gemm": (C.c_int, [P, P, P, P, P, i32, P, P]),
     "ifr_quant_gemm_swiglu": (C.c_int, [P, P, P, P, P, i32, P]),
+    "ifr_quant_gemm_variants": (C.c_int, []),
+    "ifr_quant_gemm_variant": (C.c_int, [P, P, P, P, P, i32, P, i32]),
     "ifr_model_load": (C.c_int, [P, C.POINTER(HostModel), C.POINTER(KVCfg)]),
     "ifr_seq_open": (C.c_int, [P, pi32]),
     "ifr_seq_close": (C.c_int, [P, i32]),

@@ -20,7 +20,14 @@ CSRC = HERE / "csrc"
 BUILD = HERE / "_build"
 LIB = HERE / "libintfer_amd.so"
 
-SOURCES = ["qgemm.hip", "rows.hip", "attn.hip", "lmhead.hip", "engine.cpp", "sched.cpp", "synth.cpp"]
+# (source, extra flags, object name): qgemm.hip compiles once per code width
+# (its kernels) and once without (packing and dispatch), in parallel.
+SOURCES = [("qgemm.hip", [], "qgemm"),
+           ("qgemm.hip", ["-DIFR_QGEMM_BITS=2"], "qgemm_b2"),
+           ("qgemm.hip", ["-DIFR_QGEMM_BITS=4"], "qgemm_b4"),
+           ("qgemm.hip", ["-DIFR_QGEMM_BITS=8"], "qgemm_b8"),
+           ("rows.hip", [], "rows"), ("attn.hip", [], "attn"), ("lmhead.hip", [], "lmhead"),
+           ("engine.cpp", [], "engine"), ("sched.cpp", [], "sched"), ("synth.cpp", [], "synth")]
 
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 COMMON = [
@@ -31,10 +38,16 @@ COMMON = [
 ]
 
 
-def _compile(src: str) -> Path:
+# MFMA results of the GEMMs feed VALU work at once (the per-group fold), so
+# they stay in VGPRs instead of round-tripping through AGPRs.
+EXTRA = {"qgemm.hip": ["-mllvm", "--amdgpu-mfma-vgpr-form"]}
+
+
+def _compile(item) -> Path:
+    src, defs, name = item
     s = CSRC / src
-    o = BUILD / (src + ".o")
-    cmd = [HIPCC, *COMMON, "-x", "hip", "-c", str(s), "-o", str(o)]
+    o = BUILD / (name + ".o")
+    cmd = [HIPCC, *COMMON, *EXTRA.get(src, []), *defs, "-x", "hip", "-c", str(s), "-o", str(o)]
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
         raise RuntimeError(f"hipcc failed for {src}:\n{r.stderr[-6000:]}")

@@ -213,7 +213,7 @@ __global__ __launch_bounds__(256) void combine_kernel(CombineArgs a) {
   if (threadIdx.x == 0) a.qscale[m] = sc;
   for (int i = 0; i < per; ++i) {
     const int c = ifrd::quant_half_away(x[e0 + i], inv);
-    a.q[(size_t)m * N + e0 + i] = (int8_t)c;
+    a.q[atile_off(m, e0 + i, N)] = (int8_t)c;
     codes[e0 + i] = c;
   }
   __syncthreads();

@@ -445,6 +445,23 @@ int ifr_quant_gemm_swiglu(ifr_ctx* c, const ifr_dlinear* w, const int8_t* a_d,
   return IFR_OK;
 }
 
+int ifr_quant_gemm_variants(void) { return ifrk::kQGemmVariants; }
+
+int ifr_quant_gemm_variant(ifr_ctx* c, const ifr_dlinear* w, const int8_t* a_d,
+                           const float* ascale_d, const float* gsum_d, int32_t M, uint16_t* out_d,
+                           int32_t variant) {
+  if (!c || !w) return fail(IFR_EINVAL, "null arg");
+  if (variant < 0 || variant >= ifrk::kQGemmVariants) return fail(IFR_EINVAL, "variant %d", variant);
+  ifrk::QGemmArgs a{a_d, ascale_d, gsum_d, out_d, nullptr, M, w->d.pair ? w->d.N / 2 : w->d.N};
+  const hipError_t e = ifrk::launch_qgemm_variant(w->d, a, variant, c->st);
+  if (e == hipErrorInvalidValue) {
+    (void)hipGetLastError();
+    return fail(IFR_EDECLINE, "variant %d does not apply to M=%d N=%d K=%d", variant, M, w->d.N, w->d.K);
+  }
+  HIPCHK(e);
+  return IFR_OK;
+}
+
 // ---- model load ------------------------------------------------------------------
 
 int ifr_model_load(ifr_ctx* c, const ifr_host_model* m, const ifr_kv_cfg* kvc) {
@@ -588,7 +605,7 @@ int ifr_model_load(ifr_ctx* c, const ifr_host_model* m, const ifr_kv_cfg* kvc) {
   HIPCHK(hipHostMalloc(reinterpret_cast<void**>(&c->best_h), (size_t)Mx * sizeof(int32_t), hipHostMallocDefault));
   int r = 0;
   if ((r = walloc(c, &c->rows_d, (size_t)Mx * 5)) || (r = walloc(c, &c->resid, (size_t)Mx * H)) ||
-      (r = walloc(c, &c->aq, (size_t)Mx * Kmax)) || (r = walloc(c, &c->as, (size_t)Mx)) ||
+      (r = walloc(c, &c->aq, ifrk::atile_bytes(Mx, Kmax))) || (r = walloc(c, &c->as, (size_t)Mx)) ||
       (r = walloc(c, &c->gs, (size_t)Mx * (Kmax / 128))) ||
       (r = walloc(c, &c->qkv, (size_t)Mx * (qN + 2 * kvN))) ||
       (r = walloc(c, &c->qbuf, (size_t)Mx * qN)) || (r = walloc(c, &c->y, (size_t)Mx * H)) ||
@@ -598,7 +615,7 @@ int ifr_model_load(ifr_ctx* c, const ifr_host_model* m, const ifr_kv_cfg* kvc) {
       (r = walloc(c, &c->pk.row_kind, Mx)) || (r = walloc(c, &c->pk.comb_base, Mx)) ||
       (r = walloc(c, &c->pk.comb_nsplit, Mx)) || (r = walloc(c, &c->pk.comb_tok, Mx)) ||
       (r = walloc(c, &c->pk.want_rows, Mx)) || (r = walloc(c, &c->row_tok, Mx)) ||
-      (r = walloc(c, &c->lm_aq, (size_t)Mx * H)) || (r = walloc(c, &c->lm_as, (size_t)Mx * (H / 64))) ||
+      (r = walloc(c, &c->lm_aq, ifrk::atile_bytes(Mx, H))) || (r = walloc(c, &c->lm_as, (size_t)Mx * (H / 64))) ||
       (r = walloc(c, &c->best_d, Mx)))
     return r;
   const int nparts = ifrk::lmhead_nparts(V);

@@ -15,6 +15,17 @@ namespace ifrk {
 // code j (j = 0..15) of the lane's 16 K values is stored so that a shift and
 // a mask yield the int8 operand dword d = j/4 with byte j%4 (see qgemm.hip).
 // sz: (scale, zero) fp16 pairs, [ntiles][ngroups][16].
+// Int8 GEMM activations are stored as "A tiles": 16 rows x 64 columns per
+// 1 KB tile, tiles ordered (row block, column block); inside a tile the 16
+// bytes that MFMA lane l = 16 * ((k % 64) / 16) + m % 16 consumes are
+// contiguous.  A wave reads one 16 x 64 operand with one coalesced 1 KB load.
+// A buffer for M rows holds ceil(M / 16) * 16 rows.
+__host__ __device__ inline size_t atile_off(int m, int k, int K) {
+  return ((size_t)((m >> 4) * (K >> 6) + (k >> 6)) << 10) + (size_t)((((k & 63) >> 4) << 4) + (m & 15)) * 16 +
+         (k & 15);
+}
+inline size_t atile_bytes(int M, int K) { return (size_t)((M + 15) / 16) * 16 * K; }
+
 struct DLin {
   int N = 0;       // device columns (2 * F for an interleaved gate/up pair)
   int K = 0;
@@ -36,7 +47,7 @@ void pack_linear_host(const uint8_t* codes, const uint16_t* scale, const uint16_
                       int tile_offset, uint32_t xor8);
 
 struct QGemmArgs {
-  const int8_t* a;      // [M][K]
+  const int8_t* a;      // A tiles of [M][K]
   const float* as;      // [M] per-row activation scale
   const float* gs;      // [M][K/128] per-group code sums (float)
   uint16_t* out;        // [M][ldo]
@@ -45,6 +56,10 @@ struct QGemmArgs {
   int ldo;
 };
 hipError_t launch_qgemm(const DLin& w, const QGemmArgs& a, hipStream_t st);
+// One launch shape of the table (0..kQGemmVariants-1); all give identical
+// bits.  Returns hipErrorInvalidValue where a shape does not apply.
+constexpr int kQGemmVariants = 13;
+hipError_t launch_qgemm_variant(const DLin& w, const QGemmArgs& a, int variant, hipStream_t st);
 
 // ---- row kernels -----------------------------------------------------------
 enum { SRC_X = 0, SRC_EMBED = 1, SRC_RESID = 2 };
@@ -62,7 +77,7 @@ struct RowQuantArgs {
   int rotate;              // FWHT the normed row (right site)
   int round;               // 0 half-away, 1 RNE
   int ga;                  // 0 per row, else slice width (64)
-  int8_t* q;               // [M][K]
+  int8_t* q;               // A tiles of [M][K]
   float* qscale;           // [M][K/ga or 1]
   float* gsum;             // optional [M][K/128]
   int M, K;
@@ -142,7 +157,7 @@ struct CombineArgs {
   const int32_t* comb_tok;
   int M, nq, nkv, hd;
   float* attn_out;         // optional fp32 [M][nq*hd]
-  int8_t* q;               // [M][nq*hd] per-token int8 (half-away)
+  int8_t* q;               // A tiles of [M][nq*hd], per-token int8 (half-away)
   float* qscale;           // [M]
   float* gsum;             // [M][nq*hd/128]
 };

@@ -43,13 +43,10 @@ __global__ __launch_bounds__(256) void lmhead_kernel(LmP p) {
   int tl[kWN];
 #pragma unroll
   for (int j = 0; j < kWN; ++j) tl[j] = min(tile0 + j, ntiles - 1);
-  const int8_t* arow[WM];
+  const int8_t* arow[WM];  // A tiles: one 1 KB tile per (16 rows, K step)
 #pragma unroll
-  for (int i = 0; i < WM; ++i) {
-    int r = row0 + 16 * i + lrow;
-    r = r < p.W ? r : p.W - 1;
-    arow[i] = p.a + (size_t)r * p.H + 16 * lgrp;
-  }
+  for (int i = 0; i < WM; ++i)
+    arow[i] = p.a + ((size_t)(min(row0 + 16 * i, p.W - 1) >> 4) * p.nsteps << 10) + 16 * lane;
   v4f acc[WM][kWN];
 #pragma unroll
   for (int i = 0; i < WM; ++i)
@@ -58,7 +55,7 @@ __global__ __launch_bounds__(256) void lmhead_kernel(LmP p) {
   for (int s = 0; s < p.nsteps; ++s) {
     v4i A[WM], B[kWN];
 #pragma unroll
-    for (int i = 0; i < WM; ++i) A[i] = *reinterpret_cast<const v4i*>(arow[i] + 64 * s);
+    for (int i = 0; i < WM; ++i) A[i] = *reinterpret_cast<const v4i*>(arow[i] + 1024 * s);
 #pragma unroll
     for (int j = 0; j < kWN; ++j)
       B[j] = __builtin_nontemporal_load(reinterpret_cast<const v4i*>(p.w) +

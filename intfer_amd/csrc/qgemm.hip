@@ -12,11 +12,14 @@
 // group order, so every launch shape produces the same bits.
 //
 // Tiling: a workgroup is 4 waves (256 lanes).  Each wave owns WM x WN tiles of
-// 16x16 outputs (MFMA 16x16x64).  KSPLIT=1: the 4 waves sit side by side on N
-// and each folds its own accumulators (large M, MFMA-bound).  KSPLIT=4: the 4
-// waves split the K groups of the same tile and fold after one LDS exchange
-// (small M, weight-stream bound).  Codes are read in the fragment-major layout
-// below, one fully coalesced 256*bits/8-byte block per (tile, K step).
+// 16x16 outputs (MFMA 16x16x64).  The fold-side operands (S, scale/zero) are
+// staged in LDS once per workgroup so the K loop carries only the A and B
+// fragment loads.  qgemm_rows (larger M): each wave folds its own
+// accumulators while the next R groups are in flight in registers.
+// qgemm_splitk (M <= 64, the weight-stream-bound decode shapes): the 4 waves
+// split the K groups of one tile block and fold after one LDS exchange.  Codes
+// are read in the fragment-major layout, one fully coalesced 256*bits/8-byte
+// block per (tile, K step).
 #include "ifr_dev.h"
 #include "ifr_kernels.h"
 
@@ -25,41 +28,9 @@
 #include <vector>
 
 namespace ifrk {
-namespace {
+namespace qg {
 
 constexpr int kG = 128;
-
-// Unpack one lane's codes for one 64-wide K step into the int8 B operand:
-// operand dword d holds codes j = 4d..4d+3 in bytes 0..3.
-template <int BITS>
-__device__ __forceinline__ v4i load_b(const uint32_t* __restrict__ codes, size_t idx) {
-  v4i r;
-  if constexpr (BITS == 2) {
-    const uint32_t w = __builtin_nontemporal_load(codes + idx);
-    r.x = (int)(w & 0x03030303u);
-    r.y = (int)((w >> 2) & 0x03030303u);
-    r.z = (int)((w >> 4) & 0x03030303u);
-    r.w = (int)((w >> 6) & 0x03030303u);
-  } else if constexpr (BITS == 4) {
-    typedef unsigned int v2u __attribute__((ext_vector_type(2)));
-    const v2u w = __builtin_nontemporal_load(reinterpret_cast<const v2u*>(codes) + idx);
-    r.x = (int)(w.x & 0x0F0F0F0Fu);
-    r.y = (int)((w.x >> 4) & 0x0F0F0F0Fu);
-    r.z = (int)(w.y & 0x0F0F0F0Fu);
-    r.w = (int)((w.y >> 4) & 0x0F0F0F0Fu);
-  } else {
-    r = __builtin_nontemporal_load(reinterpret_cast<const v4i*>(codes) + idx);
-  }
-  return r;
-}
-
-// INT8 codes (0..255) are stored as c - 128 so the signed-int8 MFMA sees
-// them exactly; the true T is T' + 128 * S (exact in int32).
-template <int BITS>
-__device__ __forceinline__ int32_t true_t(int32_t t, float S) {
-  if constexpr (BITS == 8) return t + 128 * (int32_t)S;
-  return t;
-}
 
 struct KParams {
   const int8_t* a;
@@ -72,199 +43,474 @@ struct KParams {
   int M, N, K, ng, nsteps, ldo;
 };
 
+// One compilation of this file per code width (IFR_QGEMM_BITS = 2, 4, 8)
+// instantiates that width's kernels; the build without it holds the packing
+// and the dispatch.
+hipError_t launch_b2(const KParams& p, int epi, int variant, hipStream_t st);
+hipError_t launch_b4(const KParams& p, int epi, int variant, hipStream_t st);
+hipError_t launch_b8(const KParams& p, int epi, int variant, hipStream_t st);
+
+}  // namespace qg
+
+#if defined(IFR_QGEMM_BITS)
+namespace qg {
+namespace {
+
+
+// Raw code dwords of one lane for one K step, and their unpacking into the
+// int8 B operand: operand dword d holds codes j = 4d..4d+3 in bytes 0..3
+// (INT2: byte b of dword d is bits [8b + 2d, +2) of the packed dword; INT4:
+// bits [8b + 4(d%2), +4) of packed dword d/2; INT8: stored directly).
+template <int BITS>
+__device__ __forceinline__ void load_raw(const uint32_t* __restrict__ base, int lane,
+                                         uint32_t (&w)[BITS / 2]) {
+  if constexpr (BITS == 2) {
+    w[0] = __builtin_nontemporal_load(base + lane);
+  } else if constexpr (BITS == 4) {
+    typedef unsigned int v2u __attribute__((ext_vector_type(2)));
+    const v2u x = __builtin_nontemporal_load(reinterpret_cast<const v2u*>(base) + lane);
+    w[0] = x.x;
+    w[1] = x.y;
+  } else {
+    const v4i x = __builtin_nontemporal_load(reinterpret_cast<const v4i*>(base) + lane);
+    w[0] = (uint32_t)x.x;
+    w[1] = (uint32_t)x.y;
+    w[2] = (uint32_t)x.z;
+    w[3] = (uint32_t)x.w;
+  }
+}
+template <int BITS>
+__device__ __forceinline__ v4i unpack_b(const uint32_t (&w)[BITS / 2]) {
+  v4i r;
+  if constexpr (BITS == 2) {
+    r.x = (int)(w[0] & 0x03030303u);
+    r.y = (int)((w[0] >> 2) & 0x03030303u);
+    r.z = (int)((w[0] >> 4) & 0x03030303u);
+    r.w = (int)((w[0] >> 6) & 0x03030303u);
+  } else if constexpr (BITS == 4) {
+    r.x = (int)(w[0] & 0x0F0F0F0Fu);
+    r.y = (int)((w[0] >> 4) & 0x0F0F0F0Fu);
+    r.z = (int)(w[1] & 0x0F0F0F0Fu);
+    r.w = (int)((w[1] >> 4) & 0x0F0F0F0Fu);
+  } else {
+    r.x = (int)w[0];
+    r.y = (int)w[1];
+    r.z = (int)w[2];
+    r.w = (int)w[3];
+  }
+  return r;
+}
+
+// INT8 codes (0..255) are stored as c - 128 so the signed-int8 MFMA sees
+// them exactly; the true T is T' + 128 * S (exact in int32).
+template <int BITS>
+__device__ __forceinline__ int32_t true_t(int32_t t, float S) {
+  if constexpr (BITS == 8) return t + 128 * (int32_t)S;
+  return t;
+}
+
+
 __device__ __forceinline__ float silu_f(float x) { return x / (1.0f + expf(-x)); }
 
-// Store one finished output element (EPI 0) or a gate/up pair (EPI 1).
-__device__ __forceinline__ void store_plain(const KParams& p, int row, int col, float acc) {
-  p.out[(size_t)row * p.ldo + col] = ifrd::f2h(p.as[row] * acc);
+__device__ __forceinline__ void store_plain(const KParams& p, int row, int col, float as, float acc) {
+  p.out[(size_t)row * p.ldo + col] = ifrd::f2h(as * acc);
 }
-__device__ __forceinline__ void store_swiglu(const KParams& p, int row, int col, float accg,
+__device__ __forceinline__ void store_swiglu(const KParams& p, int row, int col, float as, float accg,
                                              float accu) {
-  const float a = p.as[row];
-  const float g = ifrd::fp16r(a * accg);
-  const float u = ifrd::fp16r(a * accu);
+  const float g = ifrd::fp16r(as * accg);
+  const float u = ifrd::fp16r(as * accu);
   p.out[(size_t)row * p.ldo + col] = ifrd::f2h(silu_f(g) * u);
 }
 
-template <int BITS, int WM, int WN, int KSPLIT, int EPI>
-__global__ __launch_bounds__(256) void qgemm_kernel(KParams p) {
-  extern __shared__ int32_t lds[];
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int lrow = lane & 15, lgrp = lane >> 4;
-  const int ntiles = p.N >> 4;
-  const int row0 = blockIdx.y * 16 * WM;
-  int tile0, g0, g1;
-  if constexpr (KSPLIT == 1) {
-    tile0 = (blockIdx.x * 4 + wave) * WN;
-    g0 = 0;
-    g1 = p.ng;
-    if (tile0 >= ntiles) return;  // no barrier in this variant
-  } else {
-    tile0 = blockIdx.x * WN;
-    g0 = (p.ng * wave) / 4;
-    g1 = (p.ng * (wave + 1)) / 4;
-  }
+// Operands of one 128-wide K group (two MFMA K steps) of one wave.
+template <int BITS, int WM, int WN>
+struct GroupOps {
+  v4i A[2][WM];
+  uint32_t B[2][WN][BITS / 2];
+};
 
-  const int8_t* arow[WM];
+// A: tile offsets aoff[i] (bytes, per lane) from the uniform base p.a, one
+// contiguous 1 KB A tile per (16 rows, K step);
+// B: tile indices tl[j] are wave-uniform, so each (tile, step) block base is a
+// scalar and the lane adds lane * bits/2 dwords.
+template <int BITS, int WM, int WN>
+__device__ __forceinline__ void load_ops(const KParams& p, const uint32_t (&aoff)[WM],
+                                         const int (&tl)[WN], int lane, int g,
+                                         GroupOps<BITS, WM, WN>& b) {
 #pragma unroll
-  for (int i = 0; i < WM; ++i) {
-    int r = row0 + 16 * i + lrow;
-    r = r < p.M ? r : p.M - 1;
-    arow[i] = p.a + (size_t)r * p.K + 16 * lgrp;
+  for (int h = 0; h < 2; ++h) {
+    const int s = 2 * g + h;
+    const int8_t* ab = p.a + 1024 * s;
+#pragma unroll
+    for (int i = 0; i < WM; ++i) b.A[h][i] = *reinterpret_cast<const v4i*>(ab + aoff[i]);
+#pragma unroll
+    for (int j = 0; j < WN; ++j)
+      load_raw<BITS>(p.codes + ((size_t)tl[j] * p.nsteps + s) * 64 * (BITS / 2), lane, b.B[h][j]);
   }
+}
+
+template <int BITS, int WM, int WN>
+__device__ __forceinline__ void mma_group(const GroupOps<BITS, WM, WN>& b, v4i (&T)[WM][WN]) {
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    v4i B[WN];
+#pragma unroll
+    for (int j = 0; j < WN; ++j) B[j] = unpack_b<BITS>(b.B[h][j]);
+#pragma unroll
+    for (int i = 0; i < WM; ++i)
+#pragma unroll
+      for (int j = 0; j < WN; ++j)
+        T[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(b.A[h][i], B[j], h ? T[i][j] : (v4i){0, 0, 0, 0},
+                                                        0, 0, 0);
+  }
+}
+
+// Everything the fold needs besides T, staged in LDS once per workgroup:
+// S_l[g][BM] (group code sums of the block's rows) and Z_l[g][BN] (packed
+// fp16 scale | zero << 16 of the block's columns).  Rows past M read row M-1
+// and columns past N read the last tile; their outputs are never stored.
+// Up to NQ elements per thread are fetched with all loads in flight at once;
+// larger blocks (K > 128 * NQ * 256 / max(BM, BN)) take a plain loop.
+template <int BM, int BN, int NQ>
+__device__ __forceinline__ void stage_fold_operands(const KParams& p, int bm0, int bt0, float* S_l,
+                                                    uint32_t* Z_l) {
+  const int ng = p.ng, ntiles = p.N >> 4;
+  constexpr int TB = BN / 16;
+  auto s_src = [&](int t) {  // t = g * BM + r
+    return p.gs + (size_t)min(bm0 + (t % BM), p.M - 1) * ng + t / BM;
+  };
+  auto z_src = [&](int t) {  // t = (g * TB + jt) * 16 + c
+    const int c = t & 15, jt = (t >> 4) % TB, g = (t >> 4) / TB;
+    return p.sz + ((size_t)min(bt0 + jt, ntiles - 1) * ng + g) * 16 + c;
+  };
+  auto z_dst = [&](int t) {
+    const int c = t & 15, jt = (t >> 4) % TB, g = (t >> 4) / TB;
+    return g * BN + 16 * jt + c;
+  };
+  if (BM * ng <= 256 * NQ && BN * ng <= 256 * NQ) {
+    float sv[NQ];
+    uint32_t zv[NQ];
+#pragma unroll
+    for (int q = 0; q < NQ; ++q) {
+      const int t = threadIdx.x + 256 * q;
+      if (t < BM * ng) sv[q] = *s_src(t);
+      if (t < BN * ng) zv[q] = *z_src(t);
+    }
+#pragma unroll
+    for (int q = 0; q < NQ; ++q) {
+      const int t = threadIdx.x + 256 * q;
+      if (t < BM * ng) S_l[t] = sv[q];
+      if (t < BN * ng) Z_l[z_dst(t)] = zv[q];
+    }
+  } else {
+    for (int t = threadIdx.x; t < BM * ng; t += 256) S_l[t] = *s_src(t);
+    for (int t = threadIdx.x; t < BN * ng; t += 256) Z_l[z_dst(t)] = *z_src(t);
+  }
+}
+
+// ---- larger M: a workgroup computes a BM x BN block, its 4 waves arranged
+// MW x (4/MW); each wave owns WM x WN 16x16 tiles and folds its own
+// accumulators group by group while the next R groups are in flight.  The
+// loads are unconditional (R divides ng; the last R groups are peeled), so the
+// wait before each group only covers that group's operands.
+template <int BITS, int WM, int WN, int MW, int R, int EPI, bool DUMP>
+__global__ __launch_bounds__(256) void qgemm_rows(KParams p) {
+  constexpr int NW = 4 / MW;
+  constexpr int BM = 16 * WM * MW, BN = 16 * WN * NW;
+  extern __shared__ float lds_f[];
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int lrow = lane & 15, lgrp = lane >> 4;
+  const int ntiles = p.N >> 4, ng = p.ng;
+  const int bm0 = blockIdx.y * BM, bt0 = blockIdx.x * (BN / 16);
+  const int wm = wave % MW, wn = wave / MW;
+  const int row0 = bm0 + 16 * WM * wm, tile0 = bt0 + WN * wn;
+  float* S_l = lds_f;
+  uint32_t* Z_l = reinterpret_cast<uint32_t*>(lds_f + ng * BM);
+
+  uint32_t aoff[WM];
+#pragma unroll
+  for (int i = 0; i < WM; ++i) aoff[i] = (uint32_t)((min(row0 + 16 * i, p.M - 1) >> 4) * p.nsteps * 1024 + 16 * lane);
   int tl[WN];
 #pragma unroll
   for (int j = 0; j < WN; ++j) tl[j] = min(tile0 + j, ntiles - 1);
+
+  using Ops = GroupOps<BITS, WM, WN>;
+  Ops ring[R];
+#pragma unroll
+  for (int d = 0; d < R; ++d) load_ops<BITS, WM, WN>(p, aoff, tl, lane, d, ring[d]);
+  stage_fold_operands<BM, BN, 12>(p, bm0, bt0, S_l, Z_l);
+  float asr[WM][4];
+#pragma unroll
+  for (int i = 0; i < WM; ++i)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) asr[i][r] = p.as[min(row0 + 16 * i + 4 * lgrp + r, p.M - 1)];
+  __syncthreads();  // the only barrier
 
   v4i T[WM][WN];
   v4f acc[WM][WN];
 #pragma unroll
   for (int i = 0; i < WM; ++i)
 #pragma unroll
-    for (int j = 0; j < WN; ++j) {
-      T[i][j] = (v4i){0, 0, 0, 0};
-      acc[i][j] = (v4f){0.f, 0.f, 0.f, 0.f};
-    }
+    for (int j = 0; j < WN; ++j) acc[i][j] = (v4f){0.f, 0.f, 0.f, 0.f};
 
-  for (int g = g0; g < g1; ++g) {
+  auto fold = [&](int g) {
+    v4f S[WM];
 #pragma unroll
-    for (int h = 0; h < 2; ++h) {
-      const int s = 2 * g + h;
-      v4i A[WM], B[WN];
+    for (int i = 0; i < WM; ++i)
+      S[i] = *reinterpret_cast<const v4f*>(&S_l[g * BM + 16 * WM * wm + 16 * i + 4 * lgrp]);
 #pragma unroll
-      for (int i = 0; i < WM; ++i) A[i] = *reinterpret_cast<const v4i*>(arow[i] + 64 * s);
+    for (int j = 0; j < WN; ++j) {
+      const uint32_t zw = Z_l[g * BN + 16 * (WN * wn + j) + lrow];
+      const float sc = ifrd::h2f((uint16_t)(zw & 0xFFFFu));
+      const float ze = ifrd::h2f((uint16_t)(zw >> 16));
 #pragma unroll
-      for (int j = 0; j < WN; ++j)
-        B[j] = load_b<BITS>(p.codes, ((size_t)tl[j] * p.nsteps + s) * 64 + lane);
+      for (int i = 0; i < WM; ++i)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int32_t Tv = true_t<BITS>(T[i][j][r], S[i][r]);
+          const float d = fmaf(-ze, S[i][r], (float)Tv);
+          acc[i][j][r] = fmaf(sc, d, acc[i][j][r]);
+          if (DUMP && row0 + 16 * i + 4 * lgrp + r < p.M && tile0 + j < ntiles)
+            p.tdump[((size_t)(row0 + 16 * i + 4 * lgrp + r) * p.N + 16 * tl[j] + lrow) * ng + g] = Tv;
+        }
+    }
+  };
+  int g = 0;
+  for (; g + R < ng; g += R) {
+#pragma unroll
+    for (int d = 0; d < R; ++d) {
+      mma_group<BITS, WM, WN>(ring[d], T);
+      load_ops<BITS, WM, WN>(p, aoff, tl, lane, g + d + R, ring[d]);
+      fold(g + d);
+    }
+  }
+#pragma unroll
+  for (int d = 0; d < R; ++d) {
+    mma_group<BITS, WM, WN>(ring[d], T);
+    fold(g + d);
+  }
+
+#pragma unroll
+  for (int i = 0; i < WM; ++i)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int row = row0 + 16 * i + 4 * lgrp + r;
+      if (row >= p.M) continue;
+      if constexpr (EPI == 0) {
+#pragma unroll
+        for (int j = 0; j < WN; ++j)
+          if (tile0 + j < ntiles) store_plain(p, row, 16 * (tile0 + j) + lrow, asr[i][r], acc[i][j][r]);
+      } else {
+#pragma unroll
+        for (int j = 0; j < WN; j += 2)
+          if (tile0 + j + 1 < ntiles)
+            store_swiglu(p, row, 16 * ((tile0 + j) >> 1) + lrow, asr[i][r], acc[i][j][r],
+                         acc[i][j + 1][r]);
+      }
+    }
+}
+
+// ---- small M (decode, weight-stream bound): the 4 waves split the K groups
+// of one WM x WN tile block.  Each wave issues the loads of all its groups
+// (at most NGW) at entry, runs the MFMAs, and parks its int32 T in LDS; after
+// one barrier all 256 lanes fold every group in ascending order.
+template <int BITS, int WM, int WN, int NGW, int EPI, bool DUMP>
+__global__ __launch_bounds__(256) void qgemm_splitk(KParams p) {
+  extern __shared__ int32_t lds[];
+  constexpr int BM = 16 * WM, BN = 16 * WN;
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int lrow = lane & 15, lgrp = lane >> 4;
+  const int ntiles = p.N >> 4, ng = p.ng;
+  const int row0 = blockIdx.y * BM;
+  const int tile0 = blockIdx.x * WN;
+  const int g0 = (ng * wave) / 4, g1 = (ng * (wave + 1)) / 4;
+  uint32_t aoff[WM];
+#pragma unroll
+  for (int i = 0; i < WM; ++i) aoff[i] = (uint32_t)((min(row0 + 16 * i, p.M - 1) >> 4) * p.nsteps * 1024 + 16 * lane);
+  int tl[WN];
+#pragma unroll
+  for (int j = 0; j < WN; ++j) tl[j] = min(tile0 + j, ntiles - 1);
+  float* S_l = reinterpret_cast<float*>(lds + (size_t)ng * WM * WN * 256);
+  uint32_t* Z_l = reinterpret_cast<uint32_t*>(S_l + BM * ng);
+
+  using Ops = GroupOps<BITS, WM, WN>;
+  Ops ops[NGW];
+#pragma unroll
+  for (int d = 0; d < NGW; ++d) load_ops<BITS, WM, WN>(p, aoff, tl, lane, min(g0 + d, g1 - 1), ops[d]);
+  stage_fold_operands<BM, BN, 6>(p, row0, tile0, S_l, Z_l);
+  constexpr int JS = (EPI == 0) ? 1 : 2;  // swiglu: one thread folds the pair
+  constexpr int NOUT = WM * (WN / JS) * 256;
+  constexpr int NO = (NOUT + 255) / 256;
+  float asv[NO];
+#pragma unroll
+  for (int k = 0; k < NO; ++k) {
+    const int o = threadIdx.x + 256 * k;
+    const int r = o & 3, ln = (o >> 2) & 63, i = (o >> 8) / (WN / JS);
+    asv[k] = p.as[min(row0 + 16 * i + 4 * (ln >> 4) + r, p.M - 1)];
+  }
+  v4i T[WM][WN];
+#pragma unroll
+  for (int d = 0; d < NGW; ++d) {
+    if (g0 + d < g1) {
+      mma_group<BITS, WM, WN>(ops[d], T);
 #pragma unroll
       for (int i = 0; i < WM; ++i)
 #pragma unroll
         for (int j = 0; j < WN; ++j)
-          T[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(A[i], B[j], T[i][j], 0, 0, 0);
-    }
-    if constexpr (KSPLIT == 1) {
-      // Fold group g.  C layout: lane holds column lrow, rows 4*lgrp + r.
-#pragma unroll
-      for (int j = 0; j < WN; ++j) {
-        const uint32_t szw = p.sz[((size_t)tl[j] * p.ng + g) * 16 + lrow];
-        const float sc = ifrd::h2f((uint16_t)(szw & 0xFFFFu));
-        const float ze = ifrd::h2f((uint16_t)(szw >> 16));
-#pragma unroll
-        for (int i = 0; i < WM; ++i) {
-#pragma unroll
-          for (int r = 0; r < 4; ++r) {
-            int row = row0 + 16 * i + 4 * lgrp + r;
-            row = row < p.M ? row : p.M - 1;
-            const float S = p.gs[(size_t)row * p.ng + g];
-            const int32_t Tv = true_t<BITS>(T[i][j][r], S);
-            const float d = fmaf(-ze, S, (float)Tv);
-            acc[i][j][r] = fmaf(sc, d, acc[i][j][r]);
-            if (p.tdump && row0 + 16 * i + 4 * lgrp + r < p.M && tile0 + j < ntiles)
-              p.tdump[((size_t)row * p.N + 16 * tl[j] + lrow) * p.ng + g] = Tv;
-          }
-          T[i][j] = (v4i){0, 0, 0, 0};
-        }
-      }
-    } else {
-#pragma unroll
-      for (int i = 0; i < WM; ++i)
-#pragma unroll
-        for (int j = 0; j < WN; ++j) {
-          *reinterpret_cast<v4i*>(&lds[(((size_t)g * WM + i) * WN + j) * 256 + lane * 4]) = T[i][j];
-          T[i][j] = (v4i){0, 0, 0, 0};
-        }
+          *reinterpret_cast<v4i*>(&lds[(((size_t)(g0 + d) * WM + i) * WN + j) * 256 + lane * 4]) = T[i][j];
     }
   }
-
-  if constexpr (KSPLIT == 1) {
+  __syncthreads();
+  // Fold all groups in order.  Output o = ((i*(WN/JS) + jj/JS)*64 + lane')*4 + r.
 #pragma unroll
-    for (int i = 0; i < WM; ++i)
+  for (int k = 0; k < NO; ++k) {
+    const int o = threadIdx.x + 256 * k;
+    if (o >= NOUT) break;
+    const int r = o & 3, ln = (o >> 2) & 63, ij = o >> 8;
+    const int jj = (ij % (WN / JS)) * JS, i = ij / (WN / JS);
+    const int rl = 16 * i + 4 * (ln >> 4) + r, row = row0 + rl;
+    const int c = ln & 15;
+    float a0 = 0.f, a1 = 0.f;
+#pragma unroll 4
+    for (int g = 0; g < ng; ++g) {
+      const float S = S_l[g * BM + rl];
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int row = row0 + 16 * i + 4 * lgrp + r;
-        if (row >= p.M) continue;
-        if constexpr (EPI == 0) {
-#pragma unroll
-          for (int j = 0; j < WN; ++j)
-            if (tile0 + j < ntiles) store_plain(p, row, 16 * (tile0 + j) + lrow, acc[i][j][r]);
-        } else {
-#pragma unroll
-          for (int j = 0; j < WN; j += 2)
-            if (tile0 + j + 1 < ntiles)
-              store_swiglu(p, row, 16 * ((tile0 + j) >> 1) + lrow, acc[i][j][r], acc[i][j + 1][r]);
-        }
+      for (int q = 0; q < JS; ++q) {
+        const int j = jj + q;
+        const int32_t Tv = true_t<BITS>(lds[(((size_t)g * WM + i) * WN + j) * 256 + ln * 4 + r], S);
+        const uint32_t szw = Z_l[g * BN + 16 * j + c];
+        const float sc = ifrd::h2f((uint16_t)(szw & 0xFFFFu));
+        const float ze = ifrd::h2f((uint16_t)(szw >> 16));
+        const float d = fmaf(-ze, S, (float)Tv);
+        if (q == 0) a0 = fmaf(sc, d, a0); else a1 = fmaf(sc, d, a1);
+        if (DUMP && row < p.M && tile0 + j < ntiles)
+          p.tdump[((size_t)row * p.N + 16 * tl[j] + c) * ng + g] = Tv;
       }
-  } else {
-    __syncthreads();
-    // Fold all groups in order from LDS.  Output o = ((i*WN + j)*64 + lane')*4 + r.
-    constexpr int JS = (EPI == 0) ? 1 : 2;  // swiglu: one thread folds the pair
-    constexpr int NOUT = WM * (WN / JS) * 256;
-    for (int o = threadIdx.x; o < NOUT; o += 256) {
-      const int r = o & 3, ln = (o >> 2) & 63, ij = o >> 8;
-      const int jj = (ij % (WN / JS)) * JS, i = ij / (WN / JS);
-      const int row = row0 + 16 * i + 4 * (ln >> 4) + r;
-      const int c = ln & 15;
-      float a0 = 0.f, a1 = 0.f;
-      const int rr = row < p.M ? row : p.M - 1;
-      for (int g = 0; g < p.ng; ++g) {
-        const float S = p.gs[(size_t)rr * p.ng + g];
-#pragma unroll
-        for (int q = 0; q < JS; ++q) {
-          const int j = jj + q;
-          const int32_t Tv = true_t<BITS>(lds[(((size_t)g * WM + i) * WN + j) * 256 + ln * 4 + r], S);
-          const uint32_t szw = p.sz[((size_t)tl[j] * p.ng + g) * 16 + c];
-          const float sc = ifrd::h2f((uint16_t)(szw & 0xFFFFu));
-          const float ze = ifrd::h2f((uint16_t)(szw >> 16));
-          const float d = fmaf(-ze, S, (float)Tv);
-          if (q == 0) a0 = fmaf(sc, d, a0); else a1 = fmaf(sc, d, a1);
-          if (EPI == 0 && p.tdump && row < p.M && tile0 + j < ntiles)
-            p.tdump[((size_t)row * p.N + 16 * tl[j] + c) * p.ng + g] = Tv;
-        }
-      }
-      if (row >= p.M) continue;
-      if constexpr (EPI == 0) {
-        if (tile0 + jj < ntiles) store_plain(p, row, 16 * (tile0 + jj) + c, a0);
-      } else {
-        if (tile0 + jj + 1 < ntiles) store_swiglu(p, row, 16 * ((tile0 + jj) >> 1) + c, a0, a1);
-      }
+    }
+    if (row >= p.M) continue;
+    if constexpr (EPI == 0) {
+      if (tile0 + jj < ntiles) store_plain(p, row, 16 * (tile0 + jj) + c, asv[k], a0);
+    } else {
+      if (tile0 + jj + 1 < ntiles) store_swiglu(p, row, 16 * ((tile0 + jj) >> 1) + c, asv[k], a0, a1);
     }
   }
 }
 
-template <int BITS, int WM, int WN, int KSPLIT, int EPI>
-hipError_t launch_cfg(const KParams& p, hipStream_t st) {
-  const int ntiles = p.N / 16;
-  dim3 grid, block(256);
-  size_t lds = 0;
-  if (KSPLIT == 1) {
-    grid = dim3((ntiles + 4 * WN - 1) / (4 * WN), (p.M + 16 * WM - 1) / (16 * WM));
-  } else {
-    grid = dim3((ntiles + WN - 1) / WN, (p.M + 16 * WM - 1) / (16 * WM));
-    lds = (size_t)p.ng * WM * WN * 256 * sizeof(int32_t);
-    if (lds > 160 * 1024) return hipErrorInvalidValue;
-    static bool attr_set = false;
-    if (!attr_set) {
-      hipError_t e = hipFuncSetAttribute(
-          reinterpret_cast<const void*>(qgemm_kernel<BITS, WM, WN, KSPLIT, EPI>),
-          hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
-      if (e != hipSuccess) return e;
-      attr_set = true;
-    }
+template <typename F>
+hipError_t set_lds_limit(F* f) {
+  return hipFuncSetAttribute(reinterpret_cast<const void*>(f), hipFuncAttributeMaxDynamicSharedMemorySize,
+                             160 * 1024);
+}
+
+template <int BITS, int WM, int WN, int MW, int R, int EPI>
+hipError_t launch_rows(const KParams& p, hipStream_t st) {
+  constexpr int NW = 4 / MW;
+  constexpr int BM = 16 * WM * MW, BN = 16 * WN * NW;
+  if (p.ng % R != 0) return hipErrorInvalidValue;
+  const size_t lds = (size_t)p.ng * (BM + BN) * sizeof(float);
+  if (lds > 160 * 1024) return hipErrorInvalidValue;
+  static bool attr_set = false;
+  if (!attr_set) {
+    hipError_t e = set_lds_limit(qgemm_rows<BITS, WM, WN, MW, R, EPI, false>);
+    if constexpr (EPI == 0)
+      if (e == hipSuccess) e = set_lds_limit(qgemm_rows<BITS, WM, WN, MW, R, EPI, true>);
+    if (e != hipSuccess) return e;
+    attr_set = true;
   }
-  hipLaunchKernelGGL((qgemm_kernel<BITS, WM, WN, KSPLIT, EPI>), grid, block, lds, st, p);
+  const int ntiles = p.N / 16;
+  const dim3 grid((ntiles + BN / 16 - 1) / (BN / 16), (p.M + BM - 1) / BM);
+  if constexpr (EPI == 0)
+    if (p.tdump) {
+      hipLaunchKernelGGL((qgemm_rows<BITS, WM, WN, MW, R, EPI, true>), grid, dim3(256), lds, st, p);
+      return hipGetLastError();
+    }
+  hipLaunchKernelGGL((qgemm_rows<BITS, WM, WN, MW, R, EPI, false>), grid, dim3(256), lds, st, p);
   return hipGetLastError();
 }
 
+template <int BITS, int WM, int WN, int NGW, int EPI>
+hipError_t launch_splitk(const KParams& p, hipStream_t st) {
+  const int ntiles = p.N / 16;
+  const dim3 grid((ntiles + WN - 1) / WN, (p.M + 16 * WM - 1) / (16 * WM));
+  const size_t lds = ((size_t)p.ng * WM * WN * 256 + (size_t)16 * (WM + WN) * p.ng) * sizeof(int32_t);
+  if ((p.ng + 3) / 4 > NGW || lds > 160 * 1024) return hipErrorInvalidValue;
+  static bool attr_set = false;
+  if (!attr_set) {
+    hipError_t e = set_lds_limit(qgemm_splitk<BITS, WM, WN, NGW, EPI, false>);
+    if constexpr (EPI == 0)
+      if (e == hipSuccess) e = set_lds_limit(qgemm_splitk<BITS, WM, WN, NGW, EPI, true>);
+    if (e != hipSuccess) return e;
+    attr_set = true;
+  }
+  if constexpr (EPI == 0)
+    if (p.tdump) {
+      hipLaunchKernelGGL((qgemm_splitk<BITS, WM, WN, NGW, EPI, true>), grid, dim3(256), lds, st, p);
+      return hipGetLastError();
+    }
+  hipLaunchKernelGGL((qgemm_splitk<BITS, WM, WN, NGW, EPI, false>), grid, dim3(256), lds, st, p);
+  return hipGetLastError();
+}
+
+template <int BITS, int WM, int WN, int EPI>
+hipError_t launch_splitk_ng(const KParams& p, hipStream_t st) {
+  const int per = (p.ng + 3) / 4;
+  if (per <= 2) return launch_splitk<BITS, WM, WN, 2, EPI>(p, st);
+  if (per <= 4) return launch_splitk<BITS, WM, WN, 4, EPI>(p, st);
+  if (WM <= 2 && per <= 6) return launch_splitk<BITS, WM, WN, 6, EPI>(p, st);
+  return hipErrorInvalidValue;
+}
+
+// R (K groups in flight per wave) is the largest power of two <= RMAX that
+// divides ng.
+template <int BITS, int WM, int WN, int MW, int RMAX, int EPI>
+hipError_t launch_rows_r(const KParams& p, hipStream_t st) {
+  if (RMAX >= 8 && p.ng % 8 == 0) return launch_rows<BITS, WM, WN, MW, (RMAX >= 8 ? 8 : 1), EPI>(p, st);
+  if (RMAX >= 4 && p.ng % 4 == 0) return launch_rows<BITS, WM, WN, MW, (RMAX >= 4 ? 4 : 1), EPI>(p, st);
+  if (p.ng % 2 == 0) return launch_rows<BITS, WM, WN, MW, 2, EPI>(p, st);
+  return launch_rows<BITS, WM, WN, MW, 1, EPI>(p, st);
+}
+
+// Launch-shape table.  Every variant computes identical bits; the choice is
+// a pure performance decision (variant < 0: the default heuristic).
 template <int BITS, int EPI>
-hipError_t launch_bits(const KParams& p, hipStream_t st) {
+hipError_t launch_bits(const KParams& p, int variant, hipStream_t st) {
   constexpr int WNs = EPI == 0 ? 1 : 2;
-  if (p.M <= 16) return launch_cfg<BITS, 1, WNs, 4, EPI>(p, st);
-  if (p.M <= 32) return launch_cfg<BITS, 2, WNs, 4, EPI>(p, st);
-  if (p.M <= 64 && p.ng <= (EPI == 0 ? 24 : 16)) return launch_cfg<BITS, 4, WNs, 4, EPI>(p, st);
-  return launch_cfg<BITS, 2, 2, 1, EPI>(p, st);
+  if (variant < 0) {  // measured on MI355X over the serve shapes (M 1..576)
+    if (p.ng <= 24 && p.M <= 64) variant = 0;
+    else variant = (EPI == 0 && p.N <= 2048) ? 10 : 5;
+  }
+  switch (variant) {
+    case 0: return launch_splitk_ng<BITS, 1, WNs, EPI>(p, st);
+    case 1: return launch_splitk_ng<BITS, 2, WNs, EPI>(p, st);
+    case 2: return launch_splitk_ng<BITS, 4, WNs, EPI>(p, st);
+    case 3: return launch_rows_r<BITS, 2, 2, 2, 4, EPI>(p, st);   // 64 x 64 block
+    case 4: return launch_rows_r<BITS, 2, 2, 1, 4, EPI>(p, st);   // 32 x 128 block
+    case 5: return launch_rows_r<BITS, 2, 2, 1, 2, EPI>(p, st);   // 32 x 128 block, shallow
+    case 6: return launch_rows_r<BITS, 2, 4, 1, 2, EPI>(p, st);   // 32 x 256 block
+    case 7: return launch_rows_r<BITS, 4, 2, 1, 2, EPI>(p, st);   // 64 x 128 block
+    case 8: return launch_splitk_ng<BITS, 2, 2, EPI>(p, st);      // 32 x 32, split K
+    case 9: return launch_rows_r<BITS, 4, 2, 2, 2, EPI>(p, st);   // 128 x 64 block
+    case 10: return launch_rows_r<BITS, 1, 2, 1, 8, EPI>(p, st);  // 16 x 128 block, deep
+    case 11: return launch_rows_r<BITS, 4, 2, 1, 4, EPI>(p, st);  // 64 x 128 block, deep
+    case 12: return launch_rows_r<BITS, 2, 2, 1, 8, EPI>(p, st);  // 32 x 128 block, deep
+    default: return hipErrorInvalidValue;
+  }
 }
 
 }  // namespace
+
+#define IFR_QG_CAT2(a, b) a##b
+#define IFR_QG_CAT(a, b) IFR_QG_CAT2(a, b)
+hipError_t IFR_QG_CAT(launch_b, IFR_QGEMM_BITS)(const KParams& p, int epi, int variant, hipStream_t st) {
+  return epi ? launch_bits<IFR_QGEMM_BITS, 1>(p, variant, st) : launch_bits<IFR_QGEMM_BITS, 0>(p, variant, st);
+}
+
+}  // namespace qg
+#else
+
+using qg::kG;
 
 void pack_linear_host(const uint8_t* codes, const uint16_t* scale, const uint16_t* zero, int N,
                       int K, int bits, uint32_t* out_codes, uint32_t* out_sz, int tile_stride,
@@ -314,21 +560,23 @@ void pack_linear_host(const uint8_t* codes, const uint16_t* scale, const uint16_
 }
 
 hipError_t launch_qgemm(const DLin& w, const QGemmArgs& a, hipStream_t st) {
+  return launch_qgemm_variant(w, a, -1, st);
+}
+
+hipError_t launch_qgemm_variant(const DLin& w, const QGemmArgs& a, int variant, hipStream_t st) {
   if (a.M <= 0) return hipSuccess;
   if (w.K % kG != 0 || w.N % 16 != 0 || !w.codes || !a.a || !a.as || !a.gs || !a.out)
     return hipErrorInvalidValue;
   if (w.pair && (w.N % 32 != 0 || a.tdump)) return hipErrorInvalidValue;
-  KParams p{a.a, a.as, a.gs, w.codes, w.sz, a.out, a.tdump, a.M, w.N, w.K, w.ng, w.nsteps, a.ldo};
+  qg::KParams p{a.a, a.as, a.gs, w.codes, w.sz, a.out, a.tdump, a.M, w.N, w.K, w.ng, w.nsteps, a.ldo};
   const int epi = w.pair ? 1 : 0;
-  switch (w.bits * 2 + epi) {
-    case 4: return launch_bits<2, 0>(p, st);
-    case 5: return launch_bits<2, 1>(p, st);
-    case 8: return launch_bits<4, 0>(p, st);
-    case 9: return launch_bits<4, 1>(p, st);
-    case 16: return launch_bits<8, 0>(p, st);
-    case 17: return launch_bits<8, 1>(p, st);
+  switch (w.bits) {
+    case 2: return qg::launch_b2(p, epi, variant, st);
+    case 4: return qg::launch_b4(p, epi, variant, st);
+    case 8: return qg::launch_b8(p, epi, variant, st);
     default: return hipErrorInvalidValue;
   }
 }
 
+#endif
 }  // namespace ifrk

@@ -72,7 +72,7 @@ __device__ __forceinline__ int floor_pow2(int n) {
 }
 
 // Quantize x[0..K) held in LDS.  Per row (ga == 0) or per ga-slice.
-__device__ void quant_lds(const float* x, int K, int ga, int round, int8_t* q, float* qs,
+__device__ void quant_lds(const float* x, int K, int ga, int round, int8_t* q, int m, float* qs,
                           float* gsum, float* red, int* codes_lds) {
   if (ga == 0) {
     float mx = 0.0f;
@@ -83,7 +83,7 @@ __device__ void quant_lds(const float* x, int K, int ga, int round, int8_t* q, f
     if (threadIdx.x == 0) qs[0] = s;
     for (int i = threadIdx.x; i < K; i += blockDim.x) {
       const int c = round == 0 ? ifrd::quant_half_away(x[i], inv) : ifrd::quant_rne(x[i], inv);
-      q[i] = (int8_t)c;
+      q[atile_off(m, i, K)] = (int8_t)c;
       codes_lds[i] = c;
     }
   } else {
@@ -100,7 +100,7 @@ __device__ void quant_lds(const float* x, int K, int ga, int round, int8_t* q, f
     for (int i = threadIdx.x; i < K; i += blockDim.x) {
       const float inv = red[64 + i / ga];
       const int c = round == 0 ? ifrd::quant_half_away(x[i], inv) : ifrd::quant_rne(x[i], inv);
-      q[i] = (int8_t)c;
+      q[atile_off(m, i, K)] = (int8_t)c;
       codes_lds[i] = c;
     }
   }
@@ -148,7 +148,7 @@ __global__ __launch_bounds__(256) void row_quant_kernel(RowQuantArgs a) {
   if (a.rotate) fwht_lds(x, floor_pow2(K));
   __syncthreads();
   const int ns = a.ga ? K / a.ga : 1;
-  quant_lds(x, K, a.ga, a.round, a.q + (size_t)m * K, a.qscale + (size_t)m * ns,
+  quant_lds(x, K, a.ga, a.round, a.q, m, a.qscale + (size_t)m * ns,
             a.gsum ? a.gsum + (size_t)m * (K / 128) : nullptr, red, codes);
 }
 
@@ -280,7 +280,7 @@ __global__ __launch_bounds__(256) void row_quant1024_kernel(RowQuantArgs a) {
   }
   const uint32_t packed = (uint32_t)(c[0] & 0xFF) | ((uint32_t)(c[1] & 0xFF) << 8) |
                           ((uint32_t)(c[2] & 0xFF) << 16) | ((uint32_t)(c[3] & 0xFF) << 24);
-  *reinterpret_cast<uint32_t*>(a.q + (size_t)m * 1024 + 4 * t) = packed;
+  *reinterpret_cast<uint32_t*>(a.q + atile_off(m, 4 * t, 1024)) = packed;
   if (a.gsum) {  // 128-wide groups = 32 lanes (integer sums: order-free)
     int S = c[0] + c[1] + c[2] + c[3];
 #pragma unroll
@@ -317,7 +317,7 @@ __global__ __launch_bounds__(256) void quant_plain_fast(const float* xf, const u
 #pragma unroll
   for (int e = 0; e < E; ++e) {
     const int c = ifrd::quant_half_away(v[e], inv);
-    q[(size_t)m * K + e * 256 + t] = (int8_t)c;
+    q[atile_off(m, e * 256 + t, K)] = (int8_t)c;
     // element e*256 + t lies in group (e*256 + t) / 128 = 2e + (t >= 128); a wave of
     // 64 lanes stays in one group: reduce in the wave, one LDS add per wave.
     int S = c;
@@ -340,7 +340,7 @@ __global__ __launch_bounds__(256) void quant_plain_kernel(const float* xf, const
   for (int i = threadIdx.x; i < K; i += blockDim.x)
     x[i] = xf ? xf[(size_t)m * K + i] : ifrd::h2f(xh[(size_t)m * K + i]);
   __syncthreads();
-  quant_lds(x, K, 0, 0, q + (size_t)m * K, qs + m, gsum ? gsum + (size_t)m * (K / 128) : nullptr,
+  quant_lds(x, K, 0, 0, q, m, qs + m, gsum ? gsum + (size_t)m * (K / 128) : nullptr,
             red, codes);
 }
 

@@ -30,7 +30,7 @@ def _gemm_case(dev, lin, M, rng, dump=True):
     dl = C.c_void_p()
     ia.check(L.ifr_linear_upload(dev.ctx, C.byref(lin.struct), C.byref(dl)), "upload")
     try:
-        qd, sd, gd = dev.upload(q), dev.upload(s[:, 0].copy()), dev.upload(g)
+        qd, sd, gd = dev.upload(ia.atile(q)), dev.upload(s[:, 0].copy()), dev.upload(g)
         od = dev.alloc(M * lin.N * 2)
         ng = lin.K // 128
         td = dev.alloc(M * lin.N * ng * 4) if dump else None
@@ -85,7 +85,7 @@ def test_qgemm_swiglu_pair(dev, M):
     dl = C.c_void_p()
     ia.check(L.ifr_linear_upload_pair(dev.ctx, C.byref(gate.struct), C.byref(up.struct), C.byref(dl)),
              "pair")
-    qd, sd, gd = dev.upload(q), dev.upload(s[:, 0].copy()), dev.upload(g)
+    qd, sd, gd = dev.upload(ia.atile(q)), dev.upload(s[:, 0].copy()), dev.upload(g)
     od = dev.alloc(M * F * 2)
     announce(f"swiglu gemm M={M}")
     ia.check(L.ifr_quant_gemm_swiglu(dev.ctx, dl, qd.p, sd.p, gd.p, M, od.p), "swiglu")
@@ -103,6 +103,54 @@ def test_qgemm_swiglu_pair(dev, M):
     assert (out == ref).mean() > 0.99
 
 
+@pytest.mark.parametrize("bits", [2, 4, 8])
+def test_qgemm_every_launch_shape_bitexact(dev, bits):
+    """Every launch shape of the table gives the oracle's bits (plain), and
+    the same bits as every other shape (SwiGLU pair); shapes that do not
+    apply decline with IFR_EDECLINE."""
+    rng = np.random.default_rng(900 + bits)
+    nv = L.ifr_quant_gemm_variants()
+    assert nv >= 2
+    for (N, K) in ((512, 1024), (256, 3072), (384, 2048)):
+        lin = ia.make_linear(N, K, bits, rng)
+        gate, up = ia.make_linear(N, K, bits, rng), ia.make_linear(N, K, bits, rng)
+        dl, dp = C.c_void_p(), C.c_void_p()
+        ia.check(L.ifr_linear_upload(dev.ctx, C.byref(lin.struct), C.byref(dl)), "upload")
+        ia.check(L.ifr_linear_upload_pair(dev.ctx, C.byref(gate.struct), C.byref(up.struct),
+                                          C.byref(dp)), "pair")
+        try:
+            for M in (1, 37, 130):
+                x = rng.standard_normal((M, K), dtype=np.float32)
+                q, sc, g = po.act_quant(x)
+                qd, sd, gd = dev.upload(ia.atile(q)), dev.upload(sc[:, 0].copy()), dev.upload(g)
+                od = dev.alloc(M * N * 2)
+                ref = po.qgemm(q, sc[:, 0], lin)
+                pair_out, ran = None, 0
+                for v in range(nv):
+                    announce(f"qgemm variant {v} bits={bits} N={N} K={K} M={M}")
+                    rc = L.ifr_quant_gemm_variant(dev.ctx, dl, qd.p, sd.p, gd.p, M, od.p, v)
+                    if rc == ia.IFR_EDECLINE:
+                        continue
+                    ia.check(rc, f"variant {v}")
+                    out = dev.download(od, np.uint16, (M, N))
+                    assert np.array_equal(out, ref), f"variant {v} N={N} K={K} M={M}"
+                    ran += 1
+                    rc = L.ifr_quant_gemm_variant(dev.ctx, dp, qd.p, sd.p, gd.p, M, od.p, v)
+                    if rc == ia.IFR_EDECLINE:
+                        continue
+                    ia.check(rc, f"pair variant {v}")
+                    po_ = dev.download(od, np.uint16, (M, N))
+                    if pair_out is None:
+                        pair_out = po_
+                    assert np.array_equal(po_, pair_out), f"pair variant {v} N={N} K={K} M={M}"
+                assert ran >= 2
+                for b in (qd, sd, gd, od):
+                    b.free()
+        finally:
+            L.ifr_linear_free(dev.ctx, dl)
+            L.ifr_linear_free(dev.ctx, dp)
+
+
 @pytest.mark.parametrize("K,norm,rot,rnd,ga", [(1024, 1, 1, 0, 0), (1024, 0, 0, 1, 64),
                                                (2048, 0, 0, 0, 0), (3072, 1, 0, 0, 0),
                                                (5120, 1, 1, 0, 0)])
@@ -115,11 +163,12 @@ def test_act_quant_bitexact(dev, K, norm, rot, rnd, ga):
     q, s, g = po.act_quant(x, norm_w=w if norm else None, rotate=rot, round=rnd, ga=ga)
     ns = K // ga if ga else 1
     xd, wd = dev.upload(x), dev.upload(w)
-    qd, sd, gd = dev.alloc(M * K), dev.alloc(M * ns * 4), dev.alloc(M * (K // 128) * 4)
+    Mp = (M + 15) // 16 * 16
+    qd, sd, gd = dev.alloc(Mp * K), dev.alloc(M * ns * 4), dev.alloc(M * (K // 128) * 4)
     announce(f"act_quant K={K} norm={norm} rot={rot} rnd={rnd} ga={ga}")
     ia.check(L.ifr_act_quant(dev.ctx, xd.p, M, K, wd.p if norm else None, C.c_float(1e-6), rot, rnd,
                              ga, qd.p, sd.p, gd.p), "ifr_act_quant")
-    qg = dev.download(qd, np.int8, (M, K))
+    qg = ia.untile(dev.download(qd, np.int8, (Mp * K,)), M, K)
     sg = dev.download(sd, np.float32, (M, ns))
     gg = dev.download(gd, np.float32, (M, K // 128))
     for b in (xd, wd, qd, sd, gd):
