@@ -49,6 +49,10 @@ def parse():
     ap.add_argument("--kv-int8", type=int, default=0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-roofline", action="store_true")
+    ap.add_argument("--gemm-sweep", action="store_true",
+                    help="run only the cache-cold cfg2 GEMM sweep and print its JSON line")
+    ap.add_argument("--copy-calib", action="store_true",
+                    help="run only 8 device copies of 1 GiB (HBM traffic counter calibration)")
     return ap.parse_args()
 
 
@@ -118,6 +122,108 @@ def serve_roofline(cfg, weight_bytes, lm_bytes, iters_rows, kv_elem):
     return t_roof, dec
 
 
+GEMMS = ["qgemm_qkv", "qgemm_o", "qgemm_gate_up", "qgemm_down"]
+KERNELS = GEMMS + ["attention", "row_quant", "qk_rope_kv", "combine", "quant_plain", "lmhead", "pack"]
+# the rocprofv3 kernel names each timing category covers (each GEMM category:
+# qgemm_splitk<...> for M <= 64, qgemm_rows<...> above)
+ROCPROF_NAMES = {"attention": "attn_kernel<{kv}>",
+                 "combine": "combine_kernel", "row_quant": "row_quant1024_kernel",
+                 "quant_plain": "quant_plain_fast<12>", "qk_rope_kv": "qk_rope_kv_kernel",
+                 "lmhead": "lmhead_kernel<...> + argmax_final_kernel", "pack": "pack_kernel"}
+PEAK_FLOPS = {"qgemm": INT8_PEAK, "attention": FP16_PEAK, "lmhead": INT8_PEAK, **{g: INT8_PEAK for g in GEMMS}}
+
+
+def traffic_from_profile(kernel, kv_int8):
+    """HBM bytes per launch measured by rocprofv3 --pmc (FETCH_SIZE + WRITE_SIZE,
+    scaled by the copy-kernel calibration), read from the committed summary."""
+    f = ROOT / "profiles" / f"{kernel}_cfg4_c64{'_kv8' if kv_int8 else ''}_pmc.md"
+    if not f.exists():
+        return None
+    for line in f.read_text().splitlines():
+        if line.startswith("hbm_bytes_per_launch:"):
+            return float(line.split(":", 1)[1])
+    return None
+
+
+def kernel_roofline(name, st, kv_int8, brief=False):
+    """Roofline of one timing category over the load: bound = the resource
+    whose peak time (algorithmic bytes / 8 TB/s or work / MFMA peak) is larger."""
+    ms, n, b, f = st
+    sec = ms * 1e-3
+    pk = PEAK_FLOPS.get(name)
+    t_hbm = b / HBM_PEAK
+    t_cmp = f / pk if pk else 0.0
+    if pk and t_cmp > t_hbm:
+        ach = f / sec / 1e12 if sec else 0.0
+        r = {"bound": "mfma", "achieved": round(ach, 2), "peak": pk / 1e12, "unit": "TFLOP/s",
+             "frac": round(ach * 1e12 / pk, 4)}
+    else:
+        ach = b / sec / 1e9 if sec else 0.0
+        r = {"bound": "hbm", "achieved": round(ach, 1), "peak": HBM_PEAK / 1e9, "unit": "GB/s",
+             "frac": round(ach * 1e9 / HBM_PEAK, 4)}
+    r.update({"launches": n, "avg_us": round(1e3 * ms / n, 2) if n else None, "total_ms": round(ms, 2)})
+    if brief:
+        return r
+    tr = traffic_from_profile(name, kv_int8)
+    r["traffic"] = round(tr) if tr is not None else None
+    r.update({"kernel": name, "rocprof_kernel": ROCPROF_NAMES.get(name, name).format(
+                  kv="true" if kv_int8 else "false"),
+              "bytes_per_launch": round(b / n) if n else None,
+              "flops_per_launch": round(f / n) if n else None,
+              "peak_time_us": {"hbm": round(t_hbm / n * 1e6, 2) if n else None,
+                               "mfma": round(t_cmp / n * 1e6, 2) if n else None}})
+    return r
+
+
+def gemm_sweep(ia, dev, bits_list=(2, 4), Ms=(1, 8, 16, 64, 256, 1024), reps=3):
+    """cfg2: the four 0.8B GEMM shapes, cache-cold.  Each timed pass launches
+    the GEMM once on each of R distinct weight copies (R * weight bytes >
+    320 MB, above the 256 MB MALL), bracketed by HIP events on the engine
+    stream; the best of `reps` passes is reported."""
+    import ctypes as C
+    L = ia.lib()
+    shapes = [("qkv", 1024, 4096), ("o", 2048, 1024), ("gate_up", 1024, 6144), ("down", 3072, 1024)]
+    rng = np.random.default_rng(0)
+    res = []
+    Mmax = max(Ms)
+    for bits in bits_list:
+        for name, K, N in shapes:
+            lin = ia.make_linear(N, K, bits, rng)
+            wb = N * K * bits // 8 + N * (K // 128) * 4
+            R = int(np.ceil(320e6 / wb))
+            dls = []
+            for _ in range(R):
+                d = C.c_void_p()
+                ia.check(L.ifr_linear_upload(dev.ctx, C.byref(lin.struct), C.byref(d)), "upload")
+                dls.append(d)
+            q = dev.upload(rng.integers(-127, 128, size=((Mmax + 15) // 16 * 16) * K, dtype=np.int8))
+            asc = dev.upload(np.full(Mmax, 1e-3, dtype=np.float32))
+            gs = dev.upload(rng.integers(-2000, 2000, size=Mmax * (K // 128)).astype(np.float32))
+            out = dev.alloc(Mmax * N * 2)
+            for M in Ms:
+                best = None
+                for _ in range(reps + 1):  # first pass warms code and TLB
+                    dev.timer_begin()
+                    for d in dls:
+                        ia.check(L.ifr_quant_gemm(dev.ctx, d, q.p, asc.p, gs.p, M, out.p, None), "gemm")
+                    ms = dev.timer_end()
+                    best = ms if best is None else min(best, ms)
+                us = best * 1e3 / R
+                byts = wb + M * K + M * 4 + M * N * 2
+                ops = 2.0 * M * N * K
+                res.append({"shape": name, "bits": bits, "M": M, "N": N, "K": K, "us": round(us, 3),
+                            "GBps": round(byts / us / 1e3, 1), "hbm_frac": round(byts / us / 1e3 / 8000, 4),
+                            "TOPS": round(ops / us / 1e6, 1), "mfma_frac": round(ops / us / 1e6 / 5000, 4),
+                            "copies": R})
+                log(f"cfg2 {name} W{bits} M={M}: {us:.2f} us, {byts / us / 1e3:.0f} GB/s, "
+                    f"{ops / us / 1e6:.0f} TOPS")
+            for d in dls:
+                L.ifr_linear_free(dev.ctx, d)
+            for b in (q, asc, gs, out):
+                b.free()
+    return res
+
+
 def cpu_baseline(ia, model, cfg):
     """Reference CPU path on a bounded sample with the load's per-output-token
     mix: 4 decode rows at the load's mean context (1088) + one 66-row prefill
@@ -158,6 +264,29 @@ def main():
         return 2
     import intfer_amd as ia
     from intfer_amd import workloads as wl
+
+    if a.copy_calib:
+        import ctypes as C
+        dev = ia.Device(0)
+        n = 1 << 30
+        src, dst = dev.zeros(n), dev.alloc(n)
+        dev.timer_begin()
+        for _ in range(8):
+            ia.check(ia.lib().ifr_d2d(dev.ctx, dst.p, src.p, C.c_size_t(n)), "ifr_d2d")
+        ms = dev.timer_end()
+        print(json.dumps({"metric": "device copy 1 GiB x 8", "bytes_read_per_copy": n,
+                          "bytes_written_per_copy": n, "GBps": round(2 * 8 * n / ms / 1e6, 1)}))
+        dev.close()
+        return 0
+    if a.gemm_sweep:
+        dev = ia.Device(0)
+        res = gemm_sweep(ia, dev)
+        dec = [r for r in res if r["M"] <= 16]
+        print(json.dumps({"metric": "cfg2 quant-GEMM sweep (cache-cold, rotating weights > MALL)",
+                          "unit": "GB/s", "decode_best_hbm_frac": max(r["hbm_frac"] for r in dec),
+                          "results": res}))
+        dev.close()
+        return 0
 
     cfg = ia.default_cfg()
     log("building the synthetic 0.8B-class INT2 model")
@@ -203,29 +332,23 @@ def main():
         rec = []
         eng.set_timing(True)
         dt, toks, iters, rows, _ = run_load(ia, eng, prompts, max_new, chunk, record=rec)
-        kernels = ["qgemm", "attention", "row_quant", "qk_rope_kv", "combine", "quant_plain",
-                   "lmhead", "pack"]
-        stats = {k: eng.timing(k) for k in kernels}
+        stats = {k: eng.timing(k) for k in KERNELS}
         eng.set_timing(False)
         busy = sum(v[0] for v in stats.values())
-        dom = max(kernels, key=lambda k: stats[k][0])
-        ms, n, b = stats[dom]
-        ach = (b / n) / (ms / n * 1e-3) if n else 0.0
-        out["roofline"] = {"bound": "hbm", "kernel": dom, "achieved": round(ach / 1e9, 1),
-                           "peak": 8000.0, "unit": "GB/s", "frac": round(ach / HBM_PEAK, 4),
-                           "traffic": None, "launches": n, "avg_us": round(1e3 * ms / n, 2),
-                           "bytes_per_launch": round(b / n)}
-        out["kernel_ms_per_step"] = {k: round(v[0], 2) for k, v in stats.items()}
+        dom = max(KERNELS, key=lambda k: stats[k][0])
+        out["roofline"] = kernel_roofline(dom, stats[dom], a.kv_int8)
+        out["kernels"] = {k: kernel_roofline(k, v, a.kv_int8, brief=True)
+                          for k, v in stats.items() if v[1]}
         out["gpu_busy_frac"] = round(busy / (dt * 1e3), 3)
-        qms, qn, qb = stats["qgemm"]
-        out["quant_gemm"] = {"achieved_GBps": round(qb / (qms * 1e-3) / 1e9, 1),
-                             "frac_of_hbm_peak": round(qb / (qms * 1e-3) / HBM_PEAK, 4),
-                             "launches": qn, "avg_us": round(1e3 * qms / qn, 2) if qn else None,
-                             "note": "in-load W2A8 GEMMs; the cache-cold sweep is in profiles/"}
-        wbytes = sum(0 for _ in ())
+        g = [stats[k] for k in GEMMS]
+        out["quant_gemm"] = kernel_roofline("qgemm", tuple(sum(x[i] for x in g) for i in range(4)),
+                                            a.kv_int8, brief=True)
+        out["quant_gemm"]["note"] = ("all in-load W2A8 GEMMs (mixed M); the cache-cold cfg2 sweep "
+                                     "(bench.py --gemm-sweep) reports decode-shape HBM GB/s")
         kv_elem = 1 if a.kv_int8 else 2
         H, L = cfg.hidden, cfg.layers
-        per_layer = (H * (16 * 128 + 2 * 8 * 128) + 16 * 128 * H + H * 2 * cfg.inter + cfg.inter * H)
+        per_layer = (H * (cfg.n_heads * cfg.head_dim + 2 * cfg.n_kv * cfg.head_dim) +
+                     cfg.n_heads * cfg.head_dim * H + H * 2 * cfg.inter + cfg.inter * H)
         wbytes = L * per_layer * 2 / 8 + L * per_layer / 128 * 4
         lm_bytes = cfg.vocab * H + cfg.vocab * 2
         t_roof, dec = serve_roofline(cfg, wbytes, lm_bytes, rec, kv_elem)
@@ -234,7 +357,7 @@ def main():
                                  "achieved_tok_s": round(value, 1),
                                  "frac": round(value / roof_tok_s, 4),
                                  "decode_rows": dec, "iterations": len(rec)}
-        log(f"timing pass: {dt:.3f} s; dominant {dom} {ms:.1f} ms; roofline tok/s {roof_tok_s:.0f}")
+        log(f"timing pass: {dt:.3f} s; dominant {dom} {stats[dom][0]:.1f} ms; roofline tok/s {roof_tok_s:.0f}")
     if not a.no_cpu:
         log("timing the reference CPU path on a bounded sample")
         out["cpu_baseline"] = cpu_baseline(ia, model, cfg)

@@ -111,6 +111,14 @@ const char* ifr_last_error(void);
 int ifr_ctx_create(int32_t device, ifr_ctx** out);
 int ifr_ctx_destroy(ifr_ctx* ctx);
 int ifr_sync(ifr_ctx* ctx);
+/* No reference counterpart: the context's HIP stream (a hipStream_t), for
+ * callers that order their own work or timing events against the engine. */
+void* ifr_ctx_stream(ifr_ctx* ctx);
+/* No reference counterpart: HIP events on the context stream around any
+ * work enqueued between the two calls (bench hook).  ifr_timer_end waits for
+ * the end event and returns the elapsed device time in milliseconds. */
+int ifr_timer_begin(ifr_ctx* ctx);
+int ifr_timer_end(ifr_ctx* ctx, double* ms);
 
 /* Device buffers for tests and benches (no torch in the boundary). */
 int ifr_malloc(ifr_ctx* ctx, size_t bytes, void** dptr);
@@ -118,6 +126,9 @@ int ifr_free(ifr_ctx* ctx, void* dptr);
 int ifr_h2d(ifr_ctx* ctx, void* dst, const void* src, size_t bytes);
 int ifr_d2h(ifr_ctx* ctx, void* dst, const void* src, size_t bytes);
 int ifr_memset(ifr_ctx* ctx, void* dst, int value, size_t bytes);
+/* Device-to-device copy, enqueued on the context stream (not waited for);
+ * also the known-size copy that calibrates HBM traffic counters. */
+int ifr_d2d(ifr_ctx* ctx, void* dst, const void* src, size_t bytes);
 
 /* ------------------------------------------------------------------------
  * Kernel-level entry points (tests, benches, and the reference's
@@ -252,11 +263,16 @@ int ifr_forward(ifr_ctx* ctx, const ifr_row* rows, int32_t M, int32_t* best_out,
 int ifr_attention(ifr_ctx* ctx, int32_t layer, const ifr_row* rows, int32_t M,
                   const uint16_t* q_h, float* out_h);
 
-/* Per-kernel device timing of the last ifr_forward (HIP events on the
- * context stream), for the bench: names are "qgemm", "attention", ... */
+/* No reference counterpart: per-kernel device timing of ifr_forward calls
+ * since ifr_set_timing(ctx, 1) (HIP events on the context stream), for the
+ * bench.  Names: "qgemm_qkv", "qgemm_o", "qgemm_gate_up", "qgemm_down",
+ * "attention", "combine", "row_quant", "quant_plain", "qk_rope_kv", "lmhead",
+ * "pack".  bytes / flops accumulate each launch's
+ * algorithmic HBM bytes and arithmetic work (int8 ops for the GEMMs, fp
+ * flops for attention). */
 int ifr_set_timing(ifr_ctx* ctx, int32_t on);
 int ifr_get_timing(ifr_ctx* ctx, const char* kernel, double* total_ms, int64_t* launches,
-                   double* bytes);
+                   double* bytes, double* flops);
 
 /* Test hook (no reference counterpart): copies the last forward's packing
  * outputs to host buffers (any may be NULL).  units: 8 int32 per unit

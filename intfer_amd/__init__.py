@@ -188,6 +188,19 @@ class Device:
     def sync(self):
         check(lib().ifr_sync(self.ctx), "ifr_sync")
 
+    def stream(self) -> int:
+        """The context's HIP stream handle."""
+        return lib().ifr_ctx_stream(self.ctx)
+
+    def timer_begin(self):
+        check(lib().ifr_timer_begin(self.ctx), "ifr_timer_begin")
+
+    def timer_end(self) -> float:
+        """Device milliseconds since timer_begin (waits for the stream)."""
+        ms = C.c_double()
+        check(lib().ifr_timer_end(self.ctx, C.byref(ms)), "ifr_timer_end")
+        return ms.value
+
     def close(self):
         if self.ctx:
             for b in self._bufs:
@@ -258,10 +271,11 @@ class Engine:
         check(lib().ifr_set_timing(self.dev.ctx, 1 if on else 0), "ifr_set_timing")
 
     def timing(self, kernel: str):
-        ms, n, b = C.c_double(), C.c_int64(), C.c_double()
+        """(total ms, launches, algorithmic bytes, flops) since set_timing(True)."""
+        ms, n, b, f = C.c_double(), C.c_int64(), C.c_double(), C.c_double()
         check(lib().ifr_get_timing(self.dev.ctx, kernel.encode(), C.byref(ms), C.byref(n),
-                                   C.byref(b)), "ifr_get_timing")
-        return ms.value, n.value, b.value
+                                   C.byref(b), C.byref(f)), "ifr_get_timing")
+        return ms.value, n.value, b.value, f.value
 
 
 class Scheduler:

@@ -94,6 +94,10 @@ _PROTOS = {
     "ifr_quant_gemm": (C.c_int, [P, P, P, P, P, i32, P, P]),
     "ifr_quant_gemm_swiglu": (C.c_int, [P, P, P, P, P, i32, P]),
     "ifr_quant_gemm_variants": (C.c_int, []),
+    "ifr_ctx_stream": (C.c_void_p, [P]),
+    "ifr_timer_begin": (C.c_int, [P]),
+    "ifr_d2d": (C.c_int, [P, P, P, C.c_size_t]),
+    "ifr_timer_end": (C.c_int, [P, C.POINTER(C.c_double)]),
     "ifr_quant_gemm_variant": (C.c_int, [P, P, P, P, P, i32, P, i32]),
     "ifr_model_load": (C.c_int, [P, C.POINTER(HostModel), C.POINTER(KVCfg)]),
     "ifr_seq_open": (C.c_int, [P, pi32]),
@@ -106,7 +110,7 @@ _PROTOS = {
     "ifr_attention": (C.c_int, [P, i32, C.POINTER(Row), i32, P, pf32]),
     "ifr_set_timing": (C.c_int, [P, i32]),
     "ifr_get_timing": (C.c_int, [P, C.c_char_p, C.POINTER(C.c_double), C.POINTER(i64),
-                                 C.POINTER(C.c_double)]),
+                                 C.POINTER(C.c_double), C.POINTER(C.c_double)]),
     "ifr_debug_pack": (C.c_int, [P, i32, P, P, P, P, P, P, pi32, pi32]),
     "ifr_sched_create": (C.c_int, [P, C.POINTER(SchedCfg), C.POINTER(P)]),
     "ifr_sched_create_backend": (C.c_int, [C.POINTER(SchedBackend), C.POINTER(SchedCfg),

@@ -60,11 +60,11 @@ struct Layer {
 struct Timer {
   std::string name;
   hipEvent_t a, b;
-  double bytes;
+  double bytes, flops;
 };
 
 struct Stat {
-  double ms = 0, bytes = 0;
+  double ms = 0, bytes = 0, flops = 0;
   int64_t n = 0;
 };
 
@@ -129,6 +129,7 @@ struct ifr_ctx {
   size_t logits_cap = 0;
   // timing
   bool timing = false;
+  hipEvent_t tev[2] = {nullptr, nullptr};  // ifr_timer_begin / _end
   std::vector<Timer> timers;
   std::vector<std::pair<std::string, Stat>> stats;
   // last forward's split (for tests / bench notes)
@@ -157,10 +158,12 @@ struct Scope {
   ifr_ctx* c;
   Timer t;
   bool on;
-  Scope(ifr_ctx* c_, const char* name, double bytes) : c(c_), on(c_->timing) {
+  // bytes / flops: the launch's algorithmic HBM bytes and arithmetic work
+  Scope(ifr_ctx* c_, const char* name, double bytes, double flops = 0) : c(c_), on(c_->timing) {
     if (!on) return;
     t.name = name;
     t.bytes = bytes;
+    t.flops = flops;
     hipEventCreate(&t.a);
     hipEventCreate(&t.b);
     hipEventRecord(t.a, c->st);
@@ -181,6 +184,7 @@ void flush_timers(ifr_ctx* c) {
     s.ms += ms;
     s.n += 1;
     s.bytes += t.bytes;
+    s.flops += t.flops;
     hipEventDestroy(t.a);
     hipEventDestroy(t.b);
   }
@@ -334,8 +338,33 @@ int ifr_ctx_destroy(ifr_ctx* c) {
   if (!c) return IFR_OK;
   hipSetDevice(c->device);
   release_model(c);
+  for (hipEvent_t& e : c->tev)
+    if (e) hipEventDestroy(e);
   if (c->st) hipStreamDestroy(c->st);
   delete c;
+  return IFR_OK;
+}
+
+void* ifr_ctx_stream(ifr_ctx* c) { return c ? (void*)c->st : nullptr; }
+
+int ifr_timer_begin(ifr_ctx* c) {
+  if (!c) return fail(IFR_EINVAL, "ctx null");
+  if (!c->tev[0]) {
+    HIPCHK(hipEventCreate(&c->tev[0]));
+    HIPCHK(hipEventCreate(&c->tev[1]));
+  }
+  HIPCHK(hipEventRecord(c->tev[0], c->st));
+  return IFR_OK;
+}
+
+int ifr_timer_end(ifr_ctx* c, double* ms) {
+  if (!c || !ms) return fail(IFR_EINVAL, "null arg");
+  if (!c->tev[0]) return fail(IFR_ESTATE, "ifr_timer_begin not called");
+  HIPCHK(hipEventRecord(c->tev[1], c->st));
+  HIPCHK(hipEventSynchronize(c->tev[1]));
+  float f = 0;
+  HIPCHK(hipEventElapsedTime(&f, c->tev[0], c->tev[1]));
+  *ms = f;
   return IFR_OK;
 }
 
@@ -366,6 +395,11 @@ int ifr_d2h(ifr_ctx* c, void* dst, const void* src, size_t bytes) {
   if (!c) return fail(IFR_EINVAL, "ctx null");
   HIPCHK(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, c->st));
   HIPCHK(hipStreamSynchronize(c->st));
+  return IFR_OK;
+}
+int ifr_d2d(ifr_ctx* c, void* dst, const void* src, size_t bytes) {
+  if (!c) return fail(IFR_EINVAL, "ctx null");
+  HIPCHK(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToDevice, c->st));
   return IFR_OK;
 }
 int ifr_memset(ifr_ctx* c, void* dst, int v, size_t bytes) {
@@ -849,6 +883,8 @@ int ifr_forward(ifr_ctx* c, const ifr_row* rows, int32_t M, int32_t* best_out, f
     }
     attn_bytes += (double)M * qN * 2 * 2;
   }
+  double attn_flops = 0;  // QK^T + PV over each row's visible keys (pos + 1)
+  for (int m = 0; m < M; ++m) attn_flops += 4.0 * qN * (rows[m].pos + 1);
   const int ng_h = H / 128;
   for (int l = 0; l < cf.layers; ++l) {
     Layer& ly = c->layers[l];
@@ -883,7 +919,8 @@ int ifr_forward(ifr_ctx* c, const ifr_row* rows, int32_t M, int32_t* best_out, f
     // (2) QKV
     for (int j = 0; j < ly.nqkv; ++j) {
       ifrk::QGemmArgs a{c->aq, c->as, c->gs, c->qkv + ly.qkv_off[j], nullptr, M, qN + 2 * kvN};
-      Scope sc(c, "qgemm", (double)ly.qkv[j].bytes + (double)M * H + (double)M * ly.qkv[j].N * 2);
+      Scope sc(c, "qgemm_qkv", (double)ly.qkv[j].bytes + (double)M * (H + 4) + (double)M * ly.qkv[j].N * 2,
+               2.0 * M * ly.qkv[j].N * H);
       HIPCHK(ifrk::launch_qgemm(ly.qkv[j], a, c->st));
     }
     // (3) q/k norm + RoPE + KV append
@@ -897,7 +934,7 @@ int ifr_forward(ifr_ctx* c, const ifr_row* rows, int32_t M, int32_t* best_out, f
     {
       ifrk::AttnArgs a{c->pk.units, (int)nunits, c->qbuf, nq, 1.4426950408889634f / std::sqrt((float)hd),
                        c->part_o, c->part_ml};
-      Scope sc(c, "attention", attn_bytes);
+      Scope sc(c, "attention", attn_bytes, attn_flops);
       HIPCHK(ifrk::launch_attention(a, kv, c->st));
     }
     {
@@ -909,7 +946,8 @@ int ifr_forward(ifr_ctx* c, const ifr_row* rows, int32_t M, int32_t* best_out, f
     // (5) O projection
     {
       ifrk::QGemmArgs a{c->aq, c->as, c->gs, c->y, nullptr, M, H};
-      Scope sc(c, "qgemm", (double)ly.o.bytes + (double)M * qN + (double)M * H * 2);
+      Scope sc(c, "qgemm_o", (double)ly.o.bytes + (double)M * (qN + 4) + (double)M * H * 2,
+               2.0 * M * H * qN);
       HIPCHK(ifrk::launch_qgemm(ly.o, a, c->st));
     }
     // (6) residual += FWHT(o); post norm; FWHT; quant
@@ -933,12 +971,14 @@ int ifr_forward(ifr_ctx* c, const ifr_row* rows, int32_t M, int32_t* best_out, f
     // (7) gate/up + SwiGLU
     if (ly.ngu == 1) {
       ifrk::QGemmArgs a{c->aq, c->as, c->gs, c->mg, nullptr, M, F};
-      Scope sc(c, "qgemm", (double)ly.gu[0].bytes + (double)M * H + (double)M * F * 2);
+      Scope sc(c, "qgemm_gate_up", (double)ly.gu[0].bytes + (double)M * (H + 4) + (double)M * F * 2,
+               2.0 * M * 2 * F * H);
       HIPCHK(ifrk::launch_qgemm(ly.gu[0], a, c->st));
     } else {
       for (int j = 0; j < 2; ++j) {
         ifrk::QGemmArgs a{c->aq, c->as, c->gs, c->gu + j * F, nullptr, M, 2 * F};
-        Scope sc(c, "qgemm", (double)ly.gu[j].bytes + (double)M * H + (double)M * F * 2);
+        Scope sc(c, "qgemm_gate_up", (double)ly.gu[j].bytes + (double)M * (H + 4) + (double)M * F * 2,
+                 2.0 * M * F * H);
         HIPCHK(ifrk::launch_qgemm(ly.gu[j], a, c->st));
       }
       HIPCHK(ifrk::launch_swiglu(c->gu, M, F, c->mg, c->st));
@@ -950,7 +990,8 @@ int ifr_forward(ifr_ctx* c, const ifr_row* rows, int32_t M, int32_t* best_out, f
     }
     {
       ifrk::QGemmArgs a{c->aq, c->as, c->gs, c->y, nullptr, M, H};
-      Scope sc(c, "qgemm", (double)ly.down.bytes + (double)M * F + (double)M * H * 2);
+      Scope sc(c, "qgemm_down", (double)ly.down.bytes + (double)M * (F + 4) + (double)M * H * 2,
+               2.0 * M * H * F);
       HIPCHK(ifrk::launch_qgemm(ly.down, a, c->st));
     }
   }
@@ -1075,18 +1116,20 @@ int ifr_set_timing(ifr_ctx* c, int32_t on) {
 }
 
 int ifr_get_timing(ifr_ctx* c, const char* kernel, double* total_ms, int64_t* launches,
-                   double* bytes) {
+                   double* bytes, double* flops) {
   if (!c || !kernel) return fail(IFR_EINVAL, "null arg");
   for (auto& s : c->stats)
     if (s.first == kernel) {
       if (total_ms) *total_ms = s.second.ms;
       if (launches) *launches = s.second.n;
       if (bytes) *bytes = s.second.bytes;
+      if (flops) *flops = s.second.flops;
       return IFR_OK;
     }
   if (total_ms) *total_ms = 0;
   if (launches) *launches = 0;
   if (bytes) *bytes = 0;
+  if (flops) *flops = 0;
   return IFR_OK;
 }
 
