@@ -26,7 +26,10 @@ constexpr int kPage = 32;
 
 template <bool KV8>
 __global__ __launch_bounds__(256) void attn_kernel(AttnArgs p, KVLayout kv) {
-  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63;
+  // wave-uniform unit index: the unit record and block-table entries become
+  // scalar loads, which do not queue behind the vector K/V loads
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int u = blockIdx.x * 4 + w;
   if (u >= p.n_units) return;
   const AttnUnit un = p.units[u];
@@ -55,58 +58,71 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs p, KVLayout kv) {
   for (int d = 0; d < 8; ++d) o[d] = (v4f){0.f, 0.f, 0.f, 0.f};
 
   const int32_t* bt = kv.block_table + (size_t)un.seq * kv.max_pages;
-  for (int t0 = un.kv_lo; t0 < un.kv_hi; t0 += kPage) {
+  // One page = 32 tokens.  Raw K/V fragments of a page (fp16, or int8 with
+  // per-token scales); two buffers alternate so the next page's loads are in
+  // flight while the current page is computed.  Every load is unconditional
+  // (the page index is clamped to the unit's last page), so the wait before a
+  // page covers only that page's loads.
+  struct PageBuf {
+    uint32_t k[2][4][KV8 ? 2 : 4];  // K tile h, k-step i: 8 dims of token 2c + h
+    uint32_t v[8][KV8 ? 2 : 4];     // V^T tile d: 8 tokens of dim 16d + c
+    uint16_t ks[2][4], vs[8];
+  };
+  const int last = (un.kv_hi - 1 - un.kv_lo) / kPage;  // pages are [kv_lo + 32 i, +32)
+  auto load = [&](PageBuf& b, int i) {
+    const int t0 = un.kv_lo + kPage * min(i, last);
     const size_t pb = (size_t)bt[t0 / kPage] * kv.nkv + un.kvh;
-    // ---- issue K and V loads for this page
-    v8h ka[2][4];
-    v8h va[8];
-    float ks[2][4], vs[8];
-    if constexpr (!KV8) {
-      const _Float16* kp = reinterpret_cast<const _Float16*>(kv.kpool) + pb * kPage * kHD;
-      const _Float16* vp = reinterpret_cast<const _Float16*>(kv.vpool) + pb * kHD * kPage;
+    constexpr int W = KV8 ? 2 : 4;
+    const uint8_t* kp = reinterpret_cast<const uint8_t*>(kv.kpool) + pb * kPage * kHD * (KV8 ? 1 : 2);
+    const uint8_t* vp = reinterpret_cast<const uint8_t*>(kv.vpool) + pb * kHD * kPage * (KV8 ? 1 : 2);
+    // fragment-major pages: fragment f is 64 lanes x 8 elements, lane at 8 * lane
 #pragma unroll
-      for (int h = 0; h < 2; ++h)
+    for (int h = 0; h < 2; ++h)
 #pragma unroll
-        for (int i = 0; i < 4; ++i)
-          ka[h][i] = *reinterpret_cast<const v8h*>(kp + (2 * c + h) * kHD + 32 * i + 8 * g);
+      for (int i4 = 0; i4 < 4; ++i4) {
+        const size_t e = (size_t)((h * 4 + i4) * 64 + lane) * 8;  // element index
+        const uint32_t* src = reinterpret_cast<const uint32_t*>(kp + e * (KV8 ? 1 : 2));
 #pragma unroll
-      for (int d = 0; d < 8; ++d)
-        va[d] = *reinterpret_cast<const v8h*>(vp + (16 * d + c) * kPage + 8 * g);
-    } else {
-      const int8_t* kp = reinterpret_cast<const int8_t*>(kv.kpool) + pb * kPage * kHD;
-      const int8_t* vp = reinterpret_cast<const int8_t*>(kv.vpool) + pb * kHD * kPage;
-#pragma unroll
-      for (int h = 0; h < 2; ++h)
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const uint2 raw = *reinterpret_cast<const uint2*>(kp + (2 * c + h) * kHD + 32 * i + 8 * g);
-#pragma unroll
-          for (int b = 0; b < 8; ++b)
-            ka[h][i][b] = (_Float16)(int8_t)(((b < 4 ? raw.x : raw.y) >> (8 * (b & 3))) & 0xFF);
-        }
-#pragma unroll
-      for (int d = 0; d < 8; ++d) {
-        const uint2 raw = *reinterpret_cast<const uint2*>(vp + (16 * d + c) * kPage + 8 * g);
-#pragma unroll
-        for (int b = 0; b < 8; ++b)
-          va[d][b] = (_Float16)(int8_t)(((b < 4 ? raw.x : raw.y) >> (8 * (b & 3))) & 0xFF);
+        for (int q = 0; q < W; ++q) b.k[h][i4][q] = src[q];
       }
+#pragma unroll
+    for (int d = 0; d < 8; ++d) {
+      const size_t e = (size_t)(d * 64 + lane) * 8;
+      const uint32_t* src = reinterpret_cast<const uint32_t*>(vp + e * (KV8 ? 1 : 2));
+#pragma unroll
+      for (int q = 0; q < W; ++q) b.v[d][q] = src[q];
+    }
+    if constexpr (KV8) {
       const uint16_t* ksc = kv.kscale + pb * kPage;
       const uint16_t* vsc = kv.vscale + pb * kPage;
 #pragma unroll
       for (int h = 0; h < 2; ++h)
 #pragma unroll
-        for (int r = 0; r < 4; ++r) ks[h][r] = ifrd::h2f(ksc[8 * g + 2 * r + h]);
+        for (int r = 0; r < 4; ++r) b.ks[h][r] = ksc[8 * g + 2 * r + h];
 #pragma unroll
-      for (int j = 0; j < 8; ++j) vs[j] = ifrd::h2f(vsc[8 * g + j]);
+      for (int j = 0; j < 8; ++j) b.vs[j] = vsc[8 * g + j];
     }
+  };
+  auto frag = [&](const uint32_t* w) -> v8h {  // 8 fp16 from raw fp16 or int8
+    v8h f;
+    if constexpr (!KV8) {
+      f = __builtin_bit_cast(v8h, (v4i){(int)w[0], (int)w[1], (int)w[2], (int)w[3]});
+    } else {
+#pragma unroll
+      for (int j = 0; j < 8; ++j) f[j] = (_Float16)(int8_t)((w[j >> 2] >> (8 * (j & 3))) & 0xFF);
+    }
+    return f;
+  };
+  auto step = [&](const PageBuf& b, int i) {
+    const int t0 = un.kv_lo + kPage * i;
     // ---- S^T: tile h covers tokens 2c' + h; lane (c, g) reg r -> token 8g + 2r + h.
     v4f s[2];
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
       s[h] = (v4f){0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int i = 0; i < 4; ++i) s[h] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ka[h][i], qf[i], s[h], 0, 0, 0);
+      for (int i4 = 0; i4 < 4; ++i4)
+        s[h] = __builtin_amdgcn_mfma_f32_16x16x32_f16(frag(b.k[h][i4]), qf[i4], s[h], 0, 0, 0);
     }
     float sv[8];
     float mt = -INFINITY;
@@ -116,7 +132,7 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs p, KVLayout kv) {
       for (int h = 0; h < 2; ++h) {
         const int t = t0 + 8 * g + 2 * r + h;
         float v = s[h][r];
-        if constexpr (KV8) v *= ks[h][r];
+        if constexpr (KV8) v *= ifrd::h2f(b.ks[h][r]);
         v *= p.scale_log2;
         if (!colv || t > qpos || t >= un.kv_hi) v = -INFINITY;
         sv[2 * r + h] = v;
@@ -136,7 +152,7 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs p, KVLayout kv) {
     for (int j = 0; j < 8; ++j) {
       const float pf = exp2f(sv[j] - m_use);
       rs += pf;
-      const float pv = KV8 ? pf * vs[j] : pf;
+      const float pv = KV8 ? pf * ifrd::h2f(b.vs[j]) : pf;
       const _Float16 h = (_Float16)pv;
       phi[j] = h;
       plo[j] = (_Float16)(pv - (float)h);
@@ -148,9 +164,20 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs p, KVLayout kv) {
 #pragma unroll
     for (int d = 0; d < 8; ++d) {
       o[d] *= alpha;
-      o[d] = __builtin_amdgcn_mfma_f32_16x16x32_f16(va[d], phi, o[d], 0, 0, 0);
-      o[d] = __builtin_amdgcn_mfma_f32_16x16x32_f16(va[d], plo, o[d], 0, 0, 0);
+      const v8h vf = frag(b.v[d]);
+      o[d] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vf, phi, o[d], 0, 0, 0);
+      o[d] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vf, plo, o[d], 0, 0, 0);
     }
+  };
+  PageBuf bA, bB;
+  load(bA, 0);
+  for (int i = 0;; i += 2) {
+    load(bB, i + 1);
+    step(bA, i);
+    if (i + 1 > last) break;
+    load(bA, i + 2);
+    step(bB, i + 1);
+    if (i + 2 > last) break;
   }
   // ---- partials: O^T lane (c, g) reg r -> dim 16d + 4g + r of column c.
   if (colv) {
@@ -211,10 +238,17 @@ __global__ __launch_bounds__(256) void combine_kernel(CombineArgs a) {
   const float sc = mxa / 127.0f;
   const float inv = 1.0f / sc;
   if (threadIdx.x == 0) a.qscale[m] = sc;
+  int csum = 0;
   for (int i = 0; i < per; ++i) {
     const int c = ifrd::quant_half_away(x[e0 + i], inv);
     a.q[atile_off(m, e0 + i, N)] = (int8_t)c;
     codes[e0 + i] = c;
+    csum += c;
+  }
+  if (per == 8) {  // the 128 columns of group e0 / 128 are the 16 lanes of one DPP row
+    csum = ifrd::row16_sum_int(csum);
+    if ((threadIdx.x & 15) == 0) a.gsum[(size_t)m * (N / 128) + e0 / 128] = (float)csum;
+    return;
   }
   __syncthreads();
   for (int gg = threadIdx.x; gg < N / 128; gg += 256) {

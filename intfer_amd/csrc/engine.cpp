@@ -734,8 +734,9 @@ int ifr_seq_load_kv(ifr_ctx* c, int32_t slot, int32_t len, const float* k, const
   const size_t per_page = (size_t)nkv * kPage * hd;
   std::vector<uint16_t> kh(per_page), vh(per_page), ksc((size_t)nkv * kPage), vsc((size_t)nkv * kPage);
   std::vector<int8_t> kq(per_page), vq(per_page);
-  // One (token, head) vector: fp16 round, then optionally int8 (same rule as the kernel).
-  auto enc = [&](const float* x, uint16_t* h16, int8_t* q8, uint16_t* sc, size_t stride) {
+  // One (token, head) vector: fp16 round, then optionally int8 (same rule as
+  // the kernel); element d goes to block index off(d) (kv_koff / kv_voff order).
+  auto enc = [&](const float* x, uint16_t* h16, int8_t* q8, uint16_t* sc, auto off) {
     float r[128];
     float mx = 0;
     for (int d = 0; d < hd; ++d) {
@@ -743,7 +744,7 @@ int ifr_seq_load_kv(ifr_ctx* c, int32_t slot, int32_t len, const float* k, const
       mx = std::max(mx, std::fabs(r[d]));
     }
     if (!i8) {
-      for (int d = 0; d < hd; ++d) h16[d * stride] = ifr::f2h(r[d]);
+      for (int d = 0; d < hd; ++d) h16[off(d)] = ifr::f2h(r[d]);
       return;
     }
     const uint16_t s16 = ifr::f2h(mx > 0 ? mx / 127.0f : 1.0f);
@@ -752,7 +753,7 @@ int ifr_seq_load_kv(ifr_ctx* c, int32_t slot, int32_t len, const float* k, const
       const float t = r[d] * inv;
       int q = (int)(t >= 0.0f ? t + 0.5f : t - 0.5f);
       q = std::min(127, std::max(-127, q));
-      q8[d * stride] = (int8_t)q;
+      q8[off(d)] = (int8_t)q;
     }
     *sc = s16;
   };
@@ -769,10 +770,11 @@ int ifr_seq_load_kv(ifr_ctx* c, int32_t slot, int32_t len, const float* k, const
         if (t >= len) break;
         for (int h = 0; h < nkv; ++h) {
           const size_t src = (((size_t)l * len + t) * nkv + h) * hd;
-          const size_t kdst = ((size_t)h * kPage + tk) * hd;        // [h][tok][d]
-          const size_t vdst = (size_t)h * hd * kPage + tk;          // [h][d][tok]
-          enc(k + src, &kh[kdst], &kq[kdst], &ksc[(size_t)h * kPage + tk], 1);
-          enc(v + src, &vh[vdst], &vq[vdst], &vsc[(size_t)h * kPage + tk], kPage);
+          const size_t blk = (size_t)h * kPage * hd;  // this head's 32 x 128 block
+          enc(k + src, &kh[blk], &kq[blk], &ksc[(size_t)h * kPage + tk],
+              [&](int d) { return ifrk::kv_koff(tk, d); });
+          enc(v + src, &vh[blk], &vq[blk], &vsc[(size_t)h * kPage + tk],
+              [&](int d) { return ifrk::kv_voff(tk, d); });
         }
       }
       const size_t page = (size_t)s.pages[pi];

@@ -48,15 +48,80 @@ __device__ __forceinline__ void wave_sync() {
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
-__device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-  for (int o = 32; o >= 1; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+// ---- cross-lane moves without the LDS crossbar -------------------------------
+// DPP (data-parallel primitives) read a neighbour lane's VGPR inside the VALU:
+// quad_perm within 4 lanes, row_ror within 16-lane rows.  row_ror:n makes lane
+// i read lane (i - n) mod 16 of its row.  ds_bpermute (what __shfl_xor lowers
+// to) goes through the LDS crossbar and costs ~100+ cycles of latency per use.
+template <int CTRL>
+__device__ __forceinline__ int dpp_i(int x) {
+  return __builtin_amdgcn_update_dpp(0, x, CTRL, 0xF, 0xF, false);
+}
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float x) {
+  return __builtin_bit_cast(float, dpp_i<CTRL>(__builtin_bit_cast(int, x)));
+}
+constexpr int kQuadXor1 = 0xB1;  // quad_perm [1,0,3,2]
+constexpr int kQuadXor2 = 0x4E;  // quad_perm [2,3,0,1]
+constexpr int kRowRor4 = 0x124, kRowRor8 = 0x128, kRowRor12 = 0x12C;
+
+// Value of lane (lane ^ M).  M <= 8 stays inside a 16-lane row (DPP); larger
+// M crosses rows and uses the crossbar.
+template <int M>
+__device__ __forceinline__ float lane_xor(float x) {
+  if constexpr (M == 1) {
+    return dpp_f<kQuadXor1>(x);
+  } else if constexpr (M == 2) {
+    return dpp_f<kQuadXor2>(x);
+  } else if constexpr (M == 4) {
+    const float from_lo = dpp_f<kRowRor4>(x);   // lane i - 4
+    const float from_hi = dpp_f<kRowRor12>(x);  // lane i + 4
+    return (threadIdx.x & 4) ? from_lo : from_hi;
+  } else if constexpr (M == 8) {
+    return dpp_f<kRowRor8>(x);
+  } else {
+    return __shfl_xor(x, M, 64);
+  }
+}
+
+// All-reduce inside each 16-lane row (every lane gets its row's result).
+// Sum / max are order-free here (integers, or max), so any pairing is exact.
+__device__ __forceinline__ int row16_sum_int(int v) {
+  v += dpp_i<kQuadXor1>(v);
+  v += dpp_i<kQuadXor2>(v);
+  v += dpp_i<kRowRor4>(v);
+  v += dpp_i<kRowRor8>(v);
   return v;
 }
-__device__ __forceinline__ int wave_sum_int(int v) {
-#pragma unroll
-  for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o, 64);
+__device__ __forceinline__ float row16_max(float v) {
+  v = fmaxf(v, dpp_f<kQuadXor1>(v));
+  v = fmaxf(v, dpp_f<kQuadXor2>(v));
+  v = fmaxf(v, dpp_f<kRowRor4>(v));
+  v = fmaxf(v, dpp_f<kRowRor8>(v));
   return v;
+}
+// Whole-wave results, uniform across the wave: row reduction, then the four
+// row results read into scalars.
+__device__ __forceinline__ float wave_max(float v) {
+  v = row16_max(v);
+  const int i = __builtin_bit_cast(int, v);
+  const float r0 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(i, 0));
+  const float r1 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(i, 16));
+  const float r2 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(i, 32));
+  const float r3 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(i, 48));
+  return fmaxf(fmaxf(r0, r1), fmaxf(r2, r3));
+}
+__device__ __forceinline__ int wave_sum_int(int v) {
+  v = row16_sum_int(v);
+  return __builtin_amdgcn_readlane(v, 0) + __builtin_amdgcn_readlane(v, 16) +
+         __builtin_amdgcn_readlane(v, 32) + __builtin_amdgcn_readlane(v, 48);
+}
+// Sum over each 32-lane half of the wave (lanes 0-31 and 32-63), uniform per half.
+__device__ __forceinline__ int half_sum_int(int v) {
+  v = row16_sum_int(v);
+  const int lo = __builtin_amdgcn_readlane(v, 0) + __builtin_amdgcn_readlane(v, 16);
+  const int hi = __builtin_amdgcn_readlane(v, 32) + __builtin_amdgcn_readlane(v, 48);
+  return (threadIdx.x & 32) ? hi : lo;
 }
 
 }  // namespace ifrd

@@ -90,12 +90,26 @@ hipError_t launch_quant_plain(const float* xf, const uint16_t* xh, int M, int K,
                               float* qscale, float* gsum, hipStream_t st);
 
 // ---- q/k norm + RoPE + KV append --------------------------------------------
+// KV pages: one 32-token x 128-dim block per (page, kv_head), stored in the
+// order the attention MFMAs consume it, so each wave load is one contiguous
+// run of 64 lanes x 8 elements:
+//   K: fragment (h = t % 2, i = d / 32), lane 16 * ((d / 8) % 4) + t / 2,
+//      element d % 8   (S^T = K Q^T: A-operand rows are tokens 2c + h)
+//   V: fragment (d / 16), lane 16 * (t / 8) + d % 16, element t % 8
+//      (O^T = V^T P^T: A-operand rows are dims, k runs over tokens)
+// Index of token t, dim d inside its block of 32 * 128 elements:
+__host__ __device__ inline int kv_koff(int t, int d) {
+  return ((((t & 1) * 4 + (d >> 5)) * 64 + ((d >> 3) & 3) * 16 + (t >> 1)) << 3) + (d & 7);
+}
+__host__ __device__ inline int kv_voff(int t, int d) {
+  return (((d >> 4) * 64 + (t >> 3) * 16 + (d & 15)) << 3) + (t & 7);
+}
 struct KVLayout {
-  int nkv, hd, page;          // page = tokens per page (32)
+  int nkv, hd, page;          // page = tokens per page (32); hd = 128
   int max_pages;              // block-table row length
   int kv_int8;
-  void* kpool;                // this layer: [pages][nkv][page][hd]   (fp16 or int8)
-  void* vpool;                // this layer: [pages][nkv][hd][page]   (transposed)
+  void* kpool;                // this layer: [pages][nkv][32 * 128] (fp16 or int8), kv_koff order
+  void* vpool;                // this layer: [pages][nkv][32 * 128], kv_voff order
   uint16_t* kscale;           // int8: [pages][nkv][page] fp16
   uint16_t* vscale;
   const int32_t* block_table; // [max_seqs][max_pages]

@@ -158,9 +158,10 @@ __global__ __launch_bounds__(256) void row_quant_kernel(RowQuantArgs a) {
 // thread, half 4-128 across lanes of a wave (partner lane ^ half/4), half
 // 256-512 through one LDS exchange.  Every output is formed by the same adds
 // on the same operands as the sequential loop, so the result is bit-identical.
-__device__ __forceinline__ float bfly_lane(float x, int m, bool upper) {
-  const float o = __shfl_xor(x, m, 64);
-  return upper ? (o - x) : (x + o);
+template <int M>
+__device__ __forceinline__ float bfly_lane(float x) {
+  const float o = ifrd::lane_xor<M>(x);
+  return (threadIdx.x & M) ? (o - x) : (x + o);
 }
 
 __device__ void fwht1024(float (&v)[4], float* xs) {
@@ -169,13 +170,18 @@ __device__ void fwht1024(float (&v)[4], float* xs) {
   a = v[2]; b = v[3]; v[2] = a + b; v[3] = a - b;
   a = v[0]; b = v[2]; v[0] = a + b; v[2] = a - b;
   a = v[1]; b = v[3]; v[1] = a + b; v[3] = a - b;
-  const int lane = threadIdx.x & 63;
 #pragma unroll
-  for (int m = 1; m <= 32; m <<= 1) {
-    const bool up = (lane & m) != 0;
+  for (int e = 0; e < 4; ++e) v[e] = bfly_lane<1>(v[e]);
 #pragma unroll
-    for (int e = 0; e < 4; ++e) v[e] = bfly_lane(v[e], m, up);
-  }
+  for (int e = 0; e < 4; ++e) v[e] = bfly_lane<2>(v[e]);
+#pragma unroll
+  for (int e = 0; e < 4; ++e) v[e] = bfly_lane<4>(v[e]);
+#pragma unroll
+  for (int e = 0; e < 4; ++e) v[e] = bfly_lane<8>(v[e]);
+#pragma unroll
+  for (int e = 0; e < 4; ++e) v[e] = bfly_lane<16>(v[e]);
+#pragma unroll
+  for (int e = 0; e < 4; ++e) v[e] = bfly_lane<32>(v[e]);
   __syncthreads();
 #pragma unroll
   for (int e = 0; e < 4; ++e) xs[4 * threadIdx.x + e] = v[e];
@@ -268,9 +274,7 @@ __global__ __launch_bounds__(256) void row_quant1024_kernel(RowQuantArgs a) {
       c[e] = a.round == 0 ? ifrd::quant_half_away(v[e], inv) : ifrd::quant_rne(v[e], inv);
   } else {  // 64-wide slices = 16 lanes
     float mx = fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3])));
-#pragma unroll
-    for (int o = 1; o < 16; o <<= 1) mx = fmaxf(mx, __shfl_xor(mx, o, 64));
-    mx = fmaxf(1e-6f, mx);
+    mx = fmaxf(1e-6f, ifrd::row16_max(mx));
     const float s = mx / 127.0f;
     const float inv = 1.0f / s;
     if ((lane & 15) == 0) a.qscale[(size_t)m * 16 + (t >> 4)] = s;
@@ -282,9 +286,7 @@ __global__ __launch_bounds__(256) void row_quant1024_kernel(RowQuantArgs a) {
                           ((uint32_t)(c[2] & 0xFF) << 16) | ((uint32_t)(c[3] & 0xFF) << 24);
   *reinterpret_cast<uint32_t*>(a.q + atile_off(m, 4 * t, 1024)) = packed;
   if (a.gsum) {  // 128-wide groups = 32 lanes (integer sums: order-free)
-    int S = c[0] + c[1] + c[2] + c[3];
-#pragma unroll
-    for (int o = 1; o < 32; o <<= 1) S += __shfl_xor(S, o, 64);
+    const int S = ifrd::half_sum_int(c[0] + c[1] + c[2] + c[3]);
     if ((lane & 31) == 0) a.gsum[(size_t)m * 8 + (t >> 5)] = (float)S;
   }
 }
@@ -320,9 +322,7 @@ __global__ __launch_bounds__(256) void quant_plain_fast(const float* xf, const u
     q[atile_off(m, e * 256 + t, K)] = (int8_t)c;
     // element e*256 + t lies in group (e*256 + t) / 128 = 2e + (t >= 128); a wave of
     // 64 lanes stays in one group: reduce in the wave, one LDS add per wave.
-    int S = c;
-#pragma unroll
-    for (int o = 1; o < 64; o <<= 1) S += __shfl_xor(S, o, 64);
+    const int S = ifrd::wave_sum_int(c);
     if (lane == 0) atomicAdd(&gl[2 * e + (t >> 7)], S);
   }
   __syncthreads();
@@ -421,13 +421,14 @@ __global__ __launch_bounds__(256) void qk_rope_kv_kernel(QKArgs a, KVLayout kv) 
   const int tok = pos % kv.page;
   const size_t base = ((size_t)page * nkv + hh);
   if (!kv.kv_int8) {
-    if (kind == 1) {
-      uint16_t* kp = reinterpret_cast<uint16_t*>(kv.kpool) + (base * kv.page + tok) * hd;
-      *reinterpret_cast<uint32_t*>(kp + 2 * lane) = (uint32_t)ifrd::f2h(v0) | ((uint32_t)ifrd::f2h(v1) << 16);
+    if (kind == 1) {  // dims 2l, 2l + 1 are adjacent elements of one K fragment lane
+      uint16_t* kp = reinterpret_cast<uint16_t*>(kv.kpool) + base * kv.page * hd;
+      *reinterpret_cast<uint32_t*>(kp + kv_koff(tok, 2 * lane)) =
+          (uint32_t)ifrd::f2h(v0) | ((uint32_t)ifrd::f2h(v1) << 16);
     } else {
       uint16_t* vp = reinterpret_cast<uint16_t*>(kv.vpool) + base * hd * kv.page;
-      vp[(size_t)(2 * lane) * kv.page + tok] = ifrd::f2h(v0);
-      vp[(size_t)(2 * lane + 1) * kv.page + tok] = ifrd::f2h(v1);
+      vp[kv_voff(tok, 2 * lane)] = ifrd::f2h(v0);
+      vp[kv_voff(tok, 2 * lane + 1)] = ifrd::f2h(v1);
     }
   } else {
     const float mx = ifrd::wave_max(fmaxf(fabsf(v0), fabsf(v1)));
@@ -440,14 +441,14 @@ __global__ __launch_bounds__(256) void qk_rope_kv_kernel(QKArgs a, KVLayout kv) 
     q0 = min(127, max(-127, q0));
     q1 = min(127, max(-127, q1));
     if (kind == 1) {
-      int8_t* kp = reinterpret_cast<int8_t*>(kv.kpool) + (base * kv.page + tok) * hd;
-      kp[2 * lane] = (int8_t)q0;
-      kp[2 * lane + 1] = (int8_t)q1;
+      int8_t* kp = reinterpret_cast<int8_t*>(kv.kpool) + base * kv.page * hd;
+      kp[kv_koff(tok, 2 * lane)] = (int8_t)q0;
+      kp[kv_koff(tok, 2 * lane + 1)] = (int8_t)q1;
       if (lane == 0) kv.kscale[base * kv.page + tok] = sh16;
     } else {
       int8_t* vp = reinterpret_cast<int8_t*>(kv.vpool) + base * hd * kv.page;
-      vp[(size_t)(2 * lane) * kv.page + tok] = (int8_t)q0;
-      vp[(size_t)(2 * lane + 1) * kv.page + tok] = (int8_t)q1;
+      vp[kv_voff(tok, 2 * lane)] = (int8_t)q0;
+      vp[kv_voff(tok, 2 * lane + 1)] = (int8_t)q1;
       if (lane == 0) kv.vscale[base * kv.page + tok] = sh16;
     }
   }
