@@ -128,7 +128,7 @@ KERNELS = GEMMS + ["attention", "row_quant", "qk_rope_kv", "combine", "quant_pla
 # qgemm_splitk<...> for M <= 64, qgemm_rows<...> above)
 ROCPROF_NAMES = {"attention": "attn_kernel<{kv}>",
                  "combine": "combine_kernel", "row_quant": "row_quant1024_kernel",
-                 "quant_plain": "quant_plain_fast<12>", "qk_rope_kv": "qk_rope_kv_kernel",
+                 "quant_plain": "quant_plain8<384>", "qk_rope_kv": "qk_rope_kv_kernel",
                  "lmhead": "lmhead_kernel<...> + argmax_final_kernel", "pack": "pack_kernel"}
 PEAK_FLOPS = {"qgemm": INT8_PEAK, "attention": FP16_PEAK, "lmhead": INT8_PEAK, **{g: INT8_PEAK for g in GEMMS}}
 

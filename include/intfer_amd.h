@@ -280,6 +280,10 @@ int ifr_get_timing(ifr_ctx* ctx, const char* kernel, double* total_ms, int64_t* 
 int ifr_debug_pack(ifr_ctx* ctx, int32_t M, int32_t* cu_seqlens, int32_t* row_grp,
                    int32_t* comb_base, int32_t* comb_nsplit, int32_t* comb_tok, int32_t* units,
                    int32_t* n_units, int32_t* split);
+/* Test hook (no reference counterpart): the last forward's attention
+ * dispatch order (slot -> unit index, -1 idle; 4 slots per workgroup) into
+ * order[0..cap); *n_slots receives its length. */
+int ifr_debug_attn_order(ifr_ctx* ctx, int32_t* order, int32_t cap, int32_t* n_slots);
 
 /* ------------------------------------------------------------------------
  * Scheduler / serve (C++ host side above the ABI).

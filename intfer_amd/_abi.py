@@ -112,6 +112,7 @@ _PROTOS = {
     "ifr_get_timing": (C.c_int, [P, C.c_char_p, C.POINTER(C.c_double), C.POINTER(i64),
                                  C.POINTER(C.c_double), C.POINTER(C.c_double)]),
     "ifr_debug_pack": (C.c_int, [P, i32, P, P, P, P, P, P, pi32, pi32]),
+    "ifr_debug_attn_order": (C.c_int, [P, P, i32, pi32]),
     "ifr_sched_create": (C.c_int, [P, C.POINTER(SchedCfg), C.POINTER(P)]),
     "ifr_sched_create_backend": (C.c_int, [C.POINTER(SchedBackend), C.POINTER(SchedCfg),
                                            C.POINTER(P)]),

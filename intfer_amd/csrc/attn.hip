@@ -24,38 +24,68 @@ namespace {
 constexpr int kHD = 128;
 constexpr int kPage = 32;
 
-template <bool KV8>
+template <bool KV8, int NT>
 __global__ __launch_bounds__(256) void attn_kernel(AttnArgs p, KVLayout kv) {
   const int lane = threadIdx.x & 63;
   // wave-uniform unit index: the unit record and block-table entries become
   // scalar loads, which do not queue behind the vector K/V loads
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int u = blockIdx.x * 4 + w;
-  if (u >= p.n_units) return;
-  const AttnUnit un = p.units[u];
+  const int slot = blockIdx.x * 4 + w;
+  // Workgroups of the chunked region serve 4 q-blocks of one sequence with the
+  // same kv head and split: they stream each K/V page once into LDS and all 4
+  // waves read it there.  Other workgroups run 4 independent units.
+  const bool shared = blockIdx.x * 4 < p.n_shared;  // workgroup-uniform
+  if (!shared && slot >= p.n_slots) return;         // (no barrier on this path)
+  const int u = p.order[slot];
+  if (!shared && u < 0) return;
+  // In a shared workgroup an idle wave (u < 0) still loads and synchronizes;
+  // it borrows the unit of the chunk's last q-block (always present), whose
+  // KV range covers the others'.
+  int u_pg = u;
+  if (shared) {
+#pragma unroll
+    for (int q = 3; q >= 0; --q) {
+      const int uq = p.order[blockIdx.x * 4 + q];
+      if (uq >= 0) { u_pg = uq; break; }
+    }
+  }
+  const bool active = u >= 0;
+  const AttnUnit un = p.units[active ? u : u_pg];
+  const AttnUnit upg = p.units[u_pg];
   const int G = p.nq / kv.nkv;
-  const int rows = un.qn * G;
+  const int rows = un.qn * G;  // valid columns of the unit's NT x 16 column tiles
   const int c = lane & 15, g = lane >> 4;
-  const bool colv = c < rows;
-  const int qtok = c / G, qj = c % G;
-  const int qpos = un.qpos0 + qtok;
-
-  // Q^T as the B operand: MFMA i covers dims 32i + 8g .. +8 for column c.
-  v8h qf[4];
-  if (colv) {
-    const _Float16* qp = reinterpret_cast<const _Float16*>(p.q) +
-                         ((size_t)(un.row0 + qtok) * p.nq + un.kvh * G + qj) * kHD + 8 * g;
+  bool colv[NT];
+  int qpos[NT];
+  // Q^T as the B operand: column tile t, MFMA i covers dims 32i + 8g .. +8 of
+  // column 16t + c = (q token, head of the GQA group).
+  v8h qf[NT][4];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) qf[i] = *reinterpret_cast<const v8h*>(qp + 32 * i);
-  } else {
+  for (int t = 0; t < NT; ++t) {
+    const int col = 16 * t + c;
+    colv[t] = active && col < rows;
+    const int qtok = col / G, qj = col % G;
+    qpos[t] = un.qpos0 + qtok;
+    if (colv[t]) {
+      const _Float16* qp = reinterpret_cast<const _Float16*>(p.q) +
+                           ((size_t)(un.row0 + qtok) * p.nq + un.kvh * G + qj) * kHD + 8 * g;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) qf[i] = (v8h){0, 0, 0, 0, 0, 0, 0, 0};
+      for (int i = 0; i < 4; ++i) qf[t][i] = *reinterpret_cast<const v8h*>(qp + 32 * i);
+    } else {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) qf[t][i] = (v8h){0, 0, 0, 0, 0, 0, 0, 0};
+    }
   }
 
-  float m_run = -INFINITY, l_run = 0.0f;
-  v4f o[8];
+  float m_run[NT], l_run[NT];
+  v4f o[NT][8];
 #pragma unroll
-  for (int d = 0; d < 8; ++d) o[d] = (v4f){0.f, 0.f, 0.f, 0.f};
+  for (int t = 0; t < NT; ++t) {
+    m_run[t] = -INFINITY;
+    l_run[t] = 0.0f;
+#pragma unroll
+    for (int d = 0; d < 8; ++d) o[t][d] = (v4f){0.f, 0.f, 0.f, 0.f};
+  }
 
   const int32_t* bt = kv.block_table + (size_t)un.seq * kv.max_pages;
   // One page = 32 tokens.  Raw K/V fragments of a page (fp16, or int8 with
@@ -68,7 +98,8 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs p, KVLayout kv) {
     uint32_t v[8][KV8 ? 2 : 4];     // V^T tile d: 8 tokens of dim 16d + c
     uint16_t ks[2][4], vs[8];
   };
-  const int last = (un.kv_hi - 1 - un.kv_lo) / kPage;  // pages are [kv_lo + 32 i, +32)
+  // pages are [kv_lo + 32 i, +32); a shared workgroup walks its widest range
+  const int last = ((shared ? upg.kv_hi : un.kv_hi) - 1 - un.kv_lo) / kPage;
   auto load = [&](PageBuf& b, int i) {
     const int t0 = un.kv_lo + kPage * min(i, last);
     const size_t pb = (size_t)bt[t0 / kPage] * kv.nkv + un.kvh;
@@ -115,79 +146,144 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs p, KVLayout kv) {
   };
   auto step = [&](const PageBuf& b, int i) {
     const int t0 = un.kv_lo + kPage * i;
-    // ---- S^T: tile h covers tokens 2c' + h; lane (c, g) reg r -> token 8g + 2r + h.
-    v4f s[2];
+    // ---- S^T: K tile h covers tokens 2c' + h; lane (c, g) reg r -> token 8g + 2r + h.
+    v8h kf[2][4];
 #pragma unroll
-    for (int h = 0; h < 2; ++h) {
-      s[h] = (v4f){0.f, 0.f, 0.f, 0.f};
+    for (int h = 0; h < 2; ++h)
 #pragma unroll
-      for (int i4 = 0; i4 < 4; ++i4)
-        s[h] = __builtin_amdgcn_mfma_f32_16x16x32_f16(frag(b.k[h][i4]), qf[i4], s[h], 0, 0, 0);
-    }
-    float sv[8];
-    float mt = -INFINITY;
+      for (int i4 = 0; i4 < 4; ++i4) kf[h][i4] = frag(b.k[h][i4]);
+    v8h phi[NT], plo[NT];
+    float alpha[NT];
 #pragma unroll
-    for (int r = 0; r < 4; ++r)
+    for (int t = 0; t < NT; ++t) {
+      v4f s[2];
 #pragma unroll
       for (int h = 0; h < 2; ++h) {
-        const int t = t0 + 8 * g + 2 * r + h;
-        float v = s[h][r];
-        if constexpr (KV8) v *= ifrd::h2f(b.ks[h][r]);
-        v *= p.scale_log2;
-        if (!colv || t > qpos || t >= un.kv_hi) v = -INFINITY;
-        sv[2 * r + h] = v;
-        mt = fmaxf(mt, v);
-      }
-    mt = fmaxf(mt, __shfl_xor(mt, 16, 64));
-    mt = fmaxf(mt, __shfl_xor(mt, 32, 64));
-    const float m_new = fmaxf(m_run, mt);
-    const float m_use = (m_new == -INFINITY) ? 0.0f : m_new;
-    const float alpha = exp2f(m_run - m_use);
-    // P enters the PV product as an fp16 hi + lo pair (p ~ hi + lo to ~22
-    // bits): V is exact in fp16, so O carries fp32-level accuracy and the
-    // downstream per-token int8 codes match the fp32 reference loop.
-    v8h phi, plo;
-    float rs = 0.0f;
+        s[h] = (v4f){0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      const float pf = exp2f(sv[j] - m_use);
-      rs += pf;
-      const float pv = KV8 ? pf * ifrd::h2f(b.vs[j]) : pf;
-      const _Float16 h = (_Float16)pv;
-      phi[j] = h;
-      plo[j] = (_Float16)(pv - (float)h);
+        for (int i4 = 0; i4 < 4; ++i4)
+          s[h] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf[h][i4], qf[t][i4], s[h], 0, 0, 0);
+      }
+      float sv[8];
+      float mt = -INFINITY;
+#pragma unroll
+      for (int r = 0; r < 4; ++r)
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+          const int tk = t0 + 8 * g + 2 * r + h;
+          float v = s[h][r];
+          if constexpr (KV8) v *= ifrd::h2f(b.ks[h][r]);
+          v *= p.scale_log2;
+          if (!colv[t] || tk > qpos[t] || tk >= un.kv_hi) v = -INFINITY;
+          sv[2 * r + h] = v;
+          mt = fmaxf(mt, v);
+        }
+      mt = fmaxf(mt, __shfl_xor(mt, 16, 64));
+      mt = fmaxf(mt, __shfl_xor(mt, 32, 64));
+      const float m_new = fmaxf(m_run[t], mt);
+      const float m_use = (m_new == -INFINITY) ? 0.0f : m_new;
+      alpha[t] = exp2f(m_run[t] - m_use);
+      // P enters the PV product as an fp16 hi + lo pair (p ~ hi + lo to ~22
+      // bits): V is exact in fp16, so O carries fp32-level accuracy and the
+      // downstream per-token int8 codes match the fp32 reference loop.
+      float rs = 0.0f;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const float pf = exp2f(sv[j] - m_use);
+        rs += pf;
+        const float pv = KV8 ? pf * ifrd::h2f(b.vs[j]) : pf;
+        const _Float16 hh = (_Float16)pv;
+        phi[t][j] = hh;
+        plo[t][j] = (_Float16)(pv - (float)hh);
+      }
+      rs += __shfl_xor(rs, 16, 64);
+      rs += __shfl_xor(rs, 32, 64);
+      l_run[t] = l_run[t] * alpha[t] + rs;
+      m_run[t] = m_new;
     }
-    rs += __shfl_xor(rs, 16, 64);
-    rs += __shfl_xor(rs, 32, 64);
-    l_run = l_run * alpha + rs;
-    m_run = m_new;
 #pragma unroll
     for (int d = 0; d < 8; ++d) {
-      o[d] *= alpha;
       const v8h vf = frag(b.v[d]);
-      o[d] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vf, phi, o[d], 0, 0, 0);
-      o[d] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vf, plo, o[d], 0, 0, 0);
+#pragma unroll
+      for (int t = 0; t < NT; ++t) {
+        o[t][d] *= alpha[t];
+        o[t][d] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vf, phi[t], o[t][d], 0, 0, 0);
+        o[t][d] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vf, plo[t], o[t][d], 0, 0, 0);
+      }
     }
   };
-  PageBuf bA, bB;
-  load(bA, 0);
-  for (int i = 0;; i += 2) {
-    load(bB, i + 1);
-    step(bA, i);
-    if (i + 1 > last) break;
-    load(bA, i + 2);
-    step(bB, i + 1);
-    if (i + 2 > last) break;
+  if (shared) {
+    // fp16 pages only (the host sets n_shared = 0 for int8 KV).  LDS holds two
+    // pages of 16 fragments (8 K, 8 V) x 64 lanes x 16 bytes; wave w stages
+    // fragments 4w..4w+3.  One barrier per page: page i is stored into buffer
+    // i & 1, and every wave has finished page i - 1 (the other buffer's
+    // previous content) before anyone passes the barrier of page i.
+    __shared__ uint4 kvs[2][16][64];
+    // waves 0-1 stage K fragments 4w..4w+3 (h * 4 + i), waves 2-3 V fragments (d)
+    const uint8_t* kvbase = reinterpret_cast<const uint8_t*>(w < 2 ? kv.kpool : kv.vpool);
+    const int f0 = w < 2 ? 4 * w : 4 * w - 8;
+    auto src_of = [&](int i) {
+      const int t0 = un.kv_lo + kPage * min(i, last);
+      const size_t pb = (size_t)bt[t0 / kPage] * kv.nkv + un.kvh;
+      return reinterpret_cast<const uint4*>(kvbase) + pb * (kPage * kHD / 8) + (size_t)f0 * 64 + lane;
+    };
+    const uint4* sp = src_of(0);
+    uint4 s0 = sp[0], s1 = sp[64], s2 = sp[128], s3 = sp[192];
+    for (int i = 0;; ++i) {
+      uint4* dst = &kvs[i & 1][4 * w][lane];
+      dst[0] = s0;
+      dst[64] = s1;
+      dst[128] = s2;
+      dst[192] = s3;
+      sp = src_of(i + 1);
+      s0 = sp[0];
+      s1 = sp[64];
+      s2 = sp[128];
+      s3 = sp[192];
+      __syncthreads();
+      if (active) {
+        PageBuf b;
+#pragma unroll
+        for (int h = 0; h < 2; ++h)
+#pragma unroll
+          for (int i4 = 0; i4 < 4; ++i4) {
+            const uint4 x = kvs[i & 1][h * 4 + i4][lane];
+            b.k[h][i4][0] = x.x; b.k[h][i4][1] = x.y; b.k[h][i4][2] = x.z; b.k[h][i4][3] = x.w;
+          }
+#pragma unroll
+        for (int d = 0; d < 8; ++d) {
+          const uint4 x = kvs[i & 1][8 + d][lane];
+          b.v[d][0] = x.x; b.v[d][1] = x.y; b.v[d][2] = x.z; b.v[d][3] = x.w;
+        }
+        step(b, i);
+      }
+      if (i >= last) break;
+    }
+  } else {
+    PageBuf bA, bB;
+    load(bA, 0);
+    for (int i = 0;; i += 2) {
+      load(bB, i + 1);
+      step(bA, i);
+      if (i + 1 > last) break;
+      load(bA, i + 2);
+      step(bB, i + 1);
+      if (i + 2 > last) break;
+    }
   }
-  // ---- partials: O^T lane (c, g) reg r -> dim 16d + 4g + r of column c.
-  if (colv) {
-    float* po = p.part_o + ((size_t)u * 16 + c) * kHD;
+  if (!active) return;
+  // ---- partials: O^T lane (c, g) reg r -> dim 16d + 4g + r of column 16t + c.
+#pragma unroll
+  for (int t = 0; t < NT; ++t) {
+    if (!colv[t]) continue;
+    const size_t pc = (size_t)u * 16 * NT + 16 * t + c;
+    float* po = p.part_o + pc * kHD;
 #pragma unroll
     for (int d = 0; d < 8; ++d)
-      *reinterpret_cast<v4f*>(po + 16 * d + 4 * g) = o[d];
+      *reinterpret_cast<v4f*>(po + 16 * d + 4 * g) = o[t][d];
     if (g == 0) {
-      p.part_ml[((size_t)u * 16 + c) * 2 + 0] = m_run;
-      p.part_ml[((size_t)u * 16 + c) * 2 + 1] = l_run;
+      p.part_ml[pc * 2 + 0] = m_run[t];
+      p.part_ml[pc * 2 + 1] = l_run[t];
     }
   }
 }
@@ -207,18 +303,54 @@ __global__ __launch_bounds__(256) void combine_kernel(CombineArgs a) {
   const int base = a.comb_base[m] + kvh * ns;
   const int col = a.comb_tok[m] * G + j;
   float mx = -INFINITY;
-  for (int s = 0; s < ns; ++s) mx = fmaxf(mx, a.part_ml[((size_t)(base + s) * 16 + col) * 2]);
   float L = 0.0f;
   float acc[16];
   for (int i = 0; i < per; ++i) acc[i] = 0.0f;
-  for (int s = 0; s < ns; ++s) {
-    const size_t pi = (size_t)(base + s) * 16 + col;
-    const float ms = a.part_ml[pi * 2];
-    if (ms == -INFINITY) continue;
-    const float f = exp2f(ms - mx);
-    L += f * a.part_ml[pi * 2 + 1];
-    const float* po = a.part_o + pi * a.hd + d0;
-    for (int i = 0; i < per; ++i) acc[i] += f * po[i];
+  if (per == 8) {
+    // Splits in rounds of 4 with clamped (unconditional) loads, so each round
+    // is one memory latency: (m, l) of the splits first, then the partial O
+    // rows as two 16-byte loads per split, merged in split order.
+    const float2* ml2 = reinterpret_cast<const float2*>(a.part_ml);
+    for (int s0 = 0; s0 < ns; s0 += 4) {
+      float mm[4];
+#pragma unroll
+      for (int q = 0; q < 4; ++q) mm[q] = ml2[(size_t)(base + min(s0 + q, ns - 1)) * a.ucols + col].x;
+#pragma unroll
+      for (int q = 0; q < 4; ++q) mx = fmaxf(mx, mm[q]);
+    }
+    for (int s0 = 0; s0 < ns; s0 += 4) {
+      float2 mlv[4];
+      float4 ov[4][2];
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const size_t pi = (size_t)(base + min(s0 + q, ns - 1)) * a.ucols + col;
+        mlv[q] = ml2[pi];
+        const float4* po = reinterpret_cast<const float4*>(a.part_o + pi * a.hd + d0);
+        ov[q][0] = po[0];
+        ov[q][1] = po[1];
+      }
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        if (s0 + q >= ns || mlv[q].x == -INFINITY) continue;
+        const float f = exp2f(mlv[q].x - mx);
+        L += f * mlv[q].y;
+        acc[0] += f * ov[q][0].x; acc[1] += f * ov[q][0].y;
+        acc[2] += f * ov[q][0].z; acc[3] += f * ov[q][0].w;
+        acc[4] += f * ov[q][1].x; acc[5] += f * ov[q][1].y;
+        acc[6] += f * ov[q][1].z; acc[7] += f * ov[q][1].w;
+      }
+    }
+  } else {
+    for (int s = 0; s < ns; ++s) mx = fmaxf(mx, a.part_ml[((size_t)(base + s) * a.ucols + col) * 2]);
+    for (int s = 0; s < ns; ++s) {
+      const size_t pi = (size_t)(base + s) * a.ucols + col;
+      const float ms = a.part_ml[pi * 2];
+      if (ms == -INFINITY) continue;
+      const float f = exp2f(ms - mx);
+      L += f * a.part_ml[pi * 2 + 1];
+      const float* po = a.part_o + pi * a.hd + d0;
+      for (int i = 0; i < per; ++i) acc[i] += f * po[i];
+    }
   }
   const float invL = 1.0f / L;
   float* x = sh;
@@ -239,16 +371,25 @@ __global__ __launch_bounds__(256) void combine_kernel(CombineArgs a) {
   const float inv = 1.0f / sc;
   if (threadIdx.x == 0) a.qscale[m] = sc;
   int csum = 0;
+  if (per == 8) {
+    // 8 consecutive columns = half of one 16-byte A-tile lane chunk: one store
+    uint32_t w[2] = {0u, 0u};
+    for (int i = 0; i < 8; ++i) {
+      const int c = ifrd::quant_half_away(acc[i] * invL, inv);
+      w[i >> 2] |= (uint32_t)(c & 0xFF) << (8 * (i & 3));
+      csum += c;
+    }
+    *reinterpret_cast<uint2*>(a.q + atile_off(m, e0, N)) = make_uint2(w[0], w[1]);
+    // the 128 columns of group e0 / 128 are the 16 lanes of one DPP row
+    csum = ifrd::row16_sum_int(csum);
+    if ((threadIdx.x & 15) == 0) a.gsum[(size_t)m * (N / 128) + e0 / 128] = (float)csum;
+    return;
+  }
   for (int i = 0; i < per; ++i) {
     const int c = ifrd::quant_half_away(x[e0 + i], inv);
     a.q[atile_off(m, e0 + i, N)] = (int8_t)c;
     codes[e0 + i] = c;
     csum += c;
-  }
-  if (per == 8) {  // the 128 columns of group e0 / 128 are the 16 lanes of one DPP row
-    csum = ifrd::row16_sum_int(csum);
-    if ((threadIdx.x & 15) == 0) a.gsum[(size_t)m * (N / 128) + e0 / 128] = (float)csum;
-    return;
   }
   __syncthreads();
   for (int gg = threadIdx.x; gg < N / 128; gg += 256) {
@@ -263,11 +404,19 @@ __global__ __launch_bounds__(256) void combine_kernel(CombineArgs a) {
 hipError_t launch_attention(const AttnArgs& a, const KVLayout& kv, hipStream_t st) {
   if (a.n_units <= 0) return hipSuccess;
   if (kv.hd != kHD || kv.page != kPage || a.nq % kv.nkv != 0 || (a.nq / kv.nkv) > 16 ||
-      !a.units || !a.q || !a.part_o || !a.part_ml)
+      !a.units || !a.order || a.n_slots < a.n_units || !a.q || !a.part_o || !a.part_ml ||
+      a.n_shared < 0 || a.n_shared % 4 != 0 || a.n_shared > a.n_slots || (kv.kv_int8 && a.n_shared))
     return hipErrorInvalidValue;
-  const dim3 grid((a.n_units + 3) / 4), block(256);
-  if (kv.kv_int8) hipLaunchKernelGGL(attn_kernel<true>, grid, block, 0, st, a, kv);
-  else hipLaunchKernelGGL(attn_kernel<false>, grid, block, 0, st, a, kv);
+  const dim3 grid((a.n_slots + 3) / 4), block(256);
+  if (a.col_tiles == 1) {
+    if (kv.kv_int8) hipLaunchKernelGGL((attn_kernel<true, 1>), grid, block, 0, st, a, kv);
+    else hipLaunchKernelGGL((attn_kernel<false, 1>), grid, block, 0, st, a, kv);
+  } else if (a.col_tiles == 2) {
+    if (kv.kv_int8) hipLaunchKernelGGL((attn_kernel<true, 2>), grid, block, 0, st, a, kv);
+    else hipLaunchKernelGGL((attn_kernel<false, 2>), grid, block, 0, st, a, kv);
+  } else {
+    return hipErrorInvalidValue;
+  }
   return hipGetLastError();
 }
 

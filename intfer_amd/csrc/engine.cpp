@@ -46,6 +46,7 @@ int fail(int code, const char* fmt, ...) {
 constexpr int kPage = 32;
 
 constexpr int kSplit = 256;  // KV tokens per attention unit
+constexpr int kAttnTiles = 1;  // 16-column MFMA tiles per attention unit (q-block = 16 / G tokens)
 
 struct Layer {
   DLin qkv[3];     // fused QKV in qkv[0] when all widths match (nqkv = 1)
@@ -103,7 +104,7 @@ struct ifr_ctx {
   std::vector<int> free_pages;
   std::vector<Seq> seqs;
   // workspaces
-  int maxM = 0, max_units = 0;
+  int maxM = 0, max_units = 0, last_slots = 0;
   int32_t* rows_d = nullptr;
   int32_t* rows_h = nullptr;  // pinned
   float* resid = nullptr;
@@ -516,7 +517,7 @@ int ifr_model_load(ifr_ctx* c, const ifr_host_model* m, const ifr_kv_cfg* kvc) {
   release_model(c);
   c->cfg = cf;
   c->kv = *kvc;
-  c->qb = std::min(8, 16 / (cf.n_heads / cf.n_kv));
+  c->qb = 16 * kAttnTiles / (cf.n_heads / cf.n_kv);
   const int H = cf.hidden, L = cf.layers, hd = cf.head_dim, nq = cf.n_heads, nkv = cf.n_kv;
   const int qN = nq * hd, kvN = nkv * hd, F = cf.inter, V = cf.vocab;
   c->layers.resize(L);
@@ -656,9 +657,9 @@ int ifr_model_load(ifr_ctx* c, const ifr_host_model* m, const ifr_kv_cfg* kvc) {
   if ((r = walloc(c, &c->lm_pv, (size_t)nparts * Mx)) || (r = walloc(c, &c->lm_pi, (size_t)nparts * Mx)))
     return r;
   c->max_units = 32768;
-  if ((r = walloc(c, &c->pk.units, c->max_units)) ||
-      (r = walloc(c, &c->part_o, (size_t)c->max_units * 16 * hd)) ||
-      (r = walloc(c, &c->part_ml, (size_t)c->max_units * 16 * 2)))
+  if ((r = walloc(c, &c->pk.units, c->max_units)) || (r = walloc(c, &c->pk.order, 4 * (size_t)c->max_units)) ||
+      (r = walloc(c, &c->part_o, (size_t)c->max_units * 16 * kAttnTiles * hd)) ||
+      (r = walloc(c, &c->part_ml, (size_t)c->max_units * 16 * kAttnTiles * 2)))
     return r;
   HIPCHK(hipStreamSynchronize(c->st));
   c->loaded = true;
@@ -864,6 +865,10 @@ int ifr_forward(ifr_ctx* c, const ifr_row* rows, int32_t M, int32_t* best_out, f
   }
   c->last_split = split;
   c->last_units = (int)nunits;
+  long nchunked = 0;
+  const int nslots = (int)ifrk::attn_slot_count(g_pos0.data(), g_len.data(), (int)g_len.size(), nkv, split,
+                                                c->qb, &nchunked);
+  c->last_slots = nslots;
   // ---- upload rows, pack
   std::memcpy(c->rows_h, rows, (size_t)M * sizeof(ifr_row));
   HIPCHK(hipMemcpyAsync(c->rows_d, c->rows_h, (size_t)M * sizeof(ifr_row), hipMemcpyHostToDevice, c->st));
@@ -934,14 +939,14 @@ int ifr_forward(ifr_ctx* c, const ifr_row* rows, int32_t M, int32_t* best_out, f
     }
     // (4) attention + combine (emits the O-proj int8 input)
     {
-      ifrk::AttnArgs a{c->pk.units, (int)nunits, c->qbuf, nq, 1.4426950408889634f / std::sqrt((float)hd),
-                       c->part_o, c->part_ml};
+      ifrk::AttnArgs a{c->pk.units, (int)nunits, c->pk.order, nslots, c->kv.kv_int8 ? 0 : (int)nchunked, c->qbuf, nq, 1.4426950408889634f / std::sqrt((float)hd),
+                       c->part_o, c->part_ml, kAttnTiles};
       Scope sc(c, "attention", attn_bytes, attn_flops);
       HIPCHK(ifrk::launch_attention(a, kv, c->st));
     }
     {
       ifrk::CombineArgs a{c->part_o, c->part_ml, c->pk.comb_base, c->pk.comb_nsplit, c->pk.comb_tok,
-                          M, nq, nkv, hd, nullptr, c->aq, c->as, c->gs};
+                          M, nq, nkv, hd, nullptr, c->aq, c->as, c->gs, 16 * kAttnTiles};
       Scope sc(c, "combine", 0);
       HIPCHK(ifrk::launch_combine(a, c->st));
     }
@@ -1089,19 +1094,23 @@ int ifr_attention(ifr_ctx* c, int32_t layer, const ifr_row* rows, int32_t M, con
   }
   c->last_split = split;
   c->last_units = (int)nunits;
+  long nchunked = 0;
+  const int nslots = (int)ifrk::attn_slot_count(g_pos0.data(), g_len.data(), (int)g_len.size(), nkv, split,
+                                                c->qb, &nchunked);
+  c->last_slots = nslots;
   std::memcpy(c->rows_h, rows, (size_t)M * sizeof(ifr_row));
   HIPCHK(hipMemcpyAsync(c->rows_d, c->rows_h, (size_t)M * sizeof(ifr_row), hipMemcpyHostToDevice, c->st));
   HIPCHK(ifrk::launch_pack(c->rows_d, M, nkv, c->qb, split, c->pk, c->st));
   HIPCHK(hipMemcpyAsync(c->qbuf, q_h, (size_t)M * nq * hd * 2, hipMemcpyHostToDevice, c->st));
   ifrk::KVLayout kv{nkv, hd, kPage, c->max_pages, c->kv.kv_int8, c->kpool[layer], c->vpool[layer],
                     c->kscale[layer], c->vscale[layer], c->bt_d};
-  ifrk::AttnArgs a{c->pk.units, (int)nunits, c->qbuf, nq, 1.4426950408889634f / std::sqrt((float)hd),
-                   c->part_o, c->part_ml};
+  ifrk::AttnArgs a{c->pk.units, (int)nunits, c->pk.order, nslots, c->kv.kv_int8 ? 0 : (int)nchunked, c->qbuf, nq, 1.4426950408889634f / std::sqrt((float)hd),
+                   c->part_o, c->part_ml, kAttnTiles};
   HIPCHK(ifrk::launch_attention(a, kv, c->st));
   float* out_d = nullptr;
   HIPCHK(hipMalloc(reinterpret_cast<void**>(&out_d), (size_t)M * nq * hd * sizeof(float)));
   ifrk::CombineArgs cb{c->part_o, c->part_ml, c->pk.comb_base, c->pk.comb_nsplit, c->pk.comb_tok,
-                       M, nq, nkv, hd, out_d, c->aq, c->as, c->gs};
+                       M, nq, nkv, hd, out_d, c->aq, c->as, c->gs, 16 * kAttnTiles};
   hipError_t e = ifrk::launch_combine(cb, c->st);
   if (e == hipSuccess) e = hipMemcpyAsync(out_h, out_d, (size_t)M * nq * hd * sizeof(float), hipMemcpyDeviceToHost, c->st);
   if (e == hipSuccess) e = hipStreamSynchronize(c->st);
@@ -1132,6 +1141,15 @@ int ifr_get_timing(ifr_ctx* c, const char* kernel, double* total_ms, int64_t* la
   if (launches) *launches = 0;
   if (bytes) *bytes = 0;
   if (flops) *flops = 0;
+  return IFR_OK;
+}
+
+int ifr_debug_attn_order(ifr_ctx* c, int32_t* order, int32_t cap, int32_t* n_slots) {
+  if (!c || !n_slots) return fail(IFR_EINVAL, "null arg");
+  HIPCHK(hipStreamSynchronize(c->st));
+  *n_slots = c->last_slots;
+  if (order && cap > 0)
+    HIPCHK(hipMemcpy(order, c->pk.order, (size_t)std::min(cap, c->last_slots) * 4, hipMemcpyDeviceToHost));
   return IFR_OK;
 }
 

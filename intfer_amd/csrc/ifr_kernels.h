@@ -145,7 +145,17 @@ struct PackOut {
   int32_t* comb_tok;     // [M] token index inside its q-block
   AttnUnit* units;       // [n_units]
   int32_t* want_rows;    // [n_want] rows to score, in row order
+  int32_t* order;        // [n_slots] attention dispatch slot -> unit (-1: idle)
 };
+// Attention dispatch order (4 slots = the 4 waves of one workgroup).  A
+// sequence group with several q-blocks is cut into chunks of 4 consecutive
+// q-blocks; for each (chunk, kv head, split) its 4 q-blocks take the 4 waves
+// of one workgroup, so they stream the same K/V pages together (one wave
+// idles where a q-block has no such split).  Groups with one q-block (decode
+// rows) follow, their units packed densely.  The host count of the slots;
+// *chunked receives the size of the chunked region (a multiple of 4).
+long attn_slot_count(const int* g_pos0, const int* g_len, int ngroups, int nkv, int split, int qb,
+                     long* chunked = nullptr);
 // rows: device copy of ifr_row[M] (5 int32 each).  qb = q-block tokens,
 // split = kv tokens per unit (multiple of the page size).
 hipError_t launch_pack(const int32_t* rows, int M, int nkv, int qb, int split, const PackOut& o,
@@ -155,11 +165,15 @@ hipError_t launch_pack(const int32_t* rows, int M, int nkv, int qb, int split, c
 struct AttnArgs {
   const AttnUnit* units;
   int n_units;
+  const int32_t* order;    // [n_slots] dispatch slot -> unit or -1
+  int n_slots;
+  int n_shared;            // slots [0, n_shared): chunked workgroups that share K/V pages in LDS
   const uint16_t* q;       // [M][nq][hd]
   int nq;
   float scale_log2;        // log2(e) / sqrt(hd)
-  float* part_o;           // [n_units][16][hd]
-  float* part_ml;          // [n_units][16][2]
+  float* part_o;           // [n_units][16 * col_tiles][hd]
+  float* part_ml;          // [n_units][16 * col_tiles][2]
+  int col_tiles;           // 16-column MFMA tiles per unit (1 or 2): q-block = 16 * col_tiles / G tokens
 };
 hipError_t launch_attention(const AttnArgs& a, const KVLayout& kv, hipStream_t st);
 
@@ -174,6 +188,7 @@ struct CombineArgs {
   int8_t* q;               // A tiles of [M][nq*hd], per-token int8 (half-away)
   float* qscale;           // [M]
   float* gsum;             // [M][nq*hd/128]
+  int ucols;               // partial columns per unit (16 * col_tiles)
 };
 hipError_t launch_combine(const CombineArgs& a, hipStream_t st);
 

@@ -14,6 +14,8 @@
 #include "ifr_dev.h"
 #include "ifr_kernels.h"
 
+#include <algorithm>
+
 namespace ifrk {
 namespace {
 
@@ -237,14 +239,16 @@ __global__ __launch_bounds__(256) void row_quant1024_kernel(RowQuantArgs a) {
     v[0] = x4.x; v[1] = x4.y; v[2] = x4.z; v[3] = x4.w;
     *reinterpret_cast<float4*>(a.resid + (size_t)src * 1024 + 4 * t) = x4;
   } else {
+    // both loads issued together: the residual does not wait behind the
+    // rotation's barriers
     const uint2 y2 = *reinterpret_cast<const uint2*>(a.y + (size_t)src * 1024 + 4 * t);
+    float4* rp = reinterpret_cast<float4*>(a.resid + (size_t)src * 1024 + 4 * t);
+    float4 r4 = *rp;
     v[0] = ifrd::h2f((uint16_t)(y2.x & 0xFFFF));
     v[1] = ifrd::h2f((uint16_t)(y2.x >> 16));
     v[2] = ifrd::h2f((uint16_t)(y2.y & 0xFFFF));
     v[3] = ifrd::h2f((uint16_t)(y2.y >> 16));
     if (a.rot_y) fwht1024(v, xs);
-    float4* rp = reinterpret_cast<float4*>(a.resid + (size_t)src * 1024 + 4 * t);
-    float4 r4 = *rp;
     r4.x = r4.x + v[0]; r4.y = r4.y + v[1]; r4.z = r4.z + v[2]; r4.w = r4.w + v[3];
     *rp = r4;
     v[0] = r4.x; v[1] = r4.y; v[2] = r4.z; v[3] = r4.w;
@@ -291,42 +295,54 @@ __global__ __launch_bounds__(256) void row_quant1024_kernel(RowQuantArgs a) {
   }
 }
 
-// Per-token int8 quantization of an fp32 / fp16 row of K = 256 * E values.
-template <int E>
-__global__ __launch_bounds__(256) void quant_plain_fast(const float* xf, const uint16_t* xh, int8_t* q,
-                                                        float* qs, float* gsum) {
-  constexpr int K = 256 * E;
-  __shared__ float red[4];
-  __shared__ int gl[K / 128];
+// Per-token int8 quantization of an fp32 / fp16 row of K = 8 * NT values:
+// thread t owns the 8 contiguous columns 8t..8t+7, so its input is one
+// 16-byte (fp16) or two 16-byte (fp32) loads, its codes are one 8-byte A-tile
+// store, and a 128-column group is exactly one 16-lane DPP row.
+template <int NT>
+__global__ __launch_bounds__(NT) void quant_plain8(const float* xf, const uint16_t* xh, int8_t* q, float* qs,
+                                                   float* gsum) {
+  constexpr int K = 8 * NT, NW = NT / 64;
+  __shared__ float red[NW];
   const int m = blockIdx.x, t = threadIdx.x, lane = t & 63;
-  float v[E];
+  float v[8];
+  if (xf) {
+    const float4* p = reinterpret_cast<const float4*>(xf + (size_t)m * K + 8 * t);
+    const float4 a = p[0], b = p[1];
+    v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w; v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
+  } else {
+    const uint4 r = *reinterpret_cast<const uint4*>(xh + (size_t)m * K + 8 * t);
+    const uint32_t w[4] = {r.x, r.y, r.z, r.w};
 #pragma unroll
-  for (int e = 0; e < E; ++e) {
-    const size_t i = (size_t)m * K + (size_t)e * 256 + t;  // coalesced: element e*256 + t
-    v[e] = xf ? xf[i] : ifrd::h2f(xh[i]);
+    for (int i = 0; i < 4; ++i) {
+      v[2 * i] = ifrd::h2f((uint16_t)(w[i] & 0xFFFF));
+      v[2 * i + 1] = ifrd::h2f((uint16_t)(w[i] >> 16));
+    }
   }
-  if (t < K / 128) gl[t] = 0;
   float mx = 0.0f;
 #pragma unroll
-  for (int e = 0; e < E; ++e) mx = fmaxf(mx, fabsf(v[e]));
+  for (int i = 0; i < 8; ++i) mx = fmaxf(mx, fabsf(v[i]));
   mx = ifrd::wave_max(mx);
   if (lane == 0) red[t >> 6] = mx;
   __syncthreads();
-  mx = fmaxf(1e-6f, fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3])));
+  mx = red[0];
+#pragma unroll
+  for (int i = 1; i < NW; ++i) mx = fmaxf(mx, red[i]);
+  mx = fmaxf(1e-6f, mx);
   const float s = mx / 127.0f;
   const float inv = 1.0f / s;
   if (t == 0) qs[m] = s;
+  uint32_t w[2] = {0u, 0u};
+  int S = 0;
 #pragma unroll
-  for (int e = 0; e < E; ++e) {
-    const int c = ifrd::quant_half_away(v[e], inv);
-    q[atile_off(m, e * 256 + t, K)] = (int8_t)c;
-    // element e*256 + t lies in group (e*256 + t) / 128 = 2e + (t >= 128); a wave of
-    // 64 lanes stays in one group: reduce in the wave, one LDS add per wave.
-    const int S = ifrd::wave_sum_int(c);
-    if (lane == 0) atomicAdd(&gl[2 * e + (t >> 7)], S);
+  for (int i = 0; i < 8; ++i) {
+    const int c = ifrd::quant_half_away(v[i], inv);
+    w[i >> 2] |= (uint32_t)(c & 0xFF) << (8 * (i & 3));
+    S += c;
   }
-  __syncthreads();
-  if (gsum && t < K / 128) gsum[(size_t)m * (K / 128) + t] = (float)gl[t];
+  *reinterpret_cast<uint2*>(q + atile_off(m, 8 * t, K)) = make_uint2(w[0], w[1]);
+  S = ifrd::row16_sum_int(S);
+  if (gsum && (lane & 15) == 0) gsum[(size_t)m * (K / 128) + (t >> 4)] = (float)S;
 }
 
 __global__ __launch_bounds__(256) void quant_plain_kernel(const float* xf, const uint16_t* xh,
@@ -349,7 +365,10 @@ __global__ __launch_bounds__(256) void quant_plain_kernel(const float* xf, const
 __global__ __launch_bounds__(256) void qk_rope_kv_kernel(QKArgs a, KVLayout kv) {
   __shared__ float hx[4][128];
   __shared__ float red[4][8];
-  const int m = blockIdx.x, lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int m = blockIdx.x, lane = threadIdx.x & 63;
+  // wave-uniform head: the row record, block-table entry and head kind are
+  // scalar loads / values
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int hd = kv.hd, nq = a.nq, nkv = kv.nkv;
   const int h = blockIdx.y * 4 + w;
   if (h >= nq + 2 * nkv) return;  // no block-wide barrier below
@@ -359,57 +378,65 @@ __global__ __launch_bounds__(256) void qk_rope_kv_kernel(QKArgs a, KVLayout kv) 
   float* x = hx[w];
   const int kind = h < nq ? 0 : (h < nq + nkv ? 1 : 2);  // q, k, v
   const int hh = kind == 0 ? h : (kind == 1 ? h - nq : h - nq - nkv);
+  // every global load of this wave is issued here, before any use
   const uint32_t y2 = *reinterpret_cast<const uint32_t*>(a.qkv + (size_t)m * ncols + (size_t)h * hd + 2 * lane);
-  float v0 = ifrd::h2f((uint16_t)(y2 & 0xFFFF)), v1 = ifrd::h2f((uint16_t)(y2 >> 16));
-  if (kind < 2) {
-    x[2 * lane] = v0;
-    x[2 * lane + 1] = v1;
-    ifrd::wave_sync();
-    const float* nw = kind == 0 ? a.q_norm : a.k_norm;
-    if (nw) {
-      // eight sequential fused chains (reference AVX2 order, main.cpp:306-351)
-      if (lane < 8) {
-        float t[16];
+  // (unconditional: loads that a head kind does not need read valid memory
+  // and are ignored, so no branch separates them from the others)
+  const float* nwp = kind == 0 ? a.q_norm : (kind == 1 ? a.k_norm : nullptr);
+  const float* nsrc = nwp ? nwp : a.rope_cos;
+  const float nw0 = nsrc[2 * lane], nw1 = nsrc[2 * lane + 1];
+  float cs_e[2], sn_e[2];
 #pragma unroll
-        for (int i = 0; i < 16; ++i) t[i] = x[lane + 8 * i];
-        float acc = 0.0f;
-#pragma unroll
-        for (int i = 0; i < 16; ++i) acc = fmaf(t[i], t[i], acc);
-        red[w][lane] = acc;
-      }
-      ifrd::wave_sync();
-      const float s0 = red[w][0] + red[w][4], s1 = red[w][1] + red[w][5];
-      const float s2 = red[w][2] + red[w][6], s3 = red[w][3] + red[w][7];
-      const float tot = (s0 + s1) + (s2 + s3);
-      const float f = 1.0f / sqrtf(tot / (float)hd + a.eps);
-      v0 = (v0 * f) * (1.0f + nw[2 * lane]);
-      v1 = (v1 * f) * (1.0f + nw[2 * lane + 1]);
-      ifrd::wave_sync();
-      x[2 * lane] = v0;
-      x[2 * lane + 1] = v1;
-      ifrd::wave_sync();
-    }
-    // rotate-half RoPE on the first `rotary` dims (main.cpp:365-373)
-    const float* cs = a.rope_cos + (size_t)pos * half;
-    const float* sn = a.rope_sin + (size_t)pos * half;
-    float o[2] = {v0, v1};
-#pragma unroll
-    for (int e2 = 0; e2 < 2; ++e2) {
-      const int e = 2 * lane + e2;
-      if (e < half) {
-        const float p = x[e] * cs[e];
-        const float q = x[e + half] * sn[e];
-        o[e2] = p - q;
-      } else if (e < 2 * half) {
-        const int d = e - half;
-        const float p = x[d] * sn[d];
-        const float q = x[e] * cs[d];
-        o[e2] = p + q;
-      }
-    }
-    v0 = o[0];
-    v1 = o[1];
+  for (int e2 = 0; e2 < 2; ++e2) {
+    const int e = 2 * lane + e2;
+    const int ix = e < half ? e : (e < 2 * half ? e - half : 0);
+    cs_e[e2] = a.rope_cos[(size_t)pos * half + ix];
+    sn_e[e2] = a.rope_sin[(size_t)pos * half + ix];
   }
+  const int page = kv.block_table[(size_t)seq * kv.max_pages + pos / kv.page];
+  const float r0 = ifrd::h2f((uint16_t)(y2 & 0xFFFF)), r1 = ifrd::h2f((uint16_t)(y2 >> 16));
+  // q/k norm and RoPE are evaluated for every head (v heads select the raw
+  // values at the end): no branch, so the loads above stay ahead of all uses.
+  x[2 * lane] = r0;
+  x[2 * lane + 1] = r1;
+  ifrd::wave_sync();
+  // RMSNorm(1+w) of the head: eight sequential fused chains (reference AVX2
+  // order, main.cpp:306-351)
+  if (lane < 8) {
+    float t[16];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) t[i] = x[lane + 8 * i];
+    float acc = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) acc = fmaf(t[i], t[i], acc);
+    red[w][lane] = acc;
+  }
+  ifrd::wave_sync();
+  const float s0 = red[w][0] + red[w][4], s1 = red[w][1] + red[w][5];
+  const float s2 = red[w][2] + red[w][6], s3 = red[w][3] + red[w][7];
+  const float tot = (s0 + s1) + (s2 + s3);
+  const float f = 1.0f / sqrtf(tot / (float)hd + a.eps);
+  float v0 = nwp ? (r0 * f) * (1.0f + nw0) : r0;
+  float v1 = nwp ? (r1 * f) * (1.0f + nw1) : r1;
+  ifrd::wave_sync();
+  x[2 * lane] = v0;
+  x[2 * lane + 1] = v1;
+  ifrd::wave_sync();
+  // rotate-half RoPE on the first `rotary` dims (main.cpp:365-373)
+  float o[2] = {v0, v1};
+#pragma unroll
+  for (int e2 = 0; e2 < 2; ++e2) {
+    const int e = 2 * lane + e2;
+    const int d = e < half ? e : e - half;
+    const float xa = x[d], xb = x[min(d + half, hd - 1)];
+    if (e < half) {
+      o[e2] = xa * cs_e[e2] - xb * sn_e[e2];
+    } else if (e < 2 * half) {
+      o[e2] = xa * sn_e[e2] + xb * cs_e[e2];
+    }
+  }
+  v0 = kind < 2 ? o[0] : r0;
+  v1 = kind < 2 ? o[1] : r1;
   v0 = ifrd::fp16r(v0);
   v1 = ifrd::fp16r(v1);
   if (kind == 0) {
@@ -417,7 +444,6 @@ __global__ __launch_bounds__(256) void qk_rope_kv_kernel(QKArgs a, KVLayout kv) 
     *reinterpret_cast<uint32_t*>(dst + 2 * lane) = (uint32_t)ifrd::f2h(v0) | ((uint32_t)ifrd::f2h(v1) << 16);
     return;
   }
-  const int page = kv.block_table[(size_t)seq * kv.max_pages + pos / kv.page];
   const int tok = pos % kv.page;
   const size_t base = ((size_t)page * nkv + hh);
   if (!kv.kv_int8) {
@@ -566,10 +592,90 @@ __global__ __launch_bounds__(1024) void pack_kernel(const int32_t* rows, int M, 
     }
   }
   __syncthreads();
+  // ---- dispatch order (see attn_slot_count): per-group slot counts of the
+  // chunked region (flag[]) and of the dense region (bgrp[]), both free now
+  for (int g = threadIdx.x; g < ngroups; g += blockDim.x) {
+    const int nbg = nblk[g + 1] - nblk[g];
+    const int len = grp_start[g + 1] - grp_start[g];
+    const int pos0 = rows[5 * grp_start[g] + 1];
+    int cs = 0, ss = 0;
+    if (nbg == 1) {
+      ss = nkv * ((pos0 + len + split - 1) / split);
+    } else {
+      for (int j = 0; 4 * j < nbg; ++j) {
+        const int bl = min(4 * j + 3, nbg - 1);
+        cs += 4 * nkv * ((pos0 + min((bl + 1) * qb, len) + split - 1) / split);
+      }
+    }
+    flag[g] = cs;
+    bgrp[g] = ss;
+  }
+  __syncthreads();
+  const int CS = block_exscan(flag, ngroups, tmp);
+  __syncthreads();
+  block_exscan(bgrp, ngroups, tmp);
+  __syncthreads();
+  for (int gb = threadIdx.x; gb < nb; gb += blockDim.x) {
+    int g = 0;  // group of q-block gb (nblk[] holds first blocks, ascending)
+    {
+      int lo = 0, hi = ngroups - 1;
+      while (lo < hi) {
+        const int mid = (lo + hi + 1) >> 1;
+        if (nblk[mid] <= gb) lo = mid; else hi = mid - 1;
+      }
+      g = lo;
+    }
+    const int nbg = nblk[g + 1] - nblk[g], b = gb - nblk[g];
+    const int len = grp_start[g + 1] - grp_start[g];
+    const int pos0 = rows[5 * grp_start[g] + 1];
+    const int ns = (pos0 + min((b + 1) * qb, len) + split - 1) / split;
+    const int base = ucnt[gb];
+    if (nbg == 1) {
+      for (int i = 0; i < nkv * ns; ++i) o.order[CS + bgrp[g] + i] = base + i;
+      continue;
+    }
+    const int j = b >> 2, q = b & 3;
+    int off = flag[g];
+    for (int jj = 0; jj < j; ++jj) {
+      const int bl = min(4 * jj + 3, nbg - 1);
+      off += 4 * nkv * ((pos0 + min((bl + 1) * qb, len) + split - 1) / split);
+    }
+    const int bl = min(4 * j + 3, nbg - 1);
+    const int nsm = (pos0 + min((bl + 1) * qb, len) + split - 1) / split;
+    for (int kvh = 0; kvh < nkv; ++kvh)
+      for (int s = 0; s < nsm; ++s) o.order[off + (kvh * nsm + s) * 4 + q] = s < ns ? base + kvh * ns + s : -1;
+    // slots of absent q-blocks in a short last chunk
+    if (b == nbg - 1)
+      for (int qq = q + 1; qq < 4; ++qq)
+        for (int k = 0; k < nkv * nsm; ++k) o.order[off + k * 4 + qq] = -1;
+  }
+  __syncthreads();
   block_exscan(wnt, M, tmp);
   for (int m = threadIdx.x; m < M; m += blockDim.x)
     if (rows[5 * m + 4]) o.want_rows[wnt[m]] = m;
 }
+
+}  // namespace
+
+long attn_slot_count(const int* g_pos0, const int* g_len, int ngroups, int nkv, int split, int qb,
+                     long* chunked) {
+  long dense = 0, chunk = 0;
+  for (int g = 0; g < ngroups; ++g) {
+    const int nbg = (g_len[g] + qb - 1) / qb;
+    if (nbg == 1) {
+      dense += (long)nkv * ((g_pos0[g] + g_len[g] + split - 1) / split);
+      continue;
+    }
+    for (int j = 0; 4 * j < nbg; ++j) {
+      const int bl = std::min(4 * j + 3, nbg - 1);
+      chunk += 4L * nkv * ((g_pos0[g] + std::min((bl + 1) * qb, g_len[g]) + split - 1) / split);
+    }
+  }
+  if (chunked) *chunked = chunk;
+  return chunk + dense;
+}
+
+namespace {
 
 // mg = fp16(silu(g) * u) over an unpaired [M][2F] gate|up buffer (used when
 // gate and up have different bit widths and cannot share one launch).
@@ -612,11 +718,15 @@ hipError_t launch_quant_plain(const float* xf, const uint16_t* xh, int M, int K,
   if (K <= 0 || K % 128 != 0 || K > 8192 || (!xf && !xh) || !q || !qscale)
     return hipErrorInvalidValue;
   if (K == 2048) {
-    hipLaunchKernelGGL(quant_plain_fast<8>, dim3(M), dim3(256), 0, st, xf, xh, q, qscale, gsum);
+    hipLaunchKernelGGL(quant_plain8<256>, dim3(M), dim3(256), 0, st, xf, xh, q, qscale, gsum);
     return hipGetLastError();
   }
   if (K == 3072) {
-    hipLaunchKernelGGL(quant_plain_fast<12>, dim3(M), dim3(256), 0, st, xf, xh, q, qscale, gsum);
+    hipLaunchKernelGGL(quant_plain8<384>, dim3(M), dim3(384), 0, st, xf, xh, q, qscale, gsum);
+    return hipGetLastError();
+  }
+  if (K == 4096) {
+    hipLaunchKernelGGL(quant_plain8<512>, dim3(M), dim3(512), 0, st, xf, xh, q, qscale, gsum);
     return hipGetLastError();
   }
   const size_t lds = (size_t)(2 * K + 64) * sizeof(float);

@@ -262,7 +262,8 @@ def test_pack_maps_match_restatement(dev):
     nu, split = C.c_int32(), C.c_int32()
     ia.check(L.ifr_debug_pack(eng.dev.ctx, M, ptr(cu), ptr(grp), ptr(cb), ptr(cn), ptr(ct),
                               ptr(units), C.byref(nu), C.byref(split)), "debug_pack")
-    exp = pk.pack(rows, cfg.n_kv, 8, split.value)
+    qb = 16 // (cfg.n_heads // cfg.n_kv)  # one 16-column MFMA tile of (token, head) per unit
+    exp = pk.pack(rows, cfg.n_kv, qb, split.value)
     ng = len(exp["cu_seqlens"]) - 1
     assert cu[:ng + 1].tolist() == exp["cu_seqlens"]
     assert grp.tolist() == exp["row_grp"]
@@ -270,3 +271,10 @@ def test_pack_maps_match_restatement(dev):
     assert ct.tolist() == exp["comb_tok"]
     assert nu.value == len(exp["units"])
     assert units[:8 * nu.value].reshape(-1, 8).tolist() == exp["units"]
+    ns = C.c_int32()
+    order = np.zeros(4 * 65536, np.int32)
+    ia.check(L.ifr_debug_attn_order(eng.dev.ctx, ptr(order), order.size, C.byref(ns)), "order")
+    assert order[:ns.value].tolist() == exp["order"]
+    # every unit is dispatched exactly once
+    live = sorted(u for u in exp["order"] if u >= 0)
+    assert live == list(range(nu.value))

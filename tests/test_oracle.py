@@ -359,3 +359,34 @@ def test_forward_f32_tracks_a8():
     for r in range(len(toks)):
         c = np.corrcoef(a8[r], f32[r])[0, 1]
         assert c > 0.98, (r, c)
+
+
+def test_attn_dispatch_order_invariants():
+    """The attention dispatch order restatement: every unit exactly once; the
+    4 slots of a chunked workgroup hold the same (kv head, split) of 4
+    consecutive q-blocks of one sequence; single-q-block groups are dense."""
+    from oracle import pack as pk
+    rng = np.random.default_rng(12)
+    for trial in range(20):
+        rows, seq = [], 0
+        for _ in range(int(rng.integers(1, 6))):
+            n = int(rng.choice([1, 1, 3, 9, 40, 70]))
+            p0 = int(rng.integers(0, 900))
+            rows += [(seq, p0 + i, 0, 1, 0) for i in range(n)]
+            seq += 1
+        nkv, qb, split = 2, 8, 256
+        exp = pk.pack(rows, nkv, qb, split)
+        order, units = exp["order"], exp["units"]
+        assert sorted(u for u in order if u >= 0) == list(range(len(units)))
+        for i in range(0, len(order), 4):
+            wg = [units[u] for u in order[i:i + 4] if u >= 0]
+            if not wg:
+                continue
+            same = {(u[0], u[1], u[5]) for u in wg}
+            if len(wg) > 1 and len(same) == 1:
+                q0 = sorted(u[2] for u in wg)
+                assert all(b - a == qb for a, b in zip(q0, q0[1:])) or len(q0) == 1
+        # the dense tail: single-q-block groups only, in unit order
+        single = [u for u, x in enumerate(units) if sum(1 for r in rows if r[0] == x[0]) <= qb]
+        tail = [u for u in order[len(order) - len(single):]] if single else []
+        assert tail == single
