@@ -34,7 +34,8 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs p, KVLayout kv) {
   // Workgroups of the chunked region serve 4 q-blocks of one sequence with the
   // same kv head and split: they stream each K/V page once into LDS and all 4
   // waves read it there.  Other workgroups run 4 independent units.
-  const bool shared = blockIdx.x * 4 < p.n_shared;  // workgroup-uniform
+  // (fp16 pages only: the host rejects n_shared > 0 for int8 KV)
+  const bool shared = !KV8 && blockIdx.x * 4 < p.n_shared;  // workgroup-uniform
   if (!shared && slot >= p.n_slots) return;         // (no barrier on this path)
   const int u = p.order[slot];
   if (!shared && u < 0) return;
@@ -213,6 +214,7 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs p, KVLayout kv) {
     }
   };
   if (shared) {
+   if constexpr (!KV8) {
     // fp16 pages only (the host sets n_shared = 0 for int8 KV).  LDS holds two
     // pages of 16 fragments (8 K, 8 V) x 64 lanes x 16 bytes; wave w stages
     // fragments 4w..4w+3.  One barrier per page: page i is stored into buffer
@@ -259,6 +261,7 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs p, KVLayout kv) {
       }
       if (i >= last) break;
     }
+   }
   } else {
     PageBuf bA, bB;
     load(bA, 0);

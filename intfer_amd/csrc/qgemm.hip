@@ -337,8 +337,11 @@ __global__ __launch_bounds__(256) void qgemm_splitk(KParams p) {
 
   using Ops = GroupOps<BITS, WM, WN>;
   Ops ops[NGW];
+  // A wave can own no group (ng < 4); it then loads group 0, whose result it
+  // never uses, so every load stays inside the operands.
+  const int glast = max(g1 - 1, 0);
 #pragma unroll
-  for (int d = 0; d < NGW; ++d) load_ops<BITS, WM, WN>(p, aoff, tl, lane, min(g0 + d, g1 - 1), ops[d]);
+  for (int d = 0; d < NGW; ++d) load_ops<BITS, WM, WN>(p, aoff, tl, lane, min(g0 + d, glast), ops[d]);
   stage_fold_operands<BM, BN, 6>(p, row0, tile0, S_l, Z_l);
   constexpr int JS = (EPI == 0) ? 1 : 2;  // swiglu: one thread folds the pair
   constexpr int NOUT = WM * (WN / JS) * 256;

@@ -1,0 +1,354 @@
+"""Run library scenarios on the CPU emulation (test infrastructure only).
+
+Usage (the ASan runtime must be preloaded, which run_scenarios() does):
+    python tests/hipemu/runner.py <scenario> [...]
+Each scenario drives the same C-ABI calls as a GPU test, against the
+emulated library, and checks the results against the CPU oracle where the
+GPU test does.  Any out-of-bounds access aborts with an ASan report.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+import subprocess
+import sys
+import time
+from pathlib import Path
+
+import numpy as np
+
+HERE = Path(__file__).resolve().parent
+ROOT = HERE.parent.parent
+if str(ROOT) not in sys.path:
+    sys.path.insert(0, str(ROOT))
+
+SCENARIOS = {}
+
+
+def scenario(f):
+    SCENARIOS[f.__name__] = f
+    return f
+
+
+def use_emulated_library():
+    """Point intfer_amd's ctypes table at the emulated library."""
+    from intfer_amd import _abi
+    from tests.hipemu import build as eb
+    L = C.CDLL(str(eb.LIB))
+    for name, (res, args) in _abi._PROTOS.items():
+        fn = getattr(L, name)
+        fn.restype = res
+        fn.argtypes = args
+    _abi._lib = L
+    return L
+
+
+def say(msg):
+    sys.stdout.write(f"[emu] {msg}\n")
+    sys.stdout.flush()
+
+
+# ---- scenarios ---------------------------------------------------------------------
+
+@scenario
+def smoke():
+    """__graft_entry__.smoke(): tiny model, M=20 prefill."""
+    import __graft_entry__ as g
+    g.smoke()
+
+
+def _small_cfg(ia, **over):
+    base = dict(hidden=256, layers=2, n_heads=4, n_kv=2, inter=384, vocab=512)
+    base.update(over)
+    return ia.default_cfg(**base)
+
+
+@scenario
+def noop():
+    """The emulation loads and a context opens (environment check)."""
+    import intfer_amd as ia
+    ia.Device(0).close()
+
+
+@scenario
+def gemm_shapes():
+    """Every launch shape at small K/N and ragged M, bit-exact vs the oracle."""
+    _gemm_shapes((2, 4, 8), ((64, 128), (32, 256), (96, 384), (64, 1024), (32, 3072)))
+
+
+@scenario
+def gemm_small():
+    """Every launch shape, INT2 and INT8, at K below and above 4 groups."""
+    _gemm_shapes((2, 8), ((32, 256), (32, 1024)))
+
+
+def _gemm_shapes(bits_list, shapes):
+    import intfer_amd as ia
+    from oracle import pyoracle as po
+    L = ia.lib()
+    dev = ia.Device(0)
+    rng = np.random.default_rng(5)
+    nv = L.ifr_quant_gemm_variants()
+    for bits in bits_list:
+        for (N, K) in shapes:
+            lin = ia.make_linear(N, K, bits, rng)
+            gate, up = ia.make_linear(N, K, bits, rng), ia.make_linear(N, K, bits, rng)
+            dl, dp = C.c_void_p(), C.c_void_p()
+            ia.check(L.ifr_linear_upload(dev.ctx, C.byref(lin.struct), C.byref(dl)), "upload")
+            ia.check(L.ifr_linear_upload_pair(dev.ctx, C.byref(gate.struct), C.byref(up.struct),
+                                              C.byref(dp)), "pair")
+            for M in (1, 17, 70):
+                x = rng.standard_normal((M, K), dtype=np.float32)
+                q, sc, g = po.act_quant(x)
+                qd, sd, gd = dev.upload(ia.atile(q)), dev.upload(sc[:, 0].copy()), dev.upload(g)
+                od = dev.alloc(M * N * 2)
+                ref = po.qgemm(q, sc[:, 0], lin)
+                for v in range(nv):
+                    rc = L.ifr_quant_gemm_variant(dev.ctx, dl, qd.p, sd.p, gd.p, M, od.p, v)
+                    if rc == ia.IFR_EDECLINE:
+                        continue
+                    ia.check(rc, f"variant {v}")
+                    out = dev.download(od, np.uint16, (M, N))
+                    assert np.array_equal(out, ref), f"bits {bits} N {N} K {K} M {M} variant {v}"
+                    rc = L.ifr_quant_gemm_variant(dev.ctx, dp, qd.p, sd.p, gd.p, M, od.p, v)
+                    if rc != ia.IFR_EDECLINE:
+                        ia.check(rc, f"pair variant {v}")
+                for b in (qd, sd, gd, od):
+                    b.free()
+                say(f"gemm bits={bits} N={N} K={K} M={M} ok")
+            L.ifr_linear_free(dev.ctx, dl)
+            L.ifr_linear_free(dev.ctx, dp)
+    dev.close()
+
+
+def _forward_case(layers, kv_int8, steps, hidden=1024, n_heads=16, n_kv=8, inter=3072,
+                  vocab=2048):
+    import intfer_amd as ia
+    from intfer_amd import workloads as wl
+    from oracle import pyoracle as po
+    cfg = ia.default_cfg(layers=layers, hidden=hidden, n_heads=n_heads, n_kv=n_kv, inter=inter,
+                         vocab=vocab)
+    model = ia.SynthModel(cfg, seed=11, bits=2)
+    dev = ia.Device(0)
+    w = wl.cfg1(cfg, seed=1)
+    eng = ia.Engine(dev, model, max_seqs=8, max_seq_tokens=2048, pool_tokens=8 * 2048,
+                    kv_int8=kv_int8, max_rows=128)
+    ora = po.OracleEngine(model, kv_int8=kv_int8, mode=0, max_seqs=8)
+    dec_e, dec_o = [], []
+    for (k, v) in w.kv:
+        s = eng.seq_open()
+        eng.load_kv(s, k, v)
+        dec_e.append(s)
+        so = ora.seq_open()
+        kr = k.astype(np.float16).astype(np.float32)
+        vr = v.astype(np.float16).astype(np.float32)
+        if kv_int8:
+            for arr in (kr, vr):
+                flat = arr.reshape(-1, cfg.head_dim)
+                for i in range(flat.shape[0]):
+                    seg = np.ascontiguousarray(flat[i])
+                    po.oracle().or_kv_int8_round(po.ptr(seg), cfg.head_dim)
+                    flat[i] = seg
+        ora.set_kv(so, kr.reshape(cfg.layers, k.shape[1], -1), vr.reshape(cfg.layers, k.shape[1], -1))
+        dec_o.append(so)
+    pe, pq = eng.seq_open(), ora.seq_open()
+    t0 = time.time()
+    be, lg = eng.forward(wl.cfg1_rows(w, dec_e, pe), logits=True)
+    bo, lo = ora.forward(wl.cfg1_rows(w, dec_o, pq), logits=True)
+    err = float(np.abs(lg - lo).max() / lo.std())
+    say(f"cfg1 layers={layers} kv_int8={kv_int8}: {time.time() - t0:.1f}s, tokens equal "
+        f"{np.array_equal(be, bo)}, max|dlogit|/std {err:.3g}")
+    want = [i for i, r in enumerate(wl.cfg1_rows(w, dec_e, pe)) if r[4]]
+    seq_e, seq_o = dec_e + [pe], dec_o + [pq]
+    pos = [n + 1 for n in w.contexts] + [len(w.pre_tokens)]
+    tok = [int(bo[i]) for i in want]
+    for step in range(steps):
+        be2, lg2 = eng.forward([(s, p, t, 0, 1) for s, p, t in zip(seq_e, pos, tok)], logits=True)
+        bo2, lo2 = ora.forward([(s, p, t, 0, 1) for s, p, t in zip(seq_o, pos, tok)], logits=True)
+        say(f"  step {step}: agree {int((be2 == bo2).sum())}/5, max|dlogit|/std "
+            f"{float(np.abs(lg2 - lo2).max() / lo2.std()):.3g}")
+        tok = [int(x) for x in bo2]
+        pos = [p + 1 for p in pos]
+    dev.close()
+    model.close()
+    return err
+
+
+@scenario
+def forward_one_layer():
+    """test_one_layer_bit_exact at a 2048-token vocabulary."""
+    _forward_case(1, 0, 2)
+
+
+@scenario
+def forward_kv8():
+    """cfg1 with int8 KV and greedy steps (two layers)."""
+    _forward_case(2, 1, 3)
+
+
+@scenario
+def forward_fp16():
+    """cfg1 with fp16 KV and greedy steps (two layers)."""
+    _forward_case(2, 0, 3)
+
+
+@scenario
+def forward_one_layer_full_vocab():
+    """test_one_layer_bit_exact at its real shape (vocabulary 151936)."""
+    _forward_case(1, 0, 1, vocab=151936)
+
+
+@scenario
+def forward_full_fp16():
+    """test_cfg1_mixed_iteration_and_greedy64[0] at its real shape, 2 greedy steps."""
+    _forward_case(28, 0, 2, vocab=151936)
+
+
+@scenario
+def forward_full_kv8():
+    """test_cfg1_mixed_iteration_and_greedy64[1] at its real shape, 2 greedy steps."""
+    _forward_case(28, 1, 2, vocab=151936)
+
+
+@scenario
+def sched_small():
+    """Scheduler split/joint/solo and spec verify rows on a small model."""
+    import intfer_amd as ia
+    from intfer_amd import workloads as wl
+    cfg = ia.default_cfg(layers=2, vocab=2048)
+    model = ia.SynthModel(cfg, seed=11, bits=2)
+    dev = ia.Device(0)
+    eng = ia.Engine(dev, model, max_seqs=16, max_seq_tokens=1024, pool_tokens=16 * 1024, max_rows=256)
+    prompts = wl.cfg4_requests(4, seed=8, vocab=cfg.vocab, lo=40, hi=150)
+    streams = []
+    for split in (0, 1):
+        sch = ia.Scheduler(eng, chunk_m=64, live_cap=8, split_iter=split)
+        ids = [sch.submit(p, 5) for p in prompts]
+        for _ in range(200):
+            if sch.step() == 0 and all(sch.result(i)[1] for i in ids):
+                break
+        streams.append([sch.result(i)[0] for i in ids])
+        sch.close()
+    assert streams[0] == streams[1], streams
+    say("split == joint")
+    rng = np.random.default_rng(5)
+    base = rng.integers(0, cfg.vocab, size=30).astype(np.int32)
+    pr = [np.concatenate([base, base, base[:7]]).astype(np.int32), base[:25].copy()]
+    out = []
+    for k in (0, 4):
+        sch = ia.Scheduler(eng, chunk_m=64, live_cap=8, spec_k=k)
+        ids = [sch.submit(p, 8) for p in pr]
+        n = 0
+        while not all(sch.result(i)[1] for i in ids) and n < 100:
+            sch.step()
+            n += 1
+        out.append([sch.result(i)[0] for i in ids])
+        sch.close()
+    assert out[0] == out[1], out
+    say("spec == plain")
+    dev.close()
+    model.close()
+
+
+@scenario
+def attention_ragged():
+    """Joint ragged attention (decode rows of several lengths + two causal
+    chunks, one at an offset), fp16 and int8 KV, vs the oracle row loop."""
+    import intfer_amd as ia
+    from oracle import pyoracle as po
+    from oracle.pyoracle import ptr
+    for kv_int8 in (0, 1):
+        cfg = ia.default_cfg(layers=1, vocab=1024)
+        model = ia.SynthModel(cfg, seed=5)
+        dev = ia.Device(0)
+        lens = [40, 300, 257, 1000, 33]
+        chunks = [(0, 70), (520, 45)]
+        eng = ia.Engine(dev, model, max_seqs=16, max_seq_tokens=4096, pool_tokens=8192,
+                        kv_int8=kv_int8, max_rows=256)
+        rng = np.random.default_rng(33)
+        nkv, hd, nq = cfg.n_kv, cfg.head_dim, cfg.n_heads
+        seqs, stored = [], []
+        for n in lens + [o + m for o, m in chunks]:
+            s = eng.seq_open()
+            k = rng.standard_normal((1, n, nkv, hd), dtype=np.float32)
+            v = rng.standard_normal((1, n, nkv, hd), dtype=np.float32)
+            eng.load_kv(s, k, v)
+            kr = k.astype(np.float16).astype(np.float32).reshape(n, nkv * hd)
+            vr = v.astype(np.float16).astype(np.float32).reshape(n, nkv * hd)
+            if kv_int8:
+                for arr in (kr, vr):
+                    for t in range(n):
+                        for h in range(nkv):
+                            seg = np.ascontiguousarray(arr[t, h * hd:(h + 1) * hd])
+                            po.oracle().or_kv_int8_round(ptr(seg), hd)
+                            arr[t, h * hd:(h + 1) * hd] = seg
+            seqs.append(s)
+            stored.append((kr, vr))
+        rows = [(seqs[i], n - 1, 0, 0, 1) for i, n in enumerate(lens)]
+        for j, (o, m) in enumerate(chunks):
+            rows += [(seqs[len(lens) + j], o + p, 0, 1, 1) for p in range(m)]
+        M = len(rows)
+        q = rng.standard_normal((M, nq, hd), dtype=np.float32).astype(np.float16)
+        out = eng.attention(0, rows, q)
+        qf = q.astype(np.float32).reshape(M, nq * hd)
+        sidx = {s: i for i, s in enumerate(seqs)}
+        err = 0.0
+        for m in range(M):
+            s, pos = rows[m][0], rows[m][1]
+            kr, vr = stored[sidx[s]]
+            o = np.empty(nq * hd, np.float32)
+            po.oracle().or_attention_row(ptr(np.ascontiguousarray(qf[m])), ptr(np.ascontiguousarray(kr[:pos + 1])),
+                                         ptr(np.ascontiguousarray(vr[:pos + 1])), pos, nq, nkv, hd, ptr(o))
+            err = max(err, float(np.abs(out[m] - o).max()))
+        say(f"attention kv_int8={kv_int8} M={M}: max err {err:.3g}")
+        assert err < 4e-3
+        dev.close()
+        model.close()
+
+
+@scenario
+def act_quant():
+    import intfer_amd as ia
+    from oracle import pyoracle as po
+    L = ia.lib()
+    dev = ia.Device(0)
+    for (K, norm, rot, rnd, ga) in [(1024, 1, 1, 0, 0), (1024, 0, 0, 1, 64), (2048, 0, 0, 0, 0),
+                                    (3072, 1, 0, 0, 0), (5120, 1, 1, 0, 0), (256, 1, 1, 0, 0)]:
+        rng = np.random.default_rng(K)
+        M = 19
+        x = (rng.standard_normal((M, K), dtype=np.float32) * 2.5).astype(np.float32)
+        w = rng.normal(0, 0.1, size=K).astype(np.float32)
+        q, s, g = po.act_quant(x, norm_w=w if norm else None, rotate=rot, round=rnd, ga=ga)
+        ns = K // ga if ga else 1
+        xd, wd = dev.upload(x), dev.upload(w)
+        Mp = (M + 15) // 16 * 16
+        qd, sd, gd = dev.alloc(Mp * K), dev.alloc(M * ns * 4), dev.alloc(M * (K // 128) * 4)
+        ia.check(L.ifr_act_quant(dev.ctx, xd.p, M, K, wd.p if norm else None, C.c_float(1e-6), rot, rnd,
+                                 ga, qd.p, sd.p, gd.p), "ifr_act_quant")
+        qg = ia.untile(dev.download(qd, np.int8, (Mp * K,)), M, K)
+        assert np.array_equal(qg, q), K
+        say(f"act_quant K={K} ok")
+    dev.close()
+
+
+def run_scenarios(names, timeout=3600) -> int:
+    """Run scenarios in a child process with the ASan runtime preloaded."""
+    from tests.hipemu import build as eb
+    env = dict(os.environ)
+    pre = env.get("LD_PRELOAD", "")
+    env["LD_PRELOAD"] = eb.asan_runtime() + (":" + pre if pre else "")
+    env["IFR_EMU_CHILD"] = "1"
+    env["ASAN_OPTIONS"] = "detect_leaks=0:halt_on_error=1:abort_on_error=1:detect_stack_use_after_return=0"
+    r = subprocess.run([sys.executable, str(HERE / "runner.py"), *names], env=env, timeout=timeout)
+    return r.returncode
+
+
+if __name__ == "__main__":
+    if os.environ.get("IFR_EMU_CHILD") != "1":
+        sys.exit(run_scenarios(sys.argv[1:]))
+    use_emulated_library()
+    for n in sys.argv[1:]:
+        say(f"scenario {n}")
+        t = time.time()
+        SCENARIOS[n]()
+        say(f"scenario {n} passed in {time.time() - t:.1f}s")
