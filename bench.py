@@ -51,6 +51,12 @@ def parse():
     ap.add_argument("--no-roofline", action="store_true")
     ap.add_argument("--gemm-sweep", action="store_true",
                     help="run only the cache-cold cfg2 GEMM sweep and print its JSON line")
+    ap.add_argument("--gemm-variants", action="store_true",
+                    help="time every quant-GEMM launch shape on the 0.8B shapes and print a JSON line")
+    ap.add_argument("--attn-sweep", action="store_true",
+                    help="run only the attention sweep (cfg3, C=64 decode, mixed) and print its JSON line")
+    ap.add_argument("--attn-splits", default="0",
+                    help="comma-separated KV tokens per attention unit for --attn-sweep (0: default)")
     ap.add_argument("--copy-calib", action="store_true",
                     help="run only 8 device copies of 1 GiB (HBM traffic counter calibration)")
     return ap.parse_args()
@@ -224,6 +230,111 @@ def gemm_sweep(ia, dev, bits_list=(2, 4), Ms=(1, 8, 16, 64, 256, 1024), reps=3):
     return res
 
 
+def attn_sweep(ia, dev, reps=10, splits=(0,)):
+    """Joint ragged attention on one layer at the serve shapes: cfg3 (64
+    decode rows, lognormal lengths, + two 512-row causal chunks), C=64
+    decode-only rows at the cfg4 context mix, and the same rows plus one
+    512-row prefill chunk at offset 1024.  Durations come from HIP events on
+    the engine stream around each launch (attention and combine separately)."""
+    from intfer_amd import workloads as wl
+    cfg = ia.default_cfg(layers=1, vocab=1024)
+    model = ia.SynthModel(cfg, seed=5)
+    rng = np.random.default_rng(21)
+    dec4 = [len(p) + 32 for p in wl.cfg4_requests(64, seed=4, vocab=cfg.vocab)]
+    cases = [("cfg3", wl.cfg3_lengths(seed=3), [(0, 512), (1536, 512)]),
+             ("c64_decode", dec4, []),
+             ("c64_mixed", dec4, [(1024, 512)])]
+    res = []
+    plan = [(kv, c, sp) for kv in (0, 1) for c in cases for sp in splits]
+    for kv_int8, (name, lens, chunks), split in plan:
+        if True:
+            total = sum(lens) + sum(o + n for o, n in chunks)
+            eng = ia.Engine(dev, model, max_seqs=len(lens) + len(chunks) + 1, max_seq_tokens=8192,
+                            pool_tokens=total + 64 * (len(lens) + 4), kv_int8=kv_int8, max_rows=1200,
+                            attn_split=split)
+            seqs = []
+            for n in lens + [o + m for o, m in chunks]:
+                s = eng.seq_open()
+                k = rng.standard_normal((1, n, cfg.n_kv, cfg.head_dim), dtype=np.float32)
+                eng.load_kv(s, k, k)
+                seqs.append(s)
+            rows = [(seqs[i], n - 1, 0, 0, 1) for i, n in enumerate(lens)]
+            for j, (o, m) in enumerate(chunks):
+                rows += [(seqs[len(lens) + j], o + p, 0, 1, 1) for p in range(m)]
+            q = rng.standard_normal((len(rows), cfg.n_heads, cfg.head_dim), dtype=np.float32).astype(np.float16)
+            eng.attention(0, rows, q)  # warm code paths
+            eng.set_timing(True)
+            for _ in range(reps):
+                eng.attention(0, rows, q)
+            ms, n, b, f = eng.timing("attention")
+            cms, cn, _, _ = eng.timing("combine")
+            eng.set_timing(False)
+            us = 1e3 * ms / n
+            r = {"case": name, "kv_int8": kv_int8, "split": split, "rows": len(rows), "attn_us": round(us, 2),
+                 "combine_us": round(1e3 * cms / cn, 2), "bytes": round(b / n),
+                 "GBps": round(b / n / us / 1e3, 1), "hbm_frac": round(b / n / us / 1e3 / 8000, 4),
+                 "TFLOPs": round(f / n / us / 1e6, 2)}
+            res.append(r)
+            log(f"attn {name} kv_int8={kv_int8} split={split}: {r}")
+    model.close()
+    return res
+
+
+def gemm_variants(ia, dev, Ms=(128, 256, 576, 1024), bits=2, reps=3):
+    """Every launch shape of the quant GEMM on the four 0.8B shapes (gate_up
+    as the interleaved SwiGLU pair the forward runs), cache-cold as in
+    gemm_sweep; one line per (shape, M, variant)."""
+    import ctypes as C
+    L = ia.lib()
+    shapes = [("qkv", 1024, 4096, False), ("o", 2048, 1024, False), ("gate_up", 1024, 3072, True),
+              ("down", 3072, 1024, False)]
+    rng = np.random.default_rng(0)
+    res = []
+    nv = L.ifr_quant_gemm_variants()
+    Mmax = max(Ms)
+    for name, K, N, pair in shapes:
+        lins = [ia.make_linear(N, K, bits, rng) for _ in range(2 if pair else 1)]
+        wb = sum(l.N * K * bits // 8 + l.N * (K // 128) * 4 for l in lins)
+        R = int(np.ceil(320e6 / wb))
+        dls = []
+        for _ in range(R):
+            d = C.c_void_p()
+            if pair:
+                ia.check(L.ifr_linear_upload_pair(dev.ctx, C.byref(lins[0].struct), C.byref(lins[1].struct),
+                                                  C.byref(d)), "upload")
+            else:
+                ia.check(L.ifr_linear_upload(dev.ctx, C.byref(lins[0].struct), C.byref(d)), "upload")
+            dls.append(d)
+        q = dev.upload(rng.integers(-127, 128, size=((Mmax + 15) // 16 * 16) * K, dtype=np.int8))
+        asc = dev.upload(np.full(Mmax, 1e-3, dtype=np.float32))
+        gs = dev.upload(rng.integers(-2000, 2000, size=Mmax * (K // 128)).astype(np.float32))
+        out = dev.alloc(Mmax * N * 2 * 2)
+        for M in Ms:
+            for v in range(nv):
+                if L.ifr_quant_gemm_variant(dev.ctx, dls[0], q.p, asc.p, gs.p, M, out.p, v) != 0:
+                    continue
+                best = None
+                for _ in range(reps + 1):
+                    dev.timer_begin()
+                    for d in dls:
+                        ia.check(L.ifr_quant_gemm_variant(dev.ctx, d, q.p, asc.p, gs.p, M, out.p, v), "gemm")
+                    ms = dev.timer_end()
+                    best = ms if best is None else min(best, ms)
+                us = best * 1e3 / R
+                ops = 2.0 * M * N * len(lins) * K
+                res.append({"shape": name, "M": M, "variant": v, "us": round(us, 2),
+                            "TOPS": round(ops / us / 1e6, 1)})
+            row = [r for r in res if r["shape"] == name and r["M"] == M]
+            b = min(row, key=lambda r: r["us"])
+            log(f"{name} M={M}: best variant {b['variant']} {b['us']} us {b['TOPS']} TOPS; " +
+                " ".join(f"v{r['variant']}:{r['us']}" for r in row))
+        for d in dls:
+            L.ifr_linear_free(dev.ctx, d)
+        for b in (q, asc, gs, out):
+            b.free()
+    return res
+
+
 def cpu_baseline(ia, model, cfg):
     """Reference CPU path on a bounded sample with the load's per-output-token
     mix: 4 decode rows at the load's mean context (1088) + one 66-row prefill
@@ -276,6 +387,19 @@ def main():
         ms = dev.timer_end()
         print(json.dumps({"metric": "device copy 1 GiB x 8", "bytes_read_per_copy": n,
                           "bytes_written_per_copy": n, "GBps": round(2 * 8 * n / ms / 1e6, 1)}))
+        dev.close()
+        return 0
+    if a.attn_sweep:
+        dev = ia.Device(0)
+        res = attn_sweep(ia, dev, splits=tuple(int(x) for x in a.attn_splits.split(",")))
+        print(json.dumps({"metric": "ragged joint attention sweep (1 layer)", "unit": "GB/s",
+                          "results": res}))
+        dev.close()
+        return 0
+    if a.gemm_variants:
+        dev = ia.Device(0)
+        res = gemm_variants(ia, dev)
+        print(json.dumps({"metric": "quant-GEMM launch shapes (cache-cold)", "unit": "us", "results": res}))
         dev.close()
         return 0
     if a.gemm_sweep:

@@ -212,6 +212,9 @@ typedef struct ifr_kv_cfg {
   int32_t pool_tokens;    /* total KV tokens in the page pool */
   int32_t kv_int8;        /* 0 fp16 KV; 1 int8 KV with fp16 scale per (token, kv_head) */
   int32_t max_rows;       /* largest M one ifr_forward call may carry */
+  int32_t attn_split;     /* KV tokens per attention work unit, a multiple of 32
+                           * (0: 256).  Fixed per engine, so a row's attention
+                           * never depends on the rest of the batch. */
 } ifr_kv_cfg;
 
 /* Upload + repack a model (replaces Engine::load, build_shards,

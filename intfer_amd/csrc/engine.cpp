@@ -45,7 +45,7 @@ int fail(int code, const char* fmt, ...) {
 
 constexpr int kPage = 32;
 
-constexpr int kSplit = 256;  // KV tokens per attention unit
+constexpr int kSplit = 256;  // default KV tokens per attention unit
 constexpr int kAttnTiles = 1;  // 16-column MFMA tiles per attention unit (q-block = 16 / G tokens)
 
 struct Layer {
@@ -308,6 +308,24 @@ long count_units(const std::vector<int>& g_pos0, const std::vector<int>& g_len, 
   return n;
 }
 
+// Algorithmic work of one attention launch: K+V of every row's sequence
+// (plus int8 scales), Q in and O out; flops = QK^T + PV over each row's
+// visible keys (pos + 1).
+void attn_work(const ifr_ctx* c, const ifr_row* rows, int M, const std::vector<int>& g_pos0,
+               const std::vector<int>& g_len, double* bytes, double* flops) {
+  const int kvN = c->cfg.n_kv * c->cfg.head_dim, qN = c->cfg.n_heads * c->cfg.head_dim;
+  const double e = c->kv.kv_int8 ? 1.0 : 2.0;
+  double b = 0, f = 0;
+  for (size_t g = 0; g < g_len.size(); ++g) {
+    const double Ls = g_pos0[g] + g_len[g];
+    b += Ls * kvN * 2 * e + (c->kv.kv_int8 ? Ls * c->cfg.n_kv * 2 * 2 : 0);
+  }
+  b += (double)M * qN * 2 * 2;
+  for (int m = 0; m < M; ++m) f += 4.0 * qN * (rows[m].pos + 1);
+  *bytes = b;
+  *flops = f;
+}
+
 }  // namespace
 
 extern "C" {
@@ -512,7 +530,8 @@ int ifr_model_load(ifr_ctx* c, const ifr_host_model* m, const ifr_kv_cfg* kvc) {
   if (cf.rotary_dim <= 0 || cf.rotary_dim > cf.head_dim || cf.rotary_dim % 2)
     return fail(IFR_EINVAL, "rotary_dim");
   if (kvc->max_seqs <= 0 || kvc->max_seq_tokens <= 0 || kvc->pool_tokens < kPage ||
-      kvc->max_rows <= 0 || kvc->max_rows > 6144)
+      kvc->max_rows <= 0 || kvc->max_rows > 6144 || kvc->attn_split < 0 || kvc->attn_split % kPage ||
+      kvc->attn_split > 65536)
     return fail(IFR_EINVAL, "kv cfg");
   release_model(c);
   c->cfg = cf;
@@ -656,7 +675,7 @@ int ifr_model_load(ifr_ctx* c, const ifr_host_model* m, const ifr_kv_cfg* kvc) {
   const int nparts = ifrk::lmhead_nparts(V);
   if ((r = walloc(c, &c->lm_pv, (size_t)nparts * Mx)) || (r = walloc(c, &c->lm_pi, (size_t)nparts * Mx)))
     return r;
-  c->max_units = 32768;
+  c->max_units = 65536;
   if ((r = walloc(c, &c->pk.units, c->max_units)) || (r = walloc(c, &c->pk.order, 4 * (size_t)c->max_units)) ||
       (r = walloc(c, &c->part_o, (size_t)c->max_units * 16 * kAttnTiles * hd)) ||
       (r = walloc(c, &c->part_ml, (size_t)c->max_units * 16 * kAttnTiles * 2)))
@@ -857,7 +876,7 @@ int ifr_forward(ifr_ctx* c, const ifr_row* rows, int32_t M, int32_t* best_out, f
   }
   // ---- KV split: fixed, so each row's partial decomposition depends only on
   // its own sequence (batch-invariant results: split == joint, solo == loaded)
-  int split = kSplit;
+  int split = c->kv.attn_split > 0 ? c->kv.attn_split : kSplit;
   long nunits = count_units(g_pos0, g_len, nkv, split, c->qb);
   while (nunits > c->max_units) {
     split *= 2;
@@ -880,18 +899,8 @@ int ifr_forward(ifr_ctx* c, const ifr_row* rows, int32_t M, int32_t* best_out, f
   std::vector<int32_t> tok(M);
   for (int m = 0; m < M; ++m) tok[m] = rows[m].token;
   HIPCHK(hipMemcpyAsync(c->row_tok, tok.data(), M * sizeof(int32_t), hipMemcpyHostToDevice, c->st));
-  // ---- bytes accounting for the attention roofline (K+V per sequence, Q, O)
-  double attn_bytes = 0;
-  {
-    const double e = c->kv.kv_int8 ? 1.0 : 2.0;
-    for (size_t g = 0; g < g_seq.size(); ++g) {
-      const double Ls = g_pos0[g] + g_len[g];
-      attn_bytes += Ls * kvN * 2 * e + (c->kv.kv_int8 ? Ls * nkv * 2 * 2 : 0);
-    }
-    attn_bytes += (double)M * qN * 2 * 2;
-  }
-  double attn_flops = 0;  // QK^T + PV over each row's visible keys (pos + 1)
-  for (int m = 0; m < M; ++m) attn_flops += 4.0 * qN * (rows[m].pos + 1);
+  double attn_bytes = 0, attn_flops = 0;
+  attn_work(c, rows, M, g_pos0, g_len, &attn_bytes, &attn_flops);
   const int ng_h = H / 128;
   for (int l = 0; l < cf.layers; ++l) {
     Layer& ly = c->layers[l];
@@ -1086,7 +1095,7 @@ int ifr_attention(ifr_ctx* c, int32_t layer, const ifr_row* rows, int32_t M, con
       g_len.back() += 1;
     }
   }
-  int split = kSplit;
+  int split = c->kv.attn_split > 0 ? c->kv.attn_split : kSplit;
   long nunits = count_units(g_pos0, g_len, nkv, split, c->qb);
   while (nunits > c->max_units) {
     split *= 2;
@@ -1106,16 +1115,26 @@ int ifr_attention(ifr_ctx* c, int32_t layer, const ifr_row* rows, int32_t M, con
                     c->kscale[layer], c->vscale[layer], c->bt_d};
   ifrk::AttnArgs a{c->pk.units, (int)nunits, c->pk.order, nslots, c->kv.kv_int8 ? 0 : (int)nchunked, c->qbuf, nq, 1.4426950408889634f / std::sqrt((float)hd),
                    c->part_o, c->part_ml, kAttnTiles};
-  HIPCHK(ifrk::launch_attention(a, kv, c->st));
+  double attn_bytes = 0, attn_flops = 0;
+  attn_work(c, rows, M, g_pos0, g_len, &attn_bytes, &attn_flops);
+  {
+    Scope sc(c, "attention", attn_bytes, attn_flops);
+    HIPCHK(ifrk::launch_attention(a, kv, c->st));
+  }
   float* out_d = nullptr;
   HIPCHK(hipMalloc(reinterpret_cast<void**>(&out_d), (size_t)M * nq * hd * sizeof(float)));
   ifrk::CombineArgs cb{c->part_o, c->part_ml, c->pk.comb_base, c->pk.comb_nsplit, c->pk.comb_tok,
                        M, nq, nkv, hd, out_d, c->aq, c->as, c->gs, 16 * kAttnTiles};
-  hipError_t e = ifrk::launch_combine(cb, c->st);
+  hipError_t e;
+  {
+    Scope sc(c, "combine", 0);
+    e = ifrk::launch_combine(cb, c->st);
+  }
   if (e == hipSuccess) e = hipMemcpyAsync(out_h, out_d, (size_t)M * nq * hd * sizeof(float), hipMemcpyDeviceToHost, c->st);
   if (e == hipSuccess) e = hipStreamSynchronize(c->st);
   hipFree(out_d);
   HIPCHK(e);
+  if (c->timing) flush_timers(c);
   return IFR_OK;
 }
 

@@ -480,9 +480,15 @@ hipError_t launch_rows_r(const KParams& p, hipStream_t st) {
 template <int BITS, int EPI>
 hipError_t launch_bits(const KParams& p, int variant, hipStream_t st) {
   constexpr int WNs = EPI == 0 ? 1 : 2;
-  if (variant < 0) {  // measured on MI355X over the serve shapes (M 1..576)
-    if (p.ng <= 24 && p.M <= 64) variant = 0;
-    else variant = (EPI == 0 && p.N <= 2048) ? 10 : 5;
+  if (variant < 0) {
+    // Measured on MI355X, cache-cold weights (bench.py --gemm-variants), the
+    // 0.8B shapes at M = 128..1024: split-K wins while the K loop is the
+    // latency (narrow N up to M = 576 for 16 groups, 256 for 24; wide N up
+    // to M = 128); above that 32 x 128 blocks, deeper for narrow N.
+    const bool narrow = EPI == 0 && p.N <= 2048;
+    const int splitk_max = narrow ? (p.ng <= 16 ? 576 : 256) : 128;
+    if (p.ng <= 24 && p.M <= splitk_max) variant = 0;
+    else variant = narrow ? 4 : 5;
   }
   switch (variant) {
     case 0: return launch_splitk_ng<BITS, 1, WNs, EPI>(p, st);

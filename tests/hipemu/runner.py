@@ -82,7 +82,13 @@ def gemm_small():
     _gemm_shapes((2, 8), ((32, 256), (32, 1024)))
 
 
-def _gemm_shapes(bits_list, shapes):
+@scenario
+def gemm_wide():
+    """Block-sized N (full and partial column blocks), plain and SwiGLU pair."""
+    _gemm_shapes((2, 4, 8), ((256, 256), (384, 1024)), Ms=(1, 70, 130), pair_check=True)
+
+
+def _gemm_shapes(bits_list, shapes, Ms=(1, 17, 70), pair_check=False):
     import intfer_amd as ia
     from oracle import pyoracle as po
     L = ia.lib()
@@ -97,12 +103,13 @@ def _gemm_shapes(bits_list, shapes):
             ia.check(L.ifr_linear_upload(dev.ctx, C.byref(lin.struct), C.byref(dl)), "upload")
             ia.check(L.ifr_linear_upload_pair(dev.ctx, C.byref(gate.struct), C.byref(up.struct),
                                               C.byref(dp)), "pair")
-            for M in (1, 17, 70):
+            for M in Ms:
                 x = rng.standard_normal((M, K), dtype=np.float32)
                 q, sc, g = po.act_quant(x)
                 qd, sd, gd = dev.upload(ia.atile(q)), dev.upload(sc[:, 0].copy()), dev.upload(g)
                 od = dev.alloc(M * N * 2)
                 ref = po.qgemm(q, sc[:, 0], lin)
+                pair_ref = None
                 for v in range(nv):
                     rc = L.ifr_quant_gemm_variant(dev.ctx, dl, qd.p, sd.p, gd.p, M, od.p, v)
                     if rc == ia.IFR_EDECLINE:
@@ -113,6 +120,11 @@ def _gemm_shapes(bits_list, shapes):
                     rc = L.ifr_quant_gemm_variant(dev.ctx, dp, qd.p, sd.p, gd.p, M, od.p, v)
                     if rc != ia.IFR_EDECLINE:
                         ia.check(rc, f"pair variant {v}")
+                        if pair_check:
+                            po_ = dev.download(od, np.uint16, (M, N))
+                            if pair_ref is None:
+                                pair_ref = po_
+                            assert np.array_equal(po_, pair_ref), f"pair variant {v} N {N} K {K} M {M}"
                 for b in (qd, sd, gd, od):
                     b.free()
                 say(f"gemm bits={bits} N={N} K={K} M={M} ok")
