@@ -215,6 +215,11 @@ typedef struct ifr_kv_cfg {
   int32_t attn_split;     /* KV tokens per attention work unit, a multiple of 32
                            * (0: 256).  Fixed per engine, so a row's attention
                            * never depends on the rest of the batch. */
+  int32_t lanes;          /* concurrent sub-batches per forward on the
+                           * context's streams: 1 or 2 (0: 1).  Two lanes
+                           * measured no faster on the serve load: each layer
+                           * is a chain of latency-bound kernels whose time
+                           * barely shrinks with half the rows. */
 } ifr_kv_cfg;
 
 /* Upload + repack a model (replaces Engine::load, build_shards,
@@ -266,13 +271,17 @@ int ifr_forward(ifr_ctx* ctx, const ifr_row* rows, int32_t M, int32_t* best_out,
 int ifr_attention(ifr_ctx* ctx, int32_t layer, const ifr_row* rows, int32_t M,
                   const uint16_t* q_h, float* out_h);
 
-/* No reference counterpart: per-kernel device timing of ifr_forward calls
- * since ifr_set_timing(ctx, 1) (HIP events on the context stream), for the
- * bench.  Names: "qgemm_qkv", "qgemm_o", "qgemm_gate_up", "qgemm_down",
- * "attention", "combine", "row_quant", "quant_plain", "qk_rope_kv", "lmhead",
- * "pack".  bytes / flops accumulate each launch's
- * algorithmic HBM bytes and arithmetic work (int8 ops for the GEMMs, fp
- * flops for attention). */
+/* Per-kernel device timing of ifr_forward calls since ifr_set_timing(ctx, 1)
+ * (HIP events on the launching stream; while it is on, every forward runs
+ * on one stream so each kernel is timed alone), for the bench.  Names:
+ * "qgemm_qkv", "qgemm_o", "qgemm_gate_up", "qgemm_down", "attention",
+ * "combine", "row_quant", "quant_plain", "qk_rope_kv", "lmhead", "pack".
+ * bytes / flops accumulate each launch's algorithmic HBM bytes and
+ * arithmetic work (int8 ops for the GEMMs, fp flops for attention).
+ * "host_submit" / "host_wait" (host milliseconds of each forward spent
+ * enqueuing, then waiting for the device) accumulate on every forward, the
+ * counterpart of the reference engine's submit / waitblock buckets
+ * (include/intfer/engine.hpp:567-630); ifr_set_timing clears them. */
 int ifr_set_timing(ifr_ctx* ctx, int32_t on);
 int ifr_get_timing(ifr_ctx* ctx, const char* kernel, double* total_ms, int64_t* launches,
                    double* bytes, double* flops);
@@ -287,6 +296,11 @@ int ifr_debug_pack(ifr_ctx* ctx, int32_t M, int32_t* cu_seqlens, int32_t* row_gr
  * dispatch order (slot -> unit index, -1 idle; 4 slots per workgroup) into
  * order[0..cap); *n_slots receives its length. */
 int ifr_debug_attn_order(ifr_ctx* ctx, int32_t* order, int32_t cap, int32_t* n_slots);
+/* Test hook (no reference counterpart): how many sub-batches (1 or 2) the
+ * last ifr_forward ran concurrently on the context's two streams.  A batch
+ * is cut into [decode / verify rows | prefill chunks], or decode rows are
+ * halved by KV length; while per-kernel timing is on, every batch runs as one. */
+int ifr_debug_last_lanes(ifr_ctx* ctx, int32_t* lanes);
 
 /* ------------------------------------------------------------------------
  * Scheduler / serve (C++ host side above the ABI).

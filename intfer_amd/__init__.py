@@ -214,13 +214,13 @@ class Engine:
     """The device forward over one loaded model."""
 
     def __init__(self, dev: Device, model: SynthModel, max_seqs=8, max_seq_tokens=4096,
-                 pool_tokens=None, kv_int8=0, max_rows=640, attn_split=0):
+                 pool_tokens=None, kv_int8=0, max_rows=640, attn_split=0, lanes=0):
         self.dev = dev
         self.cfg = model.cfg
         kv = KVCfg()
         kv.max_seqs, kv.max_seq_tokens = max_seqs, max_seq_tokens
         kv.pool_tokens = pool_tokens or max_seqs * max_seq_tokens
-        kv.kv_int8, kv.max_rows, kv.attn_split = kv_int8, max_rows, attn_split
+        kv.kv_int8, kv.max_rows, kv.attn_split, kv.lanes = kv_int8, max_rows, attn_split, lanes
         self.kv = kv
         check(lib().ifr_model_load(dev.ctx, model.ptr, C.byref(kv)), "ifr_model_load")
 

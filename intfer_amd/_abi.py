@@ -46,7 +46,7 @@ class HostModel(C.Structure):
 class KVCfg(C.Structure):
     _fields_ = [("max_seqs", C.c_int32), ("max_seq_tokens", C.c_int32),
                 ("pool_tokens", C.c_int32), ("kv_int8", C.c_int32), ("max_rows", C.c_int32),
-                ("attn_split", C.c_int32)]
+                ("attn_split", C.c_int32), ("lanes", C.c_int32)]
 
 
 class Row(C.Structure):
@@ -114,6 +114,7 @@ _PROTOS = {
                                  C.POINTER(C.c_double), C.POINTER(C.c_double)]),
     "ifr_debug_pack": (C.c_int, [P, i32, P, P, P, P, P, P, pi32, pi32]),
     "ifr_debug_attn_order": (C.c_int, [P, P, i32, pi32]),
+    "ifr_debug_last_lanes": (C.c_int, [P, pi32]),
     "ifr_sched_create": (C.c_int, [P, C.POINTER(SchedCfg), C.POINTER(P)]),
     "ifr_sched_create_backend": (C.c_int, [C.POINTER(SchedBackend), C.POINTER(SchedCfg),
                                            C.POINTER(P)]),

@@ -8,6 +8,7 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <chrono>
 #include <cmath>
 #include <cstdarg>
 #include <cstdio>
@@ -75,6 +76,38 @@ struct Seq {
   std::vector<int> pages;
 };
 
+// One lane of the forward: a HIP stream and the workspaces of the
+// sub-batch it runs.  ifr_forward may cut a batch into two contiguous
+// sub-batches and run them on the two lanes concurrently (the kernels are
+// row-independent, so every row's result is the same either way).
+struct Lane {
+  hipStream_t st = nullptr;
+  int32_t* rows_d = nullptr;
+  int32_t* rows_h = nullptr;  // pinned
+  int32_t* tok_h = nullptr;   // pinned
+  float* resid = nullptr;
+  int8_t* aq = nullptr;
+  float* as = nullptr;
+  float* gs = nullptr;
+  uint16_t* qkv = nullptr;
+  uint16_t* qbuf = nullptr;
+  uint16_t* y = nullptr;
+  uint16_t* mg = nullptr;
+  uint16_t* gu = nullptr;
+  ifrk::PackOut pk{};
+  int32_t* row_tok = nullptr;
+  float* part_o = nullptr;
+  float* part_ml = nullptr;
+  int8_t* lm_aq = nullptr;
+  float* lm_as = nullptr;
+  float* lm_pv = nullptr;
+  int32_t* lm_pi = nullptr;
+  int32_t* best_d = nullptr;
+  int32_t* best_h = nullptr;  // pinned
+  float* logits_d = nullptr;  // grown on demand, freed by release_model
+  size_t logits_cap = 0;
+};
+
 }  // namespace
 
 struct ifr_dlinear {
@@ -103,31 +136,11 @@ struct ifr_ctx {
   int32_t* bt_h = nullptr;  // pinned
   std::vector<int> free_pages;
   std::vector<Seq> seqs;
-  // workspaces
+  // workspaces: two lanes (stream + buffers of one sub-batch each)
   int maxM = 0, max_units = 0, last_slots = 0;
-  int32_t* rows_d = nullptr;
-  int32_t* rows_h = nullptr;  // pinned
-  float* resid = nullptr;
-  int8_t* aq = nullptr;
-  float* as = nullptr;
-  float* gs = nullptr;
-  uint16_t* qkv = nullptr;
-  uint16_t* qbuf = nullptr;
-  uint16_t* y = nullptr;
-  uint16_t* mg = nullptr;
-  uint16_t* gu = nullptr;
-  ifrk::PackOut pk{};
-  int32_t* row_tok = nullptr;
-  float* part_o = nullptr;
-  float* part_ml = nullptr;
-  int8_t* lm_aq = nullptr;
-  float* lm_as = nullptr;
-  float* lm_pv = nullptr;
-  int32_t* lm_pi = nullptr;
-  int32_t* best_d = nullptr;
-  int32_t* best_h = nullptr;  // pinned
-  float* logits_d = nullptr;
-  size_t logits_cap = 0;
+  Lane lane[2];
+  hipEvent_t ev_bt = nullptr;  // block-table uploads done (lane 0 -> lane 1)
+  int last_lanes = 0;          // sub-batches of the last forward
   // timing
   bool timing = false;
   hipEvent_t tev[2] = {nullptr, nullptr};  // ifr_timer_begin / _end
@@ -157,24 +170,32 @@ Stat& stat_of(ifr_ctx* c, const std::string& n) {
 // Bracket one launch with events when timing is on.
 struct Scope {
   ifr_ctx* c;
+  hipStream_t st;
   Timer t;
   bool on;
   // bytes / flops: the launch's algorithmic HBM bytes and arithmetic work
-  Scope(ifr_ctx* c_, const char* name, double bytes, double flops = 0) : c(c_), on(c_->timing) {
+  Scope(ifr_ctx* c_, hipStream_t st_, const char* name, double bytes, double flops = 0)
+      : c(c_), st(st_), on(c_->timing) {
     if (!on) return;
     t.name = name;
     t.bytes = bytes;
     t.flops = flops;
     hipEventCreate(&t.a);
     hipEventCreate(&t.b);
-    hipEventRecord(t.a, c->st);
+    hipEventRecord(t.a, st);
   }
   ~Scope() {
     if (!on) return;
-    hipEventRecord(t.b, c->st);
+    hipEventRecord(t.b, st);
     c->timers.push_back(t);
   }
 };
+
+void add_host_time(ifr_ctx* c, const char* name, double ms) {
+  Stat& s = stat_of(c, name);
+  s.ms += ms;
+  s.n += 1;
+}
 
 void flush_timers(ifr_ctx* c) {
   for (auto& t : c->timers) {
@@ -276,12 +297,17 @@ void release_model(ifr_ctx* c) {
   if (c->st) hipStreamSynchronize(c->st);
   for (void* p : c->allocs) hipFree(p);
   c->allocs.clear();
+  if (c->lane[1].st) hipStreamSynchronize(c->lane[1].st);
   if (c->bt_h) hipHostFree(c->bt_h);
-  if (c->rows_h) hipHostFree(c->rows_h);
-  if (c->best_h) hipHostFree(c->best_h);
   c->bt_h = nullptr;
-  c->rows_h = nullptr;
-  c->best_h = nullptr;
+  for (Lane& L : c->lane) {
+    for (int32_t** hp : {&L.rows_h, &L.tok_h, &L.best_h})
+      if (*hp) hipHostFree(*hp);
+    if (L.logits_d) hipFree(L.logits_d);
+    hipStream_t st = L.st;
+    L = Lane();
+    L.st = st;
+  }
   c->layers.clear();
   c->kpool.clear();
   c->vpool.clear();
@@ -289,8 +315,6 @@ void release_model(ifr_ctx* c) {
   c->vscale.clear();
   c->seqs.clear();
   c->free_pages.clear();
-  c->logits_d = nullptr;
-  c->logits_cap = 0;
   c->loaded = false;
 }
 
@@ -326,6 +350,237 @@ void attn_work(const ifr_ctx* c, const ifr_row* rows, int M, const std::vector<i
   *flops = f;
 }
 
+// Groups of at least this many rows are prefill chunks: ifr_forward runs them
+// on lane 1 while the decode / verify rows run on lane 0.
+constexpr int kChunkRows = 32;
+// Decode-only batches of at least this many rows are halved across the lanes.
+constexpr int kMinSplitRows = 16;
+
+// One contiguous sub-batch of an ifr_forward call, run on one lane.
+struct SubBatch {
+  int lane = 0;
+  int row0 = 0, M = 0;             // rows [row0, row0 + M) of the call
+  std::vector<int> g_pos0, g_len;  // its sequence groups
+  std::vector<int> want;           // scored rows (local indices, ascending)
+  int split = 0, nslots = 0;
+  long nunits = 0, nchunked = 0;
+  double attn_bytes = 0, attn_flops = 0;
+};
+
+int prep_sub(ifr_ctx* c, const ifr_row* rows, SubBatch& sb) {
+  const ifr_row* r = rows + sb.row0;
+  for (int m = 0; m < sb.M; ++m)
+    if (r[m].want) sb.want.push_back(m);
+  const int nkv = c->cfg.n_kv;
+  // fixed KV split: each row's partial decomposition depends only on its own
+  // sequence (batch-invariant results: split == joint, solo == loaded)
+  sb.split = c->kv.attn_split > 0 ? c->kv.attn_split : kSplit;
+  sb.nunits = count_units(sb.g_pos0, sb.g_len, nkv, sb.split, c->qb);
+  while (sb.nunits > c->max_units) {
+    sb.split *= 2;
+    sb.nunits = count_units(sb.g_pos0, sb.g_len, nkv, sb.split, c->qb);
+  }
+  sb.nslots = (int)ifrk::attn_slot_count(sb.g_pos0.data(), sb.g_len.data(), (int)sb.g_len.size(), nkv,
+                                         sb.split, c->qb, &sb.nchunked);
+  attn_work(c, r, sb.M, sb.g_pos0, sb.g_len, &sb.attn_bytes, &sb.attn_flops);
+  if (sb.lane == 0) {
+    c->last_split = sb.split;
+    c->last_units = (int)sb.nunits;
+    c->last_slots = sb.nslots;
+  }
+  return IFR_OK;
+}
+
+// Rows up, packing maps, token column.
+int launch_head(ifr_ctx* c, const ifr_row* rows, const SubBatch& sb) {
+  Lane& L = c->lane[sb.lane];
+  const ifr_row* r = rows + sb.row0;
+  std::memcpy(L.rows_h, r, (size_t)sb.M * sizeof(ifr_row));
+  HIPCHK(hipMemcpyAsync(L.rows_d, L.rows_h, (size_t)sb.M * sizeof(ifr_row), hipMemcpyHostToDevice, L.st));
+  {
+    Scope sc(c, L.st, "pack", 0);
+    HIPCHK(ifrk::launch_pack(L.rows_d, sb.M, c->cfg.n_kv, c->qb, sb.split, L.pk, L.st));
+  }
+  for (int m = 0; m < sb.M; ++m) L.tok_h[m] = r[m].token;
+  HIPCHK(hipMemcpyAsync(L.row_tok, L.tok_h, (size_t)sb.M * sizeof(int32_t), hipMemcpyHostToDevice, L.st));
+  return IFR_OK;
+}
+
+// One decoder layer of a sub-batch on its lane.
+int launch_layer(ifr_ctx* c, const SubBatch& sb, int l) {
+  const ifr_model_cfg& cf = c->cfg;
+  Lane& L = c->lane[sb.lane];
+  const int M = sb.M;
+  const int H = cf.hidden, hd = cf.head_dim, nq = cf.n_heads, nkv = cf.n_kv;
+  const int qN = nq * hd, kvN = nkv * hd, F = cf.inter;
+  Layer& ly = c->layers[l];
+  ifrk::KVLayout kv{nkv, hd, kPage, c->max_pages, c->kv.kv_int8, c->kpool[l], c->vpool[l],
+                    c->kscale[l], c->vscale[l], c->bt_d};
+  // (1) layer input: embed (l == 0) or residual += FWHT(down out); RMSNorm; FWHT; quant
+  {
+    ifrk::RowQuantArgs a{};
+    if (l == 0) {
+      a.src = ifrk::SRC_EMBED;
+      a.embed = c->embed;
+      a.tokens = L.row_tok;
+    } else {
+      a.src = ifrk::SRC_RESID;
+      a.y = L.y;
+      a.rot_y = cf.rotate;
+    }
+    a.resid = L.resid;
+    a.norm_w = ly.in_ln;
+    a.eps = cf.rms_eps;
+    a.rotate = cf.rotate;
+    a.round = 0;
+    a.ga = 0;
+    a.q = L.aq;
+    a.qscale = L.as;
+    a.gsum = L.gs;
+    a.M = M;
+    a.K = H;
+    Scope sc(c, L.st, "row_quant", (double)M * H * 4 * 2);
+    HIPCHK(ifrk::launch_row_quant(a, L.st));
+  }
+  // (2) QKV
+  for (int j = 0; j < ly.nqkv; ++j) {
+    ifrk::QGemmArgs a{L.aq, L.as, L.gs, L.qkv + ly.qkv_off[j], nullptr, M, qN + 2 * kvN};
+    Scope sc(c, L.st, "qgemm_qkv", (double)ly.qkv[j].bytes + (double)M * (H + 4) + (double)M * ly.qkv[j].N * 2,
+             2.0 * M * ly.qkv[j].N * H);
+    HIPCHK(ifrk::launch_qgemm(ly.qkv[j], a, L.st));
+  }
+  // (3) q/k norm + RoPE + KV append
+  {
+    ifrk::QKArgs a{L.qkv, L.pk.row_seq, L.pk.row_pos, ly.q_norm, ly.k_norm, c->rope_cos,
+                   c->rope_sin, cf.rotary_dim, cf.rms_eps, nq, L.qbuf, M};
+    Scope sc(c, L.st, "qk_rope_kv", (double)M * (qN + 2 * kvN) * 2 * 2);
+    HIPCHK(ifrk::launch_qk_rope_kv(a, kv, L.st));
+  }
+  // (4) attention + combine (emits the O-proj int8 input)
+  {
+    ifrk::AttnArgs a{L.pk.units, (int)sb.nunits, L.pk.order, sb.nslots, c->kv.kv_int8 ? 0 : (int)sb.nchunked,
+                     L.qbuf, nq, 1.4426950408889634f / std::sqrt((float)hd), L.part_o, L.part_ml, kAttnTiles};
+    Scope sc(c, L.st, "attention", sb.attn_bytes, sb.attn_flops);
+    HIPCHK(ifrk::launch_attention(a, kv, L.st));
+  }
+  {
+    ifrk::CombineArgs a{L.part_o, L.part_ml, L.pk.comb_base, L.pk.comb_nsplit, L.pk.comb_tok,
+                        M, nq, nkv, hd, nullptr, L.aq, L.as, L.gs, 16 * kAttnTiles};
+    Scope sc(c, L.st, "combine", 0);
+    HIPCHK(ifrk::launch_combine(a, L.st));
+  }
+  // (5) O projection
+  {
+    ifrk::QGemmArgs a{L.aq, L.as, L.gs, L.y, nullptr, M, H};
+    Scope sc(c, L.st, "qgemm_o", (double)ly.o.bytes + (double)M * (qN + 4) + (double)M * H * 2,
+             2.0 * M * H * qN);
+    HIPCHK(ifrk::launch_qgemm(ly.o, a, L.st));
+  }
+  // (6) residual += FWHT(o); post norm; FWHT; quant
+  {
+    ifrk::RowQuantArgs a{};
+    a.src = ifrk::SRC_RESID;
+    a.y = L.y;
+    a.rot_y = cf.rotate;
+    a.resid = L.resid;
+    a.norm_w = ly.post_ln;
+    a.eps = cf.rms_eps;
+    a.rotate = cf.rotate;
+    a.q = L.aq;
+    a.qscale = L.as;
+    a.gsum = L.gs;
+    a.M = M;
+    a.K = H;
+    Scope sc(c, L.st, "row_quant", (double)M * H * 4 * 2);
+    HIPCHK(ifrk::launch_row_quant(a, L.st));
+  }
+  // (7) gate/up + SwiGLU
+  if (ly.ngu == 1) {
+    ifrk::QGemmArgs a{L.aq, L.as, L.gs, L.mg, nullptr, M, F};
+    Scope sc(c, L.st, "qgemm_gate_up", (double)ly.gu[0].bytes + (double)M * (H + 4) + (double)M * F * 2,
+             2.0 * M * 2 * F * H);
+    HIPCHK(ifrk::launch_qgemm(ly.gu[0], a, L.st));
+  } else {
+    for (int j = 0; j < 2; ++j) {
+      ifrk::QGemmArgs a{L.aq, L.as, L.gs, L.gu + j * F, nullptr, M, 2 * F};
+      Scope sc(c, L.st, "qgemm_gate_up", (double)ly.gu[j].bytes + (double)M * (H + 4) + (double)M * F * 2,
+               2.0 * M * F * H);
+      HIPCHK(ifrk::launch_qgemm(ly.gu[j], a, L.st));
+    }
+    HIPCHK(ifrk::launch_swiglu(L.gu, M, F, L.mg, L.st));
+  }
+  // (8) quantize mg, down projection
+  {
+    Scope sc(c, L.st, "quant_plain", (double)M * F * 3);
+    HIPCHK(ifrk::launch_quant_plain(nullptr, L.mg, M, F, L.aq, L.as, L.gs, L.st));
+  }
+  {
+    ifrk::QGemmArgs a{L.aq, L.as, L.gs, L.y, nullptr, M, H};
+    Scope sc(c, L.st, "qgemm_down", (double)ly.down.bytes + (double)M * (F + 4) + (double)M * H * 2,
+             2.0 * M * H * F);
+    HIPCHK(ifrk::launch_qgemm(ly.down, a, L.st));
+  }
+  return IFR_OK;
+}
+
+// Final residual, norm, lm_head + argmax on the scored rows; the tokens (and
+// logits, into logits_out when given) come back on the lane's stream.
+int launch_tail(ifr_ctx* c, const SubBatch& sb, float* logits_out) {
+  const ifr_model_cfg& cf = c->cfg;
+  Lane& L = c->lane[sb.lane];
+  const int nwant = (int)sb.want.size();
+  if (nwant == 0) return IFR_OK;
+  const int H = cf.hidden, V = cf.vocab;
+  {
+    ifrk::RowQuantArgs a{};
+    a.src = ifrk::SRC_RESID;
+    a.y = L.y;
+    a.rot_y = cf.rotate;
+    a.resid = L.resid;
+    a.rowmap = L.pk.want_rows;
+    a.norm_w = c->final_norm;
+    a.eps = cf.rms_eps;
+    a.rotate = 0;
+    a.round = 1;
+    a.ga = 64;
+    a.q = L.lm_aq;
+    a.qscale = L.lm_as;
+    a.gsum = nullptr;
+    a.M = nwant;
+    a.K = H;
+    Scope sc(c, L.st, "row_quant", (double)nwant * H * 4 * 2);
+    HIPCHK(ifrk::launch_row_quant(a, L.st));
+  }
+  if (logits_out && L.logits_cap < (size_t)nwant * V) {
+    HIPCHK(hipStreamSynchronize(L.st));
+    if (L.logits_d) HIPCHK(hipFree(L.logits_d));
+    L.logits_d = nullptr;
+    HIPCHK(hipMalloc(reinterpret_cast<void**>(&L.logits_d), (size_t)nwant * V * sizeof(float)));
+    L.logits_cap = (size_t)nwant * V;
+  }
+  ifrk::LmHeadArgs a{};
+  a.a = L.lm_aq;
+  a.as = L.lm_as;
+  a.wcodes = c->lm_w;
+  a.wscale = c->lm_s;
+  a.W = nwant;
+  a.V = V;
+  a.H = H;
+  a.logits = logits_out ? L.logits_d : nullptr;
+  a.part_val = L.lm_pv;
+  a.part_idx = L.lm_pi;
+  a.best = L.best_d;
+  {
+    Scope sc(c, L.st, "lmhead", (double)V * H + (double)V * 2 + (double)nwant * H);
+    HIPCHK(ifrk::launch_lmhead(a, L.st));
+  }
+  HIPCHK(hipMemcpyAsync(L.best_h, L.best_d, nwant * sizeof(int32_t), hipMemcpyDeviceToHost, L.st));
+  if (logits_out)
+    HIPCHK(hipMemcpyAsync(logits_out, L.logits_d, (size_t)nwant * V * sizeof(float), hipMemcpyDeviceToHost,
+                          L.st));
+  return IFR_OK;
+}
+
 }  // namespace
 
 extern "C" {
@@ -345,10 +600,19 @@ int ifr_ctx_create(int32_t device, ifr_ctx** out) {
     return fail(IFR_EDEVICE, "device %d is %s; this build targets gfx950", device, prop.gcnArchName);
   auto* c = new ifr_ctx();
   c->device = device;
+  // two default-priority streams: the primary one (c->st, lane 0) and lane 1
   if (hipStreamCreateWithFlags(&c->st, hipStreamNonBlocking) != hipSuccess) {
     delete c;
     return fail(IFR_EDEVICE, "hipStreamCreate");
   }
+  if (hipStreamCreateWithFlags(&c->lane[1].st, hipStreamNonBlocking) != hipSuccess ||
+      hipEventCreateWithFlags(&c->ev_bt, hipEventDisableTiming) != hipSuccess) {
+    hipStreamDestroy(c->st);
+    if (c->lane[1].st) hipStreamDestroy(c->lane[1].st);
+    delete c;
+    return fail(IFR_EDEVICE, "hipStreamCreate (lane 1)");
+  }
+  c->lane[0].st = c->st;
   *out = c;
   return IFR_OK;
 }
@@ -359,6 +623,8 @@ int ifr_ctx_destroy(ifr_ctx* c) {
   release_model(c);
   for (hipEvent_t& e : c->tev)
     if (e) hipEventDestroy(e);
+  if (c->ev_bt) hipEventDestroy(c->ev_bt);
+  if (c->lane[1].st) hipStreamDestroy(c->lane[1].st);
   if (c->st) hipStreamDestroy(c->st);
   delete c;
   return IFR_OK;
@@ -531,7 +797,7 @@ int ifr_model_load(ifr_ctx* c, const ifr_host_model* m, const ifr_kv_cfg* kvc) {
     return fail(IFR_EINVAL, "rotary_dim");
   if (kvc->max_seqs <= 0 || kvc->max_seq_tokens <= 0 || kvc->pool_tokens < kPage ||
       kvc->max_rows <= 0 || kvc->max_rows > 6144 || kvc->attn_split < 0 || kvc->attn_split % kPage ||
-      kvc->attn_split > 65536)
+      kvc->attn_split > 65536 || kvc->lanes < 0 || kvc->lanes > 2)
     return fail(IFR_EINVAL, "kv cfg");
   release_model(c);
   c->cfg = cf;
@@ -651,35 +917,36 @@ int ifr_model_load(ifr_ctx* c, const ifr_host_model* m, const ifr_kv_cfg* kvc) {
   std::memset(c->bt_h, 0, btn * sizeof(int32_t));
   if (int r = walloc(c, &c->bt_d, btn)) return r;
   HIPCHK(hipMemcpyAsync(c->bt_d, c->bt_h, btn * sizeof(int32_t), hipMemcpyHostToDevice, c->st));
-  // workspaces
+  // workspaces, one set per lane
   const int Mx = kvc->max_rows;
   c->maxM = Mx;
-  const int Kmax = std::max(std::max(H, qN), F);
-  HIPCHK(hipHostMalloc(reinterpret_cast<void**>(&c->rows_h), (size_t)Mx * 5 * sizeof(int32_t), hipHostMallocDefault));
-  HIPCHK(hipHostMalloc(reinterpret_cast<void**>(&c->best_h), (size_t)Mx * sizeof(int32_t), hipHostMallocDefault));
-  int r = 0;
-  if ((r = walloc(c, &c->rows_d, (size_t)Mx * 5)) || (r = walloc(c, &c->resid, (size_t)Mx * H)) ||
-      (r = walloc(c, &c->aq, ifrk::atile_bytes(Mx, Kmax))) || (r = walloc(c, &c->as, (size_t)Mx)) ||
-      (r = walloc(c, &c->gs, (size_t)Mx * (Kmax / 128))) ||
-      (r = walloc(c, &c->qkv, (size_t)Mx * (qN + 2 * kvN))) ||
-      (r = walloc(c, &c->qbuf, (size_t)Mx * qN)) || (r = walloc(c, &c->y, (size_t)Mx * H)) ||
-      (r = walloc(c, &c->mg, (size_t)Mx * F)) || (r = walloc(c, &c->gu, (size_t)Mx * 2 * F)) ||
-      (r = walloc(c, &c->pk.cu_seqlens, (size_t)Mx + 1)) || (r = walloc(c, &c->pk.row_grp, Mx)) ||
-      (r = walloc(c, &c->pk.row_seq, Mx)) || (r = walloc(c, &c->pk.row_pos, Mx)) ||
-      (r = walloc(c, &c->pk.row_kind, Mx)) || (r = walloc(c, &c->pk.comb_base, Mx)) ||
-      (r = walloc(c, &c->pk.comb_nsplit, Mx)) || (r = walloc(c, &c->pk.comb_tok, Mx)) ||
-      (r = walloc(c, &c->pk.want_rows, Mx)) || (r = walloc(c, &c->row_tok, Mx)) ||
-      (r = walloc(c, &c->lm_aq, ifrk::atile_bytes(Mx, H))) || (r = walloc(c, &c->lm_as, (size_t)Mx * (H / 64))) ||
-      (r = walloc(c, &c->best_d, Mx)))
-    return r;
-  const int nparts = ifrk::lmhead_nparts(V);
-  if ((r = walloc(c, &c->lm_pv, (size_t)nparts * Mx)) || (r = walloc(c, &c->lm_pi, (size_t)nparts * Mx)))
-    return r;
   c->max_units = 65536;
-  if ((r = walloc(c, &c->pk.units, c->max_units)) || (r = walloc(c, &c->pk.order, 4 * (size_t)c->max_units)) ||
-      (r = walloc(c, &c->part_o, (size_t)c->max_units * 16 * kAttnTiles * hd)) ||
-      (r = walloc(c, &c->part_ml, (size_t)c->max_units * 16 * kAttnTiles * 2)))
-    return r;
+  const int Kmax = std::max(std::max(H, qN), F);
+  const int nparts = ifrk::lmhead_nparts(V);
+  for (Lane& L : c->lane) {
+    HIPCHK(hipHostMalloc(reinterpret_cast<void**>(&L.rows_h), (size_t)Mx * 5 * sizeof(int32_t), hipHostMallocDefault));
+    HIPCHK(hipHostMalloc(reinterpret_cast<void**>(&L.tok_h), (size_t)Mx * sizeof(int32_t), hipHostMallocDefault));
+    HIPCHK(hipHostMalloc(reinterpret_cast<void**>(&L.best_h), (size_t)Mx * sizeof(int32_t), hipHostMallocDefault));
+    int r = 0;
+    if ((r = walloc(c, &L.rows_d, (size_t)Mx * 5)) || (r = walloc(c, &L.resid, (size_t)Mx * H)) ||
+        (r = walloc(c, &L.aq, ifrk::atile_bytes(Mx, Kmax))) || (r = walloc(c, &L.as, (size_t)Mx)) ||
+        (r = walloc(c, &L.gs, (size_t)Mx * (Kmax / 128))) ||
+        (r = walloc(c, &L.qkv, (size_t)Mx * (qN + 2 * kvN))) ||
+        (r = walloc(c, &L.qbuf, (size_t)Mx * qN)) || (r = walloc(c, &L.y, (size_t)Mx * H)) ||
+        (r = walloc(c, &L.mg, (size_t)Mx * F)) || (r = walloc(c, &L.gu, (size_t)Mx * 2 * F)) ||
+        (r = walloc(c, &L.pk.cu_seqlens, (size_t)Mx + 1)) || (r = walloc(c, &L.pk.row_grp, Mx)) ||
+        (r = walloc(c, &L.pk.row_seq, Mx)) || (r = walloc(c, &L.pk.row_pos, Mx)) ||
+        (r = walloc(c, &L.pk.row_kind, Mx)) || (r = walloc(c, &L.pk.comb_base, Mx)) ||
+        (r = walloc(c, &L.pk.comb_nsplit, Mx)) || (r = walloc(c, &L.pk.comb_tok, Mx)) ||
+        (r = walloc(c, &L.pk.want_rows, Mx)) || (r = walloc(c, &L.row_tok, Mx)) ||
+        (r = walloc(c, &L.lm_aq, ifrk::atile_bytes(Mx, H))) || (r = walloc(c, &L.lm_as, (size_t)Mx * (H / 64))) ||
+        (r = walloc(c, &L.best_d, Mx)) || (r = walloc(c, &L.lm_pv, (size_t)nparts * Mx)) ||
+        (r = walloc(c, &L.lm_pi, (size_t)nparts * Mx)) || (r = walloc(c, &L.pk.units, c->max_units)) ||
+        (r = walloc(c, &L.pk.order, 4 * (size_t)c->max_units)) ||
+        (r = walloc(c, &L.part_o, (size_t)c->max_units * 16 * kAttnTiles * hd)) ||
+        (r = walloc(c, &L.part_ml, (size_t)c->max_units * 16 * kAttnTiles * 2)))
+      return r;
+  }
   HIPCHK(hipStreamSynchronize(c->st));
   c->loaded = true;
   return IFR_OK;
@@ -816,15 +1083,13 @@ int ifr_seq_load_kv(ifr_ctx* c, int32_t slot, int32_t len, const float* k, const
 // ---- forward ---------------------------------------------------------------------------
 
 int ifr_forward(ifr_ctx* c, const ifr_row* rows, int32_t M, int32_t* best_out, float* logits_out) {
+  const auto t_start = std::chrono::steady_clock::now();
   if (!c || !rows || !best_out) return fail(IFR_EINVAL, "null arg");
   if (!c->loaded) return fail(IFR_ESTATE, "no model loaded");
   if (M <= 0 || M > c->maxM) return fail(IFR_EINVAL, "M=%d outside [1, %d]", M, c->maxM);
-  const ifr_model_cfg& cf = c->cfg;
-  const int H = cf.hidden, hd = cf.head_dim, nq = cf.n_heads, nkv = cf.n_kv;
-  const int qN = nq * hd, kvN = nkv * hd, F = cf.inter, V = cf.vocab;
+  const int V = c->cfg.vocab;
   // ---- validate rows (BatchItem rules: one contiguous run per sequence)
   std::vector<int> g_start, g_len, g_pos0, g_seq;
-  std::vector<int> want;
   for (int m = 0; m < M; ++m) {
     const ifr_row& r = rows[m];
     if (r.seq < 0 || r.seq >= (int)c->seqs.size() || !c->seqs[r.seq].open)
@@ -847,10 +1112,8 @@ int ifr_forward(ifr_ctx* c, const ifr_row* rows, int32_t M, int32_t* best_out, f
       if (r.pos != rows[m - 1].pos + 1) return fail(IFR_EINVAL, "row %d: positions not consecutive", m);
       g_len.back() += 1;
     }
-    if (r.want) want.push_back(m);
   }
-  const int nwant = (int)want.size();
-  // ---- pages for every new position
+  // ---- pages for every new position (block table rows go up on lane 0)
   for (size_t g = 0; g < g_seq.size(); ++g) {
     Seq& s = c->seqs[g_seq[g]];
     const int need = (g_pos0[g] + g_len[g] + kPage - 1) / kPage;
@@ -871,199 +1134,66 @@ int ifr_forward(ifr_ctx* c, const ifr_row* rows, int32_t M, int32_t* best_out, f
     if (dirty) {
       const size_t off = (size_t)g_seq[g] * c->max_pages;
       HIPCHK(hipMemcpyAsync(c->bt_d + off, c->bt_h + off, c->max_pages * sizeof(int32_t),
-                            hipMemcpyHostToDevice, c->st));
+                            hipMemcpyHostToDevice, c->lane[0].st));
     }
   }
-  // ---- KV split: fixed, so each row's partial decomposition depends only on
-  // its own sequence (batch-invariant results: split == joint, solo == loaded)
-  int split = c->kv.attn_split > 0 ? c->kv.attn_split : kSplit;
-  long nunits = count_units(g_pos0, g_len, nkv, split, c->qb);
-  while (nunits > c->max_units) {
-    split *= 2;
-    nunits = count_units(g_pos0, g_len, nkv, split, c->qb);
-  }
-  c->last_split = split;
-  c->last_units = (int)nunits;
-  long nchunked = 0;
-  const int nslots = (int)ifrk::attn_slot_count(g_pos0.data(), g_len.data(), (int)g_len.size(), nkv, split,
-                                                c->qb, &nchunked);
-  c->last_slots = nslots;
-  // ---- upload rows, pack
-  std::memcpy(c->rows_h, rows, (size_t)M * sizeof(ifr_row));
-  HIPCHK(hipMemcpyAsync(c->rows_d, c->rows_h, (size_t)M * sizeof(ifr_row), hipMemcpyHostToDevice, c->st));
-  {
-    Scope sc(c, "pack", 0);
-    HIPCHK(ifrk::launch_pack(c->rows_d, M, nkv, c->qb, split, c->pk, c->st));
-  }
-  // tokens column of the rows (stride 5) for the embedding gather
-  std::vector<int32_t> tok(M);
-  for (int m = 0; m < M; ++m) tok[m] = rows[m].token;
-  HIPCHK(hipMemcpyAsync(c->row_tok, tok.data(), M * sizeof(int32_t), hipMemcpyHostToDevice, c->st));
-  double attn_bytes = 0, attn_flops = 0;
-  attn_work(c, rows, M, g_pos0, g_len, &attn_bytes, &attn_flops);
-  const int ng_h = H / 128;
-  for (int l = 0; l < cf.layers; ++l) {
-    Layer& ly = c->layers[l];
-    ifrk::KVLayout kv{nkv, hd, kPage, c->max_pages, c->kv.kv_int8, c->kpool[l], c->vpool[l],
-                      c->kscale[l], c->vscale[l], c->bt_d};
-    // (1) layer input: embed (l == 0) or residual += FWHT(down out); RMSNorm; FWHT; quant
-    {
-      ifrk::RowQuantArgs a{};
-      if (l == 0) {
-        a.src = ifrk::SRC_EMBED;
-        a.embed = c->embed;
-        a.tokens = c->row_tok;
-      } else {
-        a.src = ifrk::SRC_RESID;
-        a.y = c->y;
-        a.rot_y = cf.rotate;
-      }
-      a.resid = c->resid;
-      a.norm_w = ly.in_ln;
-      a.eps = cf.rms_eps;
-      a.rotate = cf.rotate;
-      a.round = 0;
-      a.ga = 0;
-      a.q = c->aq;
-      a.qscale = c->as;
-      a.gsum = c->gs;
-      a.M = M;
-      a.K = H;
-      Scope sc(c, "row_quant", (double)M * H * 4 * 2);
-      HIPCHK(ifrk::launch_row_quant(a, c->st));
-    }
-    // (2) QKV
-    for (int j = 0; j < ly.nqkv; ++j) {
-      ifrk::QGemmArgs a{c->aq, c->as, c->gs, c->qkv + ly.qkv_off[j], nullptr, M, qN + 2 * kvN};
-      Scope sc(c, "qgemm_qkv", (double)ly.qkv[j].bytes + (double)M * (H + 4) + (double)M * ly.qkv[j].N * 2,
-               2.0 * M * ly.qkv[j].N * H);
-      HIPCHK(ifrk::launch_qgemm(ly.qkv[j], a, c->st));
-    }
-    // (3) q/k norm + RoPE + KV append
-    {
-      ifrk::QKArgs a{c->qkv, c->pk.row_seq, c->pk.row_pos, ly.q_norm, ly.k_norm, c->rope_cos,
-                     c->rope_sin, cf.rotary_dim, cf.rms_eps, nq, c->qbuf, M};
-      Scope sc(c, "qk_rope_kv", (double)M * (qN + 2 * kvN) * 2 * 2);
-      HIPCHK(ifrk::launch_qk_rope_kv(a, kv, c->st));
-    }
-    // (4) attention + combine (emits the O-proj int8 input)
-    {
-      ifrk::AttnArgs a{c->pk.units, (int)nunits, c->pk.order, nslots, c->kv.kv_int8 ? 0 : (int)nchunked, c->qbuf, nq, 1.4426950408889634f / std::sqrt((float)hd),
-                       c->part_o, c->part_ml, kAttnTiles};
-      Scope sc(c, "attention", attn_bytes, attn_flops);
-      HIPCHK(ifrk::launch_attention(a, kv, c->st));
-    }
-    {
-      ifrk::CombineArgs a{c->part_o, c->part_ml, c->pk.comb_base, c->pk.comb_nsplit, c->pk.comb_tok,
-                          M, nq, nkv, hd, nullptr, c->aq, c->as, c->gs, 16 * kAttnTiles};
-      Scope sc(c, "combine", 0);
-      HIPCHK(ifrk::launch_combine(a, c->st));
-    }
-    // (5) O projection
-    {
-      ifrk::QGemmArgs a{c->aq, c->as, c->gs, c->y, nullptr, M, H};
-      Scope sc(c, "qgemm_o", (double)ly.o.bytes + (double)M * (qN + 4) + (double)M * H * 2,
-               2.0 * M * H * qN);
-      HIPCHK(ifrk::launch_qgemm(ly.o, a, c->st));
-    }
-    // (6) residual += FWHT(o); post norm; FWHT; quant
-    {
-      ifrk::RowQuantArgs a{};
-      a.src = ifrk::SRC_RESID;
-      a.y = c->y;
-      a.rot_y = cf.rotate;
-      a.resid = c->resid;
-      a.norm_w = ly.post_ln;
-      a.eps = cf.rms_eps;
-      a.rotate = cf.rotate;
-      a.q = c->aq;
-      a.qscale = c->as;
-      a.gsum = c->gs;
-      a.M = M;
-      a.K = H;
-      Scope sc(c, "row_quant", (double)M * H * 4 * 2);
-      HIPCHK(ifrk::launch_row_quant(a, c->st));
-    }
-    // (7) gate/up + SwiGLU
-    if (ly.ngu == 1) {
-      ifrk::QGemmArgs a{c->aq, c->as, c->gs, c->mg, nullptr, M, F};
-      Scope sc(c, "qgemm_gate_up", (double)ly.gu[0].bytes + (double)M * (H + 4) + (double)M * F * 2,
-               2.0 * M * 2 * F * H);
-      HIPCHK(ifrk::launch_qgemm(ly.gu[0], a, c->st));
-    } else {
-      for (int j = 0; j < 2; ++j) {
-        ifrk::QGemmArgs a{c->aq, c->as, c->gs, c->gu + j * F, nullptr, M, 2 * F};
-        Scope sc(c, "qgemm_gate_up", (double)ly.gu[j].bytes + (double)M * (H + 4) + (double)M * F * 2,
-                 2.0 * M * F * H);
-        HIPCHK(ifrk::launch_qgemm(ly.gu[j], a, c->st));
-      }
-      HIPCHK(ifrk::launch_swiglu(c->gu, M, F, c->mg, c->st));
-    }
-    // (8) quantize mg, down projection
-    {
-      Scope sc(c, "quant_plain", (double)M * F * 3);
-      HIPCHK(ifrk::launch_quant_plain(nullptr, c->mg, M, F, c->aq, c->as, c->gs, c->st));
-    }
-    {
-      ifrk::QGemmArgs a{c->aq, c->as, c->gs, c->y, nullptr, M, H};
-      Scope sc(c, "qgemm_down", (double)ly.down.bytes + (double)M * (F + 4) + (double)M * H * 2,
-               2.0 * M * H * F);
-      HIPCHK(ifrk::launch_qgemm(ly.down, a, c->st));
+  // ---- cut into sub-batches: [decode / verify rows | prefill chunks], or
+  // decode rows halved by KV length; one sub-batch when timing each kernel
+  const int ng = (int)g_len.size();
+  int cut = ng;  // first group of lane 1
+  if (!c->timing && c->kv.lanes == 2 && ng >= 2) {
+    int first_chunk = ng;
+    for (int g = 0; g < ng; ++g)
+      if (g_len[g] >= kChunkRows) { first_chunk = g; break; }
+    if (first_chunk > 0 && first_chunk < ng) {
+      cut = first_chunk;
+    } else if (first_chunk == ng && M >= kMinSplitRows) {
+      double tot = 0, run = 0;
+      for (int g = 0; g < ng; ++g) tot += g_pos0[g] + g_len[g];
+      for (cut = 0; cut < ng - 1 && run + 0.5 * (g_pos0[cut] + g_len[cut]) < 0.5 * tot; ++cut)
+        run += g_pos0[cut] + g_len[cut];
+      if (cut == 0) cut = 1;
     }
   }
-  (void)ng_h;
-  // ---- final residual, norm, lm_head on the scored rows
+  std::vector<SubBatch> sbs;
+  for (int h = 0; h < 2; ++h) {
+    const int ga = h == 0 ? 0 : cut, gb = h == 0 ? cut : ng;
+    if (ga >= gb) continue;
+    SubBatch sb;
+    sb.lane = h;
+    sb.row0 = g_start[ga];
+    sb.M = (gb < ng ? g_start[gb] : M) - sb.row0;
+    sb.g_pos0.assign(g_pos0.begin() + ga, g_pos0.begin() + gb);
+    sb.g_len.assign(g_len.begin() + ga, g_len.begin() + gb);
+    if (int r = prep_sub(c, rows, sb)) return r;
+    sbs.push_back(std::move(sb));
+  }
+  c->last_lanes = (int)sbs.size();
+  if (sbs.size() == 2) {
+    HIPCHK(hipEventRecord(c->ev_bt, c->lane[0].st));
+    HIPCHK(hipStreamWaitEvent(c->lane[1].st, c->ev_bt, 0));
+  }
+  // ---- enqueue: heads, then layer by layer alternating lanes, then tails
+  for (SubBatch& sb : sbs)
+    if (int r = launch_head(c, rows, sb)) return r;
+  for (int l = 0; l < c->cfg.layers; ++l)
+    for (SubBatch& sb : sbs)
+      if (int r = launch_layer(c, sb, l)) return r;
+  int want_off = 0;
+  for (SubBatch& sb : sbs) {
+    if (int r = launch_tail(c, sb, logits_out ? logits_out + (size_t)want_off * V : nullptr)) return r;
+    want_off += (int)sb.want.size();
+  }
+  const auto t_sub = std::chrono::steady_clock::now();
+  for (SubBatch& sb : sbs) HIPCHK(hipStreamSynchronize(c->lane[sb.lane].st));
+  const auto t_end = std::chrono::steady_clock::now();
+  // host buckets (the reference engine's submit / waitblock profile,
+  // engine.hpp:567-630), kept whether or not kernels are timed
+  add_host_time(c, "host_submit", std::chrono::duration<double, std::milli>(t_sub - t_start).count());
+  add_host_time(c, "host_wait", std::chrono::duration<double, std::milli>(t_end - t_sub).count());
   for (int m = 0; m < M; ++m) best_out[m] = -1;
-  if (nwant > 0) {
-    {
-      ifrk::RowQuantArgs a{};
-      a.src = ifrk::SRC_RESID;
-      a.y = c->y;
-      a.rot_y = cf.rotate;
-      a.resid = c->resid;
-      a.rowmap = c->pk.want_rows;
-      a.norm_w = c->final_norm;
-      a.eps = cf.rms_eps;
-      a.rotate = 0;
-      a.round = 1;
-      a.ga = 64;
-      a.q = c->lm_aq;
-      a.qscale = c->lm_as;
-      a.gsum = nullptr;
-      a.M = nwant;
-      a.K = H;
-      Scope sc(c, "row_quant", (double)nwant * H * 4 * 2);
-      HIPCHK(ifrk::launch_row_quant(a, c->st));
-    }
-    if (logits_out && c->logits_cap < (size_t)nwant * V) {
-      if (c->logits_d) hipFree(c->logits_d);
-      c->logits_d = nullptr;
-      HIPCHK(hipMalloc(reinterpret_cast<void**>(&c->logits_d), (size_t)nwant * V * sizeof(float)));
-      c->logits_cap = (size_t)nwant * V;
-    }
-    ifrk::LmHeadArgs a{};
-    a.a = c->lm_aq;
-    a.as = c->lm_as;
-    a.wcodes = c->lm_w;
-    a.wscale = c->lm_s;
-    a.W = nwant;
-    a.V = V;
-    a.H = H;
-    a.logits = logits_out ? c->logits_d : nullptr;
-    a.part_val = c->lm_pv;
-    a.part_idx = c->lm_pi;
-    a.best = c->best_d;
-    {
-      Scope sc(c, "lmhead", (double)V * H + (double)V * 2 + (double)nwant * H);
-      HIPCHK(ifrk::launch_lmhead(a, c->st));
-    }
-    HIPCHK(hipMemcpyAsync(c->best_h, c->best_d, nwant * sizeof(int32_t), hipMemcpyDeviceToHost, c->st));
-    if (logits_out)
-      HIPCHK(hipMemcpyAsync(logits_out, c->logits_d, (size_t)nwant * V * sizeof(float),
-                            hipMemcpyDeviceToHost, c->st));
-  }
-  HIPCHK(hipStreamSynchronize(c->st));
-  for (int i = 0; i < nwant; ++i) best_out[want[i]] = c->best_h[i];
+  for (const SubBatch& sb : sbs)
+    for (size_t i = 0; i < sb.want.size(); ++i) best_out[sb.row0 + sb.want[i]] = c->lane[sb.lane].best_h[i];
   for (size_t g = 0; g < g_seq.size(); ++g) c->seqs[g_seq[g]].len = g_pos0[g] + g_len[g];
   if (c->timing) flush_timers(c);
   return IFR_OK;
@@ -1107,27 +1237,27 @@ int ifr_attention(ifr_ctx* c, int32_t layer, const ifr_row* rows, int32_t M, con
   const int nslots = (int)ifrk::attn_slot_count(g_pos0.data(), g_len.data(), (int)g_len.size(), nkv, split,
                                                 c->qb, &nchunked);
   c->last_slots = nslots;
-  std::memcpy(c->rows_h, rows, (size_t)M * sizeof(ifr_row));
-  HIPCHK(hipMemcpyAsync(c->rows_d, c->rows_h, (size_t)M * sizeof(ifr_row), hipMemcpyHostToDevice, c->st));
-  HIPCHK(ifrk::launch_pack(c->rows_d, M, nkv, c->qb, split, c->pk, c->st));
-  HIPCHK(hipMemcpyAsync(c->qbuf, q_h, (size_t)M * nq * hd * 2, hipMemcpyHostToDevice, c->st));
+  std::memcpy(c->lane[0].rows_h, rows, (size_t)M * sizeof(ifr_row));
+  HIPCHK(hipMemcpyAsync(c->lane[0].rows_d, c->lane[0].rows_h, (size_t)M * sizeof(ifr_row), hipMemcpyHostToDevice, c->st));
+  HIPCHK(ifrk::launch_pack(c->lane[0].rows_d, M, nkv, c->qb, split, c->lane[0].pk, c->st));
+  HIPCHK(hipMemcpyAsync(c->lane[0].qbuf, q_h, (size_t)M * nq * hd * 2, hipMemcpyHostToDevice, c->st));
   ifrk::KVLayout kv{nkv, hd, kPage, c->max_pages, c->kv.kv_int8, c->kpool[layer], c->vpool[layer],
                     c->kscale[layer], c->vscale[layer], c->bt_d};
-  ifrk::AttnArgs a{c->pk.units, (int)nunits, c->pk.order, nslots, c->kv.kv_int8 ? 0 : (int)nchunked, c->qbuf, nq, 1.4426950408889634f / std::sqrt((float)hd),
-                   c->part_o, c->part_ml, kAttnTiles};
+  ifrk::AttnArgs a{c->lane[0].pk.units, (int)nunits, c->lane[0].pk.order, nslots, c->kv.kv_int8 ? 0 : (int)nchunked, c->lane[0].qbuf, nq, 1.4426950408889634f / std::sqrt((float)hd),
+                   c->lane[0].part_o, c->lane[0].part_ml, kAttnTiles};
   double attn_bytes = 0, attn_flops = 0;
   attn_work(c, rows, M, g_pos0, g_len, &attn_bytes, &attn_flops);
   {
-    Scope sc(c, "attention", attn_bytes, attn_flops);
+    Scope sc(c, c->st, "attention", attn_bytes, attn_flops);
     HIPCHK(ifrk::launch_attention(a, kv, c->st));
   }
   float* out_d = nullptr;
   HIPCHK(hipMalloc(reinterpret_cast<void**>(&out_d), (size_t)M * nq * hd * sizeof(float)));
-  ifrk::CombineArgs cb{c->part_o, c->part_ml, c->pk.comb_base, c->pk.comb_nsplit, c->pk.comb_tok,
-                       M, nq, nkv, hd, out_d, c->aq, c->as, c->gs, 16 * kAttnTiles};
+  ifrk::CombineArgs cb{c->lane[0].part_o, c->lane[0].part_ml, c->lane[0].pk.comb_base, c->lane[0].pk.comb_nsplit, c->lane[0].pk.comb_tok,
+                       M, nq, nkv, hd, out_d, c->lane[0].aq, c->lane[0].as, c->lane[0].gs, 16 * kAttnTiles};
   hipError_t e;
   {
-    Scope sc(c, "combine", 0);
+    Scope sc(c, c->st, "combine", 0);
     e = ifrk::launch_combine(cb, c->st);
   }
   if (e == hipSuccess) e = hipMemcpyAsync(out_h, out_d, (size_t)M * nq * hd * sizeof(float), hipMemcpyDeviceToHost, c->st);
@@ -1163,12 +1293,18 @@ int ifr_get_timing(ifr_ctx* c, const char* kernel, double* total_ms, int64_t* la
   return IFR_OK;
 }
 
+int ifr_debug_last_lanes(ifr_ctx* c, int32_t* lanes) {
+  if (!c || !lanes) return fail(IFR_EINVAL, "null arg");
+  *lanes = c->last_lanes;
+  return IFR_OK;
+}
+
 int ifr_debug_attn_order(ifr_ctx* c, int32_t* order, int32_t cap, int32_t* n_slots) {
   if (!c || !n_slots) return fail(IFR_EINVAL, "null arg");
   HIPCHK(hipStreamSynchronize(c->st));
   *n_slots = c->last_slots;
   if (order && cap > 0)
-    HIPCHK(hipMemcpy(order, c->pk.order, (size_t)std::min(cap, c->last_slots) * 4, hipMemcpyDeviceToHost));
+    HIPCHK(hipMemcpy(order, c->lane[0].pk.order, (size_t)std::min(cap, c->last_slots) * 4, hipMemcpyDeviceToHost));
   return IFR_OK;
 }
 
@@ -1178,12 +1314,12 @@ int ifr_debug_pack(ifr_ctx* c, int32_t M, int32_t* cu, int32_t* row_grp, int32_t
                    int32_t* split) {
   if (!c || !c->loaded) return fail(IFR_ESTATE, "no model loaded");
   HIPCHK(hipStreamSynchronize(c->st));
-  if (cu) HIPCHK(hipMemcpy(cu, c->pk.cu_seqlens, (M + 1) * 4, hipMemcpyDeviceToHost));
-  if (row_grp) HIPCHK(hipMemcpy(row_grp, c->pk.row_grp, M * 4, hipMemcpyDeviceToHost));
-  if (comb_base) HIPCHK(hipMemcpy(comb_base, c->pk.comb_base, M * 4, hipMemcpyDeviceToHost));
-  if (comb_nsplit) HIPCHK(hipMemcpy(comb_nsplit, c->pk.comb_nsplit, M * 4, hipMemcpyDeviceToHost));
-  if (comb_tok) HIPCHK(hipMemcpy(comb_tok, c->pk.comb_tok, M * 4, hipMemcpyDeviceToHost));
-  if (units) HIPCHK(hipMemcpy(units, c->pk.units, (size_t)c->last_units * sizeof(ifrk::AttnUnit), hipMemcpyDeviceToHost));
+  if (cu) HIPCHK(hipMemcpy(cu, c->lane[0].pk.cu_seqlens, (M + 1) * 4, hipMemcpyDeviceToHost));
+  if (row_grp) HIPCHK(hipMemcpy(row_grp, c->lane[0].pk.row_grp, M * 4, hipMemcpyDeviceToHost));
+  if (comb_base) HIPCHK(hipMemcpy(comb_base, c->lane[0].pk.comb_base, M * 4, hipMemcpyDeviceToHost));
+  if (comb_nsplit) HIPCHK(hipMemcpy(comb_nsplit, c->lane[0].pk.comb_nsplit, M * 4, hipMemcpyDeviceToHost));
+  if (comb_tok) HIPCHK(hipMemcpy(comb_tok, c->lane[0].pk.comb_tok, M * 4, hipMemcpyDeviceToHost));
+  if (units) HIPCHK(hipMemcpy(units, c->lane[0].pk.units, (size_t)c->last_units * sizeof(ifrk::AttnUnit), hipMemcpyDeviceToHost));
   if (n_units) *n_units = c->last_units;
   if (split) *split = c->last_split;
   return IFR_OK;

@@ -492,6 +492,9 @@ hipError_t hipEventCreate(hipEvent_t* e) {
   *e = reinterpret_cast<hipEvent_t>(new double(0.0));
   return hipSuccess;
 }
+hipError_t hipEventCreateWithFlags(hipEvent_t* e, unsigned) { return hipEventCreate(e); }
+// launches run synchronously in the emulation, so stream order is program order
+hipError_t hipStreamWaitEvent(hipStream_t, hipEvent_t, unsigned) { return hipSuccess; }
 hipError_t hipEventDestroy(hipEvent_t e) {
   delete reinterpret_cast<double*>(e);
   return hipSuccess;

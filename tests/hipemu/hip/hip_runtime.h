@@ -45,6 +45,7 @@ enum hipMemcpyKind {
 };
 enum { hipStreamDefault = 0, hipStreamNonBlocking = 1 };
 enum { hipHostMallocDefault = 0 };
+enum { hipEventDefault = 0, hipEventDisableTiming = 2 };
 enum hipFuncAttribute { hipFuncAttributeMaxDynamicSharedMemorySize = 8 };
 
 struct hipDeviceProp_t {
@@ -223,6 +224,8 @@ hipError_t hipStreamDestroy(hipStream_t s);
 hipError_t hipStreamSynchronize(hipStream_t s);
 hipError_t hipDeviceSynchronize();
 hipError_t hipEventCreate(hipEvent_t* e);
+hipError_t hipEventCreateWithFlags(hipEvent_t* e, unsigned flags);
+hipError_t hipStreamWaitEvent(hipStream_t s, hipEvent_t e, unsigned flags);
 hipError_t hipEventDestroy(hipEvent_t e);
 hipError_t hipEventRecord(hipEvent_t e, hipStream_t s = nullptr);
 hipError_t hipEventSynchronize(hipEvent_t e);

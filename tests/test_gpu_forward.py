@@ -19,6 +19,8 @@ against the oracle except attention (fp32-accurate, not bit-identical), so:
     can only happen where the oracle's top-2 margin is below the two logits'
     error difference, which the bounds already limit; the count is reported.
 """
+import ctypes as C
+
 import numpy as np
 import pytest
 
@@ -138,6 +140,49 @@ def test_cfg1_mixed_iteration_and_greedy64(dev, model, kv_int8):
     assert agree >= MIN_AGREE * 320
     # a non-degenerate stream: the model does not just repeat a few tokens
     assert len(set(np.array(stream).reshape(-1).tolist())) > 20
+
+
+def _lanes(eng):
+    n = C.c_int32()
+    ia.check(ia.lib().ifr_debug_last_lanes(eng.dev.ctx, C.byref(n)), "lanes")
+    return n.value
+
+
+def test_two_lanes_match_one_lane(dev, model):
+    """A forward cut into two sub-batches on the context's two streams gives
+    bit-identical logits to the same forward on one stream (per-kernel
+    timing runs every batch on one lane): [decode rows | prefill chunk] and
+    decode rows halved."""
+    cfg = model.cfg
+    eng = ia.Engine(dev, model, max_seqs=24, max_seq_tokens=2048, pool_tokens=24 * 2048, max_rows=128,
+                    lanes=2)
+    rng = np.random.default_rng(17)
+    lens = rng.integers(20, 1500, size=20).tolist()
+    seqs = []
+    for n in lens:
+        s = eng.seq_open()
+        k = rng.standard_normal((cfg.layers, n, cfg.n_kv, cfg.head_dim), dtype=np.float32)
+        eng.load_kv(s, k, k)
+        seqs.append(s)
+    pre = eng.seq_open()
+    toks = rng.integers(0, cfg.vocab, size=len(lens) + 50).tolist()
+    cases = {"decode+chunk": [(s, n, toks[i], 0, 1) for i, (s, n) in enumerate(zip(seqs[:4], lens[:4]))] +
+             [(pre, p, toks[20 + p], 1, int(p == 49)) for p in range(50)],
+             "decode halves": [(s, n, toks[i], 0, 1) for i, (s, n) in enumerate(zip(seqs, lens))]}
+    for name, rows in cases.items():
+        announce(f"two lanes vs one: {name}")
+        outs = []
+        for timing in (True, False):
+            eng.set_timing(timing)
+            b, lg = eng.forward(rows, logits=True)
+            outs.append((b, lg, _lanes(eng)))
+            eng.set_timing(False)
+            for s, n in zip(seqs, lens):
+                eng.seq_truncate(s, n)
+            eng.seq_truncate(pre, 0)
+        (b1, l1, n1), (b2, l2, n2) = outs
+        assert n1 == 1 and n2 == 2, (name, n1, n2)
+        assert np.array_equal(b1, b2) and np.array_equal(l1.view(np.uint32), l2.view(np.uint32)), name
 
 
 def test_split_equals_joint_and_solo_equals_loaded(dev, model):
