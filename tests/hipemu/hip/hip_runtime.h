@@ -165,6 +165,16 @@ inline T __shfl(T v, int src, int width = 64) {
   return emu::lane_value<T>(s, base + (src % width));
 }
 
+inline unsigned long long __ballot(int pred) {
+  const uint64_t live = emu::live_mask_of_current_wave();
+  const int v = pred != 0;
+  const unsigned char* s = emu::wave_exchange(&v, 4, emu::kOpShfl);
+  unsigned long long m = 0;
+  for (int l = 0; l < 64; ++l)
+    if (((live >> l) & 1) && emu::lane_value<int>(s, l)) m |= 1ull << l;
+  return m;
+}
+
 inline int emu_readlane(int v, int l) {
   const unsigned char* s = emu::wave_exchange(&v, 4, emu::kOpReadlane);
   return emu::lane_value<int>(s, l);
