@@ -65,14 +65,17 @@ typedef struct ifr_model_cfg {
  *           reference packing, src/quant/dashq.cpp:387-402, applied row-major)
  *   scale : fp16 [N][K/group]
  *   zero  : fp16 [N][K/group]
- * Dequantized weight: w(n,k) = scale(n,g) * (code(n,k) - zero(n,g)), g = k/group.
- * The reference codebook (dashq.cpp:405-417, (2c-C)/C) is the special case
- * zero = C/2, scale = 2*s_ref/C with C = 2^b - 1. */
+ *   post  : fp32 factor on every output of the linear (0 is read as 1)
+ * Dequantized weight: w(n,k) = post * scale(n,g) * (code(n,k) - zero(n,g)),
+ * g = k/group.  The reference codebook (dashq.cpp:405-417, (2c-C)/C with
+ * C = 2^b - 1) scaled by s_g * alpha (dashq.cpp:531-575) is the special case
+ * scale = s_g, zero = C/2, post = 2*alpha/C: every factor is stored exactly. */
 typedef struct ifr_linear {
   int32_t N, K, bits, group;
   const uint8_t* codes;
   const uint16_t* scale;
   const uint16_t* zero;
+  float post;
 } ifr_linear;
 
 typedef struct ifr_layer_w {
@@ -85,17 +88,25 @@ typedef struct ifr_layer_w {
 
 typedef struct ifr_host_model {
   ifr_model_cfg cfg;
-  const float* embed;      /* [vocab][hidden] fp32, tied with lm_head */
+  const float* embed;      /* [vocab][hidden] fp32 */
   const float* final_norm; /* [hidden] */
   const ifr_layer_w* layers; /* [layers] */
+  const float* lm_head;    /* [vocab][hidden] untied output projection; NULL:
+                            * tied with embed (the 0.8B case, main.cpp:8302-8307) */
 } ifr_host_model;
 
 /* Synthetic seeded model (portable splitmix64 + Box-Muller; see the
  * generator source for distributions).  bits_mode 2 or 4 = every linear at
  * that width; bits_mode 0 = seeded per-tensor 70 % INT2 / 30 % INT4 split.
- * The returned model owns its buffers; free with ifr_synth_free. */
+ * OR-ing IFR_SYNTH_INTFER into bits_mode draws the weights in the form the
+ * .intfer container stores exactly: one fp16 scale per K-group shared by
+ * all rows, zero = C/2, post = 2/C, embedding and norms rounded to fp16.
+ * The returned model owns its buffers; free with ifr_host_model_free. */
+#define IFR_SYNTH_INTFER 0x100
 ifr_host_model* ifr_synth_model(const ifr_model_cfg* cfg, uint64_t seed, int32_t bits_mode);
-void ifr_synth_free(ifr_host_model* m);
+/* Frees a model returned by ifr_synth_model or ifr_intfer_host_model. */
+void ifr_host_model_free(ifr_host_model* m);
+void ifr_synth_free(ifr_host_model* m); /* same as ifr_host_model_free */
 
 /* Default 0.8B-class configuration. */
 void ifr_default_cfg(ifr_model_cfg* out);
@@ -176,7 +187,7 @@ int ifr_act_quant(ifr_ctx* ctx, const float* x_d, int32_t M, int32_t K,
  *   S(m,g)   = sum_{k in g} a_q(m,k)                         (gsum_d)
  *   acc(m,n) = fold over g ascending of
  *                d = fma(-zero(n,g), S(m,g), T(m,n,g)); acc = fma(scale(n,g), d, acc)
- *   y(m,n)   = fp16_rne(ascale(m) * acc(m,n))
+ *   y(m,n)   = fp16_rne((ascale(m) * post) * acc(m,n))
  * a_d holds the int8 activations in the A-tile layout (IFR_ATILE_OFF), as
  * ifr_act_quant writes them.  out_d fp16 [M][N].  tdump_d, if non-NULL,
  * receives T as int32 [M][N][K/128]. */
@@ -301,6 +312,112 @@ int ifr_debug_attn_order(ifr_ctx* ctx, int32_t* order, int32_t cap, int32_t* n_s
  * is cut into [decode / verify rows | prefill chunks], or decode rows are
  * halved by KV length; while per-kernel timing is on, every batch runs as one. */
 int ifr_debug_last_lanes(ifr_ctx* ctx, int32_t* lanes);
+
+/* ------------------------------------------------------------------------
+ * .intfer model files (the INTFER1 container of ModelIR + RotationSet).
+ *
+ * Layout (writer src/quant/output.cpp:396-482, reader :484-595): a 54-byte
+ * little-endian header {"INTFER1\0", u32 version, u32 n_tensors, u64
+ * code_len, u64 scale_len, u64 global_len, u32 n_rotations, u16 reserved,
+ * u64 json_len}; json_len bytes of JSON metadata (model_id, n_layers,
+ * version, tensors[], rotations[]); the code, scale and global regions; the
+ * fp32 rotation matrices (dim x dim, row-major, at each rotation's offset).
+ * A quantized tensor's codes are group-major, idx[g*N*G + n*G + (k - g*G)],
+ * packed least-significant bits first (dashq.cpp:387-402, :636-672); its
+ * scales are one fp16 per K-group shared by all N rows; its global region
+ * optionally holds an fp32 alpha.  FP16 tensors hold raw fp16 [N][K].
+ * ---------------------------------------------------------------------- */
+/* QuantScheme, TensorRole and RotationSite values of include/intfer/quant_spec.h:13-33
+ * and include/intfer/spinquant.hpp:45. */
+enum { IFR_SCHEME_FP16 = 0, IFR_SCHEME_INT8 = 1, IFR_SCHEME_INT4 = 2, IFR_SCHEME_INT2 = 3 };
+enum {
+  IFR_ROLE_EMBED = 0, IFR_ROLE_LM_HEAD = 1, IFR_ROLE_ATTN_Q = 2, IFR_ROLE_ATTN_K = 3,
+  IFR_ROLE_ATTN_V = 4, IFR_ROLE_ATTN_O = 5, IFR_ROLE_MLP_GATE = 6, IFR_ROLE_MLP_UP = 7,
+  IFR_ROLE_MLP_DOWN = 8, IFR_ROLE_NORM = 9, IFR_ROLE_ROPE = 10, IFR_ROLE_OTHER = 17
+};
+enum { IFR_SITE_QKV = 0, IFR_SITE_O = 1, IFR_SITE_FFN_IN = 2, IFR_SITE_FFN_OUT = 3, IFR_SITE_NONE = 4 };
+
+typedef struct ifr_intfer ifr_intfer;
+
+/* One TensorIR entry (quant_spec.h:48-72) as stored in the file. */
+typedef struct ifr_intfer_tensor {
+  const char* name;  /* valid while the handle lives */
+  int32_t role;      /* IFR_ROLE_* (names outside the table read as OTHER) */
+  int32_t N, K;
+  int32_t scheme;    /* IFR_SCHEME_* */
+  int32_t group_size;
+  int32_t scale_dtype;        /* 0 FP16, 1 FP8_E4M3 */
+  int32_t has_global_divisor;
+  int32_t act;                /* 0 FP16, 1 BF16, 2 INT8_G64 (recorded, not used) */
+  int32_t rotation_id;
+  uint64_t code_offset, code_bytes, scale_offset, scale_bytes, global_offset, global_bytes;
+  float est_error;
+} ifr_intfer_tensor;
+
+typedef struct ifr_intfer_rotation {
+  int32_t id, site, dim;
+  int32_t hadamard; /* 1: exactly the canonical Sylvester H_p / sqrt(p) (with an
+                     * identity tail past p = the largest power of two <= dim),
+                     * the only rotation the quantizer emits (spinquant.cpp:99-125) */
+} ifr_intfer_rotation;
+
+/* Parse a file image (deserialize_intfer_borrowed, output.cpp:484-603).  The
+ * handle borrows blob, which must outlive it.  IFR_EINVAL for a malformed or
+ * truncated image (the reference's `false`). */
+int ifr_intfer_open(const void* blob, size_t n, ifr_intfer** out);
+int ifr_intfer_close(ifr_intfer* f);
+/* Counts and the JSON's model_id (copied NUL-terminated into buf[0..cap)). */
+int ifr_intfer_counts(const ifr_intfer* f, int32_t* n_tensors, int32_t* n_rotations,
+                      int32_t* n_layers);
+int ifr_intfer_model_id(const ifr_intfer* f, char* buf, size_t cap);
+int ifr_intfer_tensor_info(const ifr_intfer* f, int32_t i, ifr_intfer_tensor* out);
+/* Index of the tensor named `name` (the last one, if repeated); IFR_EINVAL if absent. */
+int ifr_intfer_find(const ifr_intfer* f, const char* name, int32_t* index);
+/* Rotation i; mat (may be NULL) receives its dim*dim fp32 matrix. */
+int ifr_intfer_rotation_info(const ifr_intfer* f, int32_t i, ifr_intfer_rotation* out, float* mat);
+/* Dequantize tensor i to fp32 [N][K] (dequant_tensor, dashq.cpp:696-707,
+ * QuantResult::dequant :531-575): w = (fp16(s_g) * alpha) * cb[code] with
+ * the canonical codebook cb[c] = (2c - C)/C (INT2 {-1, -1/3, 1/3, 1},
+ * :405-417), or the raw fp16 value for an FP16 tensor. */
+int ifr_intfer_dequant(const ifr_intfer* f, int32_t i, float* out);
+
+/* Build a host model from the file for the architecture `cfg` (the
+ * reference reads it from config.json, main.cpp:10705-10755).  Tensors are
+ * found by their Hugging Face names (main.cpp:4225-4270, :10838-10870):
+ * model.language_model.{embed_tokens,norm}.weight, [model.language_model.]
+ * lm_head.weight (optional, else tied), and per layer L
+ * model.language_model.layers.L.{input_layernorm,post_attention_layernorm,
+ * self_attn.q_norm,self_attn.k_norm,self_attn.{q,k,v,o}_proj,
+ * mlp.{gate,up,down}_proj}.weight.  Linears are mapped exactly (row-major
+ * codes, scale(n,g) = s_g, zero = C/2, post = 2*alpha/C, shard_weight
+ * engine.cpp:434-549); FP16 or quantized embeddings and norms are
+ * dequantized to fp32.  cfg->rotate is set from the file: 1 when every
+ * linear's rotation (looked up by rotation_id, main.cpp:839-850) is the
+ * canonical Hadamard of the hidden size, 0 when none has one.
+ * IFR_EDECLINE for content this engine does not run: FP16 / FP8-scale /
+ * non-128-group linears, gated q_proj (2 * n_heads * head_dim rows), dense
+ * rotations, or a mix of rotated and unrotated linears.  Free the model
+ * with ifr_host_model_free; it does not borrow the file. */
+int ifr_intfer_host_model(const ifr_intfer* f, const ifr_model_cfg* cfg, ifr_host_model** out);
+
+/* Serialize a host model (serialize_intfer, output.cpp:396-482, byte for
+ * byte the reference writer's output for the same ModelIR).  Each linear
+ * must have the container's form (one scale per group for all rows, zero =
+ * C/2, group 128; else IFR_EDECLINE); alpha = post*C/2 is written as a
+ * global divisor unless it is 1.  Embedding, norms and lm_head are written
+ * as FP16 tensors.  With cfg.rotate the four shared Hadamard rotations of
+ * the hidden size are written (ids 1 + site, spinquant.cpp:505-513).  *out
+ * is allocated by the library; release it with ifr_intfer_buffer_free. */
+int ifr_intfer_write(const ifr_host_model* m, const char* model_id, void** out, size_t* n);
+void ifr_intfer_buffer_free(void* p);
+
+/* ifr_intfer_host_model + ifr_model_load in one call (replaces Engine::load
+ * of an .intfer path + ensure_shard_built, engine.cpp:552-743); the file
+ * variant maps the file read-only for the duration of the call. */
+int ifr_model_load_intfer(ifr_ctx* ctx, const void* blob, size_t n, const ifr_model_cfg* cfg,
+                          const ifr_kv_cfg* kv);
+int ifr_model_load_intfer_file(ifr_ctx* ctx, const char* path, const ifr_model_cfg* cfg,
+                               const ifr_kv_cfg* kv);
 
 /* ------------------------------------------------------------------------
  * Scheduler / serve (C++ host side above the ABI).

@@ -18,7 +18,7 @@ from ._abi import (KVCfg, Linear, ModelCfg, Row, SchedBackend, SchedCfg, ROW_DEC
                    ROW_VERIFY, IFR_OK, IFR_EDECLINE, IFR_EINVAL, IFR_ENOMEM, IFR_EDEVICE, IFR_ESTATE,
                    IfrError, check, lib)
 
-__all__ = ["Device", "Engine", "Scheduler", "SynthModel", "default_cfg", "make_linear", "rows_array",
+__all__ = ["Device", "Engine", "Scheduler", "SynthModel", "HostModelHandle", "IntferFile", "default_cfg", "make_linear", "rows_array",
            "atile", "untile",
            "ROW_DECODE", "ROW_PREFILL", "ROW_VERIFY", "IfrError", "ModelCfg", "KVCfg", "SchedCfg",
            "Row", "Linear", "lib"]
@@ -32,14 +32,12 @@ def default_cfg(**over) -> ModelCfg:
     return c
 
 
-class SynthModel:
-    """Seeded synthetic decoder (owned by the library)."""
+class HostModelHandle:
+    """A host model owned by the library (synthetic or parsed from an
+    .intfer file); released with ifr_host_model_free."""
 
-    def __init__(self, cfg: ModelCfg, seed: int, bits: int = 2):
-        self.cfg = cfg
-        self.ptr = lib().ifr_synth_model(C.byref(cfg), C.c_uint64(seed), bits)
-        if not self.ptr:
-            raise ValueError("ifr_synth_model rejected the configuration")
+    cfg: ModelCfg
+    ptr = None
 
     @property
     def model(self):
@@ -54,7 +52,102 @@ class SynthModel:
 
     def close(self):
         if self.ptr:
-            lib().ifr_synth_free(self.ptr)
+            lib().ifr_host_model_free(self.ptr)
+            self.ptr = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def write_intfer(self, model_id: str = "intfer-amd-synthetic") -> bytes:
+        """Serialize to the INTFER1 container (ifr_intfer_write)."""
+        buf, n = C.c_void_p(), C.c_size_t()
+        check(lib().ifr_intfer_write(self.ptr, model_id.encode(), C.byref(buf), C.byref(n)),
+              "ifr_intfer_write")
+        try:
+            return C.string_at(buf, n.value)
+        finally:
+            lib().ifr_intfer_buffer_free(buf)
+
+
+class SynthModel(HostModelHandle):
+    """Seeded synthetic decoder (owned by the library).  intfer_form draws
+    it in the form an .intfer file stores exactly (IFR_SYNTH_INTFER)."""
+
+    def __init__(self, cfg: ModelCfg, seed: int, bits: int = 2, intfer_form: bool = False):
+        self.cfg = cfg
+        mode = bits | (_abi.IFR_SYNTH_INTFER if intfer_form else 0)
+        self.ptr = lib().ifr_synth_model(C.byref(cfg), C.c_uint64(seed), mode)
+        if not self.ptr:
+            raise ValueError("ifr_synth_model rejected the configuration")
+
+
+class IntferFile:
+    """A parsed .intfer (INTFER1) image; keeps the bytes alive while open."""
+
+    def __init__(self, blob: bytes):
+        self._blob = C.create_string_buffer(bytes(blob), len(blob))
+        self.ptr = C.c_void_p()
+        check(lib().ifr_intfer_open(self._blob, len(blob), C.byref(self.ptr)), "ifr_intfer_open")
+
+    def counts(self):
+        nt, nr, nl = C.c_int32(), C.c_int32(), C.c_int32()
+        check(lib().ifr_intfer_counts(self.ptr, C.byref(nt), C.byref(nr), C.byref(nl)),
+              "ifr_intfer_counts")
+        return nt.value, nr.value, nl.value
+
+    def model_id(self) -> str:
+        buf = C.create_string_buffer(512)
+        check(lib().ifr_intfer_model_id(self.ptr, buf, 512), "ifr_intfer_model_id")
+        return buf.value.decode()
+
+    def tensor(self, i: int) -> dict:
+        t = _abi.IntferTensor()
+        check(lib().ifr_intfer_tensor_info(self.ptr, i, C.byref(t)), "ifr_intfer_tensor_info")
+        d = {f: getattr(t, f) for f, _ in t._fields_}
+        d["name"] = t.name.decode()
+        return d
+
+    def tensors(self) -> list:
+        return [self.tensor(i) for i in range(self.counts()[0])]
+
+    def find(self, name: str) -> int:
+        i = C.c_int32()
+        check(lib().ifr_intfer_find(self.ptr, name.encode(), C.byref(i)), "ifr_intfer_find")
+        return i.value
+
+    def rotation(self, i: int, with_matrix: bool = False):
+        r = _abi.IntferRotation()
+        mat = None
+        if with_matrix:
+            r0 = _abi.IntferRotation()
+            check(lib().ifr_intfer_rotation_info(self.ptr, i, C.byref(r0), None), "ifr_intfer_rotation_info")
+            mat = np.empty((r0.dim, r0.dim), np.float32)
+        check(lib().ifr_intfer_rotation_info(self.ptr, i, C.byref(r),
+                                             mat.ctypes.data_as(_abi.pf32) if mat is not None else None),
+              "ifr_intfer_rotation_info")
+        d = {f: getattr(r, f) for f, _ in r._fields_}
+        return (d, mat) if with_matrix else d
+
+    def dequant(self, i: int) -> np.ndarray:
+        t = self.tensor(i)
+        out = np.empty((t["N"], t["K"]), np.float32)
+        check(lib().ifr_intfer_dequant(self.ptr, i, out.ctypes.data_as(_abi.pf32)), "ifr_intfer_dequant")
+        return out
+
+    def host_model(self, cfg: ModelCfg) -> HostModelHandle:
+        h = HostModelHandle()
+        ptr = C.POINTER(_abi.HostModel)()
+        check(lib().ifr_intfer_host_model(self.ptr, C.byref(cfg), C.byref(ptr)), "ifr_intfer_host_model")
+        h.ptr = ptr
+        h.cfg = ModelCfg.from_buffer_copy(ptr.contents.cfg)
+        return h
+
+    def close(self):
+        if self.ptr:
+            lib().ifr_intfer_close(self.ptr)
             self.ptr = None
 
     def __del__(self):
@@ -74,11 +167,13 @@ class HostLinear:
     scale: np.ndarray   # uint16 fp16 bits [N][K/128]
     zero: np.ndarray    # uint16 fp16 bits [N][K/128]
     values: np.ndarray  # unpacked uint8 [N][K]
+    post: float = 0.0   # output factor (0 reads as 1)
 
     @property
     def struct(self) -> Linear:
         s = Linear()
         s.N, s.K, s.bits, s.group = self.N, self.K, self.bits, 128
+        s.post = self.post
         s.codes = self.codes.ctypes.data_as(C.POINTER(C.c_uint8))
         s.scale = self.scale.ctypes.data_as(C.POINTER(C.c_uint16))
         s.zero = self.zero.ctypes.data_as(C.POINTER(C.c_uint16))
@@ -99,7 +194,7 @@ def pack_codes(vals: np.ndarray, bits: int) -> np.ndarray:
 
 
 def make_linear(N: int, K: int, bits: int, rng: np.random.Generator, scale_sigma=0.02,
-                zero=None) -> HostLinear:
+                zero=None, post: float = 0.0) -> HostLinear:
     vals = rng.integers(0, 1 << bits, size=(N, K), dtype=np.uint8)
     ng = K // 128
     sc = np.abs(rng.normal(0.0, scale_sigma, size=(N, ng))).astype(np.float16).view(np.uint16)
@@ -108,7 +203,7 @@ def make_linear(N: int, K: int, bits: int, rng: np.random.Generator, scale_sigma
         zz = np.full((N, ng), z, dtype=np.float16).view(np.uint16)
     else:
         zz = np.asarray(z, dtype=np.float16).reshape(N, ng).view(np.uint16)
-    return HostLinear(N, K, bits, pack_codes(vals, bits), sc.copy(), zz.copy(), vals)
+    return HostLinear(N, K, bits, pack_codes(vals, bits), sc.copy(), zz.copy(), vals, post)
 
 
 def atile(q: np.ndarray) -> np.ndarray:
@@ -213,16 +308,26 @@ class Device:
 class Engine:
     """The device forward over one loaded model."""
 
-    def __init__(self, dev: Device, model: SynthModel, max_seqs=8, max_seq_tokens=4096,
-                 pool_tokens=None, kv_int8=0, max_rows=640, attn_split=0, lanes=0):
+    def __init__(self, dev: Device, model: HostModelHandle, max_seqs=8, max_seq_tokens=4096,
+                 pool_tokens=None, kv_int8=0, max_rows=640, attn_split=0, lanes=0, intfer=None):
+        """Load `model` (a host model), or with intfer= an .intfer file path
+        or image for the architecture `model` (a ModelCfg)."""
         self.dev = dev
-        self.cfg = model.cfg
+        self.cfg = model if isinstance(model, ModelCfg) else model.cfg
         kv = KVCfg()
         kv.max_seqs, kv.max_seq_tokens = max_seqs, max_seq_tokens
         kv.pool_tokens = pool_tokens or max_seqs * max_seq_tokens
         kv.kv_int8, kv.max_rows, kv.attn_split, kv.lanes = kv_int8, max_rows, attn_split, lanes
         self.kv = kv
-        check(lib().ifr_model_load(dev.ctx, model.ptr, C.byref(kv)), "ifr_model_load")
+        if intfer is None:
+            check(lib().ifr_model_load(dev.ctx, model.ptr, C.byref(kv)), "ifr_model_load")
+        elif isinstance(intfer, (bytes, bytearray)):
+            buf = C.create_string_buffer(bytes(intfer), len(intfer))
+            check(lib().ifr_model_load_intfer(dev.ctx, buf, len(intfer), C.byref(self.cfg), C.byref(kv)),
+                  "ifr_model_load_intfer")
+        else:
+            check(lib().ifr_model_load_intfer_file(dev.ctx, str(intfer).encode(), C.byref(self.cfg),
+                                                   C.byref(kv)), "ifr_model_load_intfer_file")
 
     def seq_open(self) -> int:
         s = C.c_int32()

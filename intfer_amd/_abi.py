@@ -29,7 +29,7 @@ class ModelCfg(C.Structure):
 class Linear(C.Structure):
     _fields_ = [("N", C.c_int32), ("K", C.c_int32), ("bits", C.c_int32), ("group", C.c_int32),
                 ("codes", C.POINTER(C.c_uint8)), ("scale", C.POINTER(C.c_uint16)),
-                ("zero", C.POINTER(C.c_uint16))]
+                ("zero", C.POINTER(C.c_uint16)), ("post", C.c_float)]
 
 
 class LayerW(C.Structure):
@@ -40,7 +40,27 @@ class LayerW(C.Structure):
 
 class HostModel(C.Structure):
     _fields_ = [("cfg", ModelCfg), ("embed", C.POINTER(C.c_float)),
-                ("final_norm", C.POINTER(C.c_float)), ("layers", C.POINTER(LayerW))]
+                ("final_norm", C.POINTER(C.c_float)), ("layers", C.POINTER(LayerW)),
+                ("lm_head", C.POINTER(C.c_float))]
+
+
+IFR_SYNTH_INTFER = 0x100
+SCHEME_FP16, SCHEME_INT8, SCHEME_INT4, SCHEME_INT2 = 0, 1, 2, 3
+SITE_QKV, SITE_O, SITE_FFN_IN, SITE_FFN_OUT, SITE_NONE = 0, 1, 2, 3, 4
+
+
+class IntferTensor(C.Structure):
+    _fields_ = [("name", C.c_char_p), ("role", C.c_int32), ("N", C.c_int32), ("K", C.c_int32),
+                ("scheme", C.c_int32), ("group_size", C.c_int32), ("scale_dtype", C.c_int32),
+                ("has_global_divisor", C.c_int32), ("act", C.c_int32), ("rotation_id", C.c_int32),
+                ("code_offset", C.c_uint64), ("code_bytes", C.c_uint64),
+                ("scale_offset", C.c_uint64), ("scale_bytes", C.c_uint64),
+                ("global_offset", C.c_uint64), ("global_bytes", C.c_uint64),
+                ("est_error", C.c_float)]
+
+
+class IntferRotation(C.Structure):
+    _fields_ = [("id", C.c_int32), ("site", C.c_int32), ("dim", C.c_int32), ("hadamard", C.c_int32)]
 
 
 class KVCfg(C.Structure):
@@ -78,6 +98,20 @@ _PROTOS = {
     "ifr_last_error": (C.c_char_p, []),
     "ifr_synth_model": (C.POINTER(HostModel), [C.POINTER(ModelCfg), C.c_uint64, i32]),
     "ifr_synth_free": (None, [C.POINTER(HostModel)]),
+    "ifr_host_model_free": (None, [C.POINTER(HostModel)]),
+    "ifr_intfer_open": (C.c_int, [P, sz, C.POINTER(P)]),
+    "ifr_intfer_close": (C.c_int, [P]),
+    "ifr_intfer_counts": (C.c_int, [P, pi32, pi32, pi32]),
+    "ifr_intfer_model_id": (C.c_int, [P, C.c_char_p, sz]),
+    "ifr_intfer_tensor_info": (C.c_int, [P, i32, C.POINTER(IntferTensor)]),
+    "ifr_intfer_find": (C.c_int, [P, C.c_char_p, pi32]),
+    "ifr_intfer_rotation_info": (C.c_int, [P, i32, C.POINTER(IntferRotation), pf32]),
+    "ifr_intfer_dequant": (C.c_int, [P, i32, pf32]),
+    "ifr_intfer_host_model": (C.c_int, [P, C.POINTER(ModelCfg), C.POINTER(C.POINTER(HostModel))]),
+    "ifr_intfer_write": (C.c_int, [C.POINTER(HostModel), C.c_char_p, C.POINTER(P), C.POINTER(sz)]),
+    "ifr_intfer_buffer_free": (None, [P]),
+    "ifr_model_load_intfer": (C.c_int, [P, P, sz, C.POINTER(ModelCfg), C.POINTER(KVCfg)]),
+    "ifr_model_load_intfer_file": (C.c_int, [P, C.c_char_p, C.POINTER(ModelCfg), C.POINTER(KVCfg)]),
     "ifr_default_cfg": (None, [C.POINTER(ModelCfg)]),
     "ifr_ctx_create": (C.c_int, [i32, C.POINTER(P)]),
     "ifr_ctx_destroy": (C.c_int, [P]),

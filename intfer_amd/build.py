@@ -27,7 +27,8 @@ SOURCES = [("qgemm.hip", [], "qgemm"),
            ("qgemm.hip", ["-DIFR_QGEMM_BITS=4"], "qgemm_b4"),
            ("qgemm.hip", ["-DIFR_QGEMM_BITS=8"], "qgemm_b8"),
            ("rows.hip", [], "rows"), ("attn.hip", [], "attn"), ("lmhead.hip", [], "lmhead"),
-           ("engine.cpp", [], "engine"), ("sched.cpp", [], "sched"), ("synth.cpp", [], "synth")]
+           ("engine.cpp", [], "engine"), ("sched.cpp", [], "sched"), ("synth.cpp", [], "synth"),
+           ("intfer_file.cpp", [], "intfer_file")]
 
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 COMMON = [

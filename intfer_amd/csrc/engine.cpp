@@ -17,12 +17,13 @@
 #include <vector>
 
 #include "ifr_half.h"
+#include "host_model.h"
 #include "ifr_kernels.h"
 #include "intfer_amd.h"
 
 using ifrk::DLin;
 
-namespace {
+namespace ifrh {
 
 thread_local std::string g_err;
 
@@ -35,6 +36,12 @@ int fail(int code, const char* fmt, ...) {
   g_err = buf;
   return code;
 }
+
+}  // namespace ifrh
+
+namespace {
+
+using ifrh::fail;
 
 #define HIPCHK(expr)                                                                   \
   do {                                                                                 \
@@ -221,8 +228,11 @@ int check_linear(const ifr_linear* w) {
   if (w->group != 128) return fail(IFR_EDECLINE, "linear: group %d != 128", w->group);
   if (w->N <= 0 || w->K <= 0 || w->N % 16 || w->K % 128)
     return fail(IFR_EDECLINE, "linear: N %d must be a multiple of 16, K %d of 128", w->N, w->K);
+  if (!std::isfinite(w->post)) return fail(IFR_EINVAL, "linear: post not finite");
   return IFR_OK;
 }
+
+float post_of(const ifr_linear& w) { return w.post == 0.0f ? 1.0f : w.post; }
 
 size_t code_bytes(int N, int K, int bits) { return (size_t)N * K * bits / 8; }
 size_t sz_bytes(int N, int K) { return (size_t)N * (K / 128) * 4; }
@@ -236,6 +246,7 @@ int upload_group(ifr_ctx* c, const ifr_linear* const* ws, int count, int pair, D
   for (int i = 0; i < count; ++i) {
     if (int r = check_linear(ws[i])) return r;
     if (ws[i]->K != K || ws[i]->bits != bits) return fail(IFR_EINVAL, "group: K/bits mismatch");
+    if (post_of(*ws[i]) != post_of(*ws[0])) return fail(IFR_EINVAL, "group: post mismatch");
     N += ws[i]->N;
   }
   if (pair && (count != 2 || ws[0]->N != ws[1]->N)) return fail(IFR_EINVAL, "pair: shape mismatch");
@@ -245,6 +256,7 @@ int upload_group(ifr_ctx* c, const ifr_linear* const* ws, int count, int pair, D
   d.ng = K / 128;
   d.nsteps = K / 64;
   d.pair = pair;
+  d.post = post_of(*ws[0]);
   const size_t cb = code_bytes(N, K, bits), sb = sz_bytes(N, K);
   std::vector<uint32_t> hc(cb / 4), hs(sb / 4);
   int tile_off = 0;
@@ -585,7 +597,7 @@ int launch_tail(ifr_ctx* c, const SubBatch& sb, float* logits_out) {
 
 extern "C" {
 
-const char* ifr_last_error(void) { return g_err.c_str(); }
+const char* ifr_last_error(void) { return ifrh::g_err.c_str(); }
 
 int ifr_ctx_create(int32_t device, ifr_ctx** out) {
   if (!out) return fail(IFR_EINVAL, "out is null");
@@ -812,7 +824,8 @@ int ifr_model_load(ifr_ctx* c, const ifr_host_model* m, const ifr_kv_cfg* kvc) {
     if (lw.q.N != qN || lw.k.N != kvN || lw.v.N != kvN || lw.o.N != H || lw.o.K != qN ||
         lw.gate.N != F || lw.up.N != F || lw.down.N != H || lw.down.K != F || lw.q.K != H)
       return fail(IFR_EINVAL, "layer %d: linear shapes do not match the config", l);
-    if (lw.q.bits == lw.k.bits && lw.q.bits == lw.v.bits) {
+    if (lw.q.bits == lw.k.bits && lw.q.bits == lw.v.bits && post_of(lw.q) == post_of(lw.k) &&
+        post_of(lw.q) == post_of(lw.v)) {
       const ifr_linear* ws[3] = {&lw.q, &lw.k, &lw.v};
       ly.nqkv = 1;
       if (int r = upload_group(c, ws, 3, 0, ly.qkv[0], true)) return r;
@@ -832,7 +845,7 @@ int ifr_model_load(ifr_ctx* c, const ifr_host_model* m, const ifr_kv_cfg* kvc) {
       const ifr_linear* wd[1] = {&lw.down};
       if (int r = upload_group(c, wd, 1, 0, ly.down, true)) return r;
     }
-    if (lw.gate.bits == lw.up.bits) {
+    if (lw.gate.bits == lw.up.bits && post_of(lw.gate) == post_of(lw.up)) {
       const ifr_linear* ws[2] = {&lw.gate, &lw.up};
       ly.ngu = 1;
       if (int r = upload_group(c, ws, 2, 1, ly.gu[0], true)) return r;
@@ -852,12 +865,14 @@ int ifr_model_load(ifr_ctx* c, const ifr_host_model* m, const ifr_kv_cfg* kvc) {
   }
   if (int r = upload(c, &c->embed, m->embed, (size_t)V * H)) return r;
   if (int r = upload(c, &c->final_norm, m->final_norm, H)) return r;
-  // lm_head: per-row symmetric int8 of the tied embedding (main.cpp:1745-1761).
+  // lm_head: per-row symmetric int8 of the output projection, the tied
+  // embedding unless the model has its own (main.cpp:1745-1761).
   {
+    const float* lmw = m->lm_head ? m->lm_head : m->embed;
     std::vector<uint8_t> q((size_t)V * H);
     std::vector<uint16_t> s(V);
     for (int r = 0; r < V; ++r) {
-      const float* Wr = m->embed + (size_t)r * H;
+      const float* Wr = lmw + (size_t)r * H;
       float mx = 0;
       for (int k = 0; k < H; ++k) mx = std::max(mx, std::fabs(Wr[k]));
       const float sc = (mx > 0) ? mx / 127.0f : 1.0f;

@@ -33,6 +33,7 @@ struct DLin {
   int ng = 0;      // K / 128
   int nsteps = 0;  // K / 64
   int pair = 0;    // 1: tiles alternate gate / up (SwiGLU epilogue)
+  float post = 1.0f;  // factor on every output: y = fp16((ascale * post) * acc)
   uint32_t* codes = nullptr;
   uint32_t* sz = nullptr;
   size_t bytes = 0;

@@ -7,7 +7,8 @@
 //     S(m,g)   = sum_k a_q(m,k)                  from the activation producer
 //     d   = fma(-zero(n,g), S, T)
 //     acc = fma(scale(n,g), d, acc)              groups strictly ascending
-// y(m,n) = fp16_rne(ascale(m) * acc).  The fold order is fixed per output
+// y(m,n) = fp16_rne((ascale(m) * post) * acc), post a per-linear fp32 factor
+// (1 leaves ascale unchanged).  The fold order is fixed per output
 // element: split-K variants exchange the int32 T through LDS and fold them in
 // group order, so every launch shape produces the same bits.
 //
@@ -41,6 +42,7 @@ struct KParams {
   uint16_t* out;
   int32_t* tdump;
   int M, N, K, ng, nsteps, ldo;
+  float post;  // folded into the row scale: (ascale * post) * acc
 };
 
 // One compilation of this file per code width (IFR_QGEMM_BITS = 2, 4, 8)
@@ -244,7 +246,7 @@ __global__ __launch_bounds__(256) void qgemm_rows(KParams p) {
 #pragma unroll
   for (int i = 0; i < WM; ++i)
 #pragma unroll
-    for (int r = 0; r < 4; ++r) asr[i][r] = p.as[min(row0 + 16 * i + 4 * lgrp + r, p.M - 1)];
+    for (int r = 0; r < 4; ++r) asr[i][r] = p.as[min(row0 + 16 * i + 4 * lgrp + r, p.M - 1)] * p.post;
   __syncthreads();  // the only barrier
 
   v4i T[WM][WN];
@@ -351,7 +353,7 @@ __global__ __launch_bounds__(256) void qgemm_splitk(KParams p) {
   for (int k = 0; k < NO; ++k) {
     const int o = threadIdx.x + 256 * k;
     const int r = o & 3, ln = (o >> 2) & 63, i = (o >> 8) / (WN / JS);
-    asv[k] = p.as[min(row0 + 16 * i + 4 * (ln >> 4) + r, p.M - 1)];
+    asv[k] = p.as[min(row0 + 16 * i + 4 * (ln >> 4) + r, p.M - 1)] * p.post;
   }
   v4i T[WM][WN];
 #pragma unroll
@@ -577,7 +579,8 @@ hipError_t launch_qgemm_variant(const DLin& w, const QGemmArgs& a, int variant, 
   if (w.K % kG != 0 || w.N % 16 != 0 || !w.codes || !a.a || !a.as || !a.gs || !a.out)
     return hipErrorInvalidValue;
   if (w.pair && (w.N % 32 != 0 || a.tdump)) return hipErrorInvalidValue;
-  qg::KParams p{a.a, a.as, a.gs, w.codes, w.sz, a.out, a.tdump, a.M, w.N, w.K, w.ng, w.nsteps, a.ldo};
+  qg::KParams p{a.a, a.as, a.gs, w.codes, w.sz, a.out, a.tdump, a.M, w.N, w.K, w.ng, w.nsteps, a.ldo,
+                w.post};
   const int epi = w.pair ? 1 : 0;
   switch (w.bits) {
     case 2: return qg::launch_b2(p, epi, variant, st);

@@ -22,10 +22,51 @@
 #include <mutex>
 #include <vector>
 
-#include "intfer_amd.h"
+#include "host_model.h"
 #include "ifr_half.h"
 
+namespace ifrh {
+
+void OwnedModel::publish() {
+  const int L = pub.cfg.layers;
+  layers.resize(L);
+  for (int l = 0; l < L; ++l) {
+    ifr_layer_w& w = layers[l];
+    w.in_ln = norms[(size_t)l * 4 + 0].data();
+    w.post_ln = norms[(size_t)l * 4 + 1].data();
+    w.q_norm = norms[(size_t)l * 4 + 2].empty() ? nullptr : norms[(size_t)l * 4 + 2].data();
+    w.k_norm = norms[(size_t)l * 4 + 3].empty() ? nullptr : norms[(size_t)l * 4 + 3].data();
+    ifr_linear* slots[7] = {&w.q, &w.k, &w.v, &w.o, &w.gate, &w.up, &w.down};
+    for (int j = 0; j < 7; ++j) {
+      const OwnedLinear& o = lin[(size_t)l * 7 + j];
+      slots[j]->codes = o.codes.data();
+      slots[j]->scale = o.scale.data();
+      slots[j]->zero = o.zero.data();
+    }
+  }
+  pub.embed = embed.data();
+  pub.final_norm = final_norm.data();
+  pub.layers = layers.data();
+  pub.lm_head = lm_head.empty() ? nullptr : lm_head.data();
+}
+
 namespace {
+std::mutex g_models_mu;
+std::map<ifr_host_model*, OwnedModel*> g_models;
+}  // namespace
+
+ifr_host_model* adopt(OwnedModel* m) {
+  std::lock_guard<std::mutex> lk(g_models_mu);
+  g_models[&m->pub] = m;
+  return &m->pub;
+}
+
+}  // namespace ifrh
+
+namespace {
+
+using ifrh::OwnedLinear;
+using ifrh::OwnedModel;
 
 inline uint64_t splitmix64(uint64_t& s) {
   uint64_t z = (s += 0x9E3779B97F4A7C15ull);
@@ -41,10 +82,6 @@ inline uint64_t stream_seed(uint64_t seed, uint64_t tensor, uint64_t chunk) {
 }
 
 constexpr size_t kChunk = 65536;
-
-struct OwnedModel;
-std::mutex g_models_mu;
-std::map<ifr_host_model*, OwnedModel*> g_models;
 
 // Fill out[0..n) with N(0, sigma) (Box-Muller, both outputs used).
 void fill_normal(float* out, size_t n, float sigma, uint64_t seed, uint64_t tensor) {
@@ -81,38 +118,30 @@ void fill_codes(uint8_t* out, size_t ncodes, int bits, uint64_t seed, uint64_t t
   }
 }
 
-struct OwnedLinear {
-  std::vector<uint8_t> codes;
-  std::vector<uint16_t> scale, zero;
-};
-
-struct OwnedModel {
-  ifr_host_model pub;
-  std::vector<float> embed, final_norm;
-  std::vector<ifr_layer_w> layers;
-  std::vector<std::vector<float>> norms;  // 4 per layer
-  std::vector<OwnedLinear> lin;           // 7 per layer
-};
-
+// intfer_form: one scale per K-group shared by all rows (drawn per group),
+// post = 2/C, so the linear is exactly what an .intfer file stores.
 void make_linear(OwnedLinear& o, ifr_linear& L, int N, int K, int bits, int group,
-                 uint64_t seed, uint64_t tid) {
+                 uint64_t seed, uint64_t tid, bool intfer_form) {
   const size_t n = (size_t)N * K;
   o.codes.resize(n * (size_t)bits / 8);
   fill_codes(o.codes.data(), n, bits, seed, tid * 4 + 0);
-  const size_t ng = (size_t)N * (K / group);
-  std::vector<float> sc(ng);
-  fill_normal(sc.data(), ng, 0.02f, seed, tid * 4 + 1);
+  const size_t ngk = (size_t)(K / group), ng = (size_t)N * ngk;
+  std::vector<float> sc(intfer_form ? ngk : ng);
+  fill_normal(sc.data(), sc.size(), 0.02f, seed, tid * 4 + 1);
   o.scale.resize(ng);
   o.zero.resize(ng);
-  const uint16_t z = ifr::f2h((float)((1 << bits) - 1) * 0.5f);
+  const int C = (1 << bits) - 1;
+  const uint16_t z = ifr::f2h((float)C * 0.5f);
   for (size_t i = 0; i < ng; ++i) {
-    o.scale[i] = ifr::f2h(std::fabs(sc[i]));
+    o.scale[i] = ifr::f2h(std::fabs(sc[intfer_form ? i % ngk : i]));
     o.zero[i] = z;
   }
   L.N = N; L.K = K; L.bits = bits; L.group = group;
-  L.codes = o.codes.data();
-  L.scale = o.scale.data();
-  L.zero = o.zero.data();
+  L.post = intfer_form ? 2.0f / (float)C : 0.0f;
+}
+
+void round_fp16(std::vector<float>& v) {
+  for (float& x : v) x = ifr::h2f(ifr::f2h(x));
 }
 
 }  // namespace
@@ -137,6 +166,8 @@ extern "C" void ifr_default_cfg(ifr_model_cfg* c) {
 extern "C" ifr_host_model* ifr_synth_model(const ifr_model_cfg* cfg, uint64_t seed,
                                            int32_t bits_mode) {
   if (!cfg || cfg->hidden <= 0 || cfg->layers <= 0 || cfg->group_size <= 0) return nullptr;
+  const bool intfer_form = (bits_mode & IFR_SYNTH_INTFER) != 0;
+  bits_mode &= ~IFR_SYNTH_INTFER;
   if (bits_mode != 0 && bits_mode != 2 && bits_mode != 4 && bits_mode != 8) return nullptr;
   auto* m = new OwnedModel();
   m->pub.cfg = *cfg;
@@ -157,11 +188,8 @@ extern "C" ifr_host_model* ifr_synth_model(const ifr_model_cfg* cfg, uint64_t se
       auto& v = m->norms[(size_t)l * 4 + j];
       v.resize(dims[j]);
       fill_normal(v.data(), dims[j], 0.1f, seed, 100 + (uint64_t)l * 8 + j);
+      if (intfer_form) round_fp16(v);
     }
-    w.in_ln = m->norms[(size_t)l * 4 + 0].data();
-    w.post_ln = m->norms[(size_t)l * 4 + 1].data();
-    w.q_norm = m->norms[(size_t)l * 4 + 2].data();
-    w.k_norm = m->norms[(size_t)l * 4 + 3].data();
     ifr_linear* slots[7] = {&w.q, &w.k, &w.v, &w.o, &w.gate, &w.up, &w.down};
     const int Ns[7] = {qN, kvN, kvN, H, F, F, H};
     const int Ks[7] = {H, H, H, qN, H, H, F};
@@ -169,26 +197,28 @@ extern "C" ifr_host_model* ifr_synth_model(const ifr_model_cfg* cfg, uint64_t se
       int bits = bits_mode;
       if (bits_mode == 0) bits = ((splitmix64(split) >> 11) % 10 < 7) ? 2 : 4;
       make_linear(m->lin[(size_t)l * 7 + j], *slots[j], Ns[j], Ks[j], bits, G, seed,
-                  1000 + (uint64_t)l * 16 + j);
+                  1000 + (uint64_t)l * 16 + j, intfer_form);
     }
   }
-  m->pub.embed = m->embed.data();
-  m->pub.final_norm = m->final_norm.data();
-  m->pub.layers = m->layers.data();
-  std::lock_guard<std::mutex> lk(g_models_mu);
-  g_models[&m->pub] = m;
-  return &m->pub;
+  if (intfer_form) {
+    round_fp16(m->embed);
+    round_fp16(m->final_norm);
+  }
+  m->publish();
+  return ifrh::adopt(m);
 }
 
-extern "C" void ifr_synth_free(ifr_host_model* p) {
+extern "C" void ifr_host_model_free(ifr_host_model* p) {
   if (!p) return;
   OwnedModel* m = nullptr;
   {
-    std::lock_guard<std::mutex> lk(g_models_mu);
-    auto it = g_models.find(p);
-    if (it == g_models.end()) return;
+    std::lock_guard<std::mutex> lk(ifrh::g_models_mu);
+    auto it = ifrh::g_models.find(p);
+    if (it == ifrh::g_models.end()) return;
     m = it->second;
-    g_models.erase(it);
+    ifrh::g_models.erase(it);
   }
   delete m;
 }
+
+extern "C" void ifr_synth_free(ifr_host_model* p) { ifr_host_model_free(p); }

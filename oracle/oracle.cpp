@@ -169,6 +169,7 @@ struct Unpacked {
   int N = 0, K = 0, G = 0;
   std::vector<uint8_t> c;       // [N][K]
   std::vector<float> s, z;      // [N][K/G]
+  float post = 1.0f;            // per-linear output factor (0 in ifr_linear reads as 1)
 };
 
 void unpack(const ifr_linear& w, Unpacked& u) {
@@ -180,12 +181,13 @@ void unpack(const ifr_linear& w, Unpacked& u) {
   const size_t ng = (size_t)w.N * (w.K / w.group);
   u.s.resize(ng); u.z.resize(ng);
   for (size_t i = 0; i < ng; ++i) { u.s[i] = h2f(w.scale[i]); u.z[i] = h2f(w.zero[i]); }
+  u.post = w.post == 0.0f ? 1.0f : w.post;
 }
 
 // ---- quant GEMM contract (the W2A8 integer contract of dpas48_tiled,
 // quant_gemm.cpp:3602-3736, with per-(row,group) scale + zero):
 //   T = sum a_q*c (int32), S = sum a_q, d = fma(-z, S, T), acc = fma(s, d, acc)
-//   over groups ascending; y = fp16(as * acc).
+//   over groups ascending; y = fp16((as * post) * acc).
 void qgemm_rows(const int8_t* a, const float* as, int M, const Unpacked& u, float* y /*[M][N]*/,
                 int32_t* tdump) {
   const int N = u.N, K = u.K, G = u.G, ng = K / G;
@@ -202,7 +204,7 @@ void qgemm_rows(const int8_t* a, const float* as, int M, const Unpacked& u, floa
       const float d = std::fmaf(-u.z[(size_t)n * ng + g], (float)S, (float)T);
       acc = std::fmaf(u.s[(size_t)n * ng + g], d, acc);
     }
-    y[r] = fp16r(as[m] * acc);
+    y[r] = fp16r((as[m] * u.post) * acc);
   }
 }
 
@@ -226,7 +228,7 @@ void dequant(const Unpacked& u, std::vector<float>& out) {
   for (long n = 0; n < u.N; ++n)
     for (int k = 0; k < u.K; ++k) {
       const size_t gi = (size_t)n * ng + k / u.G;
-      out[(size_t)n * u.K + k] = u.s[gi] * ((float)u.c[(size_t)n * u.K + k] - u.z[gi]);
+      out[(size_t)n * u.K + k] = u.post * (u.s[gi] * ((float)u.c[(size_t)n * u.K + k] - u.z[gi]));
     }
 }
 
@@ -500,10 +502,12 @@ int forward(Engine& e, const ifr_row* rows, int M, int32_t* best, float* logits_
                         &as[(size_t)i * ng + gg]);
     lmhead_rows(aq.data(), as.data(), W, e.lm_q.data(), e.lm_s.data(), c.vocab, H, lg.data());
   } else {
-    // tied-embedding lm_head, serial as in the reference (main.cpp:8302-8307)
+    // fp32 lm_head (the tied embedding unless the model has its own),
+    // serial as in the reference (main.cpp:8302-8307)
+    const float* lmw = e.m->lm_head ? e.m->lm_head : e.m->embed;
     for (int i = 0; i < W; ++i)
       for (int v = 0; v < c.vocab; ++v) {
-        const float* er = e.m->embed + (size_t)v * H;
+        const float* er = lmw + (size_t)v * H;
         const float* f = &fn[(size_t)i * H];
         float s = 0;
         for (int k = 0; k < H; ++k) s += f[k] * er[k];
@@ -686,7 +690,8 @@ void* or_engine_create(const ifr_host_model* m, int kv_int8, int mode, int max_s
       for (int j = 0; j < 7; ++j) unpack(lin_of(m->layers[l], j), e->lin[(size_t)l * 7 + j]);
     e->lm_q.resize((size_t)e->c.vocab * e->c.hidden);
     e->lm_s.resize(e->c.vocab);
-    lmhead_quant(m->embed, e->c.vocab, e->c.hidden, e->lm_q.data(), e->lm_s.data());
+    lmhead_quant(m->lm_head ? m->lm_head : m->embed, e->c.vocab, e->c.hidden, e->lm_q.data(),
+                 e->lm_s.data());
   } else {
     e->wf.resize((size_t)L * 7);
     for (int l = 0; l < L; ++l)

@@ -82,6 +82,10 @@ def ref() -> C.CDLL | None:
             "ref_canonical_codebook": (None, [C.c_int, P]),
             "ref_dequant": (None, [C.c_int, C.c_uint32, C.c_uint32, C.c_uint16, P, sz, P,
                                    C.c_uint32, P]),
+            "ref_intfer_reserialize": (C.c_int, [P, sz, C.POINTER(P), C.POINTER(sz)]),
+            "ref_intfer_dequant": (C.c_long, [P, sz, C.c_char_p, P, sz]),
+            "ref_intfer_rotation_is_hadamard": (C.c_int, [P, sz, C.c_int]),
+            "ref_free": (None, [P]),
         }
         for n, (res, args) in protos.items():
             fn = getattr(L, n)
@@ -92,6 +96,30 @@ def ref() -> C.CDLL | None:
 
 def ptr(a: np.ndarray) -> C.c_void_p:
     return a.ctypes.data_as(C.c_void_p)
+
+
+# ---- the reference's own INTFER1 reader / writer / dequant (needs _ref) ----------
+
+def ref_intfer_reserialize(blob: bytes) -> bytes | None:
+    """The image read by the reference reader and written back by the
+    reference writer; None if the reader rejects it."""
+    out, n = C.c_void_p(), C.c_size_t()
+    if ref().ref_intfer_reserialize(blob, len(blob), C.byref(out), C.byref(n)) != 0:
+        return None
+    try:
+        return C.string_at(out, n.value)
+    finally:
+        ref().ref_free(out)
+
+
+def ref_intfer_dequant(blob: bytes, name: str, N: int, K: int) -> np.ndarray | None:
+    out = np.empty((N, K), np.float32)
+    got = ref().ref_intfer_dequant(blob, len(blob), name.encode(), ptr(out), out.size)
+    return out if got == N * K else None
+
+
+def ref_intfer_rotation_is_hadamard(blob: bytes, i: int) -> int:
+    return ref().ref_intfer_rotation_is_hadamard(blob, len(blob), i)
 
 
 # ---- numpy-level helpers --------------------------------------------------------

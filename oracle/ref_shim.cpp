@@ -6,12 +6,15 @@
 // (git-ignored) and is used only by tests/ to pin the oracle restatement
 // against the reference's code: fp16 conversion (src/quant/dashq.cpp:338-384),
 // act-quant (dashq.cpp:221-336), the canonical codebook + dequant
-// (dashq.cpp:405-417, :531-575) and the FWHT rotation (src/spinquant.cpp:99-125,
-// :303-312, :586-629).
+// (dashq.cpp:405-417, :531-575), the FWHT rotation (src/spinquant.cpp:99-125,
+// :303-312, :586-629) and the INTFER1 container (src/quant/output.cpp:396-603).
 #include <cstdint>
 #include <cstring>
 #include <vector>
 
+#include <cstdlib>
+
+#include "intfer/output.hpp"
 #include "intfer/quant/dashq.hpp"
 #include "intfer/quant_spec.h"
 #include "intfer/spinquant.hpp"
@@ -69,5 +72,47 @@ void ref_dequant(int bits, uint32_t N, uint32_t K, uint16_t G, const uint8_t* co
   r.dequant(o, N, K);
   std::memcpy(out, o.data(), o.size() * sizeof(float));
 }
+
+// Read an INTFER1 image with the reference reader and write it back with the
+// reference writer.  Returns -1 if the reader rejects the image; else 0 and a
+// malloc'd copy of the re-serialized bytes (free with ref_free).
+int ref_intfer_reserialize(const uint8_t* blob, size_t n, uint8_t** out, size_t* out_n) {
+  ModelIR m;
+  RotationSet rs;
+  if (!deserialize_intfer(blob, n, m, rs)) return -1;
+  std::vector<uint8_t> b = serialize_intfer(m, rs);
+  *out = static_cast<uint8_t*>(std::malloc(b.size() ? b.size() : 1));
+  std::memcpy(*out, b.data(), b.size());
+  *out_n = b.size();
+  return 0;
+}
+
+// Reference dequant_tensor of the tensor named `name`: writes N*K floats to
+// out (capacity cap) and returns N*K, or -1 if unreadable / absent / too big.
+long ref_intfer_dequant(const uint8_t* blob, size_t n, const char* name, float* out, size_t cap) {
+  ModelIR m;
+  RotationSet rs;
+  if (!deserialize_intfer_borrowed(blob, n, m, rs)) return -1;
+  for (const TensorIR& t : m.tensors) {
+    if (t.name != name) continue;
+    std::vector<float> o;
+    dashq::dequant_tensor(m, t, o);
+    if (o.size() > cap) return -1;
+    std::memcpy(out, o.data(), o.size() * sizeof(float));
+    return (long)o.size();
+  }
+  return -1;
+}
+
+// The reference's Hadamard shape check of rotation i (rotation_is_hadamard,
+// spinquant.cpp:607-629): 1 / 0, or -1 if unreadable.
+int ref_intfer_rotation_is_hadamard(const uint8_t* blob, size_t n, int i) {
+  ModelIR m;
+  RotationSet rs;
+  if (!deserialize_intfer(blob, n, m, rs) || i < 0 || (size_t)i >= rs.rotations.size()) return -1;
+  return rotation_is_hadamard(rs.rotations[i]) ? 1 : 0;
+}
+
+void ref_free(void* p) { std::free(p); }
 
 }  // extern "C"

@@ -343,6 +343,48 @@ def act_quant():
     dev.close()
 
 
+@scenario
+def intfer_load():
+    """An .intfer image (container-form model, post = 2/C, mixed widths)
+    loaded through ifr_model_load_intfer runs one prefill chunk like the
+    oracle; then truncated / corrupted images through the parser and the
+    host-model mapping, every access bounds-checked."""
+    import intfer_amd as ia
+    from oracle import pyoracle as po
+    cfg = _small_cfg(ia, layers=1, n_heads=2, n_kv=1)
+    model = ia.SynthModel(cfg, seed=5, bits=0, intfer_form=True)
+    blob = model.write_intfer("emu")
+    dev = ia.Device(0)
+    eng = ia.Engine(dev, cfg, max_seqs=2, max_seq_tokens=256, max_rows=64, intfer=blob)
+    ora = po.OracleEngine(model, kv_int8=0, mode=0, max_seqs=2)
+    se, so = eng.seq_open(), ora.seq_open()
+    rows = [(p, 7 + 3 * p) for p in range(20)]
+    be, lg = eng.forward([(se, p, t, 1, 1) for p, t in rows], logits=True)
+    bo, lo = ora.forward([(so, p, t, 1, 1) for p, t in rows], logits=True)
+    err = float(np.abs(lg - lo).max() / lo.std())
+    say(f"intfer forward: tokens equal {np.array_equal(be, bo)}, max|dlogit|/std {err:.3g}")
+    assert np.array_equal(be, bo) and err < 2e-3
+    rng = np.random.default_rng(1)
+    js_len = int.from_bytes(blob[46:54], "little")
+    n_err = 0
+    for trial in range(60):
+        img = bytearray(blob[:54 + js_len + 4096]) if trial % 2 else bytearray(blob)
+        if trial % 3 == 0:
+            img = img[:int(rng.integers(0, len(img)))]
+        else:
+            for _ in range(int(rng.integers(1, 4))):
+                img[int(rng.integers(0, 54 + js_len))] = int(rng.integers(0, 256))
+        try:
+            f = ia.IntferFile(bytes(img))
+            f.host_model(cfg).close()
+            f.close()
+        except ia.IfrError:
+            n_err += 1
+    say(f"intfer parse fuzz: {n_err}/60 refused cleanly")
+    dev.close()
+    model.close()
+
+
 def run_scenarios(names, timeout=3600) -> int:
     """Run scenarios in a child process with the ASan runtime preloaded."""
     from tests.hipemu import build as eb

@@ -45,11 +45,11 @@ def model():
     m.close()
 
 
-def _setup(dev, model, kv_int8):
+def _setup(dev, model, kv_int8, intfer=None):
     cfg = model.cfg
     w = wl.cfg1(cfg, seed=1)
-    eng = ia.Engine(dev, model, max_seqs=8, max_seq_tokens=2048, pool_tokens=8 * 2048,
-                    kv_int8=kv_int8, max_rows=128)
+    eng = ia.Engine(dev, model if intfer is None else cfg, max_seqs=8, max_seq_tokens=2048,
+                    pool_tokens=8 * 2048, kv_int8=kv_int8, max_rows=128, intfer=intfer)
     ora = po.OracleEngine(model, kv_int8=kv_int8, mode=0, max_seqs=8)
     dec_e, dec_o = [], []
     for (k, v) in w.kv:
@@ -98,6 +98,35 @@ def test_one_layer_bit_exact(dev):
         exact = sum(np.array_equal(lg[r].view(np.uint32), lo[r].view(np.uint32)) for r in range(5))
         dmax = float(np.abs(lg - lo).max())
         print(f"[one layer] bit-identical logit rows {exact}/5, max |dlogit| {dmax:.3g}")
+        assert exact >= 3 and dmax <= 2e-3 * float(lo.std())
+    finally:
+        m.close()
+
+
+def test_intfer_file_load_one_layer(dev, tmp_path):
+    """A model loaded from its .intfer file (the mmap entry point) runs
+    bit-identically to the host model it was written from, and meets the
+    one-layer oracle bound above.  The container form puts post = 2/C on
+    every linear; bits_mode 0 mixes INT2 / INT4 widths inside the layer."""
+    cfg = ia.default_cfg(layers=1)
+    m = ia.SynthModel(cfg, seed=12, bits=0, intfer_form=True)
+    path = tmp_path / "one_layer.intfer"
+    path.write_bytes(m.write_intfer("one-layer"))
+    try:
+        w, eng, ora, dec_e, dec_o, pe, pq = _setup(dev, m, 0)
+        announce("intfer-form one-layer forward from the host model")
+        be, lg = eng.forward(wl.cfg1_rows(w, dec_e, pe), logits=True)
+        bo, lo = ora.forward(wl.cfg1_rows(w, dec_o, pq), logits=True)
+        del eng, ora
+        w, eng, ora, dec_e, dec_o, pe, pq = _setup(dev, m, 0, intfer=path)
+        announce("intfer-form one-layer forward from the .intfer file")
+        bf, lf = eng.forward(wl.cfg1_rows(w, dec_e, pe), logits=True)
+        assert np.array_equal(bf, be)
+        assert np.array_equal(lf.view(np.uint32), lg.view(np.uint32))
+        assert np.array_equal(be, bo)
+        exact = sum(np.array_equal(lg[r].view(np.uint32), lo[r].view(np.uint32)) for r in range(5))
+        dmax = float(np.abs(lg - lo).max())
+        print(f"[intfer one layer] bit-identical logit rows {exact}/5, max |dlogit| {dmax:.3g}")
         assert exact >= 3 and dmax <= 2e-3 * float(lo.std())
     finally:
         m.close()

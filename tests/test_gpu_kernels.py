@@ -75,6 +75,22 @@ def test_qgemm_general_zero_and_int8(dev):
             assert np.array_equal(out, po.qgemm(q, s[:, 0], lin))
 
 
+@pytest.mark.parametrize("bits,post", [(2, 2.0 / 3.0), (4, 2.0 * 0.37 / 15.0), (8, 2.0 / 255.0)])
+def test_qgemm_post_scale_bitexact(dev, bits, post):
+    """A per-linear output factor (the .intfer form post = 2*alpha/C) folds
+    into the row scale: y = fp16((ascale * post) * acc), bit-exact."""
+    rng = np.random.default_rng(500 + bits)
+    post = float(np.float32(post))
+    lin = ia.make_linear(1024, 2048, bits, rng, post=post)
+    for M in (1, 64, 300):
+        q, s, out, T = _gemm_case(dev, lin, M, rng, dump=False)
+        ref = po.qgemm(q, s[:, 0], lin)
+        assert np.array_equal(out, ref), f"bits={bits} M={M}: {(out != ref).sum()} outputs differ"
+        unit = po.qgemm(q, s[:, 0], ia.HostLinear(lin.N, lin.K, bits, lin.codes, lin.scale, lin.zero,
+                                                  lin.values, 0.0))
+        assert not np.array_equal(out, unit)  # the factor is applied
+
+
 @pytest.mark.parametrize("M", [1, 16, 64, 200])
 def test_qgemm_swiglu_pair(dev, M):
     rng = np.random.default_rng(300 + M)
