@@ -134,13 +134,13 @@ def _gemm_shapes(bits_list, shapes, Ms=(1, 17, 70), pair_check=False):
 
 
 def _forward_case(layers, kv_int8, steps, hidden=1024, n_heads=16, n_kv=8, inter=3072,
-                  vocab=2048):
+                  vocab=2048, bits=2, intfer_form=False, seed=11):
     import intfer_amd as ia
     from intfer_amd import workloads as wl
     from oracle import pyoracle as po
     cfg = ia.default_cfg(layers=layers, hidden=hidden, n_heads=n_heads, n_kv=n_kv, inter=inter,
                          vocab=vocab)
-    model = ia.SynthModel(cfg, seed=11, bits=2)
+    model = ia.SynthModel(cfg, seed=seed, bits=bits, intfer_form=intfer_form)
     dev = ia.Device(0)
     w = wl.cfg1(cfg, seed=1)
     eng = ia.Engine(dev, model, max_seqs=8, max_seq_tokens=2048, pool_tokens=8 * 2048,
@@ -228,7 +228,7 @@ def sched_small():
     import intfer_amd as ia
     from intfer_amd import workloads as wl
     cfg = ia.default_cfg(layers=2, vocab=2048)
-    model = ia.SynthModel(cfg, seed=11, bits=2)
+    model = ia.SynthModel(cfg, seed=seed, bits=bits, intfer_form=intfer_form)
     dev = ia.Device(0)
     eng = ia.Engine(dev, model, max_seqs=16, max_seq_tokens=1024, pool_tokens=16 * 1024, max_rows=256)
     prompts = wl.cfg4_requests(4, seed=8, vocab=cfg.vocab, lo=40, hi=150)
