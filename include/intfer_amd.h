@@ -461,6 +461,48 @@ int ifr_sched_result(ifr_sched* s, int64_t id, int32_t* out, int32_t cap, int32_
 /* Row list of the last forward the scheduler ran (for replay parity). */
 int ifr_sched_last_rows(ifr_sched* s, ifr_row* out, int32_t cap, int32_t* n);
 
+/* Streamed output of the scheduler, the events the reference's serve loop
+ * prints (run_serve, main.cpp:9285-9291, :9349-9363): one per generated
+ * token of a decode or verify row, in row order (the token that completes
+ * a prefill is not streamed), then one done event per request that
+ * finished in the step, in live order. */
+typedef struct ifr_sched_event {
+  int64_t id;        /* request id */
+  int32_t token;     /* the token, or -1 for a done event */
+  int32_t done;      /* 1: the request finished */
+  int32_t generated; /* tokens generated so far (done: the final count) */
+  int32_t reserved;
+} ifr_sched_event;
+/* Start (on = 1) or stop recording events; stopping drops undrained ones. */
+int ifr_sched_record_events(ifr_sched* s, int32_t on);
+/* Move up to cap recorded events, oldest first, into out; *n = how many. */
+int ifr_sched_events(ifr_sched* s, ifr_sched_event* out, int32_t cap, int32_t* n);
+/* Forget a finished request (IFR_ESTATE while it still runs). */
+int ifr_sched_release(ifr_sched* s, int64_t id);
+/* Queue sizes and the per-sequence KV capacity in tokens. */
+int ifr_sched_info(ifr_sched* s, int32_t* live, int32_t* prefill, int32_t* pending,
+                   int32_t* kv_capacity);
+
+/* The --serve JSON-lines loop (run_serve, main.cpp:9260-9377), over file
+ * descriptors.  Each input line is one request,
+ *   {"prompt_ids":[t0,t1,...], "max_new":N, "id":K}
+ * (max_new defaults to cfg->default_max_new and is clamped to [1, 4096]; a
+ * missing id takes the next free one, main.cpp:9329-9342).  Token ids stand
+ * in for the reference's "prompt" text: this build has no tokenizer, so a
+ * line with only "prompt" is answered with an error, as are sampling keys
+ * asking for more than greedy decoding.  Output lines, flushed per
+ * iteration: {"id":K,"token":T} per streamed token, {"id":K,"done":true,
+ * "generated":n} when a request finishes, {"error":"..."} (with "id" when
+ * known) for a line that is refused.  Input is polled between iterations
+ * and read blocking only while nothing runs; the call returns IFR_OK after
+ * end of input once every admitted request has finished, or the first
+ * forward error. */
+typedef struct ifr_serve_cfg {
+  int32_t default_max_new; /* 0: 64 (ServeOpts, main.cpp:8563-8568) */
+  int32_t vocab;           /* token ids must be below it (0: checked by the forward) */
+} ifr_serve_cfg;
+int ifr_serve(ifr_sched* s, int32_t in_fd, int32_t out_fd, const ifr_serve_cfg* cfg);
+
 #ifdef __cplusplus
 }
 #endif

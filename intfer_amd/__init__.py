@@ -429,6 +429,43 @@ class Scheduler:
         check(lib().ifr_sched_last_rows(self.h, arr, n.value, C.byref(n)), "ifr_sched_last_rows")
         return [(r.seq, r.pos, r.token, r.kind, r.want) for r in arr[:n.value]]
 
+    def info(self):
+        """(live, prefill queue, pending, per-sequence KV capacity)."""
+        v = [C.c_int32() for _ in range(4)]
+        check(lib().ifr_sched_info(self.h, *[C.byref(x) for x in v]), "ifr_sched_info")
+        return tuple(x.value for x in v)
+
+    def serve(self, lines, vocab: int = 0, default_max_new: int = 64):
+        """Run the JSON-lines serve loop (ifr_serve) over pipes on `lines`
+        (one request per string); returns (output events as dicts, status)."""
+        import json
+        import os
+        import threading
+        rin, win = os.pipe()
+        rout, wout = os.pipe()
+        cfg = _abi.ServeCfg(default_max_new, vocab)
+        res = {}
+
+        def run():
+            try:
+                res["rc"] = lib().ifr_serve(self.h, rin, wout, C.byref(cfg))
+            finally:
+                os.close(wout)
+
+        def feed():
+            with os.fdopen(win, "wb") as f:
+                f.write("".join(ln + "\n" for ln in lines).encode())
+
+        th, tw = threading.Thread(target=run), threading.Thread(target=feed)
+        th.start()
+        tw.start()
+        with os.fdopen(rout, "rb") as f:
+            out = f.read()
+        th.join()
+        tw.join()
+        os.close(rin)
+        return [json.loads(ln) for ln in out.decode().splitlines() if ln.strip()], res.get("rc", -1)
+
     def close(self):
         if self.h:
             lib().ifr_sched_destroy(self.h)

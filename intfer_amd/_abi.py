@@ -85,6 +85,15 @@ SEQ_TRUNC = C.CFUNCTYPE(C.c_int, C.c_void_p, C.c_int32, C.c_int32)
 FORWARD = C.CFUNCTYPE(C.c_int, C.c_void_p, C.POINTER(Row), C.c_int32, C.POINTER(C.c_int32))
 
 
+class SchedEvent(C.Structure):
+    _fields_ = [("id", C.c_int64), ("token", C.c_int32), ("done", C.c_int32), ("generated", C.c_int32),
+                ("reserved", C.c_int32)]
+
+
+class ServeCfg(C.Structure):
+    _fields_ = [("default_max_new", C.c_int32), ("vocab", C.c_int32)]
+
+
 class SchedBackend(C.Structure):
     _fields_ = [("user", C.c_void_p), ("seq_open", SEQ_OPEN), ("seq_close", SEQ_CLOSE),
                 ("seq_truncate", SEQ_TRUNC), ("forward", FORWARD), ("kv_capacity", C.c_int32)]
@@ -157,6 +166,11 @@ _PROTOS = {
     "ifr_sched_step": (C.c_int, [P, pi32]),
     "ifr_sched_result": (C.c_int, [P, i64, pi32, i32, pi32, pi32]),
     "ifr_sched_last_rows": (C.c_int, [P, C.POINTER(Row), i32, pi32]),
+    "ifr_sched_record_events": (C.c_int, [P, i32]),
+    "ifr_sched_events": (C.c_int, [P, C.POINTER(SchedEvent), i32, pi32]),
+    "ifr_sched_release": (C.c_int, [P, i64]),
+    "ifr_sched_info": (C.c_int, [P, pi32, pi32, pi32, pi32]),
+    "ifr_serve": (C.c_int, [P, i32, i32, C.POINTER(ServeCfg)]),
 }
 
 _lib = None

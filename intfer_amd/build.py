@@ -28,7 +28,8 @@ SOURCES = [("qgemm.hip", [], "qgemm"),
            ("qgemm.hip", ["-DIFR_QGEMM_BITS=8"], "qgemm_b8"),
            ("rows.hip", [], "rows"), ("attn.hip", [], "attn"), ("lmhead.hip", [], "lmhead"),
            ("engine.cpp", [], "engine"), ("sched.cpp", [], "sched"), ("synth.cpp", [], "synth"),
-           ("intfer_file.cpp", [], "intfer_file")]
+           ("intfer_file.cpp", [], "intfer_file"), ("serve.cpp", [], "serve")]
+SERVE_BIN = HERE / "intfer_serve"  # the --serve command line (serve_main.cpp)
 
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 COMMON = [
@@ -70,6 +71,14 @@ def build(jobs: int = 8) -> Path:
     if r.returncode != 0:
         raise RuntimeError(f"link failed:\n{r.stderr[-4000:]}")
     os.replace(tmp, LIB)
+    # The command line links the library in place (found next to itself).
+    tmpb = SERVE_BIN.with_suffix(".tmp")
+    cmd = ["g++", "-O2", "-std=c++17", "-Wall", f"-I{ROOT / 'include'}", str(CSRC / "serve_main.cpp"),
+           f"-L{HERE}", "-lintfer_amd", "-Wl,-rpath,$ORIGIN", "-o", str(tmpb)]
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    if r.returncode != 0:
+        raise RuntimeError(f"intfer_serve link failed:\n{r.stderr[-4000:]}")
+    os.replace(tmpb, SERVE_BIN)
     return LIB
 
 

@@ -76,6 +76,15 @@ struct ifr_sched {
   std::vector<ifr_row> last_rows;
   std::vector<ifr_row> rows;
   std::vector<int32_t> best;
+  bool record = false;                 // ifr_sched_record_events
+  std::deque<ifr_sched_event> events;
+
+  // A streamed token: where the reference's emit hook fires (decode rows in
+  // live order, main.cpp:8405 / :8505; accepted drafts + correction of a
+  // verify group).  The token that ends a prefill is not streamed.
+  void emit(const Req& q, int32_t tok) {
+    if (record) events.push_back({q.id, tok, 0, (int32_t)q.generated.size(), 0});
+  }
 
   struct DecodeItem {
     Req* r;
@@ -116,6 +125,7 @@ struct ifr_sched {
         const int next = best[(size_t)it.row0];
         q.generated.push_back(next);
         q.pos++;
+        emit(q, next);
         q.token = next;
         if (is_eos(next)) q.finished = true;
         if ((int)q.generated.size() >= q.max_new + 1) q.finished = true;
@@ -125,21 +135,24 @@ struct ifr_sched {
       int a = 0;
       while (a < K && best[(size_t)it.row0 + a] == it.drafts[(size_t)a]) a++;
       const int corr = best[(size_t)it.row0 + a];
-      std::vector<int32_t> emit;
+      std::vector<int32_t> acc;
       for (int i = 0; i < a; ++i) {
-        emit.push_back(it.drafts[(size_t)i]);
+        acc.push_back(it.drafts[(size_t)i]);
         if (is_eos(it.drafts[(size_t)i])) break;
       }
-      bool stopped = !emit.empty() && is_eos(emit.back());
-      if (!stopped) emit.push_back(corr);
+      bool stopped = !acc.empty() && is_eos(acc.back());
+      if (!stopped) acc.push_back(corr);
       int budget = q.max_new + 1 - (int)q.generated.size();
       if (budget < 1) budget = 1;
-      while ((int)emit.size() > budget) emit.pop_back();
-      stopped = !emit.empty() && is_eos(emit.back());
-      const int n_draft_emit = (int)emit.size() - (stopped ? 0 : 1);
+      while ((int)acc.size() > budget) acc.pop_back();
+      stopped = !acc.empty() && is_eos(acc.back());
+      const int n_draft_emit = (int)acc.size() - (stopped ? 0 : 1);
       const int pend = q.pos + n_draft_emit;
       if (int r = be.seq_truncate(be.user, q.slot, pend + 1)) return r;
-      for (int t : emit) q.generated.push_back(t);
+      for (int t : acc) {
+        q.generated.push_back(t);
+        emit(q, t);
+      }
       q.token = q.generated.back();
       q.pos = pend + 1;
       if (stopped) q.finished = true;
@@ -301,12 +314,14 @@ int ifr_sched_step(ifr_sched* s, int32_t* rows_run) {
   }
   int r = s->cfg.split_iter ? s->split(rows_run) : s->joint(rows_run);
   if (r) return r;
-  // live compaction; finished requests release their KV
+  // live compaction; finished requests release their KV and report done
+  // (run_serve's {"done"} accounting, main.cpp:9349-9363)
   std::vector<Req*> still;
   for (Req* q : s->live) {
     if (q->finished) {
       if (q->slot >= 0) s->be.seq_close(s->be.user, q->slot);
       q->slot = -1;
+      if (s->record) s->events.push_back({q->id, -1, 1, (int32_t)q->generated.size(), 0});
     } else {
       still.push_back(q);
     }
@@ -324,6 +339,43 @@ int ifr_sched_result(ifr_sched* s, int64_t id, int32_t* out, int32_t cap, int32_
   for (int i = 0; i < k && out; ++i) out[i] = q.generated[(size_t)i];
   if (n) *n = (int32_t)q.generated.size();
   if (done) *done = q.finished ? 1 : 0;
+  return IFR_OK;
+}
+
+int ifr_sched_record_events(ifr_sched* s, int32_t on) {
+  if (!s) return IFR_EINVAL;
+  s->record = on != 0;
+  if (!s->record) s->events.clear();
+  return IFR_OK;
+}
+
+int ifr_sched_events(ifr_sched* s, ifr_sched_event* out, int32_t cap, int32_t* n) {
+  if (!s || (cap > 0 && !out) || !n) return IFR_EINVAL;
+  int32_t k = 0;
+  while (k < cap && !s->events.empty()) {
+    out[k++] = s->events.front();
+    s->events.pop_front();
+  }
+  *n = k;
+  return IFR_OK;
+}
+
+int ifr_sched_release(ifr_sched* s, int64_t id) {
+  if (!s) return IFR_EINVAL;
+  auto it = s->pool.find(id);
+  if (it == s->pool.end()) return IFR_EINVAL;
+  if (!it->second->finished) return IFR_ESTATE;
+  s->pool.erase(it);
+  return IFR_OK;
+}
+
+int ifr_sched_info(ifr_sched* s, int32_t* live, int32_t* prefill, int32_t* pending,
+                   int32_t* kv_capacity) {
+  if (!s) return IFR_EINVAL;
+  if (live) *live = (int32_t)s->live.size();
+  if (prefill) *prefill = (int32_t)s->prefill_q.size();
+  if (pending) *pending = (int32_t)s->pending.size();
+  if (kv_capacity) *kv_capacity = s->max_seq_tokens;
   return IFR_OK;
 }
 
