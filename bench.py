@@ -59,6 +59,8 @@ def parse():
                     help="comma-separated KV tokens per attention unit for --attn-sweep (0: default)")
     ap.add_argument("--copy-calib", action="store_true",
                     help="run only 8 device copies of 1 GiB (HBM traffic counter calibration)")
+    ap.add_argument("--cfg5", action="store_true",
+                    help="run only the cfg5 27B-class mixed iteration (M ~ 2160) and print its JSON line")
     return ap.parse_args()
 
 
@@ -366,6 +368,118 @@ def cpu_baseline(ia, model, cfg):
                       f"(the load's ~16.5 prefill tokens per output token); {dt:.1f} s"}
 
 
+def cfg5_bench(ia, a):
+    """cfg5: one mixed iteration of the 27B-class model (hidden 5120, 64
+    layers, 40 q / 8 kv heads, FFN 17408, seeded 70 / 30 INT2 / INT4 split,
+    INT8 KV): 48 decode sequences with contexts U[512, 4096] -- 16 of them
+    speculating with 4 n-gram drafts each, so their decode row becomes a
+    5-row verify group -- plus one 2048-token prefill chunk: M = 32 + 80 +
+    2048 = 2160.  The contexts are built by real prefill forwards of
+    uniform random tokens; after every iteration the sequences are cut back
+    (seq_truncate) so each timed iteration runs the same rows."""
+    from intfer_amd import workloads as wl  # noqa: F401  (same seeded style as the other configs)
+    cfg = ia.default_cfg(hidden=5120, layers=64, n_heads=40, n_kv=8, inter=17408)
+    t0 = time.perf_counter()
+    model = ia.SynthModel(cfg, seed=27, bits=0)
+    log(f"27B-class synthetic model built in {time.perf_counter() - t0:.1f} s")
+    dev = ia.Device(0)
+    rng = np.random.default_rng(5)
+    ctx = rng.integers(512, 4097, size=48).tolist()
+    spec = set(rng.choice(48, size=16, replace=False).tolist())
+    cap = 4224
+    t0 = time.perf_counter()
+    eng = ia.Engine(dev, model, max_seqs=50, max_seq_tokens=cap, pool_tokens=sum(ctx) + 48 * 64 + 2048 + 4096,
+                    kv_int8=1, max_rows=2304)
+    # device bytes of the quantized linears (codes + fp16 scale/zero pairs), exact per tensor
+    wbytes = 0.0
+    for l in range(cfg.layers):
+        lw = model.layer(l)
+        for nm in ("q", "k", "v", "o", "gate", "up", "down"):
+            t = getattr(lw, nm)
+            wbytes += t.N * t.K * t.bits / 8 + t.N * (t.K // 128) * 4
+    model.close()
+    log(f"model loaded in {time.perf_counter() - t0:.1f} s")
+    V = cfg.vocab
+    seqs = []
+    t0 = time.perf_counter()
+    for n in ctx:
+        s = eng.seq_open()
+        toks = rng.integers(0, V, size=n).tolist()
+        for c0 in range(0, n, 2048):
+            eng.forward([(s, p, toks[p], ia.ROW_PREFILL, 0) for p in range(c0, min(n, c0 + 2048))])
+        seqs.append(s)
+    log(f"48 contexts ({sum(ctx)} tokens) prefilled in {time.perf_counter() - t0:.1f} s")
+    pre = eng.seq_open()
+    it_toks = rng.integers(0, V, size=48 * 5 + 2048).tolist()
+    rows = []
+    k = 0
+    for j, s in enumerate(seqs):
+        if j in spec:
+            for d in range(5):
+                rows.append((s, ctx[j] + d, it_toks[k], ia.ROW_VERIFY, 1))
+                k += 1
+        else:
+            rows.append((s, ctx[j], it_toks[k], ia.ROW_DECODE, 1))
+            k += 1
+    for p in range(2048):
+        rows.append((pre, p, it_toks[k], ia.ROW_PREFILL, int(p == 2047)))
+        k += 1
+    arr = ia.rows_array(rows)
+    M = len(rows)
+
+    def once():
+        eng.forward(arr)
+        for j, s in enumerate(seqs):
+            eng.seq_truncate(s, ctx[j])
+        eng.seq_truncate(pre, 0)
+
+    for _ in range(a.warmup):
+        once()
+    dev.sync()
+    t0 = time.perf_counter()
+    for _ in range(a.steps):
+        once()
+    dev.sync()
+    ms = 1e3 * (time.perf_counter() - t0) / a.steps
+    # roofline of the iteration (SURVEY 8(d) formulas)
+    H, L, nq, nkv, hd, F = cfg.hidden, cfg.layers, cfg.n_heads, cfg.n_kv, cfg.head_dim, cfg.inter
+    per_layer = H * (nq * hd + 2 * nkv * hd) + nq * hd * H + H * 2 * F + F * H
+    nwant = sum(r[4] for r in rows)
+    lm_bytes = V * H + V * 2
+    kv_tok = L * nkv * hd * 2 * (1 + 2 / hd)      # int8 K+V + fp16 scale per (token, kv head)
+    vis = [r[1] + 1 for r in rows]                 # causal: a row sees pos + 1 tokens
+    kv_bytes = sum(ctx) * kv_tok + 2048 * kv_tok   # each sequence's cache read once per layer
+    ops = 2.0 * M * L * per_layer + 2.0 * nwant * V * H
+    flops = sum(4.0 * nq * hd * v for v in vis) * L
+    t_hbm = (wbytes + lm_bytes + kv_bytes) / HBM_PEAK
+    t_mfma = ops / INT8_PEAK + flops / FP16_PEAK
+    t_roof = max(t_hbm, t_mfma)
+    out = {"metric": "cfg5 27B-class mixed iteration (1 GPU)", "value": round(M / ms * 1e3, 1),
+           "unit": "rows/s", "ms_per_iteration": round(ms, 3), "steps": a.steps, "warmup": a.warmup,
+           "higher_is_better": True, "dtype": "int8 x int2/int4 -> int32 GEMM, int8 KV",
+           "data": "synthetic (seeded random-init weights, uniform token ids)",
+           "config": {"workload": "cfg5: 32 decode + 16 x (1 + 4 drafts) verify + 2048 prefill rows",
+                      "M": M, "contexts_mean": round(float(np.mean(ctx)), 1)},
+           "roofline": {"bound": "mfma" if t_mfma >= t_hbm else "hbm",
+                        "t_roof_ms": round(1e3 * t_roof, 3), "t_hbm_ms": round(1e3 * t_hbm, 3),
+                        "t_mfma_ms": round(1e3 * t_mfma, 3), "frac": round(1e3 * t_roof / ms, 4),
+                        "int8_ops": ops, "attn_flops": flops,
+                        "bytes": wbytes + lm_bytes + kv_bytes}}
+    if not a.no_roofline:
+        eng.set_timing(True)
+        once()
+        stats = {k2: eng.timing(k2) for k2 in KERNELS}
+        eng.set_timing(False)
+        out["kernels_ms"] = {k2: round(v[0], 3) for k2, v in stats.items() if v[1]}
+        g = [stats[k2] for k2 in GEMMS]
+        gms = sum(x[0] for x in g)
+        out["quant_gemm"] = {"ms": round(gms, 3), "TOPS": round(sum(x[3] for x in g) / gms / 1e9, 1),
+                             "frac_int8_peak": round(sum(x[3] for x in g) / gms / 1e9 / 5000, 4)}
+    print(json.dumps(out))
+    dev.close()
+    return 0
+
+
 def main():
     a = parse()
     if a.gpus != 1:
@@ -389,6 +503,8 @@ def main():
                           "bytes_written_per_copy": n, "GBps": round(2 * 8 * n / ms / 1e6, 1)}))
         dev.close()
         return 0
+    if a.cfg5:
+        return cfg5_bench(ia, a)
     if a.attn_sweep:
         dev = ia.Device(0)
         res = attn_sweep(ia, dev, splits=tuple(int(x) for x in a.attn_splits.split(",")))

@@ -293,13 +293,31 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs p, KVLayout kv) {
 
 // Merge the KV-split partials of one row for all heads, then per-token int8
 // quantization (half-away) of the [nq*hd] attention row for the O projection.
+// Thread t owns the CS consecutive dims [CS t, CS t + CS) of the row (CS a
+// power of two dividing hd, so a chunk never straddles a head; threads past
+// nq*hd/CS idle).  The merge runs the splits in order: the max over all
+// splits first, then l and O accumulated split by split, loaded in rounds of
+// 4 with clamped (unconditional) indices so each round is one memory latency.
+template <int CS>
+__device__ __forceinline__ int group_sum_int(int v) {
+  // the 128 columns of one K group are 128 / CS consecutive lanes
+  if constexpr (CS == 8) {
+    return ifrd::row16_sum_int(v);
+  } else {
+    v += __shfl_xor(v, 1, 64);
+    v += __shfl_xor(v, 2, 64);
+    if constexpr (CS == 16) v += __shfl_xor(v, 4, 64);
+    return v;
+  }
+}
+
+template <int CS>
 __global__ __launch_bounds__(256) void combine_kernel(CombineArgs a) {
-  extern __shared__ float sh[];
   const int m = blockIdx.x;
-  const int N = a.nq * a.hd;       // 2048
-  const int per = N / 256;         // dims per thread (8)
+  const int N = a.nq * a.hd;
   const int G = a.nq / a.nkv;
-  const int e0 = threadIdx.x * per;
+  const bool own = (int)threadIdx.x * CS < N;
+  const int e0 = own ? threadIdx.x * CS : 0;
   const int h = e0 / a.hd, d0 = e0 % a.hd;
   const int kvh = h / G, j = h % G;
   const int ns = a.comb_nsplit[m];
@@ -307,65 +325,52 @@ __global__ __launch_bounds__(256) void combine_kernel(CombineArgs a) {
   const int col = a.comb_tok[m] * G + j;
   float mx = -INFINITY;
   float L = 0.0f;
-  float acc[16];
-  for (int i = 0; i < per; ++i) acc[i] = 0.0f;
-  if (per == 8) {
-    // Splits in rounds of 4 with clamped (unconditional) loads, so each round
-    // is one memory latency: (m, l) of the splits first, then the partial O
-    // rows as two 16-byte loads per split, merged in split order.
-    const float2* ml2 = reinterpret_cast<const float2*>(a.part_ml);
-    for (int s0 = 0; s0 < ns; s0 += 4) {
-      float mm[4];
+  float acc[CS];
 #pragma unroll
-      for (int q = 0; q < 4; ++q) mm[q] = ml2[(size_t)(base + min(s0 + q, ns - 1)) * a.ucols + col].x;
+  for (int i = 0; i < CS; ++i) acc[i] = 0.0f;
+  const float2* ml2 = reinterpret_cast<const float2*>(a.part_ml);
+  for (int s0 = 0; s0 < ns; s0 += 4) {
+    float mm[4];
 #pragma unroll
-      for (int q = 0; q < 4; ++q) mx = fmaxf(mx, mm[q]);
+    for (int q = 0; q < 4; ++q) mm[q] = ml2[(size_t)(base + min(s0 + q, ns - 1)) * a.ucols + col].x;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) mx = fmaxf(mx, mm[q]);
+  }
+  for (int s0 = 0; s0 < ns; s0 += 4) {
+    float2 mlv[4];
+    float4 ov[4][CS / 4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const size_t pi = (size_t)(base + min(s0 + q, ns - 1)) * a.ucols + col;
+      mlv[q] = ml2[pi];
+      const float4* po = reinterpret_cast<const float4*>(a.part_o + pi * a.hd + d0);
+#pragma unroll
+      for (int r = 0; r < CS / 4; ++r) ov[q][r] = po[r];
     }
-    for (int s0 = 0; s0 < ns; s0 += 4) {
-      float2 mlv[4];
-      float4 ov[4][2];
 #pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        const size_t pi = (size_t)(base + min(s0 + q, ns - 1)) * a.ucols + col;
-        mlv[q] = ml2[pi];
-        const float4* po = reinterpret_cast<const float4*>(a.part_o + pi * a.hd + d0);
-        ov[q][0] = po[0];
-        ov[q][1] = po[1];
-      }
+    for (int q = 0; q < 4; ++q) {
+      if (s0 + q >= ns || mlv[q].x == -INFINITY) continue;
+      const float f = exp2f(mlv[q].x - mx);
+      L += f * mlv[q].y;
 #pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        if (s0 + q >= ns || mlv[q].x == -INFINITY) continue;
-        const float f = exp2f(mlv[q].x - mx);
-        L += f * mlv[q].y;
-        acc[0] += f * ov[q][0].x; acc[1] += f * ov[q][0].y;
-        acc[2] += f * ov[q][0].z; acc[3] += f * ov[q][0].w;
-        acc[4] += f * ov[q][1].x; acc[5] += f * ov[q][1].y;
-        acc[6] += f * ov[q][1].z; acc[7] += f * ov[q][1].w;
+      for (int r = 0; r < CS / 4; ++r) {
+        acc[4 * r + 0] += f * ov[q][r].x;
+        acc[4 * r + 1] += f * ov[q][r].y;
+        acc[4 * r + 2] += f * ov[q][r].z;
+        acc[4 * r + 3] += f * ov[q][r].w;
       }
-    }
-  } else {
-    for (int s = 0; s < ns; ++s) mx = fmaxf(mx, a.part_ml[((size_t)(base + s) * a.ucols + col) * 2]);
-    for (int s = 0; s < ns; ++s) {
-      const size_t pi = (size_t)(base + s) * a.ucols + col;
-      const float ms = a.part_ml[pi * 2];
-      if (ms == -INFINITY) continue;
-      const float f = exp2f(ms - mx);
-      L += f * a.part_ml[pi * 2 + 1];
-      const float* po = a.part_o + pi * a.hd + d0;
-      for (int i = 0; i < per; ++i) acc[i] += f * po[i];
     }
   }
   const float invL = 1.0f / L;
-  float* x = sh;
-  int* codes = reinterpret_cast<int*>(sh + N);
-  __shared__ float red[8];
+  __shared__ float red[4];
   float amax = 0.0f;
-  for (int i = 0; i < per; ++i) {
+#pragma unroll
+  for (int i = 0; i < CS; ++i) {
     const float v = acc[i] * invL;
-    x[e0 + i] = v;
     amax = fmaxf(amax, fabsf(v));
-    if (a.attn_out) a.attn_out[(size_t)m * N + e0 + i] = v;
+    if (own && a.attn_out) a.attn_out[(size_t)m * N + e0 + i] = v;
   }
+  if (!own) amax = 0.0f;
   amax = ifrd::wave_max(amax);
   if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = amax;
   __syncthreads();
@@ -373,33 +378,28 @@ __global__ __launch_bounds__(256) void combine_kernel(CombineArgs a) {
   const float sc = mxa / 127.0f;
   const float inv = 1.0f / sc;
   if (threadIdx.x == 0) a.qscale[m] = sc;
+  // CS consecutive columns sit in one or two 16-byte A-tile lane chunks
+  uint32_t w[CS / 4];
   int csum = 0;
-  if (per == 8) {
-    // 8 consecutive columns = half of one 16-byte A-tile lane chunk: one store
-    uint32_t w[2] = {0u, 0u};
-    for (int i = 0; i < 8; ++i) {
-      const int c = ifrd::quant_half_away(acc[i] * invL, inv);
-      w[i >> 2] |= (uint32_t)(c & 0xFF) << (8 * (i & 3));
-      csum += c;
-    }
-    *reinterpret_cast<uint2*>(a.q + atile_off(m, e0, N)) = make_uint2(w[0], w[1]);
-    // the 128 columns of group e0 / 128 are the 16 lanes of one DPP row
-    csum = ifrd::row16_sum_int(csum);
-    if ((threadIdx.x & 15) == 0) a.gsum[(size_t)m * (N / 128) + e0 / 128] = (float)csum;
-    return;
-  }
-  for (int i = 0; i < per; ++i) {
-    const int c = ifrd::quant_half_away(x[e0 + i], inv);
-    a.q[atile_off(m, e0 + i, N)] = (int8_t)c;
-    codes[e0 + i] = c;
+#pragma unroll
+  for (int i = 0; i < CS / 4; ++i) w[i] = 0u;
+#pragma unroll
+  for (int i = 0; i < CS; ++i) {
+    const int c = ifrd::quant_half_away(acc[i] * invL, inv);
+    w[i >> 2] |= (uint32_t)(c & 0xFF) << (8 * (i & 3));
     csum += c;
   }
-  __syncthreads();
-  for (int gg = threadIdx.x; gg < N / 128; gg += 256) {
-    int S = 0;
-    for (int k = gg * 128; k < gg * 128 + 128; ++k) S += codes[k];
-    a.gsum[(size_t)m * (N / 128) + gg] = (float)S;
+  csum = group_sum_int<CS>(csum);
+  if (!own) return;
+  if constexpr (CS == 8) {
+    *reinterpret_cast<uint2*>(a.q + atile_off(m, e0, N)) = make_uint2(w[0], w[1]);
+  } else {
+#pragma unroll
+    for (int r = 0; r < CS / 16; ++r)
+      *reinterpret_cast<uint4*>(a.q + atile_off(m, e0 + 16 * r, N)) =
+          make_uint4(w[4 * r], w[4 * r + 1], w[4 * r + 2], w[4 * r + 3]);
   }
+  if (threadIdx.x % (128 / CS) == 0) a.gsum[(size_t)m * (N / 128) + e0 / 128] = (float)csum;
 }
 
 }  // namespace
@@ -426,10 +426,11 @@ hipError_t launch_attention(const AttnArgs& a, const KVLayout& kv, hipStream_t s
 hipError_t launch_combine(const CombineArgs& a, hipStream_t st) {
   if (a.M <= 0) return hipSuccess;
   const int N = a.nq * a.hd;
-  if (N % 256 != 0 || N / 256 > 16 || N % 128 != 0 || a.hd != kHD || !a.q || !a.qscale || !a.gsum)
+  if (N % 128 != 0 || N > 256 * 32 || a.hd != kHD || !a.q || !a.qscale || !a.gsum)
     return hipErrorInvalidValue;
-  const size_t lds = (size_t)2 * N * sizeof(float);
-  hipLaunchKernelGGL(combine_kernel, dim3(a.M), dim3(256), lds, st, a);
+  if (N <= 256 * 8) hipLaunchKernelGGL(combine_kernel<8>, dim3(a.M), dim3(256), 0, st, a);
+  else if (N <= 256 * 16) hipLaunchKernelGGL(combine_kernel<16>, dim3(a.M), dim3(256), 0, st, a);
+  else hipLaunchKernelGGL(combine_kernel<32>, dim3(a.M), dim3(256), 0, st, a);
   return hipGetLastError();
 }
 

@@ -803,7 +803,7 @@ int ifr_model_load(ifr_ctx* c, const ifr_host_model* m, const ifr_kv_cfg* kvc) {
   if (cf.n_heads % cf.n_kv != 0 || cf.n_heads / cf.n_kv > 8)
     return fail(IFR_EDECLINE, "GQA group %d/%d unsupported", cf.n_heads, cf.n_kv);
   if (cf.hidden % 256 || cf.hidden > 8192 || (cf.n_heads * cf.head_dim) % 256 ||
-      cf.inter % 128 || cf.inter > 8192 || cf.vocab % 16)
+      cf.inter % 128 || cf.inter > ifrk::kQuantPlainMaxK || cf.vocab % 16)
     return fail(IFR_EDECLINE, "model shape unsupported");
   if (cf.rotary_dim <= 0 || cf.rotary_dim > cf.head_dim || cf.rotary_dim % 2)
     return fail(IFR_EINVAL, "rotary_dim");

@@ -696,6 +696,17 @@ __global__ void gather_rows_kernel(const float* src, const int32_t* rows, int H,
 
 }  // namespace
 
+// The generic row kernels stage a row in LDS; rows past 64 KB (K > 8000
+// floats of staging) need the 160 KB dynamic-LDS limit, set once per kernel.
+template <typename F>
+hipError_t allow_big_lds(F* f, bool& done) {
+  if (done) return hipSuccess;
+  hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(f),
+                                     hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
+  if (e == hipSuccess) done = true;
+  return e;
+}
+
 hipError_t launch_row_quant(const RowQuantArgs& a, hipStream_t st) {
   if (a.M <= 0) return hipSuccess;
   if (a.K <= 0 || a.K % 128 != 0 || a.K > 8192 || !a.q || !a.qscale) return hipErrorInvalidValue;
@@ -708,6 +719,8 @@ hipError_t launch_row_quant(const RowQuantArgs& a, hipStream_t st) {
     return hipGetLastError();
   }
   const size_t lds = (size_t)(2 * a.K + 64 + a.K / 64) * sizeof(float);
+  static bool big = false;
+  if (hipError_t e = allow_big_lds(row_quant_kernel, big)) return e;
   hipLaunchKernelGGL(row_quant_kernel, dim3(a.M), dim3(256), lds, st, a);
   return hipGetLastError();
 }
@@ -715,7 +728,7 @@ hipError_t launch_row_quant(const RowQuantArgs& a, hipStream_t st) {
 hipError_t launch_quant_plain(const float* xf, const uint16_t* xh, int M, int K, int8_t* q,
                               float* qscale, float* gsum, hipStream_t st) {
   if (M <= 0) return hipSuccess;
-  if (K <= 0 || K % 128 != 0 || K > 8192 || (!xf && !xh) || !q || !qscale)
+  if (K <= 0 || K % 128 != 0 || K > kQuantPlainMaxK || (!xf && !xh) || !q || !qscale)
     return hipErrorInvalidValue;
   if (K == 2048) {
     hipLaunchKernelGGL(quant_plain8<256>, dim3(M), dim3(256), 0, st, xf, xh, q, qscale, gsum);
@@ -730,6 +743,8 @@ hipError_t launch_quant_plain(const float* xf, const uint16_t* xh, int M, int K,
     return hipGetLastError();
   }
   const size_t lds = (size_t)(2 * K + 64) * sizeof(float);
+  static bool big = false;
+  if (hipError_t e = allow_big_lds(quant_plain_kernel, big)) return e;
   hipLaunchKernelGGL(quant_plain_kernel, dim3(M), dim3(256), lds, st, xf, xh, K, q, qscale, gsum);
   return hipGetLastError();
 }

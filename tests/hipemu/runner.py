@@ -263,14 +263,14 @@ def sched_small():
 
 
 @scenario
-def attention_ragged():
+def attention_ragged(heads=(16, 8)):
     """Joint ragged attention (decode rows of several lengths + two causal
     chunks, one at an offset), fp16 and int8 KV, vs the oracle row loop."""
     import intfer_amd as ia
     from oracle import pyoracle as po
     from oracle.pyoracle import ptr
     for kv_int8 in (0, 1):
-        cfg = ia.default_cfg(layers=1, vocab=1024)
+        cfg = ia.default_cfg(layers=1, vocab=1024, n_heads=heads[0], n_kv=heads[1])
         model = ia.SynthModel(cfg, seed=5)
         dev = ia.Device(0)
         lens = [40, 300, 257, 1000, 33]
@@ -316,6 +316,25 @@ def attention_ragged():
         assert err < 4e-3
         dev.close()
         model.close()
+
+
+@scenario
+def forward_gqa5():
+    """A layer of the 27B-class shape family at small width: 40 q / 8 kv
+    heads (GQA group 5), hidden 1280 (non-power-of-two Hadamard), an FFN of
+    17 groups, mixed INT2 / INT4 widths, int8 KV."""
+    err = _forward_case(1, 1, 1, hidden=1280, n_heads=40, n_kv=8, inter=2176, vocab=512, bits=0)
+    # attention is fp32-accurate, not bit-identical: an int8 activation code
+    # flip moves a logit row by a few hundredths of its sigma; a wrong head
+    # or group mapping moves it by whole sigmas
+    assert err < 0.2, err
+
+
+@scenario
+def attention_ragged_g5():
+    """The same with a GQA group of 5 (the 27B-class 40 q / 8 kv heads),
+    whose q-block of 3 tokens fills 15 of the 16 MFMA columns."""
+    attention_ragged(heads=(10, 2))
 
 
 @scenario

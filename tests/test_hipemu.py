@@ -44,3 +44,7 @@ def test_every_gemm_launch_shape_in_bounds(emu_lib):
 
 def test_intfer_load_and_parser_in_bounds(emu_lib):
     assert runner.run_scenarios(["intfer_load"], timeout=600) == 0
+
+
+def test_gqa_group5_shapes_in_bounds(emu_lib):
+    assert runner.run_scenarios(["attention_ragged_g5", "forward_gqa5"], timeout=900) == 0
