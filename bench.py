@@ -53,6 +53,8 @@ def parse():
                     help="run only the cache-cold cfg2 GEMM sweep and print its JSON line")
     ap.add_argument("--gemm-variants", action="store_true",
                     help="time every quant-GEMM launch shape on the 0.8B shapes and print a JSON line")
+    ap.add_argument("--gemm-variants-27b", action="store_true",
+                    help="the same on the 27B-class (cfg5) shapes at M = 512 and 2160")
     ap.add_argument("--attn-sweep", action="store_true",
                     help="run only the attention sweep (cfg3, C=64 decode, mixed) and print its JSON line")
     ap.add_argument("--attn-splits", default="0",
@@ -282,14 +284,18 @@ def attn_sweep(ia, dev, reps=10, splits=(0,)):
     return res
 
 
-def gemm_variants(ia, dev, Ms=(128, 256, 576, 1024), bits=2, reps=3):
-    """Every launch shape of the quant GEMM on the four 0.8B shapes (gate_up
-    as the interleaved SwiGLU pair the forward runs), cache-cold as in
-    gemm_sweep; one line per (shape, M, variant)."""
+SHAPES_08B = [("qkv", 1024, 4096, False), ("o", 2048, 1024, False), ("gate_up", 1024, 3072, True),
+              ("down", 3072, 1024, False)]
+SHAPES_27B = [("qkv", 5120, 7168, False), ("o", 5120, 5120, False), ("gate_up", 5120, 17408, True),
+              ("down", 17408, 5120, False)]
+
+
+def gemm_variants(ia, dev, Ms=(128, 256, 576, 1024), bits=2, reps=3, shapes=SHAPES_08B):
+    """Every launch shape of the quant GEMM on the four projection shapes
+    (gate_up as the interleaved SwiGLU pair the forward runs), cache-cold as
+    in gemm_sweep; one line per (shape, M, variant)."""
     import ctypes as C
     L = ia.lib()
-    shapes = [("qkv", 1024, 4096, False), ("o", 2048, 1024, False), ("gate_up", 1024, 3072, True),
-              ("down", 3072, 1024, False)]
     rng = np.random.default_rng(0)
     res = []
     nv = L.ifr_quant_gemm_variants()
@@ -512,9 +518,10 @@ def main():
                           "results": res}))
         dev.close()
         return 0
-    if a.gemm_variants:
+    if a.gemm_variants or a.gemm_variants_27b:
         dev = ia.Device(0)
-        res = gemm_variants(ia, dev)
+        res = gemm_variants(ia, dev) if a.gemm_variants else \
+            gemm_variants(ia, dev, Ms=(512, 2160), shapes=SHAPES_27B, reps=2)
         print(json.dumps({"metric": "quant-GEMM launch shapes (cache-cold)", "unit": "us", "results": res}))
         dev.close()
         return 0

@@ -86,8 +86,8 @@ struct RowQuantArgs {
 hipError_t launch_row_quant(const RowQuantArgs& a, hipStream_t st);
 
 // Plain per-token quantization of an fp32 or fp16 [M][K] buffer (no norm, no
-// rotation), K a multiple of 128 and <= kQuantPlainMaxK (a row of fp32 values
-// and int codes staged in 160 KB of LDS).
+// rotation), K a multiple of 128 and <= kQuantPlainMaxK (a row held in the
+// registers of one 256-thread workgroup, 8 values per thread per 2048).
 constexpr int kQuantPlainMaxK = 20352;
 hipError_t launch_quant_plain(const float* xf, const uint16_t* xh, int M, int K, int8_t* q,
                               float* qscale, float* gsum, hipStream_t st);

@@ -491,6 +491,14 @@ hipError_t launch_bits(const KParams& p, int variant, hipStream_t st) {
     const int splitk_max = narrow ? (p.ng <= 16 ? 576 : 256) : 128;
     if (p.ng <= 24 && p.M <= splitk_max) variant = 0;
     else variant = narrow ? 4 : 5;
+    // The 27B-class shapes (K >= 4096; bench.py --gemm-variants-27b, M = 512
+    // and 2160): the 136-group down projection keeps its A and B tiles
+    // resident best in 64 x 64 blocks; the others gain from 32 x 256 once M
+    // or N is large.
+    if (p.K >= 4096 && p.M > 256) {
+      if (p.ng >= 96) variant = 3;
+      else if (p.M >= 1024 || p.N >= 6144) variant = 6;
+    }
   }
   switch (variant) {
     case 0: return launch_splitk_ng<BITS, 1, WNs, EPI>(p, st);

@@ -345,19 +345,67 @@ __global__ __launch_bounds__(NT) void quant_plain8(const float* xf, const uint16
   if (gsum && (lane & 15) == 0) gsum[(size_t)m * (K / 128) + (t >> 4)] = (float)S;
 }
 
-__global__ __launch_bounds__(256) void quant_plain_kernel(const float* xf, const uint16_t* xh,
-                                                          int K, int8_t* q, float* qs,
-                                                          float* gsum) {
-  extern __shared__ float sh[];
-  float* x = sh;
-  int* codes = reinterpret_cast<int*>(sh + K);
-  float* red = sh + 2 * K;
-  const int m = blockIdx.x;
-  for (int i = threadIdx.x; i < K; i += blockDim.x)
-    x[i] = xf ? xf[(size_t)m * K + i] : ifrd::h2f(xh[(size_t)m * K + i]);
+// Any K (a multiple of 128, up to 2048 * CH): 256 threads per row, thread t
+// holds the 8-element chunks t, t + 256, ... in registers, so the row is read
+// once and each chunk is written as one 8-byte A-tile store.  The 16 chunks
+// of a 128-column group sit on the 16 lanes of one DPP row, whatever the
+// round, because 256 is a multiple of 16.  Same rule as quant_plain8.
+template <int CH>
+__global__ __launch_bounds__(256) void quant_plain_wide(const float* xf, const uint16_t* xh, int K,
+                                                        int8_t* q, float* qs, float* gsum) {
+  __shared__ float red[4];
+  const int m = blockIdx.x, t = threadIdx.x, lane = t & 63;
+  const int nch = K / 8;
+  float v[CH][8];
+  float mx = 0.0f;
+#pragma unroll
+  for (int i = 0; i < CH; ++i) {
+    const int c = t + 256 * i;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) v[i][e] = 0.0f;
+    if (c < nch) {
+      if (xf) {
+        const float4* p = reinterpret_cast<const float4*>(xf + (size_t)m * K + 8 * c);
+        const float4 a = p[0], b = p[1];
+        v[i][0] = a.x; v[i][1] = a.y; v[i][2] = a.z; v[i][3] = a.w;
+        v[i][4] = b.x; v[i][5] = b.y; v[i][6] = b.z; v[i][7] = b.w;
+      } else {
+        const uint4 r = *reinterpret_cast<const uint4*>(xh + (size_t)m * K + 8 * c);
+        const uint32_t w[4] = {r.x, r.y, r.z, r.w};
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          v[i][2 * e] = ifrd::h2f((uint16_t)(w[e] & 0xFFFF));
+          v[i][2 * e + 1] = ifrd::h2f((uint16_t)(w[e] >> 16));
+        }
+      }
+    }
+#pragma unroll
+    for (int e = 0; e < 8; ++e) mx = fmaxf(mx, fabsf(v[i][e]));
+  }
+  mx = ifrd::wave_max(mx);
+  if (lane == 0) red[t >> 6] = mx;
   __syncthreads();
-  quant_lds(x, K, 0, 0, q, m, qs + m, gsum ? gsum + (size_t)m * (K / 128) : nullptr,
-            red, codes);
+  mx = fmaxf(1e-6f, fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3])));
+  const float s = mx / 127.0f;
+  const float inv = 1.0f / s;
+  if (t == 0) qs[m] = s;
+#pragma unroll
+  for (int i = 0; i < CH; ++i) {
+    const int c = t + 256 * i;
+    uint32_t w[2] = {0u, 0u};
+    int S = 0;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const int cq = ifrd::quant_half_away(v[i][e], inv);
+      w[e >> 2] |= (uint32_t)(cq & 0xFF) << (8 * (e & 3));
+      S += cq;
+    }
+    S = ifrd::row16_sum_int(S);  // every lane takes part (DPP)
+    if (c < nch) {
+      *reinterpret_cast<uint2*>(q + atile_off(m, 8 * c, K)) = make_uint2(w[0], w[1]);
+      if (gsum && (lane & 15) == 0) gsum[(size_t)m * (K / 128) + (c >> 4)] = (float)S;
+    }
+  }
 }
 
 // ---- q/k norm + RoPE + KV append --------------------------------------------
@@ -742,10 +790,16 @@ hipError_t launch_quant_plain(const float* xf, const uint16_t* xh, int M, int K,
     hipLaunchKernelGGL(quant_plain8<512>, dim3(M), dim3(512), 0, st, xf, xh, q, qscale, gsum);
     return hipGetLastError();
   }
-  const size_t lds = (size_t)(2 * K + 64) * sizeof(float);
-  static bool big = false;
-  if (hipError_t e = allow_big_lds(quant_plain_kernel, big)) return e;
-  hipLaunchKernelGGL(quant_plain_kernel, dim3(M), dim3(256), lds, st, xf, xh, K, q, qscale, gsum);
+  switch ((K + 2047) / 2048) {
+#define IFR_QPW(CH)                                                                         \
+  case CH:                                                                                   \
+    hipLaunchKernelGGL(quant_plain_wide<CH>, dim3(M), dim3(256), 0, st, xf, xh, K, q, qscale, gsum); \
+    break;
+    IFR_QPW(1) IFR_QPW(2) IFR_QPW(3) IFR_QPW(4) IFR_QPW(5)
+    IFR_QPW(6) IFR_QPW(7) IFR_QPW(8) IFR_QPW(9) IFR_QPW(10)
+#undef IFR_QPW
+    default: return hipErrorInvalidValue;
+  }
   return hipGetLastError();
 }
 
