@@ -49,6 +49,8 @@ def parse():
     ap.add_argument("--kv-int8", type=int, default=0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-roofline", action="store_true")
+    ap.add_argument("--no-packed", action="store_true",
+                    help="skip the secondary pack_prefill measurement of the same load")
     ap.add_argument("--gemm-sweep", action="store_true",
                     help="run only the cache-cold cfg2 GEMM sweep and print its JSON line")
     ap.add_argument("--gemm-variants", action="store_true",
@@ -71,8 +73,8 @@ def log(msg):
     sys.stderr.flush()
 
 
-def run_load(ia, eng, prompts, max_new, chunk, record=None):
-    sch = ia.Scheduler(eng, chunk_m=chunk, live_cap=64)
+def run_load(ia, eng, prompts, max_new, chunk, record=None, pack=0):
+    sch = ia.Scheduler(eng, chunk_m=chunk, live_cap=64, pack_prefill=pack)
     ids = [sch.submit(p, max_new) for p in prompts]
     done_at = {}
     iters = rows = 0
@@ -605,6 +607,19 @@ def main():
                                  "frac": round(value / roof_tok_s, 4),
                                  "decode_rows": dec, "iterations": len(rec)}
         log(f"timing pass: {dt:.3f} s; dominant {dom} {stats[dom][0]:.1f} ms; roofline tok/s {roof_tok_s:.0f}")
+    if not a.no_packed:
+        # the same load with the chunk budget filled from several queued
+        # prompts (pack_prefill; the reference fills it from the head only):
+        # same token streams, fewer iterations; reported beside `value`
+        run_load(ia, eng, prompts, max_new, chunk, pack=1)
+        dev.sync()
+        dt, toks, iters, rows, done = run_load(ia, eng, prompts, max_new, chunk, pack=1)
+        dev.sync()
+        out["packed_prefill"] = {"value": round(toks / dt, 2), "unit": "tok/s", "iterations": iters,
+                                 "ms_per_step": round(1e3 * dt, 3), "p50_latency_s": round(pct(done, 50), 4),
+                                 "p99_latency_s": round(pct(done, 99), 4),
+                                 "note": "scheduler option pack_prefill=1 (not the reference policy)"}
+        log(f"packed prefill: {dt:.3f} s, {iters} iterations, {toks / dt:.0f} tok/s")
     if not a.no_cpu:
         log("timing the reference CPU path on a bounded sample")
         out["cpu_baseline"] = cpu_baseline(ia, model, cfg)

@@ -430,6 +430,11 @@ typedef struct ifr_sched_cfg {
   int32_t split_iter; /* 1: split path (chunk forward, then decode forward) */
   int32_t round_robin;/* 1: rotate unfilled prefill heads (INTFER_PREFILL_RR) */
   int32_t spec_k;     /* n-gram draft width for verify rows; 0 = off */
+  int32_t pack_prefill; /* no reference counterpart (its chunk holds only the
+                         * queue head's rows, main.cpp:8447-8470): 1 fills
+                         * the chunk_m budget from the prefill queue in
+                         * order, so a prompt ending mid-chunk leaves its
+                         * room to the next.  Token streams are unchanged. */
 } ifr_sched_cfg;
 
 int ifr_sched_create(ifr_ctx* ctx, const ifr_sched_cfg* cfg, ifr_sched** out);

@@ -76,7 +76,7 @@ class Row(C.Structure):
 
 class SchedCfg(C.Structure):
     _fields_ = [("chunk_m", C.c_int32), ("live_cap", C.c_int32), ("split_iter", C.c_int32),
-                ("round_robin", C.c_int32), ("spec_k", C.c_int32)]
+                ("round_robin", C.c_int32), ("spec_k", C.c_int32), ("pack_prefill", C.c_int32)]
 
 
 SEQ_OPEN = C.CFUNCTYPE(C.c_int, C.c_void_p, C.POINTER(C.c_int32))

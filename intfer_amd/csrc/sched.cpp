@@ -169,61 +169,71 @@ struct ifr_sched {
     live.push_back(pq);
   }
 
+  // One chunk's prefill rows, appended to `rows`: the queue head's next
+  // rows (main.cpp:8447-8470), or with pack_prefill the chunk budget filled
+  // from the queue in order (a request whose prompt ends inside the chunk
+  // leaves room for the next).  Returns the (request, rows) pieces.
+  struct Piece {
+    Req* q;
+    int row0, n;
+  };
+  std::vector<Piece> build_prefill() {
+    std::vector<Piece> pieces;
+    int budget = cfg.chunk_m;
+    for (Req* q : prefill_q) {
+      if (budget == 0) break;
+      const int Sr = (int)q->prompt.size();
+      const int n = std::min(budget, Sr - q->fill);
+      pieces.push_back({q, (int)rows.size(), n});
+      for (int k = 0; k < n; ++k) {
+        const int pos = q->fill + k;
+        rows.push_back({q->slot, pos, q->prompt[(size_t)pos], IFR_ROW_PREFILL,
+                        (q->fill + n == Sr && k == n - 1) ? 1 : 0});
+      }
+      budget -= n;
+      if (!cfg.pack_prefill) break;
+    }
+    return pieces;
+  }
+
+  // After the forward: filled requests join live in queue order; an unfilled
+  // head rotates to the back (serve_rotate_unfilled, main.cpp:9187-9195).
+  void finish_prefill(const std::vector<Piece>& pieces) {
+    for (const Piece& pc : pieces) {
+      Req* q = pc.q;
+      const int Sr = (int)q->prompt.size();
+      q->fill += pc.n;
+      if (q->fill == Sr) {
+        prefill_q.erase(std::find(prefill_q.begin(), prefill_q.end(), q));
+        prefill_done(q, best[(size_t)pc.row0 + pc.n - 1]);
+      } else if (cfg.round_robin && prefill_q.size() > 1 && prefill_q.front() == q) {
+        prefill_q.pop_front();
+        prefill_q.push_back(q);
+      }
+    }
+  }
+
   int joint(int32_t* nrun) {
     rows.clear();
     std::vector<DecodeItem> items;
     build_decode(items);
-    Req* pq = prefill_q.empty() ? nullptr : prefill_q.front();
-    int P = 0, p0 = (int)rows.size();
-    if (pq) {
-      const int Sr = (int)pq->prompt.size();
-      P = std::min(cfg.chunk_m, Sr - pq->fill);
-      for (int k = 0; k < P; ++k) {
-        const int pos = pq->fill + k;
-        rows.push_back({pq->slot, pos, pq->prompt[(size_t)pos], IFR_ROW_PREFILL,
-                        (pq->fill + P == Sr && k == P - 1) ? 1 : 0});
-      }
-    }
+    const std::vector<Piece> pieces = build_prefill();
     *nrun = (int32_t)rows.size();
     if (rows.empty()) return IFR_OK;
     if (int r = forward()) return r;
     if (int r = finish_decode(items)) return r;
-    if (pq) {
-      const int Sr = (int)pq->prompt.size();
-      pq->fill += P;
-      if (pq->fill == Sr) {
-        prefill_q.pop_front();
-        prefill_done(pq, best[(size_t)p0 + P - 1]);
-      } else if (cfg.round_robin && prefill_q.size() > 1) {
-        prefill_q.pop_front();
-        prefill_q.push_back(pq);
-      }
-    }
+    finish_prefill(pieces);
     return IFR_OK;
   }
 
   int split(int32_t* nrun) {
     *nrun = 0;
     if (!prefill_q.empty()) {
-      Req* q = prefill_q.front();
-      const int Sr = (int)q->prompt.size();
-      const int cm = std::min(cfg.chunk_m, Sr - q->fill);
       rows.clear();
-      for (int k = 0; k < cm; ++k) {
-        const int pos = q->fill + k;
-        rows.push_back({q->slot, pos, q->prompt[(size_t)pos], IFR_ROW_PREFILL,
-                        (q->fill + cm == Sr && k == cm - 1) ? 1 : 0});
-      }
+      const std::vector<Piece> pieces = build_prefill();
       if (int r = forward()) return r;
-      *nrun += cm;
-      q->fill += cm;
-      if (q->fill == Sr) {
-        prefill_q.pop_front();
-        prefill_done(q, best[(size_t)cm - 1]);
-      } else if (cfg.round_robin && prefill_q.size() > 1 && prefill_q.front() == q) {
-        prefill_q.pop_front();
-        prefill_q.push_back(q);
-      }
+      *nrun += (int32_t)rows.size();
+      finish_prefill(pieces);
     }
     if (!live.empty()) {
       rows.clear();
@@ -256,7 +266,7 @@ int ifr_sched_create_backend(const ifr_sched_backend* be, const ifr_sched_cfg* c
   if (!be || !cfg || !out || !be->seq_open || !be->seq_close || !be->seq_truncate || !be->forward)
     return IFR_EINVAL;
   if (cfg->chunk_m < 1 || cfg->chunk_m > 4096 || cfg->live_cap < 1 || cfg->spec_k < 0 ||
-      cfg->spec_k > 15 || be->kv_capacity <= 0)
+      cfg->spec_k > 15 || cfg->pack_prefill < 0 || cfg->pack_prefill > 1 || be->kv_capacity <= 0)
     return IFR_EINVAL;
   auto* s = new ifr_sched();
   s->be = *be;

@@ -20,7 +20,8 @@ void usage() {
                "usage: intfer_serve (-m MODEL.intfer | --synth SEED [--bits 2|4|0] [--intfer-form])\n"
                "  [--hidden H --layers L --heads NQ --kv-heads NKV --inter F --vocab V]\n"
                "  [--kv-int8] [--max-new N] [--chunk-m N] [--live-cap N] [--split-iter] [--no-rr]\n"
-               "  [--spec-k K] [--max-seq-tokens N] [--max-seqs N] [--pool-tokens N] [--device D]\n");
+               "  [--spec-k K] [--pack-prefill] [--max-seq-tokens N] [--max-seqs N] [--pool-tokens N]\n"
+               "  [--device D]\n");
 }
 
 int env_int(const char* name, int dflt, int lo, int hi) {
@@ -42,7 +43,7 @@ int main(int argc, char** argv) {
   int live_cap = env_int("INTFER_SERVE_MAX", 64, 1, 64);
   int split_iter = std::getenv("INTFER_SPLIT_ITER") ? 1 : 0;
   int rr = (std::getenv("INTFER_PREFILL_RR") && std::string(std::getenv("INTFER_PREFILL_RR")) == "0") ? 0 : 1;
-  int max_seq_tokens = 4096, max_seqs = 0;
+  int max_seq_tokens = 4096, max_seqs = 0, pack = 0;
   long long pool_tokens = 0;
   for (int i = 1; i < argc; ++i) {
     const std::string a = argv[i];
@@ -70,6 +71,7 @@ int main(int argc, char** argv) {
     else if (a == "--split-iter") split_iter = 1;
     else if (a == "--no-rr") rr = 0;
     else if (a == "--spec-k") spec_k = std::atoi(next());
+    else if (a == "--pack-prefill") pack = 1;
     else if (a == "--max-seq-tokens") max_seq_tokens = std::atoi(next());
     else if (a == "--max-seqs") max_seqs = std::atoi(next());
     else if (a == "--pool-tokens") pool_tokens = std::atoll(next());
@@ -118,6 +120,7 @@ int main(int argc, char** argv) {
   sc.split_iter = split_iter;
   sc.round_robin = rr;
   sc.spec_k = spec_k;
+  sc.pack_prefill = pack;
   ifr_sched* s = nullptr;
   if (ifr_sched_create(ctx, &sc, &s) != IFR_OK) {
     std::fprintf(stderr, "FAIL: scheduler: %s\n", ifr_last_error());

@@ -151,6 +151,29 @@ def test_row_list_structure_and_budgets():
             assert all(r[4] == 0 for r in pre[:-1])
 
 
+def test_pack_prefill_keeps_streams_and_fills_chunks():
+    """pack_prefill (no reference counterpart) fills the chunk budget from
+    several queued prompts; every stream is unchanged and the iteration count
+    drops, with every prefill chunk full while enough prompt rows wait."""
+    ps = prompts_of(12, 21, lo=10, hi=120)
+    chunk = 64
+    a, la = run(ps, 6, chunk_m=chunk, live_cap=8)
+    b, lb = run(ps, 6, chunk_m=chunk, live_cap=8, pack_prefill=1)
+    c, lc = run(ps, 6, chunk_m=chunk, live_cap=8, pack_prefill=1, split_iter=1)
+    assert a == b == c
+    assert len(lb.forwards) < len(la.forwards)
+    pre = [sum(1 for r in f if r[3] == ia.ROW_PREFILL) for f in lb.forwards]
+    total = sum(len(p) for p in ps)
+    full = total // chunk
+    assert pre[:full] == [chunk] * full  # all 12 prompts are queued from the first step
+    # a chunk may now carry several requests, each one contiguous
+    multi = [f for f in lb.forwards if len({r[0] for r in f if r[3] == ia.ROW_PREFILL}) > 1]
+    assert multi
+    for f in multi:
+        seqs = [r[0] for r in f if r[3] == ia.ROW_PREFILL]
+        assert all(seqs[i] == seqs[i + 1] or seqs[i + 1] not in seqs[:i + 1] for i in range(len(seqs) - 1))
+
+
 def test_round_robin_rotates_unfilled_heads():
     ps = [list(range(60)), list(range(1, 61)), list(range(2, 62))]
     _, lm = run(ps, 2, chunk_m=16, live_cap=8, round_robin=1)
