@@ -295,6 +295,281 @@ __global__ __launch_bounds__(256) void row_quant1024_kernel(RowQuantArgs a) {
   }
 }
 
+// ---- any K (a multiple of 256, up to 8192): the row in registers -----------
+//
+// The row splits into the power-of-two head [0, P) the FWHT rotates
+// (blockdiag(H_P, I), spinquant.cpp:586-604) and the tail [P, K).  Thread t
+// holds the E = P / 256 contiguous head elements [E t, E t + E) and the
+// ET = (K - P) / 256 contiguous tail elements [P + ET t, +ET).  FWHT stages
+// in the reference order: half < E inside the thread, half = E .. 32 E across
+// the lanes of a wave (partner lane ^ half / E), the last two (half = P / 4,
+// P / 2, across the four waves) through one LDS exchange, as fwht1024 does.
+// Every output is formed by the same adds on the same operands as the
+// sequential loop, and the RMS sum runs the reference's eight sequential
+// chains over the LDS copy of the row, so the result is bit-identical to the
+// LDS kernel it replaces.
+template <int M, int E>
+__device__ __forceinline__ void bfly_lanes(float (&v)[E]) {
+#pragma unroll
+  for (int e = 0; e < E; ++e) v[e] = bfly_lane<M>(v[e]);
+}
+
+template <int E>
+__device__ void fwht_regs(float (&v)[E], float* xs) {
+  constexpr int P = 256 * E;
+#pragma unroll
+  for (int half = 1; half < E; half <<= 1)
+#pragma unroll
+    for (int e = 0; e < E; ++e)
+      if ((e & half) == 0) {
+        const float a = v[e], b = v[e + half];
+        v[e] = a + b;
+        v[e + half] = a - b;
+      }
+  bfly_lanes<1>(v);
+  bfly_lanes<2>(v);
+  bfly_lanes<4>(v);
+  bfly_lanes<8>(v);
+  bfly_lanes<16>(v);
+  bfly_lanes<32>(v);
+  __syncthreads();
+#pragma unroll
+  for (int e = 0; e < E; ++e) xs[E * threadIdx.x + e] = v[e];
+  __syncthreads();
+  const int q = threadIdx.x >> 6;  // quarter of the P head elements
+  const float inv = 1.0f / sqrtf((float)P);
+#pragma unroll
+  for (int e = 0; e < E; ++e) {
+    const int base = (E * threadIdx.x + e) & (P / 4 - 1);
+    const float a0 = xs[base], a1 = xs[base + P / 4], a2 = xs[base + P / 2], a3 = xs[base + 3 * P / 4];
+    const float b0 = a0 + a1, b1 = a0 - a1, b2 = a2 + a3, b3 = a2 - a3;
+    const float c = q == 0 ? b0 + b2 : q == 1 ? b1 + b3 : q == 2 ? b0 - b2 : b1 - b3;
+    v[e] = c * inv;
+  }
+}
+
+// n (<= N) contiguous fp32 values between p and r: 16-byte accesses when n
+// is a multiple of 4 (p is then 16-byte aligned), single floats otherwise,
+// never past p[n - 1].
+template <int N>
+__device__ __forceinline__ void ld_f32(const float* p, float* r, int n) {
+  if (N % 4 == 0 && n % 4 == 0) {
+#pragma unroll
+    for (int i = 0; i < N / 4; ++i) {
+      if (4 * i >= n) break;
+      const float4 x = reinterpret_cast<const float4*>(p)[i];
+      r[4 * i] = x.x; r[4 * i + 1] = x.y; r[4 * i + 2] = x.z; r[4 * i + 3] = x.w;
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < N; ++i)
+      if (i < n) r[i] = p[i];
+  }
+}
+template <int N>
+__device__ __forceinline__ void st_f32(float* p, const float* r, int n) {
+  if (N % 4 == 0 && n % 4 == 0) {
+#pragma unroll
+    for (int i = 0; i < N / 4; ++i) {
+      if (4 * i >= n) break;
+      reinterpret_cast<float4*>(p)[i] = make_float4(r[4 * i], r[4 * i + 1], r[4 * i + 2], r[4 * i + 3]);
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < N; ++i)
+      if (i < n) p[i] = r[i];
+  }
+}
+template <int N>
+__device__ __forceinline__ void ld_f16(const uint16_t* p, float* r, int n) {
+#pragma unroll
+  for (int i = 0; i < N; ++i)
+    if (i < n) r[i] = ifrd::h2f(p[i]);
+}
+
+// Sum over aligned groups of n lanes (n a power of two; n > 64: the whole wave).
+__device__ __forceinline__ int group_lanes_sum(int v, int n) {
+  for (int off = 1; off < n && off < 64; off <<= 1) v += __shfl_xor(v, off, 64);
+  return v;
+}
+__device__ __forceinline__ float group_lanes_max(float v, int n) {
+  for (int off = 1; off < n && off < 64; off <<= 1) v = fmaxf(v, __shfl_xor(v, off, 64));
+  return v;
+}
+
+// n (<= N) int8 codes for the consecutive columns k0.. of row m, k0 a multiple
+// of min(n, 16): whole 16-byte lane chunks where n >= 16, else one 4- or
+// 8-byte piece of a chunk, else single bytes.
+template <int N>
+__device__ __forceinline__ void store_codes(int8_t* q, int m, int k0, int K, const int* c, int n) {
+  if (n >= 16) {
+#pragma unroll
+    for (int j = 0; j < N / 16; ++j) {
+      if (16 * j >= n) break;
+      uint32_t w[4] = {0u, 0u, 0u, 0u};
+#pragma unroll
+      for (int i = 0; i < 16; ++i) w[i >> 2] |= (uint32_t)(c[16 * j + i] & 0xFF) << (8 * (i & 3));
+      *reinterpret_cast<uint4*>(q + atile_off(m, k0 + 16 * j, K)) = make_uint4(w[0], w[1], w[2], w[3]);
+    }
+  } else if (n == 8 || n == 4) {
+    uint32_t w[2] = {0u, 0u};
+#pragma unroll
+    for (int i = 0; i < (N < 8 ? N : 8); ++i)
+      if (i < n) w[i >> 2] |= (uint32_t)(c[i] & 0xFF) << (8 * (i & 3));
+    if (n == 8) *reinterpret_cast<uint2*>(q + atile_off(m, k0, K)) = make_uint2(w[0], w[1]);
+    else *reinterpret_cast<uint32_t*>(q + atile_off(m, k0, K)) = w[0];
+  } else {
+#pragma unroll
+    for (int i = 0; i < (N < 4 ? N : 4); ++i)
+      if (i < n) q[atile_off(m, k0 + i, K)] = (int8_t)c[i];
+  }
+}
+
+template <int E>
+__global__ __launch_bounds__(256) void row_quant_wide(RowQuantArgs a) {
+  __shared__ float xs[8192];
+  __shared__ float red[16];
+  constexpr int P = 256 * E;
+  const int K = a.K, ET = (K - P) / 256;
+  const int m = blockIdx.x, t = threadIdx.x, lane = t & 63;
+  const int src = a.rowmap ? a.rowmap[m] : m;
+  const size_t h0 = (size_t)src * K + (size_t)E * t, t0 = (size_t)src * K + P + (size_t)ET * t;
+  float v[E], w[E];  // head, tail (ET <= E - 1 values used)
+#pragma unroll
+  for (int e = 0; e < E; ++e) w[e] = 0.0f;
+  if (a.src == SRC_X) {
+    ld_f32<E>(a.x + h0, v, E);
+    ld_f32<E>(a.x + t0, w, ET);
+  } else if (a.src == SRC_EMBED) {
+    const float* er = a.embed + (size_t)a.tokens[src] * K;
+    ld_f32<E>(er + (size_t)E * t, v, E);
+    ld_f32<E>(er + P + (size_t)ET * t, w, ET);
+    st_f32<E>(a.resid + h0, v, E);
+    st_f32<E>(a.resid + t0, w, ET);
+  } else {
+    float rv[E], rw[E];
+    ld_f32<E>(a.resid + h0, rv, E);
+    ld_f32<E>(a.resid + t0, rw, ET);
+    ld_f16<E>(a.y + h0, v, E);
+    ld_f16<E>(a.y + t0, w, ET);
+    if (a.rot_y) fwht_regs<E>(v, xs);
+#pragma unroll
+    for (int e = 0; e < E; ++e) {
+      v[e] = rv[e] + v[e];
+      w[e] = rw[e] + w[e];
+    }
+    st_f32<E>(a.resid + h0, v, E);
+    st_f32<E>(a.resid + t0, w, ET);
+  }
+  if (a.norm_w) {
+    // the row in LDS for the eight sequential chains (rms_factor's order)
+    __syncthreads();
+#pragma unroll
+    for (int e = 0; e < E; ++e) xs[E * t + e] = v[e];
+#pragma unroll
+    for (int e = 0; e < E; ++e)
+      if (e < ET) xs[P + ET * t + e] = w[e];
+    __syncthreads();
+    if (t < 8) {
+      float acc = 0.0f;
+      for (int n0 = 0; n0 < K / 8; n0 += 16) {
+        float x16[16];
+#pragma unroll
+        for (int i = 0; i < 16; ++i) x16[i] = (n0 + i < K / 8) ? xs[t + 8 * (n0 + i)] : 0.0f;
+#pragma unroll
+        for (int i = 0; i < 16; ++i)
+          if (n0 + i < K / 8) acc = fmaf(x16[i], x16[i], acc);
+      }
+      red[t] = acc;
+    }
+    __syncthreads();
+    const float s0 = red[0] + red[4], s1 = red[1] + red[5], s2 = red[2] + red[6], s3 = red[3] + red[7];
+    const float tot = (s0 + s1) + (s2 + s3);
+    const float f = 1.0f / sqrtf(tot / (float)K + a.eps);
+    float nv[E], nw[E];
+    ld_f32<E>(a.norm_w + (size_t)E * t, nv, E);
+    ld_f32<E>(a.norm_w + P + (size_t)ET * t, nw, ET);
+#pragma unroll
+    for (int e = 0; e < E; ++e) {
+      v[e] = (v[e] * f) * (1.0f + nv[e]);
+      if (e < ET) w[e] = (w[e] * f) * (1.0f + nw[e]);
+    }
+  }
+  if (a.rotate) fwht_regs<E>(v, xs);
+  // quantization: per row (ga 0) or per 64-wide slice (ga 64)
+  float sh_ = 0.0f, st_ = 0.0f;  // scale of the head / tail element slices
+  float ih = 0.0f, it = 0.0f;
+  if (a.ga == 0) {
+    float mx = 0.0f;
+#pragma unroll
+    for (int e = 0; e < E; ++e) {
+      mx = fmaxf(mx, fabsf(v[e]));
+      if (e < ET) mx = fmaxf(mx, fabsf(w[e]));
+    }
+    mx = ifrd::wave_max(mx);
+    __syncthreads();
+    if (lane == 0) red[8 + (t >> 6)] = mx;
+    __syncthreads();
+    mx = fmaxf(1e-6f, fmaxf(fmaxf(red[8], red[9]), fmaxf(red[10], red[11])));
+    sh_ = st_ = mx / 127.0f;
+    ih = it = 1.0f / sh_;
+    if (t == 0) a.qscale[m] = sh_;
+  } else {
+    // a 64-wide slice is 64 / E head lanes or 64 / ET tail lanes: reduce
+    // over aligned groups of that many lanes (E, ET powers of two here)
+    float mh = 0.0f, mt = 0.0f;
+#pragma unroll
+    for (int e = 0; e < E; ++e) {
+      mh = fmaxf(mh, fabsf(v[e]));
+      if (e < ET) mt = fmaxf(mt, fabsf(w[e]));
+    }
+    mh = group_lanes_max(mh, 64 / E);
+    if (ET > 0) mt = group_lanes_max(mt, 64 / ET);
+    mh = fmaxf(1e-6f, mh);
+    mt = fmaxf(1e-6f, mt);
+    sh_ = mh / 127.0f;
+    st_ = mt / 127.0f;
+    ih = 1.0f / sh_;
+    it = 1.0f / st_;
+    if ((E * t) % 64 == 0) a.qscale[(size_t)m * (K / 64) + (E * t) / 64] = sh_;
+    if (ET > 0 && (ET * t) % 64 == 0) a.qscale[(size_t)m * (K / 64) + (P + ET * t) / 64] = st_;
+  }
+  int ch[E], ctl[E];
+  int Sh = 0, St = 0;
+#pragma unroll
+  for (int e = 0; e < E; ++e) {
+    ch[e] = a.round == 0 ? ifrd::quant_half_away(v[e], ih) : ifrd::quant_rne(v[e], ih);
+    Sh += ch[e];
+    ctl[e] = 0;
+    if (e < ET) {
+      ctl[e] = a.round == 0 ? ifrd::quant_half_away(w[e], it) : ifrd::quant_rne(w[e], it);
+      St += ctl[e];
+    }
+  }
+  // A-tile stores: the E head codes of a thread are E consecutive columns
+  // starting at a multiple of E, inside one 16-byte lane chunk (E <= 16) or
+  // spanning E / 16 chunks
+  store_codes<E>(a.q, m, E * t, K, ch, E);
+  store_codes<E>(a.q, m, P + ET * t, K, ctl, ET);
+  if (a.gsum) {  // 128-wide groups: 128 / E head lanes, 128 / ET tail lanes
+    Sh = group_lanes_sum(Sh, 128 / E);
+    if (ET > 0) St = group_lanes_sum(St, 128 / ET);
+    __syncthreads();
+    int* sred = reinterpret_cast<int*>(xs);
+    if (lane == 0) {  // per-wave sums, for groups of 128 lanes (E or ET = 1)
+      sred[t >> 6] = Sh;
+      sred[8 + (t >> 6)] = St;
+    }
+    __syncthreads();
+    if ((E * t) % 128 == 0)
+      a.gsum[(size_t)m * (K / 128) + (E * t) / 128] =
+          (float)(128 / E > 64 ? sred[t >> 6] + sred[(t >> 6) + 1] : Sh);
+    if (ET > 0 && (ET * t) % 128 == 0)
+      a.gsum[(size_t)m * (K / 128) + (P + ET * t) / 128] =
+          (float)(128 / ET > 64 ? sred[8 + (t >> 6)] + sred[8 + (t >> 6) + 1] : St);
+  }
+}
+
 // Per-token int8 quantization of an fp32 / fp16 row of K = 8 * NT values:
 // thread t owns the 8 contiguous columns 8t..8t+7, so its input is one
 // 16-byte (fp16) or two 16-byte (fp32) loads, its codes are one 8-byte A-tile
@@ -765,6 +1040,24 @@ hipError_t launch_row_quant(const RowQuantArgs& a, hipStream_t st) {
   if (a.K == 1024 && (a.ga == 0 || a.ga == 64)) {
     hipLaunchKernelGGL(row_quant1024_kernel, dim3(a.M), dim3(256), 0, st, a);
     return hipGetLastError();
+  }
+  {
+    // the register kernel: K a multiple of 256, head P = floor_pow2(K) and a
+    // tail (K - P) / 256 per thread that is 0 or a power of two
+    int P = 256;
+    while (2 * P <= a.K) P *= 2;
+    const int et = (a.K - P) / 256;
+    if (a.K % 256 == 0 && (et & (et - 1)) == 0) {
+      switch (P / 256) {
+        case 1: hipLaunchKernelGGL(row_quant_wide<1>, dim3(a.M), dim3(256), 0, st, a); return hipGetLastError();
+        case 2: hipLaunchKernelGGL(row_quant_wide<2>, dim3(a.M), dim3(256), 0, st, a); return hipGetLastError();
+        case 4: hipLaunchKernelGGL(row_quant_wide<4>, dim3(a.M), dim3(256), 0, st, a); return hipGetLastError();
+        case 8: hipLaunchKernelGGL(row_quant_wide<8>, dim3(a.M), dim3(256), 0, st, a); return hipGetLastError();
+        case 16: hipLaunchKernelGGL(row_quant_wide<16>, dim3(a.M), dim3(256), 0, st, a); return hipGetLastError();
+        case 32: hipLaunchKernelGGL(row_quant_wide<32>, dim3(a.M), dim3(256), 0, st, a); return hipGetLastError();
+        default: break;
+      }
+    }
   }
   const size_t lds = (size_t)(2 * a.K + 64 + a.K / 64) * sizeof(float);
   static bool big = false;

@@ -343,8 +343,14 @@ def act_quant():
     from oracle import pyoracle as po
     L = ia.lib()
     dev = ia.Device(0)
+    # 1024 has its own kernel; the register kernel takes every K whose tail
+    # per thread is 0 or a power of two (P = floor_pow2(K)): 256, 512, 768,
+    # 1280, 2048, 2304, 3072, 5120, 6144, 8192; 1792 (tail 3) takes the LDS one
     for (K, norm, rot, rnd, ga) in [(1024, 1, 1, 0, 0), (1024, 0, 0, 1, 64), (2048, 0, 0, 0, 0),
-                                    (3072, 1, 0, 0, 0), (5120, 1, 1, 0, 0), (256, 1, 1, 0, 0)]:
+                                    (3072, 1, 0, 0, 0), (5120, 1, 1, 0, 0), (256, 1, 1, 0, 0),
+                                    (512, 1, 1, 0, 64), (768, 1, 1, 0, 0), (1280, 1, 1, 1, 64),
+                                    (2304, 1, 1, 0, 0), (5120, 1, 1, 1, 64), (6144, 1, 1, 0, 0),
+                                    (8192, 0, 1, 0, 64), (1792, 1, 1, 0, 0)]:
         rng = np.random.default_rng(K)
         M = 19
         x = (rng.standard_normal((M, K), dtype=np.float32) * 2.5).astype(np.float32)
@@ -358,7 +364,9 @@ def act_quant():
                                  ga, qd.p, sd.p, gd.p), "ifr_act_quant")
         qg = ia.untile(dev.download(qd, np.int8, (Mp * K,)), M, K)
         assert np.array_equal(qg, q), K
-        say(f"act_quant K={K} ok")
+        assert np.array_equal(dev.download(sd, np.float32, (M, ns)).view(np.uint32), s.view(np.uint32)), K
+        assert np.array_equal(dev.download(gd, np.float32, (M, K // 128)), g), K
+        say(f"act_quant K={K} norm={norm} rot={rot} round={rnd} ga={ga} ok")
     dev.close()
 
 
