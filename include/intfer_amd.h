@@ -246,6 +246,12 @@ int ifr_seq_truncate(ifr_ctx* ctx, int32_t slot, int32_t len);
 int ifr_seq_len(ifr_ctx* ctx, int32_t slot, int32_t* len);
 /* Per-sequence KV capacity in tokens of the loaded model. */
 int ifr_kv_capacity(ifr_ctx* ctx, int32_t* tokens);
+/* Fill the empty sequence dst with the first len cached positions of src
+ * (a device page copy; every layer, K, V and int8 scales).  Replaces the
+ * prefix cache's host KV snapshot restore (PrefixCache::install,
+ * main.cpp:9614-9680): the KV of a position depends only on the tokens up
+ * to it, so the copy equals what prefilling that prefix would append. */
+int ifr_seq_copy_prefix(ifr_ctx* ctx, int32_t dst, int32_t src, int32_t len);
 /* Fill an open, empty sequence with len cached positions: k, v are fp32
  * host arrays [layers][len][n_kv][head_dim]; values are stored exactly as
  * the forward stores them (fp16 round, or int8 with an fp16 scale per
@@ -435,6 +441,12 @@ typedef struct ifr_sched_cfg {
                          * the chunk_m budget from the prefill queue in
                          * order, so a prompt ending mid-chunk leaves its
                          * room to the next.  Token streams are unchanged. */
+  int32_t prefix_cache; /* prefix reuse entries (PrefixCache, main.cpp:
+                         * 9469-9726, INTFER_PCACHE_N, at most 16); 0 = off.
+                         * A finished request's stream and KV stay cached
+                         * (LRU); an admitted prompt sharing a prefix with a
+                         * cached stream copies that KV and prefills only the
+                         * rest.  Token streams are unchanged. */
 } ifr_sched_cfg;
 
 int ifr_sched_create(ifr_ctx* ctx, const ifr_sched_cfg* cfg, ifr_sched** out);
@@ -450,6 +462,8 @@ typedef struct ifr_sched_backend {
   int (*seq_truncate)(void* user, int32_t slot, int32_t len);
   int (*forward)(void* user, const ifr_row* rows, int32_t M, int32_t* best);
   int32_t kv_capacity;
+  /* ifr_seq_copy_prefix; may be NULL (no prefix cache) */
+  int (*seq_copy_prefix)(void* user, int32_t dst, int32_t src, int32_t len);
 } ifr_sched_backend;
 int ifr_sched_create_backend(const ifr_sched_backend* be, const ifr_sched_cfg* cfg,
                              ifr_sched** out);

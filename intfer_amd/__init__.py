@@ -340,6 +340,10 @@ class Engine:
     def seq_truncate(self, s: int, n: int):
         check(lib().ifr_seq_truncate(self.dev.ctx, s, n), "ifr_seq_truncate")
 
+    def seq_copy_prefix(self, dst: int, src: int, n: int):
+        """Give the empty sequence `dst` the first n positions of `src`'s KV."""
+        check(lib().ifr_seq_copy_prefix(self.dev.ctx, dst, src, n), "ifr_seq_copy_prefix")
+
     def seq_len(self, s: int) -> int:
         n = C.c_int32()
         check(lib().ifr_seq_len(self.dev.ctx, s, C.byref(n)), "ifr_seq_len")
@@ -388,10 +392,12 @@ class Scheduler:
     backend table (SchedBackend) for CPU-side checks."""
 
     def __init__(self, engine: Engine | None = None, chunk_m=128, live_cap=64, split_iter=0,
-                 round_robin=1, spec_k=0, backend: SchedBackend | None = None, pack_prefill=0):
+                 round_robin=1, spec_k=0, backend: SchedBackend | None = None, pack_prefill=0,
+                 prefix_cache=0):
         cfg = SchedCfg()
         cfg.chunk_m, cfg.live_cap, cfg.split_iter = chunk_m, live_cap, split_iter
         cfg.round_robin, cfg.spec_k, cfg.pack_prefill = round_robin, spec_k, pack_prefill
+        cfg.prefix_cache = prefix_cache
         self.h = C.c_void_p()
         self._keep = backend
         if backend is not None:

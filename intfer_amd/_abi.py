@@ -76,13 +76,15 @@ class Row(C.Structure):
 
 class SchedCfg(C.Structure):
     _fields_ = [("chunk_m", C.c_int32), ("live_cap", C.c_int32), ("split_iter", C.c_int32),
-                ("round_robin", C.c_int32), ("spec_k", C.c_int32), ("pack_prefill", C.c_int32)]
+                ("round_robin", C.c_int32), ("spec_k", C.c_int32), ("pack_prefill", C.c_int32),
+                ("prefix_cache", C.c_int32)]
 
 
 SEQ_OPEN = C.CFUNCTYPE(C.c_int, C.c_void_p, C.POINTER(C.c_int32))
 SEQ_CLOSE = C.CFUNCTYPE(C.c_int, C.c_void_p, C.c_int32)
 SEQ_TRUNC = C.CFUNCTYPE(C.c_int, C.c_void_p, C.c_int32, C.c_int32)
 FORWARD = C.CFUNCTYPE(C.c_int, C.c_void_p, C.POINTER(Row), C.c_int32, C.POINTER(C.c_int32))
+SEQ_COPY = C.CFUNCTYPE(C.c_int, C.c_void_p, C.c_int32, C.c_int32, C.c_int32)
 
 
 class SchedEvent(C.Structure):
@@ -96,7 +98,8 @@ class ServeCfg(C.Structure):
 
 class SchedBackend(C.Structure):
     _fields_ = [("user", C.c_void_p), ("seq_open", SEQ_OPEN), ("seq_close", SEQ_CLOSE),
-                ("seq_truncate", SEQ_TRUNC), ("forward", FORWARD), ("kv_capacity", C.c_int32)]
+                ("seq_truncate", SEQ_TRUNC), ("forward", FORWARD), ("kv_capacity", C.c_int32),
+                ("seq_copy_prefix", SEQ_COPY)]
 
 
 P = C.c_void_p
@@ -148,6 +151,7 @@ _PROTOS = {
     "ifr_seq_close": (C.c_int, [P, i32]),
     "ifr_seq_truncate": (C.c_int, [P, i32, i32]),
     "ifr_seq_len": (C.c_int, [P, i32, pi32]),
+    "ifr_seq_copy_prefix": (C.c_int, [P, i32, i32, i32]),
     "ifr_kv_capacity": (C.c_int, [P, pi32]),
     "ifr_seq_load_kv": (C.c_int, [P, i32, i32, pf32, pf32]),
     "ifr_forward": (C.c_int, [P, C.POINTER(Row), i32, pi32, pf32]),

@@ -140,6 +140,9 @@ struct ifr_ctx {
   std::vector<void*> kpool, vpool;
   std::vector<uint16_t*> kscale, vscale;
   int32_t* bt_d = nullptr;
+  void** pools_d = nullptr;        // every KV pool (K, V [, scales] per layer), for page copies
+  int npools = 0;
+  int32_t* copy_idx_d = nullptr;   // [2][max_pages] source / destination pages
   int32_t* bt_h = nullptr;  // pinned
   std::vector<int> free_pages;
   std::vector<Seq> seqs;
@@ -924,6 +927,20 @@ int ifr_model_load(ifr_ctx* c, const ifr_host_model* m, const ifr_kv_cfg* kvc) {
       HIPCHK(hipMemsetAsync(c->vscale[l], 0, sb, c->st));
     }
   }
+  {
+    std::vector<void*> pools;
+    for (int l = 0; l < L; ++l) {
+      pools.push_back(c->kpool[l]);
+      pools.push_back(c->vpool[l]);
+      if (kvc->kv_int8) {
+        pools.push_back(c->kscale[l]);
+        pools.push_back(c->vscale[l]);
+      }
+    }
+    c->npools = (int)pools.size();
+    if (int r = upload(c, &c->pools_d, pools.data(), pools.size())) return r;
+    if (int r = walloc(c, &c->copy_idx_d, (size_t)2 * c->max_pages)) return r;
+  }
   c->free_pages.clear();
   for (int p = c->n_pages - 1; p >= 0; --p) c->free_pages.push_back(p);
   c->seqs.assign(kvc->max_seqs, Seq());
@@ -999,6 +1016,50 @@ int ifr_seq_truncate(ifr_ctx* c, int32_t slot, int32_t len) {
 int ifr_seq_close(ifr_ctx* c, int32_t slot) {
   if (int r = ifr_seq_truncate(c, slot, 0)) return r;
   c->seqs[slot].open = false;
+  return IFR_OK;
+}
+
+int ifr_seq_copy_prefix(ifr_ctx* c, int32_t dst, int32_t src, int32_t len) {
+  if (!c || !c->loaded) return fail(IFR_ESTATE, "no model loaded");
+  const int ns = (int)c->seqs.size();
+  if (dst < 0 || dst >= ns || !c->seqs[dst].open) return fail(IFR_EINVAL, "slot %d", dst);
+  if (src < 0 || src >= ns || !c->seqs[src].open || src == dst) return fail(IFR_EINVAL, "slot %d", src);
+  Seq& d = c->seqs[dst];
+  const Seq& sq = c->seqs[src];
+  if (d.len != 0) return fail(IFR_ESTATE, "sequence %d is not empty", dst);
+  if (len < 0 || len > sq.len) return fail(IFR_EINVAL, "prefix %d > length %d", len, sq.len);
+  if (len == 0) return IFR_OK;
+  const int need = (len + kPage - 1) / kPage;
+  if (need > (int)c->free_pages.size()) return fail(IFR_ENOMEM, "KV pool exhausted");
+  std::vector<int32_t> idx((size_t)2 * need);
+  for (int i = 0; i < need; ++i) {
+    const int p = c->free_pages.back();
+    c->free_pages.pop_back();
+    c->bt_h[(size_t)dst * c->max_pages + i] = p;
+    d.pages.push_back(p);
+    idx[i] = sq.pages[i];
+    idx[need + i] = p;
+  }
+  HIPCHK(hipSetDevice(c->device));
+  // the context stream is in order: the copy lands before any later forward
+  HIPCHK(hipMemcpyAsync(c->bt_d + (size_t)dst * c->max_pages, c->bt_h + (size_t)dst * c->max_pages,
+                        c->max_pages * sizeof(int32_t), hipMemcpyHostToDevice, c->st));
+  HIPCHK(hipMemcpyAsync(c->copy_idx_d, idx.data(), idx.size() * sizeof(int32_t), hipMemcpyHostToDevice,
+                        c->st));
+  const size_t esz = c->kv.kv_int8 ? 1 : 2;
+  ifrk::PageCopyArgs a{};
+  a.pools = c->pools_d;
+  a.npools = c->npools;
+  a.per = c->kv.kv_int8 ? 4 : 2;
+  a.page_bytes[0] = a.page_bytes[1] = (size_t)c->cfg.n_kv * kPage * c->cfg.head_dim * esz;
+  a.page_bytes[2] = a.page_bytes[3] = (size_t)c->cfg.n_kv * kPage * 2;
+  a.sp = c->copy_idx_d;
+  a.dp = c->copy_idx_d + need;
+  a.n = need;
+  HIPCHK(ifrk::launch_copy_pages(a, c->st));
+  // idx is a host temporary: wait for the staged copies before it goes
+  HIPCHK(hipStreamSynchronize(c->st));
+  d.len = len;
   return IFR_OK;
 }
 
@@ -1128,12 +1189,17 @@ int ifr_forward(ifr_ctx* c, const ifr_row* rows, int32_t M, int32_t* best_out, f
       g_len.back() += 1;
     }
   }
-  // ---- pages for every new position (block table rows go up on lane 0)
-  for (size_t g = 0; g < g_seq.size(); ++g) {
-    Seq& s = c->seqs[g_seq[g]];
-    const int need = (g_pos0[g] + g_len[g] + kPage - 1) / kPage;
-    if (need - (int)s.pages.size() > (int)c->free_pages.size())
-      return fail(IFR_ENOMEM, "KV pool exhausted (%zu free pages)", c->free_pages.size());
+  // ---- pages for every new position (block table rows go up on lane 0);
+  // checked for the whole batch first, so a refusal changes nothing
+  {
+    size_t more = 0;
+    for (size_t g = 0; g < g_seq.size(); ++g) {
+      const Seq& s = c->seqs[g_seq[g]];
+      const int need = (g_pos0[g] + g_len[g] + kPage - 1) / kPage;
+      if (need > (int)s.pages.size()) more += (size_t)(need - (int)s.pages.size());
+    }
+    if (more > c->free_pages.size())
+      return fail(IFR_ENOMEM, "KV pool exhausted (%zu pages needed, %zu free)", more, c->free_pages.size());
   }
   for (size_t g = 0; g < g_seq.size(); ++g) {
     Seq& s = c->seqs[g_seq[g]];

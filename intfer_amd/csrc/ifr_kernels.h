@@ -133,6 +133,20 @@ struct QKArgs {
 };
 hipError_t launch_qk_rope_kv(const QKArgs& a, const KVLayout& kv, hipStream_t st);
 
+// ---- KV page copy (prefix reuse) ----------------------------------------------
+// Copies n pages, sp[i] -> dp[i] (device page indices), in each of npools
+// pools; pools[j] is a device pool whose pages are page_bytes[j % per]
+// bytes (per = pools per layer: K, V [, K scales, V scales]).
+struct PageCopyArgs {
+  void* const* pools;        // device array [npools]
+  int npools, per;
+  size_t page_bytes[4];      // multiples of 16
+  const int32_t* sp;
+  const int32_t* dp;
+  int n;
+};
+hipError_t launch_copy_pages(const PageCopyArgs& a, hipStream_t st);
+
 // ---- ragged batch packing ---------------------------------------------------
 struct AttnUnit {
   int seq, kvh, row0, qn, qpos0, kv_lo, kv_hi, pad;

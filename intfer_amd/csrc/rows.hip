@@ -1030,6 +1030,29 @@ hipError_t allow_big_lds(F* f, bool& done) {
   return e;
 }
 
+namespace {
+
+// grid (n pages, npools): one workgroup copies one page of one pool.
+__global__ __launch_bounds__(256) void copy_pages_kernel(PageCopyArgs a) {
+  const int i = blockIdx.x, j = blockIdx.y;
+  const size_t words = a.page_bytes[j % a.per] / 16;
+  const uint4* src = reinterpret_cast<const uint4*>(a.pools[j]) + (size_t)a.sp[i] * words;
+  uint4* dst = reinterpret_cast<uint4*>(a.pools[j]) + (size_t)a.dp[i] * words;
+  for (size_t w = threadIdx.x; w < words; w += blockDim.x) dst[w] = src[w];
+}
+
+}  // namespace
+
+hipError_t launch_copy_pages(const PageCopyArgs& a, hipStream_t st) {
+  if (a.n <= 0) return hipSuccess;
+  if (!a.pools || !a.sp || !a.dp || a.npools <= 0 || a.per < 1 || a.per > 4 || a.npools % a.per != 0)
+    return hipErrorInvalidValue;
+  for (int k = 0; k < a.per; ++k)
+    if (a.page_bytes[k] == 0 || a.page_bytes[k] % 16 != 0) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(copy_pages_kernel, dim3(a.n, a.npools), dim3(256), 0, st, a);
+  return hipGetLastError();
+}
+
 hipError_t launch_row_quant(const RowQuantArgs& a, hipStream_t st) {
   if (a.M <= 0) return hipSuccess;
   if (a.K <= 0 || a.K % 128 != 0 || a.K > 8192 || !a.q || !a.qscale) return hipErrorInvalidValue;

@@ -15,6 +15,7 @@
 // request contributes its token and K drafts as one causal verify group.
 #include <algorithm>
 #include <deque>
+#include <iterator>
 #include <map>
 #include <memory>
 #include <string>
@@ -64,6 +65,16 @@ bool is_eos(int t) { return t == kEos0 || t == kEos1; }
 
 }  // namespace
 
+// A finished request kept for prefix reuse (PrefixCache::Entry,
+// main.cpp:9472-9493, the HTTP dispatcher's cache): its KV slot stays open
+// and holds state_len positions of stream = prompt + generated (the last
+// generated id was never forwarded, main.cpp:9540-9544).
+struct CacheEntry {
+  int slot;
+  std::vector<int32_t> stream;
+  int state_len;
+};
+
 struct ifr_sched {
   ifr_sched_backend be{};
   ifr_sched_cfg cfg{};
@@ -78,6 +89,91 @@ struct ifr_sched {
   std::vector<int32_t> best;
   bool record = false;                 // ifr_sched_record_events
   std::deque<ifr_sched_event> events;
+  std::deque<CacheEntry> cache;        // most recently used first
+
+  bool caching() const { return cfg.prefix_cache > 0 && be.seq_copy_prefix; }
+
+  // Drop the least recently used entry other than the one holding slot keep.
+  bool evict_lru(int keep = -1) {
+    for (auto it = cache.rbegin(); it != cache.rend(); ++it) {
+      if (it->slot == keep) continue;
+      be.seq_close(be.user, it->slot);
+      cache.erase(std::next(it).base());
+      return true;
+    }
+    return false;
+  }
+
+  // Retire a finished request: its slot becomes a cache entry
+  // (PrefixCache::snapshot, main.cpp:9518-9546; only once the whole prompt
+  // is in, main.cpp:9944-9945), or closes.
+  void retire(Req* q) {
+    if (q->slot < 0) return;
+    if (caching() && !q->prompt.empty() && !q->generated.empty() &&
+        q->fill == (int)q->prompt.size()) {
+      CacheEntry e;
+      e.slot = q->slot;
+      e.stream = q->prompt;
+      e.stream.insert(e.stream.end(), q->generated.begin(), q->generated.end());
+      e.state_len = std::min((int)e.stream.size() - 1, q->pos);
+      cache.push_front(std::move(e));
+      while ((int)cache.size() > cfg.prefix_cache) evict_lru();
+    } else {
+      be.seq_close(be.user, q->slot);
+    }
+    q->slot = -1;
+  }
+
+  // Longest prefix of the prompt held by an entry (PrefixCache::match,
+  // main.cpp:9603-9619; the most recently used entry wins ties), capped
+  // below the whole prompt so the last prompt row still runs and scores the
+  // first token (main.cpp:9874-9878).  Returns the length, *slot the entry's slot.
+  int match(const Req& q, int* slot) const {
+    int best = 0;
+    *slot = -1;
+    for (const CacheEntry& e : cache) {
+      const size_t n = std::min({e.stream.size(), q.prompt.size(), (size_t)e.state_len});
+      size_t h = 0;
+      while (h < n && e.stream[h] == q.prompt[h]) ++h;
+      if ((int)h > best) {
+        best = (int)h;
+        *slot = e.slot;
+      }
+    }
+    if (best >= (int)q.prompt.size()) best = (int)q.prompt.size() - 1;
+    return best;
+  }
+
+  // Admission of the pending head into a fresh slot, resuming from a cached
+  // prefix where one matches (PrefixCache::install, main.cpp:9633-9716; the
+  // call site main.cpp:9871-9886).  The copy covers the whole hit: the
+  // reference resumes at the largest recurrent-state grid row <= hit, and
+  // attention-only KV truncates anywhere.  Cache entries give way when slots
+  // or pages run out; a copy that still cannot get pages prefills in full.
+  bool admit(Req* q) {
+    int src = -1;
+    const int hit = caching() ? match(*q, &src) : 0;
+    int32_t slot = -1;
+    while (be.seq_open(be.user, &slot) != IFR_OK)
+      if (!evict_lru(src)) return false;
+    q->slot = slot;
+    if (hit > 0) {
+      int r;
+      while ((r = be.seq_copy_prefix(be.user, slot, src, hit)) == IFR_ENOMEM)
+        if (!evict_lru(src)) break;
+      if (r == IFR_OK) {
+        q->fill = hit;
+        for (auto it = cache.begin(); it != cache.end(); ++it)
+          if (it->slot == src) {
+            CacheEntry e = std::move(*it);
+            cache.erase(it);
+            cache.push_front(std::move(e));
+            break;
+          }
+      }
+    }
+    return true;
+  }
 
   // A streamed token: where the reference's emit hook fires (decode rows in
   // live order, main.cpp:8405 / :8505; accepted drafts + correction of a
@@ -95,7 +191,12 @@ struct ifr_sched {
   int forward() {
     best.assign(rows.size(), -1);
     last_rows = rows;
-    return be.forward(be.user, rows.data(), (int32_t)rows.size(), best.data());
+    int r;
+    // a refused forward (KV pages exhausted) changed nothing: cached
+    // prefixes give their pages back first
+    while ((r = be.forward(be.user, rows.data(), (int32_t)rows.size(), best.data())) == IFR_ENOMEM)
+      if (!evict_lru()) break;
+    return r;
   }
 
   // Decode (or verify) rows for every live request (main.cpp:8438-8446).
@@ -260,13 +361,17 @@ int eng_trunc(void* u, int32_t slot, int32_t len) {
 int eng_fwd(void* u, const ifr_row* rows, int32_t M, int32_t* best) {
   return ifr_forward(static_cast<ifr_ctx*>(u), rows, M, best, nullptr);
 }
+int eng_copy(void* u, int32_t dst, int32_t src, int32_t len) {
+  return ifr_seq_copy_prefix(static_cast<ifr_ctx*>(u), dst, src, len);
+}
 }  // namespace
 
 int ifr_sched_create_backend(const ifr_sched_backend* be, const ifr_sched_cfg* cfg, ifr_sched** out) {
   if (!be || !cfg || !out || !be->seq_open || !be->seq_close || !be->seq_truncate || !be->forward)
     return IFR_EINVAL;
   if (cfg->chunk_m < 1 || cfg->chunk_m > 4096 || cfg->live_cap < 1 || cfg->spec_k < 0 ||
-      cfg->spec_k > 15 || cfg->pack_prefill < 0 || cfg->pack_prefill > 1 || be->kv_capacity <= 0)
+      cfg->spec_k > 15 || cfg->pack_prefill < 0 || cfg->pack_prefill > 1 || cfg->prefix_cache < 0 ||
+      cfg->prefix_cache > 16 || be->kv_capacity <= 0)
     return IFR_EINVAL;
   auto* s = new ifr_sched();
   s->be = *be;
@@ -284,6 +389,7 @@ int ifr_sched_create(ifr_ctx* ctx, const ifr_sched_cfg* cfg, ifr_sched** out) {
   be.seq_close = eng_close;
   be.seq_truncate = eng_trunc;
   be.forward = eng_fwd;
+  be.seq_copy_prefix = eng_copy;
   if (int r = ifr_kv_capacity(ctx, &be.kv_capacity)) return r;
   return ifr_sched_create_backend(&be, cfg, out);
 }
@@ -292,6 +398,7 @@ int ifr_sched_destroy(ifr_sched* s) {
   if (!s) return IFR_OK;
   for (auto& kv : s->pool)
     if (kv.second->slot >= 0) s->be.seq_close(s->be.user, kv.second->slot);
+  for (const CacheEntry& e : s->cache) s->be.seq_close(s->be.user, e.slot);
   delete s;
   return IFR_OK;
 }
@@ -316,9 +423,7 @@ int ifr_sched_step(ifr_sched* s, int32_t* rows_run) {
   // admission: FIFO while live < cap and a KV slot is free
   while (!s->pending.empty() && (int)s->live.size() < s->cfg.live_cap) {
     Req* q = s->pending.front();
-    int32_t slot = -1;
-    if (s->be.seq_open(s->be.user, &slot) != IFR_OK) break;
-    q->slot = slot;
+    if (!s->admit(q)) break;
     s->pending.pop_front();
     s->prefill_q.push_back(q);
   }
@@ -329,8 +434,7 @@ int ifr_sched_step(ifr_sched* s, int32_t* rows_run) {
   std::vector<Req*> still;
   for (Req* q : s->live) {
     if (q->finished) {
-      if (q->slot >= 0) s->be.seq_close(s->be.user, q->slot);
-      q->slot = -1;
+      s->retire(q);
       if (s->record) s->events.push_back({q->id, -1, 1, (int32_t)q->generated.size(), 0});
     } else {
       still.push_back(q);

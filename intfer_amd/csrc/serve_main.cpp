@@ -20,8 +20,8 @@ void usage() {
                "usage: intfer_serve (-m MODEL.intfer | --synth SEED [--bits 2|4|0] [--intfer-form])\n"
                "  [--hidden H --layers L --heads NQ --kv-heads NKV --inter F --vocab V]\n"
                "  [--kv-int8] [--max-new N] [--chunk-m N] [--live-cap N] [--split-iter] [--no-rr]\n"
-               "  [--spec-k K] [--pack-prefill] [--max-seq-tokens N] [--max-seqs N] [--pool-tokens N]\n"
-               "  [--device D]\n");
+               "  [--spec-k K] [--pack-prefill] [--prefix-cache N] [--max-seq-tokens N] [--max-seqs N]\n"
+               "  [--pool-tokens N] [--device D]\n");
 }
 
 int env_int(const char* name, int dflt, int lo, int hi) {
@@ -43,7 +43,7 @@ int main(int argc, char** argv) {
   int live_cap = env_int("INTFER_SERVE_MAX", 64, 1, 64);
   int split_iter = std::getenv("INTFER_SPLIT_ITER") ? 1 : 0;
   int rr = (std::getenv("INTFER_PREFILL_RR") && std::string(std::getenv("INTFER_PREFILL_RR")) == "0") ? 0 : 1;
-  int max_seq_tokens = 4096, max_seqs = 0, pack = 0;
+  int max_seq_tokens = 4096, max_seqs = 0, pack = 0, pcache = 0;
   long long pool_tokens = 0;
   for (int i = 1; i < argc; ++i) {
     const std::string a = argv[i];
@@ -72,6 +72,7 @@ int main(int argc, char** argv) {
     else if (a == "--no-rr") rr = 0;
     else if (a == "--spec-k") spec_k = std::atoi(next());
     else if (a == "--pack-prefill") pack = 1;
+    else if (a == "--prefix-cache") pcache = std::atoi(next());
     else if (a == "--max-seq-tokens") max_seq_tokens = std::atoi(next());
     else if (a == "--max-seqs") max_seqs = std::atoi(next());
     else if (a == "--pool-tokens") pool_tokens = std::atoll(next());
@@ -85,7 +86,8 @@ int main(int argc, char** argv) {
     usage();
     return 2;
   }
-  if (max_seqs <= 0) max_seqs = live_cap + 4;
+  // cached prefixes hold a sequence slot each
+  if (max_seqs <= 0) max_seqs = live_cap + 4 + pcache;
   if (pool_tokens <= 0) pool_tokens = (long long)max_seqs * max_seq_tokens;
   ifr_kv_cfg kv{};
   kv.max_seqs = max_seqs;
@@ -121,15 +123,17 @@ int main(int argc, char** argv) {
   sc.round_robin = rr;
   sc.spec_k = spec_k;
   sc.pack_prefill = pack;
+  sc.prefix_cache = pcache;
   ifr_sched* s = nullptr;
   if (ifr_sched_create(ctx, &sc, &s) != IFR_OK) {
     std::fprintf(stderr, "FAIL: scheduler: %s\n", ifr_last_error());
     ifr_ctx_destroy(ctx);
     return 1;
   }
-  std::fprintf(stderr, "[intfer] serve: live cap %d, chunk %d, %s, spec_k %d, KV %s, %d x %d tokens\n",
+  std::fprintf(stderr,
+               "[intfer] serve: live cap %d, chunk %d, %s, spec_k %d, KV %s, %d x %d tokens, prefix cache %d\n",
                live_cap, chunk_m, split_iter ? "split" : "joint", spec_k, kv_int8 ? "int8" : "fp16",
-               max_seqs, max_seq_tokens);
+               max_seqs, max_seq_tokens, pcache);
   ifr_serve_cfg scfg{};
   scfg.default_max_new = max_new;
   scfg.vocab = cfg.vocab;

@@ -228,7 +228,7 @@ def sched_small():
     import intfer_amd as ia
     from intfer_amd import workloads as wl
     cfg = ia.default_cfg(layers=2, vocab=2048)
-    model = ia.SynthModel(cfg, seed=seed, bits=bits, intfer_form=intfer_form)
+    model = ia.SynthModel(cfg, seed=3, bits=2)
     dev = ia.Device(0)
     eng = ia.Engine(dev, model, max_seqs=16, max_seq_tokens=1024, pool_tokens=16 * 1024, max_rows=256)
     prompts = wl.cfg4_requests(4, seed=8, vocab=cfg.vocab, lo=40, hi=150)
@@ -335,6 +335,63 @@ def attention_ragged_g5():
     """The same with a GQA group of 5 (the 27B-class 40 q / 8 kv heads),
     whose q-block of 3 tokens fills 15 of the 16 MFMA columns."""
     attention_ragged(heads=(10, 2))
+
+
+@scenario
+def prefix_copy():
+    """ifr_seq_copy_prefix (the prefix cache's page copy) with fp16 and int8
+    KV: a copied prefix plus the recomputed rest gives the same logits, bit
+    for bit, as the sequence it was copied from; then the scheduler's cache
+    reproduces the uncached streams of two chat turns."""
+    import intfer_amd as ia
+    cfg = _small_cfg(ia, layers=2)
+    model = ia.SynthModel(cfg, seed=5, bits=2)
+    dev = ia.Device(0)
+    rng = np.random.default_rng(9)
+    prompt = rng.integers(0, cfg.vocab, size=70).tolist()
+    for kv8 in (0, 1):
+        eng = ia.Engine(dev, model, max_seqs=4, max_seq_tokens=256, pool_tokens=4 * 256,
+                        kv_int8=kv8, max_rows=96)
+        a = eng.seq_open()
+        ba, la = eng.forward([(a, p, t, ia.ROW_PREFILL, int(p == 69)) for p, t in enumerate(prompt)],
+                             logits=True)
+        for cut in (45, 64, 1):
+            b = eng.seq_open()
+            eng.seq_copy_prefix(b, a, cut)
+            bb, lb = eng.forward([(b, p, prompt[p], ia.ROW_PREFILL, int(p == 69))
+                                  for p in range(cut, 70)], logits=True)
+            assert np.array_equal(la, lb), (kv8, cut, float(np.abs(la - lb).max()))
+            # and one decode step on both
+            t = int(ba[-1])
+            _, da = eng.forward([(a, 70, t, ia.ROW_DECODE, 1)], logits=True)
+            _, db = eng.forward([(b, 70, t, ia.ROW_DECODE, 1)], logits=True)
+            assert np.array_equal(da, db), (kv8, cut)
+            eng.seq_truncate(a, 70)
+            eng.seq_close(b)
+        say(f"copy prefix kv_int8={kv8}: logits bit-identical at cuts 45, 64, 1")
+        p2 = prompt[:50]
+        outs = []
+        for n in (0, 2):
+            sch = ia.Scheduler(eng, chunk_m=32, live_cap=4, prefix_cache=n)
+            g1 = _drive(sch, p2, 3)
+            g2 = _drive(sch, p2 + g1 + prompt[50:60], 3)
+            outs.append((g1, g2))
+            sch.close()
+        assert outs[0] == outs[1], outs
+        say(f"scheduler prefix cache kv_int8={kv8}: streams equal")
+        eng.seq_close(a)
+    dev.close()
+    model.close()
+
+
+def _drive(sch, prompt, max_new):
+    rid = sch.submit(prompt, max_new)
+    for _ in range(200):
+        if sch.step() == 0 and sch.result(rid)[1]:
+            break
+    out, done = sch.result(rid)
+    assert done
+    return out
 
 
 @scenario

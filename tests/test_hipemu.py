@@ -48,3 +48,7 @@ def test_intfer_load_and_parser_in_bounds(emu_lib):
 
 def test_gqa_group5_shapes_in_bounds(emu_lib):
     assert runner.run_scenarios(["attention_ragged_g5", "forward_gqa5"], timeout=900) == 0
+
+
+def test_prefix_copy_and_cache_in_bounds(emu_lib):
+    assert runner.run_scenarios(["prefix_copy"], timeout=900) == 0

@@ -33,13 +33,33 @@ V = 97
 
 
 class MockLM:
-    def __init__(self, slots=16, cap=4096):
+    """`pool` bounds the tokens held over all slots (None: unbounded), the
+    way KV pages bound the engine: a forward or copy that would exceed it is
+    refused with IFR_ENOMEM and changes nothing.  `copy` installs the
+    seq_copy_prefix callback (prefix reuse)."""
+
+    def __init__(self, slots=16, cap=4096, copy=True, pool=None):
         self.hist = {}
         self.free = list(range(slots))
         self.forwards = []
+        self.copies = []
+        self.pool = pool
         self._cb = (_abi.SEQ_OPEN(self._open), _abi.SEQ_CLOSE(self._close),
                     _abi.SEQ_TRUNC(self._trunc), _abi.FORWARD(self._fwd))
-        self.table = _abi.SchedBackend(None, *self._cb, cap)
+        self._copy_cb = _abi.SEQ_COPY(self._copy) if copy else _abi.SEQ_COPY()
+        self.table = _abi.SchedBackend(None, *self._cb, cap, self._copy_cb)
+
+    def used(self):
+        return sum(len(h) for h in self.hist.values())
+
+    def _copy(self, user, dst, src, n):
+        if dst not in self.hist or src not in self.hist or self.hist[dst] or n > len(self.hist[src]):
+            return ia.IFR_EINVAL
+        if self.pool is not None and self.used() + n > self.pool:
+            return ia.IFR_ENOMEM
+        self.hist[dst] = self.hist[src][:n]
+        self.copies.append((dst, src, n))
+        return 0
 
     def _open(self, user, slot):
         if not self.free:
@@ -68,6 +88,8 @@ class MockLM:
 
     def _fwd(self, user, rows, M, best):
         rs = [(rows[i].seq, rows[i].pos, rows[i].token, rows[i].kind, rows[i].want) for i in range(M)]
+        if self.pool is not None and self.used() + M > self.pool:
+            return ia.IFR_ENOMEM
         self.forwards.append(rs)
         for i, (s, p, t, k, w) in enumerate(rs):
             h = self.hist[s]
