@@ -49,12 +49,17 @@ def parse():
     ap.add_argument("--kv-int8", type=int, default=0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-roofline", action="store_true")
+    ap.add_argument("--no-gemm", action="store_true", help="skip the decode-GEMM secondary measurement")
     ap.add_argument("--no-packed", action="store_true",
                     help="skip the secondary pack_prefill measurement of the same load")
     ap.add_argument("--gemm-sweep", action="store_true",
                     help="run only the cache-cold cfg2 GEMM sweep and print its JSON line")
     ap.add_argument("--gemm-variants", action="store_true",
                     help="time every quant-GEMM launch shape on the 0.8B shapes and print a JSON line")
+    ap.add_argument("--gemm-decode", action="store_true",
+                    help="every launch shape at decode M (1, 8, 16) on the 0.8B projections")
+    ap.add_argument("--gemm-decode-27b", action="store_true",
+                    help="every launch shape at decode M (1, 8, 16) on the 27B-class projections")
     ap.add_argument("--gemm-variants-27b", action="store_true",
                     help="the same on the 27B-class (cfg5) shapes at M = 512 and 2160")
     ap.add_argument("--attn-sweep", action="store_true",
@@ -332,12 +337,64 @@ def gemm_variants(ia, dev, Ms=(128, 256, 576, 1024), bits=2, reps=3, shapes=SHAP
                     best = ms if best is None else min(best, ms)
                 us = best * 1e3 / R
                 ops = 2.0 * M * N * len(lins) * K
+                byts = wb + M * K + M * 4 + M * N * len(lins) * 2
                 res.append({"shape": name, "M": M, "variant": v, "us": round(us, 2),
-                            "TOPS": round(ops / us / 1e6, 1)})
+                            "TOPS": round(ops / us / 1e6, 1), "GBps": round(byts / us / 1e3, 1),
+                            "hbm_frac": round(byts / us / 1e3 / 8000, 4)})
             row = [r for r in res if r["shape"] == name and r["M"] == M]
             b = min(row, key=lambda r: r["us"])
-            log(f"{name} M={M}: best variant {b['variant']} {b['us']} us {b['TOPS']} TOPS; " +
+            log(f"{name} M={M}: best variant {b['variant']} {b['us']} us {b['TOPS']} TOPS "
+                f"{b['GBps']} GB/s; " +
                 " ".join(f"v{r['variant']}:{r['us']}" for r in row))
+        for d in dls:
+            L.ifr_linear_free(dev.ctx, d)
+        for b in (q, asc, gs, out):
+            b.free()
+    return res
+
+
+def decode_gemm_brief(ia, dev, reps=3):
+    """The W2A8 decode GEMM (M = 1, the library's default launch shape),
+    cache-cold as in gemm_sweep: the 0.8B gate/up pair and the 27B-class
+    gate/up pair and down projection (the largest weight streams)."""
+    import ctypes as C
+    L = ia.lib()
+    rng = np.random.default_rng(1)
+    res = []
+    for name, K, N, pair in (("gate_up_0.8b", 1024, 3072, True), ("gate_up_27b", 5120, 17408, True),
+                             ("down_27b", 17408, 5120, False)):
+        lins = [ia.make_linear(N, K, 2, rng) for _ in range(2 if pair else 1)]
+        wb = sum(l.N * K * 2 // 8 + l.N * (K // 128) * 4 for l in lins)
+        R = int(np.ceil(320e6 / wb))
+        dls = []
+        for _ in range(R):
+            d = C.c_void_p()
+            if pair:
+                ia.check(L.ifr_linear_upload_pair(dev.ctx, C.byref(lins[0].struct), C.byref(lins[1].struct),
+                                                  C.byref(d)), "upload")
+            else:
+                ia.check(L.ifr_linear_upload(dev.ctx, C.byref(lins[0].struct), C.byref(d)), "upload")
+            dls.append(d)
+        q = dev.upload(rng.integers(-127, 128, size=16 * K, dtype=np.int8))
+        asc = dev.upload(np.full(16, 1e-3, dtype=np.float32))
+        gs = dev.upload(rng.integers(-2000, 2000, size=16 * (K // 128)).astype(np.float32))
+        out = dev.alloc(16 * N * 2 * 2)
+        best = None
+        for _ in range(reps + 1):
+            dev.timer_begin()
+            for d in dls:
+                if pair:
+                    ia.check(L.ifr_quant_gemm_swiglu(dev.ctx, d, q.p, asc.p, gs.p, 1, out.p), "swiglu")
+                else:
+                    ia.check(L.ifr_quant_gemm(dev.ctx, d, q.p, asc.p, gs.p, 1, out.p, None), "gemm")
+            ms = dev.timer_end()
+            best = ms if best is None else min(best, ms)
+        us = best * 1e3 / R
+        byts = wb + K + 4 + N * 2
+        res.append({"shape": name, "M": 1, "K": K, "N": N * len(lins), "weight_MB": round(wb / 1e6, 2),
+                    "us": round(us, 2), "GBps": round(byts / us / 1e3, 1),
+                    "hbm_frac": round(byts / us / 1e3 / 8000, 4)})
+        log(f"decode GEMM {name} M=1: {us:.2f} us, {byts / us / 1e3:.0f} GB/s")
         for d in dls:
             L.ifr_linear_free(dev.ctx, d)
         for b in (q, asc, gs, out):
@@ -520,10 +577,16 @@ def main():
                           "results": res}))
         dev.close()
         return 0
-    if a.gemm_variants or a.gemm_variants_27b:
+    if a.gemm_variants or a.gemm_variants_27b or a.gemm_decode_27b or a.gemm_decode:
         dev = ia.Device(0)
-        res = gemm_variants(ia, dev) if a.gemm_variants else \
-            gemm_variants(ia, dev, Ms=(512, 2160), shapes=SHAPES_27B, reps=2)
+        if a.gemm_variants:
+            res = gemm_variants(ia, dev)
+        elif a.gemm_decode:
+            res = gemm_variants(ia, dev, Ms=(1, 8, 16), shapes=SHAPES_08B, reps=3)
+        elif a.gemm_variants_27b:
+            res = gemm_variants(ia, dev, Ms=(512, 2160), shapes=SHAPES_27B, reps=2)
+        else:
+            res = gemm_variants(ia, dev, Ms=(1, 8, 16), shapes=SHAPES_27B, reps=3)
         print(json.dumps({"metric": "quant-GEMM launch shapes (cache-cold)", "unit": "us", "results": res}))
         dev.close()
         return 0
@@ -620,6 +683,11 @@ def main():
                                  "p99_latency_s": round(pct(done, 99), 4),
                                  "note": "scheduler option pack_prefill=1 (not the reference policy)"}
         log(f"packed prefill: {dt:.3f} s, {iters} iterations, {toks / dt:.0f} tok/s")
+    if not a.no_gemm:
+        out["decode_gemm"] = {
+            "note": "W2A8 decode GEMM at M=1, cache-cold (rotating weight copies > MALL), HIP events "
+                    "around back-to-back launches (each includes the ~2.3 us launch floor)",
+            "results": decode_gemm_brief(ia, dev)}
     if not a.no_cpu:
         log("timing the reference CPU path on a bounded sample")
         out["cpu_baseline"] = cpu_baseline(ia, model, cfg)

@@ -59,7 +59,7 @@ struct QGemmArgs {
 hipError_t launch_qgemm(const DLin& w, const QGemmArgs& a, hipStream_t st);
 // One launch shape of the table (0..kQGemmVariants-1); all give identical
 // bits.  Returns hipErrorInvalidValue where a shape does not apply.
-constexpr int kQGemmVariants = 13;
+constexpr int kQGemmVariants = 16;
 hipError_t launch_qgemm_variant(const DLin& w, const QGemmArgs& a, int variant, hipStream_t st);
 
 // ---- row kernels -----------------------------------------------------------

@@ -403,6 +403,167 @@ __global__ __launch_bounds__(256) void qgemm_splitk(KParams p) {
   }
 }
 
+// ---- decode on large weights (M <= 16): the weight stream.  A workgroup of
+// NWV waves owns WN column tiles over the whole K; wave w takes the K groups
+// [ng w / NWV, ng (w + 1) / NWV) (at most NGW) and issues all their loads at
+// entry, so a CU keeps NWV * NGW groups of codes in flight.  Only the row
+// quads that hold real rows are kept: A fragments of rows >= M are zero and
+// not fetched, and the int32 T parked in LDS covers ceil(M / 4) quads.  After
+// one barrier each output's groups fold in ascending order, as everywhere.
+template <int BITS, int WN, int NWV, int NGW, int EPI, bool ALDS, bool DUMP>
+__global__ __launch_bounds__(64 * NWV) void qgemm_stream(KParams p) {
+  extern __shared__ int32_t lds[];
+  constexpr int BN = 16 * WN, NT = 64 * NWV;
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int ntiles = p.N >> 4, ng = p.ng, M = p.M;
+  const int MQ = (M + 3) >> 2;
+  const int tile0 = blockIdx.x * WN;
+  const int g0 = (ng * wave) / NWV, g1 = (ng * (wave + 1)) / NWV;
+  int tl[WN];
+#pragma unroll
+  for (int j = 0; j < WN; ++j) tl[j] = min(tile0 + j, ntiles - 1);
+  int32_t* T_l = lds;  // [ng][WN][16 MQ lanes][4]
+  float* S_l = reinterpret_cast<float*>(lds + (size_t)ng * WN * MQ * 64);  // [ng][16]
+  uint32_t* Z_l = reinterpret_cast<uint32_t*>(S_l + 16 * ng);              // [ng][BN]
+
+  // The fold operands (S of the M rows, scale | zero of the WN tiles) are
+  // fetched first, each thread's share at once, so that storing them to LDS
+  // waits only for them while the code stream is still in flight.
+  constexpr int SQ = (NGW + 3) / 4, ZQ = (WN * NGW + 3) / 4;
+  float sv[SQ];
+  uint32_t zv[ZQ];
+#pragma unroll
+  for (int q = 0; q < SQ; ++q) {
+    const int t = threadIdx.x + NT * q;
+    const int r = t / ng, g = t - r * ng;
+    sv[q] = t < M * ng ? p.gs[(size_t)r * ng + g] : 0.f;
+  }
+#pragma unroll
+  for (int q = 0; q < ZQ; ++q) {
+    const int t = threadIdx.x + NT * q;
+    const int c = t & 15, g = (t >> 4) % ng, jt = min((t >> 4) / ng, WN - 1);
+    zv[q] = t < WN * ng * 16 ? p.sz[((size_t)tl[jt] * ng + g) * 16 + c] : 0u;
+  }
+  // ALDS (M <= 4): the block fetches the M real rows of A once, 16-byte
+  // chunks (row, step, quarter) at As[((row * nsteps + step) * 4 + quarter) * 16],
+  // instead of every wave reading its 16-row fragments from L2.
+  constexpr bool alds = ALDS;
+  int8_t* As = reinterpret_cast<int8_t*>(Z_l + (size_t)ng * BN);
+  constexpr int AQ = ALDS ? (NGW + 1) / 2 : 1;  // chunks per thread: M * 8 ng <= 4 * NT * AQ
+  v4i av[AQ];
+  if constexpr (ALDS) {
+#pragma unroll
+    for (int q = 0; q < AQ; ++q) {
+      const int ch = threadIdx.x + NT * q;
+      const int r = ch % M, sq = ch / M;  // sq = step * 4 + quarter
+      av[q] = ch < M * 4 * p.nsteps
+                  ? *reinterpret_cast<const v4i*>(p.a + 1024 * (sq >> 2) + 16 * (16 * (sq & 3) + r))
+                  : (v4i){0, 0, 0, 0};
+    }
+  }
+  // A row (lane & 15) of the single 16-row tile; rows >= M contribute zeros
+  const bool arow = (lane & 15) < M;
+  GroupOps<BITS, 1, WN> ops[NGW];
+  const int glast = max(g1 - 1, 0);
+#pragma unroll
+  for (int d = 0; d < NGW; ++d) {
+    const int g = min(g0 + d, glast);
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const int st = 2 * g + h;
+      ops[d].A[h][0] = (arow && !alds) ? *reinterpret_cast<const v4i*>(p.a + 1024 * st + 16 * lane)
+                                        : (v4i){0, 0, 0, 0};
+#pragma unroll
+      for (int j = 0; j < WN; ++j)
+        load_raw<BITS>(p.codes + ((size_t)tl[j] * p.nsteps + st) * 64 * (BITS / 2), lane, ops[d].B[h][j]);
+    }
+  }
+#pragma unroll
+  for (int q = 0; q < SQ; ++q) {
+    const int t = threadIdx.x + NT * q;
+    const int r = t / ng, g = t - r * ng;
+    if (t < M * ng) S_l[g * 16 + r] = sv[q];
+  }
+#pragma unroll
+  for (int q = 0; q < ZQ; ++q) {
+    const int t = threadIdx.x + NT * q;
+    const int c = t & 15, g = (t >> 4) % ng, jt = (t >> 4) / ng;
+    if (t < WN * ng * 16) Z_l[g * BN + 16 * jt + c] = zv[q];
+  }
+  if constexpr (ALDS) {
+#pragma unroll
+    for (int q = 0; q < AQ; ++q) {
+      const int ch = threadIdx.x + NT * q;
+      const int r = ch % M, sq = ch / M;
+      if (ch < M * 4 * p.nsteps) *reinterpret_cast<v4i*>(As + ((size_t)r * p.nsteps * 4 + sq) * 16) = av[q];
+    }
+  }
+  __syncthreads();
+  // The fold in two passes.  Each wave turns the T of its own groups into
+  // d = fma(-zero, S, T) in registers right after the MFMAs and parks d, and
+  // the group's scale as fp32 in place of the packed pair; then each output
+  // runs only the dependent chain acc = fma(scale, d, acc), groups ascending.
+  const int lrow = lane & 15, lgrp = lane >> 4;
+  v4i T[1][WN];
+#pragma unroll
+  for (int d = 0; d < NGW; ++d) {
+    if (g0 + d < g1) {
+      const int g = g0 + d;
+      if (ALDS && arow)
+#pragma unroll
+        for (int h = 0; h < 2; ++h)
+          ops[d].A[h][0] = *reinterpret_cast<const v4i*>(
+              As + (((size_t)(lane & 15) * p.nsteps + 2 * g + h) * 4 + (lane >> 4)) * 16);
+      mma_group<BITS, 1, WN>(ops[d], T);
+      if (lgrp < MQ) {
+        // rows 4 lgrp .. +3 (S of rows >= M is never written: their d is unused)
+        const v4f S4 = *reinterpret_cast<const v4f*>(&S_l[g * 16 + 4 * lgrp]);
+#pragma unroll
+        for (int j = 0; j < WN; ++j) {
+          const uint32_t zw = Z_l[g * BN + 16 * j + lrow];
+          const float ze = ifrd::h2f((uint16_t)(zw >> 16));
+          v4i dv;
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const int32_t Tv = true_t<BITS>(T[0][j][r], S4[r]);
+            dv[r] = __float_as_int(fmaf(-ze, S4[r], (float)Tv));
+            if (DUMP && 4 * lgrp + r < M && tile0 + j < ntiles)
+              p.tdump[((size_t)(4 * lgrp + r) * p.N + 16 * tl[j] + lrow) * ng + g] = Tv;
+          }
+          *reinterpret_cast<v4i*>(&T_l[(((size_t)g * WN + j) * MQ * 16 + lane) * 4]) = dv;
+          // every lane of the wave has read the pair above before this store
+          if (lgrp == 0) Z_l[g * BN + 16 * j + lrow] = __float_as_uint(ifrd::h2f((uint16_t)(zw & 0xFFFFu)));
+        }
+      }
+    }
+  }
+  __syncthreads();
+  constexpr int JS = (EPI == 0) ? 1 : 2;  // swiglu: one thread folds the pair
+  const int nout = M * 16 * (WN / JS);
+  for (int o = threadIdx.x; o < nout; o += NT) {
+    const int c = o & 15, row = (o >> 4) % M, jj = ((o >> 4) / M) * JS;
+    const int ln = 16 * (row >> 2) + c, r = row & 3;
+    float a0 = 0.f, a1 = 0.f;
+#pragma unroll 8
+    for (int g = 0; g < ng; ++g) {
+#pragma unroll
+      for (int q = 0; q < JS; ++q) {
+        const int j = jj + q;
+        const float d = __int_as_float(T_l[(((size_t)g * WN + j) * MQ * 16 + ln) * 4 + r]);
+        const float sc = __uint_as_float(Z_l[g * BN + 16 * j + c]);
+        if (q == 0) a0 = fmaf(sc, d, a0); else a1 = fmaf(sc, d, a1);
+      }
+    }
+    const float as = p.as[row] * p.post;
+    if constexpr (EPI == 0) {
+      if (tile0 + jj < ntiles) store_plain(p, row, 16 * (tile0 + jj) + c, as, a0);
+    } else {
+      if (tile0 + jj + 1 < ntiles) store_swiglu(p, row, 16 * ((tile0 + jj) >> 1) + c, as, a0, a1);
+    }
+  }
+}
+
 template <typename F>
 hipError_t set_lds_limit(F* f) {
   return hipFuncSetAttribute(reinterpret_cast<const void*>(f), hipFuncAttributeMaxDynamicSharedMemorySize,
@@ -467,6 +628,54 @@ hipError_t launch_splitk_ng(const KParams& p, hipStream_t st) {
   return hipErrorInvalidValue;
 }
 
+template <int BITS, int WN, int NWV, int NGW, int EPI>
+hipError_t launch_stream(const KParams& p, hipStream_t st) {
+  // the operand registers (8 for A and WN * BITS for B per group) must fit
+  // the 128 VGPRs of a 16-wave workgroup without spilling
+  if constexpr (NGW * (8 + WN * BITS) + (NGW + 3) / 4 + (WN * NGW + 3) / 4 > 120) {
+    return hipErrorInvalidValue;
+  } else {
+  const int MQ = (p.M + 3) / 4;
+  size_t lds = ((size_t)p.ng * WN * MQ * 64 + (size_t)p.ng * (16 + 16 * WN)) * sizeof(int32_t);
+  if (p.M > 16 || (p.ng + NWV - 1) / NWV > NGW || lds > 160 * 1024) return hipErrorInvalidValue;
+  const bool alds = p.M <= 4 && lds + (size_t)p.M * p.K <= 160 * 1024;
+  if (alds) lds += (size_t)p.M * p.K;
+  static bool attr_set = false;
+  if (!attr_set) {
+    hipError_t e = set_lds_limit(qgemm_stream<BITS, WN, NWV, NGW, EPI, false, false>);
+    if (e == hipSuccess) e = set_lds_limit(qgemm_stream<BITS, WN, NWV, NGW, EPI, true, false>);
+    if constexpr (EPI == 0) {
+      if (e == hipSuccess) e = set_lds_limit(qgemm_stream<BITS, WN, NWV, NGW, EPI, false, true>);
+      if (e == hipSuccess) e = set_lds_limit(qgemm_stream<BITS, WN, NWV, NGW, EPI, true, true>);
+    }
+    if (e != hipSuccess) return e;
+    attr_set = true;
+  }
+  const dim3 grid((p.N / 16 + WN - 1) / WN), block(64 * NWV);
+  if constexpr (EPI == 0)
+    if (p.tdump) {
+      if (alds) hipLaunchKernelGGL((qgemm_stream<BITS, WN, NWV, NGW, EPI, true, true>), grid, block, lds, st, p);
+      else hipLaunchKernelGGL((qgemm_stream<BITS, WN, NWV, NGW, EPI, false, true>), grid, block, lds, st, p);
+      return hipGetLastError();
+    }
+  if (alds) hipLaunchKernelGGL((qgemm_stream<BITS, WN, NWV, NGW, EPI, true, false>), grid, block, lds, st, p);
+  else hipLaunchKernelGGL((qgemm_stream<BITS, WN, NWV, NGW, EPI, false, false>), grid, block, lds, st, p);
+  return hipGetLastError();
+  }
+}
+
+// NGW: the smallest instantiated depth that holds ceil(ng / NWV) groups.
+template <int BITS, int WN, int NWV, int EPI>
+hipError_t launch_stream_ng(const KParams& p, hipStream_t st) {
+  const int per = (p.ng + NWV - 1) / NWV;
+  if (per <= 1) return launch_stream<BITS, WN, NWV, 1, EPI>(p, st);
+  if (per <= 2) return launch_stream<BITS, WN, NWV, 2, EPI>(p, st);
+  if (per <= 3) return launch_stream<BITS, WN, NWV, 3, EPI>(p, st);
+  if (per <= 5) return launch_stream<BITS, WN, NWV, 5, EPI>(p, st);
+  if (per <= 9) return launch_stream<BITS, WN, NWV, 9, EPI>(p, st);
+  return hipErrorInvalidValue;
+}
+
 // R (K groups in flight per wave) is the largest power of two <= RMAX that
 // divides ng.
 template <int BITS, int WM, int WN, int MW, int RMAX, int EPI>
@@ -499,6 +708,23 @@ hipError_t launch_bits(const KParams& p, int variant, hipStream_t st) {
       if (p.ng >= 96) variant = 3;
       else if (p.M >= 1024 || p.N >= 6144) variant = 6;
     }
+    // Decode rows on those shapes (bench.py --gemm-decode-27b, M = 1, 8, 16):
+    // the weight stream, two tiles per workgroup for the plain projections
+    // (one for the deep down projection above M = 4, where the T of two
+    // tiles no longer fits LDS) and one tile of 8 waves for the SwiGLU pair
+    // up to M = 8.
+    // A shape a stream variant cannot hold (registers or LDS for wider codes)
+    // falls back to the next one, then to the choice above.
+    if (p.K >= 4096 && p.M <= 16) {
+      hipError_t e = hipErrorInvalidValue;
+      if (EPI == 1) {
+        if (p.M <= 8) e = launch_bits<BITS, EPI>(p, 14, st);
+      } else {
+        if (!(p.ng >= 96 && p.M > 4)) e = launch_bits<BITS, EPI>(p, 15, st);
+        if (e == hipErrorInvalidValue) e = launch_bits<BITS, EPI>(p, 13, st);
+      }
+      if (e != hipErrorInvalidValue) return e;
+    }
   }
   switch (variant) {
     case 0: return launch_splitk_ng<BITS, 1, WNs, EPI>(p, st);
@@ -514,6 +740,9 @@ hipError_t launch_bits(const KParams& p, int variant, hipStream_t st) {
     case 10: return launch_rows_r<BITS, 1, 2, 1, 8, EPI>(p, st);  // 16 x 128 block, deep
     case 11: return launch_rows_r<BITS, 4, 2, 1, 4, EPI>(p, st);  // 64 x 128 block, deep
     case 12: return launch_rows_r<BITS, 2, 2, 1, 8, EPI>(p, st);  // 32 x 128 block, deep
+    case 13: return launch_stream_ng<BITS, WNs, 16, EPI>(p, st);  // decode stream, 16 waves
+    case 14: return launch_stream_ng<BITS, WNs, 8, EPI>(p, st);   // decode stream, 8 waves
+    case 15: return launch_stream_ng<BITS, 2 * WNs, 16, EPI>(p, st);  // 2 tiles, 16 waves
     default: return hipErrorInvalidValue;
   }
 }

@@ -88,6 +88,13 @@ def gemm_wide():
     _gemm_shapes((2, 4, 8), ((256, 256), (384, 1024)), Ms=(1, 70, 130), pair_check=True)
 
 
+@scenario
+def gemm_stream():
+    """The decode weight-stream shapes at the 27B-class depths (K = 5120 and
+    17408) and M = 1, 5, 16, INT2 and INT4."""
+    _gemm_shapes((2, 4), ((32, 5120), (16, 17408)), Ms=(1, 5, 16), pair_check=True)
+
+
 def _gemm_shapes(bits_list, shapes, Ms=(1, 17, 70), pair_check=False):
     import intfer_amd as ia
     from oracle import pyoracle as po

@@ -135,7 +135,7 @@ def test_qgemm_every_launch_shape_bitexact(dev, bits):
         ia.check(L.ifr_linear_upload_pair(dev.ctx, C.byref(gate.struct), C.byref(up.struct),
                                           C.byref(dp)), "pair")
         try:
-            for M in (1, 37, 130):
+            for M in (1, 5, 16, 37, 130):
                 x = rng.standard_normal((M, K), dtype=np.float32)
                 q, sc, g = po.act_quant(x)
                 qd, sd, gd = dev.upload(ia.atile(q)), dev.upload(sc[:, 0].copy()), dev.upload(g)
@@ -160,6 +160,59 @@ def test_qgemm_every_launch_shape_bitexact(dev, bits):
                         pair_out = po_
                     assert np.array_equal(po_, pair_out), f"pair variant {v} N={N} K={K} M={M}"
                 assert ran >= 2
+                for b in (qd, sd, gd, od):
+                    b.free()
+        finally:
+            L.ifr_linear_free(dev.ctx, dl)
+            L.ifr_linear_free(dev.ctx, dp)
+
+
+@pytest.mark.parametrize("bits", [2, 4, 8])
+def test_qgemm_decode_stream_large_k_bitexact(dev, bits):
+    """The decode weight-stream shapes (variants 13-15: M <= 16, the whole K
+    of a column tile per workgroup) at the 27B-class depths K = 5120 and
+    17408 (136 groups, the deepest register ring), against the oracle's
+    bits, for the plain linear and the SwiGLU pair."""
+    rng = np.random.default_rng(950 + bits)
+    for (N, K) in ((96, 5120), (64, 17408)):
+        lin = ia.make_linear(N, K, bits, rng)
+        gate, up = ia.make_linear(N, K, bits, rng), ia.make_linear(N, K, bits, rng)
+        dl, dp = C.c_void_p(), C.c_void_p()
+        ia.check(L.ifr_linear_upload(dev.ctx, C.byref(lin.struct), C.byref(dl)), "upload")
+        ia.check(L.ifr_linear_upload_pair(dev.ctx, C.byref(gate.struct), C.byref(up.struct),
+                                          C.byref(dp)), "pair")
+        try:
+            for M in (1, 3, 16):
+                x = rng.standard_normal((M, K), dtype=np.float32)
+                q, sc, g = po.act_quant(x)
+                qd, sd, gd = dev.upload(ia.atile(q)), dev.upload(sc[:, 0].copy()), dev.upload(g)
+                od = dev.alloc(M * N * 2)
+                ref = po.qgemm(q, sc[:, 0], lin)
+                ran = 0
+                pair_ref = None
+                for v in (13, 14, 15, 0):
+                    announce(f"qgemm stream variant {v} bits={bits} N={N} K={K} M={M}")
+                    rc = L.ifr_quant_gemm_variant(dev.ctx, dl, qd.p, sd.p, gd.p, M, od.p, v)
+                    if rc != ia.IFR_EDECLINE:
+                        ia.check(rc, f"variant {v}")
+                        out = dev.download(od, np.uint16, (M, N))
+                        assert np.array_equal(out, ref), f"variant {v} N={N} K={K} M={M}"
+                        ran += 1
+                    rc = L.ifr_quant_gemm_variant(dev.ctx, dp, qd.p, sd.p, gd.p, M, od.p, v)
+                    if rc != ia.IFR_EDECLINE:
+                        ia.check(rc, f"pair variant {v}")
+                        po_ = dev.download(od, np.uint16, (M, N))
+                        if pair_ref is None:
+                            pair_ref = po_
+                        assert np.array_equal(po_, pair_ref), f"pair variant {v} N={N} K={K} M={M}"
+                # the heuristic's own choice (a stream shape, or its fallback
+                # where one cannot hold the codes) gives the same bits
+                ia.check(L.ifr_quant_gemm(dev.ctx, dl, qd.p, sd.p, gd.p, M, od.p, None), "default")
+                assert np.array_equal(dev.download(od, np.uint16, (M, N)), ref)
+                ia.check(L.ifr_quant_gemm_swiglu(dev.ctx, dp, qd.p, sd.p, gd.p, M, od.p), "pair default")
+                if pair_ref is not None:
+                    assert np.array_equal(dev.download(od, np.uint16, (M, N)), pair_ref)
+                assert ran >= (1 if bits < 8 else 0)
                 for b in (qd, sd, gd, od):
                     b.free()
         finally:
