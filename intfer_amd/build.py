@@ -40,9 +40,10 @@ COMMON = [
 ]
 
 
-# MFMA results of the GEMMs feed VALU work at once (the per-group fold), so
-# they stay in VGPRs instead of round-tripping through AGPRs.
-EXTRA = {"qgemm.hip": ["-mllvm", "--amdgpu-mfma-vgpr-form"]}
+# MFMA results of the GEMMs feed VALU work at once (the per-group fold), and
+# attention rescales its O accumulators between MFMAs, so both keep MFMA
+# results in VGPRs instead of round-tripping through AGPRs.
+EXTRA = {"qgemm.hip": ["-mllvm", "--amdgpu-mfma-vgpr-form"], "attn.hip": ["-mllvm", "--amdgpu-mfma-vgpr-form"]}
 
 
 def _compile(item) -> Path:

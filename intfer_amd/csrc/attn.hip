@@ -155,6 +155,11 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs p, KVLayout kv) {
       for (int i4 = 0; i4 < 4; ++i4) kf[h][i4] = frag(b.k[h][i4]);
     v8h phi[NT], plo[NT];
     float alpha[NT];
+    // A page wholly below the unit's first query position and its KV end
+    // masks nothing for a valid column (columns past the unit's rows carry
+    // q = 0, finite scores, and are never stored), so only boundary pages
+    // pay for the mask.  Wave-uniform.
+    const bool interior = t0 + kPage - 1 <= un.qpos0 && t0 + kPage <= un.kv_hi;
 #pragma unroll
     for (int t = 0; t < NT; ++t) {
       v4f s[2];
@@ -175,7 +180,7 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs p, KVLayout kv) {
           float v = s[h][r];
           if constexpr (KV8) v *= ifrd::h2f(b.ks[h][r]);
           v *= p.scale_log2;
-          if (!colv[t] || tk > qpos[t] || tk >= un.kv_hi) v = -INFINITY;
+          if (!interior && (!colv[t] || tk > qpos[t] || tk >= un.kv_hi)) v = -INFINITY;
           sv[2 * r + h] = v;
           mt = fmaxf(mt, v);
         }
@@ -183,14 +188,14 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs p, KVLayout kv) {
       mt = fmaxf(mt, __shfl_xor(mt, 32, 64));
       const float m_new = fmaxf(m_run[t], mt);
       const float m_use = (m_new == -INFINITY) ? 0.0f : m_new;
-      alpha[t] = exp2f(m_run[t] - m_use);
+      alpha[t] = __builtin_amdgcn_exp2f(m_run[t] - m_use);
       // P enters the PV product as an fp16 hi + lo pair (p ~ hi + lo to ~22
       // bits): V is exact in fp16, so O carries fp32-level accuracy and the
       // downstream per-token int8 codes match the fp32 reference loop.
       float rs = 0.0f;
 #pragma unroll
       for (int j = 0; j < 8; ++j) {
-        const float pf = exp2f(sv[j] - m_use);
+        const float pf = __builtin_amdgcn_exp2f(sv[j] - m_use);
         rs += pf;
         const float pv = KV8 ? pf * ifrd::h2f(b.vs[j]) : pf;
         const _Float16 hh = (_Float16)pv;
@@ -202,12 +207,17 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs p, KVLayout kv) {
       l_run[t] = l_run[t] * alpha[t] + rs;
       m_run[t] = m_new;
     }
+    // rescale O only when some column's running max moved (x * 1 is exact)
+#pragma unroll
+    for (int t = 0; t < NT; ++t)
+      if (!__all(alpha[t] == 1.0f))
+#pragma unroll
+        for (int d = 0; d < 8; ++d) o[t][d] *= alpha[t];
 #pragma unroll
     for (int d = 0; d < 8; ++d) {
       const v8h vf = frag(b.v[d]);
 #pragma unroll
       for (int t = 0; t < NT; ++t) {
-        o[t][d] *= alpha[t];
         o[t][d] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vf, phi[t], o[t][d], 0, 0, 0);
         o[t][d] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vf, plo[t], o[t][d], 0, 0, 0);
       }
@@ -329,14 +339,45 @@ __global__ __launch_bounds__(256) void combine_kernel(CombineArgs a) {
 #pragma unroll
   for (int i = 0; i < CS; ++i) acc[i] = 0.0f;
   const float2* ml2 = reinterpret_cast<const float2*>(a.part_ml);
-  for (int s0 = 0; s0 < ns; s0 += 4) {
+  // Up to R1 splits: one round of loads, the max taken from the loaded
+  // (m, l) pairs; more: a max pass, then the weighted sum.  Either way the
+  // splits are summed in ascending order with the same operands.
+  constexpr int R1 = CS == 8 ? 8 : 4;
+  if (ns <= R1) {
+    float2 mlv[R1];
+    float4 ov[R1][CS / 4];
+#pragma unroll
+    for (int q = 0; q < R1; ++q) {
+      const size_t pi = (size_t)(base + min(q, ns - 1)) * a.ucols + col;
+      mlv[q] = ml2[pi];
+      const float4* po = reinterpret_cast<const float4*>(a.part_o + pi * a.hd + d0);
+#pragma unroll
+      for (int r = 0; r < CS / 4; ++r) ov[q][r] = po[r];
+    }
+#pragma unroll
+    for (int q = 0; q < R1; ++q) mx = fmaxf(mx, mlv[q].x);
+#pragma unroll
+    for (int q = 0; q < R1; ++q) {
+      if (q >= ns || mlv[q].x == -INFINITY) continue;
+      const float f = exp2f(mlv[q].x - mx);
+      L += f * mlv[q].y;
+#pragma unroll
+      for (int r = 0; r < CS / 4; ++r) {
+        acc[4 * r + 0] += f * ov[q][r].x;
+        acc[4 * r + 1] += f * ov[q][r].y;
+        acc[4 * r + 2] += f * ov[q][r].z;
+        acc[4 * r + 3] += f * ov[q][r].w;
+      }
+    }
+  }
+  for (int s0 = 0; s0 < (ns <= R1 ? 0 : ns); s0 += 4) {
     float mm[4];
 #pragma unroll
     for (int q = 0; q < 4; ++q) mm[q] = ml2[(size_t)(base + min(s0 + q, ns - 1)) * a.ucols + col].x;
 #pragma unroll
     for (int q = 0; q < 4; ++q) mx = fmaxf(mx, mm[q]);
   }
-  for (int s0 = 0; s0 < ns; s0 += 4) {
+  for (int s0 = 0; s0 < (ns <= R1 ? 0 : ns); s0 += 4) {
     float2 mlv[4];
     float4 ov[4][CS / 4];
 #pragma unroll
