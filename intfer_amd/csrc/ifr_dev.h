@@ -65,8 +65,11 @@ constexpr int kQuadXor1 = 0xB1;  // quad_perm [1,0,3,2]
 constexpr int kQuadXor2 = 0x4E;  // quad_perm [2,3,0,1]
 constexpr int kRowRor4 = 0x124, kRowRor8 = 0x128, kRowRor12 = 0x12C;
 
-// Value of lane (lane ^ M).  M <= 8 stays inside a 16-lane row (DPP); larger
-// M crosses rows and uses the crossbar.
+// Value of lane (lane ^ M).  M <= 8 stays inside a 16-lane row (DPP); 16 and
+// 32 use the gfx950 lane swaps (VALU, no LDS crossbar): with both operands x,
+// v_permlane16_swap returns (x with odd rows replaced by the even rows below,
+// x with even rows replaced by the odd rows above), v_permlane32_swap the same
+// for the two 32-lane halves.
 template <int M>
 __device__ __forceinline__ float lane_xor(float x) {
   if constexpr (M == 1) {
@@ -79,6 +82,11 @@ __device__ __forceinline__ float lane_xor(float x) {
     return (threadIdx.x & 4) ? from_lo : from_hi;
   } else if constexpr (M == 8) {
     return dpp_f<kRowRor8>(x);
+  } else if constexpr (M == 16 || M == 32) {
+    const int i = __builtin_bit_cast(int, x);
+    const auto r = M == 16 ? __builtin_amdgcn_permlane16_swap(i, i, false, false)
+                           : __builtin_amdgcn_permlane32_swap(i, i, false, false);
+    return __builtin_bit_cast(float, (int)((threadIdx.x & M) ? r[0] : r[1]));
   } else {
     return __shfl_xor(x, M, 64);
   }

@@ -376,6 +376,23 @@ int emu_update_dpp(int old, int src, int ctrl, int row_mask, int bank_mask, bool
   return emu::lane_value<int>(s, from);
 }
 
+// v_permlane16_swap / v_permlane32_swap (CDNA4 ISA): the odd 16-lane rows
+// (upper 32-lane half) of the first operand trade places with the even rows
+// (lower half) of the second; returns (new first, new second).
+static emu_v2u permlane_swap(unsigned vdst, unsigned vsrc, int span) {
+  const unsigned pair[2] = {vdst, vsrc};
+  const unsigned char* s = emu::wave_exchange(pair, 8, emu::kOpShfl);
+  const int l = emu::cur()->lane;
+  auto at = [&](int lane, int k) { return emu::lane_value<unsigned long long>(s, lane) >> (32 * k) & 0xFFFFFFFFu; };
+  emu_v2u r;
+  const bool upper = (l & span) != 0;
+  r[0] = upper ? (unsigned)at(l - span, 1) : (unsigned)at(l, 0);
+  r[1] = upper ? (unsigned)at(l, 1) : (unsigned)at(l + span, 0);
+  return r;
+}
+emu_v2u emu_permlane16_swap(unsigned vdst, unsigned vsrc, bool, bool) { return permlane_swap(vdst, vsrc, 16); }
+emu_v2u emu_permlane32_swap(unsigned vdst, unsigned vsrc, bool, bool) { return permlane_swap(vdst, vsrc, 32); }
+
 emu_v4i emu_mfma_i32_16x16x64_i8(emu_v4i a, emu_v4i b, emu_v4i c) {
   struct P {
     emu_v4i a, b;

@@ -185,6 +185,11 @@ int emu_update_dpp(int old, int src, int ctrl, int row_mask, int bank_mask, bool
 #define __builtin_amdgcn_readlane(...) emu_readlane(__VA_ARGS__)
 #define __builtin_amdgcn_readfirstlane(...) emu_readfirstlane(__VA_ARGS__)
 #define __builtin_amdgcn_update_dpp(...) emu_update_dpp(__VA_ARGS__)
+typedef unsigned int emu_v2u __attribute__((ext_vector_type(2)));
+emu_v2u emu_permlane16_swap(unsigned vdst, unsigned vsrc, bool fi, bool bc);
+emu_v2u emu_permlane32_swap(unsigned vdst, unsigned vsrc, bool fi, bool bc);
+#define __builtin_amdgcn_permlane16_swap(...) emu_permlane16_swap(__VA_ARGS__)
+#define __builtin_amdgcn_permlane32_swap(...) emu_permlane32_swap(__VA_ARGS__)
 #define __builtin_amdgcn_wave_barrier() ::emu::wave_barrier()
 #define __builtin_amdgcn_fence(...) ((void)0)
 #define __builtin_amdgcn_s_barrier() __syncthreads()
