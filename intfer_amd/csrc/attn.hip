@@ -140,8 +140,20 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs p, KVLayout kv) {
     if constexpr (!KV8) {
       f = __builtin_bit_cast(v8h, (v4i){(int)w[0], (int)w[1], (int)w[2], (int)w[3]});
     } else {
+      // int8 b -> fp16 exactly: byte b ^ 0x80 = b + 128 under the exponent
+      // byte 0x64 is the half 1024 + (b + 128); subtracting 1152 leaves b.
+      typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+      const h2 bias = {(_Float16)1152.0f, (_Float16)1152.0f};
 #pragma unroll
-      for (int j = 0; j < 8; ++j) f[j] = (_Float16)(int8_t)((w[j >> 2] >> (8 * (j & 3))) & 0xFF);
+      for (int q = 0; q < 2; ++q) {
+        const uint32_t u = w[q] ^ 0x80808080u;
+        const h2 lo = __builtin_bit_cast(h2, __builtin_amdgcn_perm(0x64646464u, u, 0x04010400u)) - bias;
+        const h2 hi = __builtin_bit_cast(h2, __builtin_amdgcn_perm(0x64646464u, u, 0x04030402u)) - bias;
+        f[4 * q + 0] = lo[0];
+        f[4 * q + 1] = lo[1];
+        f[4 * q + 2] = hi[0];
+        f[4 * q + 3] = hi[1];
+      }
     }
     return f;
   };

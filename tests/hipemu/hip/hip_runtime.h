@@ -188,6 +188,22 @@ int emu_update_dpp(int old, int src, int ctrl, int row_mask, int bank_mask, bool
 typedef unsigned int emu_v2u __attribute__((ext_vector_type(2)));
 emu_v2u emu_permlane16_swap(unsigned vdst, unsigned vsrc, bool fi, bool bc);
 emu_v2u emu_permlane32_swap(unsigned vdst, unsigned vsrc, bool fi, bool bc);
+// v_perm_b32: result byte i = byte sel_i of the 8 bytes {s0 (4-7), s1 (0-3)};
+// selector 0x0C gives 0x00, 0x0D..0x0F give 0xFF (only 0..7 are used here).
+inline unsigned emu_perm(unsigned s0, unsigned s1, unsigned sel) {
+  const unsigned long long cat = ((unsigned long long)s0 << 32) | s1;
+  unsigned r = 0;
+  for (int i = 0; i < 4; ++i) {
+    const unsigned k = (sel >> (8 * i)) & 0xFF;
+    unsigned byte = 0;
+    if (k < 8) byte = (unsigned)(cat >> (8 * k)) & 0xFF;
+    else if (k == 0x0C) byte = 0;
+    else if (k >= 0x0D) byte = 0xFF;
+    r |= byte << (8 * i);
+  }
+  return r;
+}
+#define __builtin_amdgcn_perm(a, b, c) emu_perm((a), (b), (c))
 #define __builtin_amdgcn_permlane16_swap(...) emu_permlane16_swap(__VA_ARGS__)
 #define __builtin_amdgcn_permlane32_swap(...) emu_permlane32_swap(__VA_ARGS__)
 #define __builtin_amdgcn_wave_barrier() ::emu::wave_barrier()
