@@ -43,6 +43,11 @@ struct KParams {
   int32_t* tdump;
   int M, N, K, ng, nsteps, ldo;
   float post;  // folded into the row scale: (ascale * post) * acc
+  // qgemm_rows block order: swz > 0 launches a 1-D grid of nbx * nby blocks
+  // in which the blocks of each XCD (block id mod 8) own the column blocks
+  // of that residue and walk all row blocks over swz of them at a time, so
+  // the weight columns in flight on an XCD stay inside its L2.
+  int nbx, nby, swz;
 };
 
 // One compilation of this file per code width (IFR_QGEMM_BITS = 2, 4, 8)
@@ -224,7 +229,16 @@ __global__ __launch_bounds__(256) void qgemm_rows(KParams p) {
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int lrow = lane & 15, lgrp = lane >> 4;
   const int ntiles = p.N >> 4, ng = p.ng;
-  const int bm0 = blockIdx.y * BM, bt0 = blockIdx.x * (BN / 16);
+  int bx = blockIdx.x, by = blockIdx.y;
+  if (p.swz > 0) {
+    const int x = blockIdx.x & 7, local = blockIdx.x >> 3, per = p.nbx >> 3;
+    const int G = min(p.swz, per);
+    const int gi = local / (G * p.nby), r = local - gi * G * p.nby;
+    const int Gg = min(G, per - gi * G);
+    by = r / Gg;
+    bx = x + 8 * (gi * G + (r - by * Gg));
+  }
+  const int bm0 = by * BM, bt0 = bx * (BN / 16);
   const int wm = wave % MW, wn = wave / MW;
   const int row0 = bm0 + 16 * WM * wm, tile0 = bt0 + WN * wn;
   float* S_l = lds_f;
@@ -586,13 +600,23 @@ hipError_t launch_rows(const KParams& p, hipStream_t st) {
     attr_set = true;
   }
   const int ntiles = p.N / 16;
-  const dim3 grid((ntiles + BN / 16 - 1) / (BN / 16), (p.M + BM - 1) / BM);
+  KParams q = p;
+  q.nbx = (ntiles + BN / 16 - 1) / (BN / 16);
+  q.nby = (p.M + BM - 1) / BM;
+  // XCD-grouped order when the column blocks split evenly over the 8 XCDs
+  // and an XCD's share of the weights (codes + scales) would not stay in its
+  // 4 MB L2 (bench.py --cfg5: gate/up 56.7 -> 53.9 ms; no gain below that):
+  // groups of column blocks that fill about 2 MB
+  const size_t colblock_bytes = (size_t)BN * p.K * BITS / 8 + (size_t)BN * p.ng * 4;
+  q.swz = (q.nbx % 8 == 0 && q.nby >= 2 && (size_t)(q.nbx / 8) * colblock_bytes > ((size_t)3 << 20))
+              ? (int)std::max<size_t>(1, ((size_t)2 << 20) / colblock_bytes) : 0;
+  const dim3 grid = q.swz ? dim3(q.nbx * q.nby) : dim3(q.nbx, q.nby);
   if constexpr (EPI == 0)
     if (p.tdump) {
-      hipLaunchKernelGGL((qgemm_rows<BITS, WM, WN, MW, R, EPI, true>), grid, dim3(256), lds, st, p);
+      hipLaunchKernelGGL((qgemm_rows<BITS, WM, WN, MW, R, EPI, true>), grid, dim3(256), lds, st, q);
       return hipGetLastError();
     }
-  hipLaunchKernelGGL((qgemm_rows<BITS, WM, WN, MW, R, EPI, false>), grid, dim3(256), lds, st, p);
+  hipLaunchKernelGGL((qgemm_rows<BITS, WM, WN, MW, R, EPI, false>), grid, dim3(256), lds, st, q);
   return hipGetLastError();
 }
 
@@ -817,7 +841,7 @@ hipError_t launch_qgemm_variant(const DLin& w, const QGemmArgs& a, int variant, 
     return hipErrorInvalidValue;
   if (w.pair && (w.N % 32 != 0 || a.tdump)) return hipErrorInvalidValue;
   qg::KParams p{a.a, a.as, a.gs, w.codes, w.sz, a.out, a.tdump, a.M, w.N, w.K, w.ng, w.nsteps, a.ldo,
-                w.post};
+                w.post, 0, 0, 0};
   const int epi = w.pair ? 1 : 0;
   switch (w.bits) {
     case 2: return qg::launch_b2(p, epi, variant, st);

@@ -89,6 +89,13 @@ def gemm_wide():
 
 
 @scenario
+def gemm_grouped():
+    """Enough column blocks (N = 4096) for the XCD-grouped block order of the
+    larger-M shapes, ragged M."""
+    _gemm_shapes((2,), ((4096, 128),), Ms=(70, 130))
+
+
+@scenario
 def gemm_stream():
     """The decode weight-stream shapes at the 27B-class depths (K = 5120 and
     17408) and M = 1, 5, 16, INT2 and INT4."""

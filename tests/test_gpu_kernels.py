@@ -167,6 +167,40 @@ def test_qgemm_every_launch_shape_bitexact(dev, bits):
             L.ifr_linear_free(dev.ctx, dp)
 
 
+def test_qgemm_xcd_grouped_order_bitexact(dev):
+    """A weight set large enough for the XCD-grouped block order of the
+    larger-M shapes (INT8, N = 4096, K = 8192: 4 MB of codes per XCD share):
+    every launch shape, and the default, give the oracle's bits."""
+    rng = np.random.default_rng(977)
+    N, K, M = 4096, 8192, 40
+    lin = ia.make_linear(N, K, 8, rng)
+    dl = C.c_void_p()
+    ia.check(L.ifr_linear_upload(dev.ctx, C.byref(lin.struct), C.byref(dl)), "upload")
+    try:
+        x = rng.standard_normal((M, K), dtype=np.float32)
+        q, sc, g = po.act_quant(x)
+        qd, sd, gd = dev.upload(ia.atile(q)), dev.upload(sc[:, 0].copy()), dev.upload(g)
+        od = dev.alloc(M * N * 2)
+        ref = po.qgemm(q, sc[:, 0], lin)
+        ran = 0
+        for v in list(range(L.ifr_quant_gemm_variants())) + [-1]:
+            announce(f"qgemm grouped order variant {v} N={N} K={K} M={M}")
+            if v < 0:
+                rc = L.ifr_quant_gemm(dev.ctx, dl, qd.p, sd.p, gd.p, M, od.p, None)
+            else:
+                rc = L.ifr_quant_gemm_variant(dev.ctx, dl, qd.p, sd.p, gd.p, M, od.p, v)
+            if rc == ia.IFR_EDECLINE:
+                continue
+            ia.check(rc, f"variant {v}")
+            assert np.array_equal(dev.download(od, np.uint16, (M, N)), ref), f"variant {v}"
+            ran += 1
+        assert ran >= 5
+        for b in (qd, sd, gd, od):
+            b.free()
+    finally:
+        L.ifr_linear_free(dev.ctx, dl)
+
+
 @pytest.mark.parametrize("bits", [2, 4, 8])
 def test_qgemm_decode_stream_large_k_bitexact(dev, bits):
     """The decode weight-stream shapes (variants 13-15: M <= 16, the whole K
