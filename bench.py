@@ -143,7 +143,7 @@ GEMMS = ["qgemm_qkv", "qgemm_o", "qgemm_gate_up", "qgemm_down"]
 KERNELS = GEMMS + ["attention", "row_quant", "qk_rope_kv", "combine", "quant_plain", "lmhead", "pack"]
 # the rocprofv3 kernel names each timing category covers (each GEMM category:
 # qgemm_splitk<...> for M <= 64, qgemm_rows<...> above)
-ROCPROF_NAMES = {"attention": "attn_kernel<{kv}>",
+ROCPROF_NAMES = {"attention": "attn_kernel<{kv}, 1>",
                  "combine": "combine_kernel", "row_quant": "row_quant1024_kernel",
                  "quant_plain": "quant_plain8<384>", "qk_rope_kv": "qk_rope_kv_kernel",
                  "lmhead": "lmhead_kernel<...> + argmax_final_kernel", "pack": "pack_kernel"}
