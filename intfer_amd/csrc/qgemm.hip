@@ -43,10 +43,12 @@ struct KParams {
   int32_t* tdump;
   int M, N, K, ng, nsteps, ldo;
   float post;  // folded into the row scale: (ascale * post) * acc
-  // qgemm_rows block order: swz > 0 launches a 1-D grid of nbx * nby blocks
-  // in which the blocks of each XCD (block id mod 8) own the column blocks
-  // of that residue and walk all row blocks over swz of them at a time, so
-  // the weight columns in flight on an XCD stay inside its L2.
+  // qgemm_rows block order.  swz > 0: a 1-D grid in which the blocks of
+  // each XCD (block id mod 8) own the column blocks of that residue and walk
+  // all row blocks over swz of them at a time, so the weight columns in
+  // flight on an XCD stay inside its L2.  swz < 0: the same with the roles
+  // of rows and columns exchanged (activation rows kept, for a larger A).
+  // The owned dimension is padded to a multiple of 8; padding blocks exit.
   int nbx, nby, swz;
 };
 
@@ -230,13 +232,17 @@ __global__ __launch_bounds__(256) void qgemm_rows(KParams p) {
   const int lrow = lane & 15, lgrp = lane >> 4;
   const int ntiles = p.N >> 4, ng = p.ng;
   int bx = blockIdx.x, by = blockIdx.y;
-  if (p.swz > 0) {
-    const int x = blockIdx.x & 7, local = blockIdx.x >> 3, per = p.nbx >> 3;
-    const int G = min(p.swz, per);
-    const int gi = local / (G * p.nby), r = local - gi * G * p.nby;
+  if (p.swz != 0) {
+    const bool cols = p.swz > 0;
+    const int own = cols ? p.nbx : p.nby, other = cols ? p.nby : p.nbx;
+    const int x = blockIdx.x & 7, local = blockIdx.x >> 3, per = (own + 7) >> 3;
+    const int G = min(cols ? p.swz : -p.swz, per);
+    const int gi = local / (G * other), r = local - gi * G * other;
     const int Gg = min(G, per - gi * G);
-    by = r / Gg;
-    bx = x + 8 * (gi * G + (r - by * Gg));
+    const int o = r / Gg, w = x + 8 * (gi * G + (r - o * Gg));
+    bx = cols ? w : o;
+    by = cols ? o : w;
+    if (bx >= p.nbx || by >= p.nby) return;  // padding (before any barrier)
   }
   const int bm0 = by * BM, bt0 = bx * (BN / 16);
   const int wm = wave % MW, wn = wave / MW;
@@ -530,13 +536,14 @@ __global__ __launch_bounds__(64 * NWV) void qgemm_stream(KParams p) {
           ops[d].A[h][0] = *reinterpret_cast<const v4i*>(
               As + (((size_t)(lane & 15) * p.nsteps + 2 * g + h) * 4 + (lane >> 4)) * 16);
       mma_group<BITS, 1, WN>(ops[d], T);
+      uint32_t zw[WN];
       if (lgrp < MQ) {
         // rows 4 lgrp .. +3 (S of rows >= M is never written: their d is unused)
         const v4f S4 = *reinterpret_cast<const v4f*>(&S_l[g * 16 + 4 * lgrp]);
 #pragma unroll
         for (int j = 0; j < WN; ++j) {
-          const uint32_t zw = Z_l[g * BN + 16 * j + lrow];
-          const float ze = ifrd::h2f((uint16_t)(zw >> 16));
+          zw[j] = Z_l[g * BN + 16 * j + lrow];
+          const float ze = ifrd::h2f((uint16_t)(zw[j] >> 16));
           v4i dv;
 #pragma unroll
           for (int r = 0; r < 4; ++r) {
@@ -546,10 +553,14 @@ __global__ __launch_bounds__(64 * NWV) void qgemm_stream(KParams p) {
               p.tdump[((size_t)(4 * lgrp + r) * p.N + 16 * tl[j] + lrow) * ng + g] = Tv;
           }
           *reinterpret_cast<v4i*>(&T_l[(((size_t)g * WN + j) * MQ * 16 + lane) * 4]) = dv;
-          // every lane of the wave has read the pair above before this store
-          if (lgrp == 0) Z_l[g * BN + 16 * j + lrow] = __float_as_uint(ifrd::h2f((uint16_t)(zw & 0xFFFFu)));
         }
       }
+      // every lane of the wave has read the packed pairs before they are
+      // replaced by the fp32 scale
+      ifrd::wave_sync();
+      if (lgrp == 0)
+#pragma unroll
+        for (int j = 0; j < WN; ++j) Z_l[g * BN + 16 * j + lrow] = __float_as_uint(ifrd::h2f((uint16_t)(zw[j] & 0xFFFFu)));
     }
   }
   __syncthreads();
@@ -603,14 +614,18 @@ hipError_t launch_rows(const KParams& p, hipStream_t st) {
   KParams q = p;
   q.nbx = (ntiles + BN / 16 - 1) / (BN / 16);
   q.nby = (p.M + BM - 1) / BM;
-  // XCD-grouped order when the column blocks split evenly over the 8 XCDs
-  // and an XCD's share of the weights (codes + scales) would not stay in its
-  // 4 MB L2 (bench.py --cfg5: gate/up 56.7 -> 53.9 ms; no gain below that):
-  // groups of column blocks that fill about 2 MB
+  // XCD-grouped order by weight columns when an XCD's share of the weights
+  // would not stay in its 4 MB L2, in groups that fill about 2 MB
+  // (bench.py --cfg5: gate/up 56.7 -> 54 ms; no gain below that size).
+  // Grouping by activation rows instead (swz < 0) made the 27B down
+  // projection, whose A is larger than its weights, slower (32.6 -> 38.7
+  // ms), so the host does not choose it.
   const size_t colblock_bytes = (size_t)BN * p.K * BITS / 8 + (size_t)BN * p.ng * 4;
-  q.swz = (q.nbx % 8 == 0 && q.nby >= 2 && (size_t)(q.nbx / 8) * colblock_bytes > ((size_t)3 << 20))
-              ? (int)std::max<size_t>(1, ((size_t)2 << 20) / colblock_bytes) : 0;
-  const dim3 grid = q.swz ? dim3(q.nbx * q.nby) : dim3(q.nbx, q.nby);
+  const size_t mb2 = (size_t)2 << 20, mb3 = (size_t)3 << 20;
+  q.swz = (q.nbx >= 8 && q.nby >= 2 && (size_t)((q.nbx + 7) / 8) * colblock_bytes > mb3)
+              ? (int)std::max<size_t>(1, mb2 / colblock_bytes) : 0;
+  const dim3 grid = q.swz > 0 ? dim3((q.nbx + 7) / 8 * 8 * q.nby)
+                    : q.swz < 0 ? dim3((q.nby + 7) / 8 * 8 * q.nbx) : dim3(q.nbx, q.nby);
   if constexpr (EPI == 0)
     if (p.tdump) {
       hipLaunchKernelGGL((qgemm_rows<BITS, WM, WN, MW, R, EPI, true>), grid, dim3(256), lds, st, q);

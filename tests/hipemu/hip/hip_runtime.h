@@ -175,6 +175,16 @@ inline unsigned long long __ballot(int pred) {
   return m;
 }
 
+// 1 when the predicate holds on every live lane of the wave (HIP __all)
+inline int __all(int pred) { return __ballot(!pred) == 0; }
+
+inline float __int_as_float(int x) { float f; std::memcpy(&f, &x, 4); return f; }
+inline float __uint_as_float(unsigned x) { float f; std::memcpy(&f, &x, 4); return f; }
+inline int __float_as_int(float f) { int x; std::memcpy(&x, &f, 4); return x; }
+inline unsigned __float_as_uint(float f) { unsigned x; std::memcpy(&x, &f, 4); return x; }
+// v_exp_f32 (2^x); the host's exp2f stands in for the hardware approximation
+#define __builtin_amdgcn_exp2f(x) exp2f(x)
+
 inline int emu_readlane(int v, int l) {
   const unsigned char* s = emu::wave_exchange(&v, 4, emu::kOpReadlane);
   return emu::lane_value<int>(s, l);
