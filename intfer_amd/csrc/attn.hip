@@ -24,6 +24,21 @@ namespace {
 constexpr int kHD = 128;
 constexpr int kPage = 32;
 
+// One lane's W dwords of a K or V fragment.  fp16 pages (16 bytes a lane)
+// are a streaming read (each page of a decode or verify unit is read once):
+// c64 decode rows 62.4 -> 59.9 us (bench.py --attn-sweep); the 8-byte int8
+// fragments were slower that way and keep plain loads.
+template <int W>
+__device__ __forceinline__ void load_frag(const uint32_t* src, uint32_t (&dst)[W]) {
+  if constexpr (W == 4) {
+    const v4i x = __builtin_nontemporal_load(reinterpret_cast<const v4i*>(src));
+    dst[0] = (uint32_t)x.x; dst[1] = (uint32_t)x.y; dst[2] = (uint32_t)x.z; dst[3] = (uint32_t)x.w;
+  } else {
+#pragma unroll
+    for (int q = 0; q < W; ++q) dst[q] = src[q];
+  }
+}
+
 template <bool KV8, int NT>
 __global__ __launch_bounds__(256) void attn_kernel(AttnArgs p, KVLayout kv) {
   const int lane = threadIdx.x & 63;
@@ -114,15 +129,13 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs p, KVLayout kv) {
       for (int i4 = 0; i4 < 4; ++i4) {
         const size_t e = (size_t)((h * 4 + i4) * 64 + lane) * 8;  // element index
         const uint32_t* src = reinterpret_cast<const uint32_t*>(kp + e * (KV8 ? 1 : 2));
-#pragma unroll
-        for (int q = 0; q < W; ++q) b.k[h][i4][q] = src[q];
+        load_frag<W>(src, b.k[h][i4]);
       }
 #pragma unroll
     for (int d = 0; d < 8; ++d) {
       const size_t e = (size_t)(d * 64 + lane) * 8;
       const uint32_t* src = reinterpret_cast<const uint32_t*>(vp + e * (KV8 ? 1 : 2));
-#pragma unroll
-      for (int q = 0; q < W; ++q) b.v[d][q] = src[q];
+      load_frag<W>(src, b.v[d]);
     }
     if constexpr (KV8) {
       const uint16_t* ksc = kv.kscale + pb * kPage;
