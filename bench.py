@@ -427,7 +427,14 @@ def cpu_baseline(ia, model, cfg):
     ora.forward(rows)
     dt = time.perf_counter() - t0
     ora.close()
+    model_name = ""
+    try:
+        with open("/proc/cpuinfo") as f:
+            model_name = next((ln.split(":", 1)[1].strip() for ln in f if ln.startswith("model name")), "")
+    except OSError:
+        pass
     return {"value": D / dt, "unit": "tok/s", "cores": threads, "kind": "port",
+            "host_cpu": model_name, "host_nproc": os.cpu_count(),
             "sample": f"one mixed iteration of the 28-layer f32 CPU path: {D} decode rows at "
                       f"context {ctx} + a {P}-row prefill chunk at offset {off} "
                       f"(the load's ~16.5 prefill tokens per output token); {dt:.1f} s"}
