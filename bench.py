@@ -513,7 +513,7 @@ def cfg5_bench(ia, a):
         once()
     dev.sync()
     ms = 1e3 * (time.perf_counter() - t0) / a.steps
-    # roofline of the iteration (SURVEY 8(d) formulas)
+    # roofline of the iteration: t = max(bytes / HBM peak, int8 ops / int8 peak + attention flops / fp16 peak)
     H, L, nq, nkv, hd, F = cfg.hidden, cfg.layers, cfg.n_heads, cfg.n_kv, cfg.head_dim, cfg.inter
     per_layer = H * (nq * hd + 2 * nkv * hd) + nq * hd * H + H * 2 * F + F * H
     nwant = sum(r[4] for r in rows)
@@ -556,7 +556,7 @@ def main():
     a = parse()
     if a.gpus != 1:
         print(f"bench.py: this build measures one GPU; --gpus {a.gpus} is not supported "
-              "(the path shards as independent data-parallel engines, see DESIGN.md)",
+              "(the path shards as independent data-parallel engines, one per GPU)",
               file=sys.stderr)
         return 2
     import intfer_amd as ia
