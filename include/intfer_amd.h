@@ -231,6 +231,10 @@ typedef struct ifr_kv_cfg {
                            * measured no faster on the serve load: each layer
                            * is a chain of latency-bound kernels whose time
                            * barely shrinks with half the rows. */
+  int32_t separate_qk;    /* 0: the q/k norm + RoPE + KV append runs as the
+                           * QKV GEMM's epilogue where the launch shape is one
+                           * head per workgroup (bit-identical); 1: always as
+                           * its own pass */
 } ifr_kv_cfg;
 
 /* Upload + repack a model (replaces Engine::load, build_shards,

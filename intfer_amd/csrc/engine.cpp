@@ -199,6 +199,13 @@ struct Scope {
     hipEventRecord(t.b, st);
     c->timers.push_back(t);
   }
+  // nothing was launched: drop the interval
+  void cancel() {
+    if (!on) return;
+    hipEventDestroy(t.a);
+    hipEventDestroy(t.b);
+    on = false;
+  }
 };
 
 void add_host_time(ifr_ctx* c, const char* name, double ms) {
@@ -457,19 +464,33 @@ int launch_layer(ifr_ctx* c, const SubBatch& sb, int l) {
     Scope sc(c, L.st, "row_quant", (double)M * H * 4 * 2);
     HIPCHK(ifrk::launch_row_quant(a, L.st));
   }
-  // (2) QKV
-  for (int j = 0; j < ly.nqkv; ++j) {
-    ifrk::QGemmArgs a{L.aq, L.as, L.gs, L.qkv + ly.qkv_off[j], nullptr, M, qN + 2 * kvN};
-    Scope sc(c, L.st, "qgemm_qkv", (double)ly.qkv[j].bytes + (double)M * (H + 4) + (double)M * ly.qkv[j].N * 2,
-             2.0 * M * ly.qkv[j].N * H);
-    HIPCHK(ifrk::launch_qgemm(ly.qkv[j], a, L.st));
+  // (2) QKV and (3) q/k norm + RoPE + KV append: one launch when the QKV
+  // GEMM's launch shape holds one head per workgroup, else two passes
+  const ifrk::QKArgs qka{L.qkv, L.pk.row_seq, L.pk.row_pos, ly.q_norm, ly.k_norm, c->rope_cos,
+                         c->rope_sin, cf.rotary_dim, cf.rms_eps, nq, L.qbuf, M};
+  bool fused = false;
+  if (!c->kv.separate_qk && ly.nqkv == 1) {
+    ifrk::QGemmArgs a{L.aq, L.as, L.gs, nullptr, nullptr, M, qN + 2 * kvN};
+    Scope sc(c, L.st, "qgemm_qkv", (double)ly.qkv[0].bytes + (double)M * (H + 4) + (double)M * ly.qkv[0].N * 2,
+             2.0 * M * ly.qkv[0].N * H);
+    const hipError_t e = ifrk::launch_qgemm_qkrope(ly.qkv[0], a, qka, kv, -1, L.st);
+    if (e == hipErrorInvalidValue) {
+      (void)hipGetLastError();
+      sc.cancel();
+    } else {
+      HIPCHK(e);
+      fused = true;
+    }
   }
-  // (3) q/k norm + RoPE + KV append
-  {
-    ifrk::QKArgs a{L.qkv, L.pk.row_seq, L.pk.row_pos, ly.q_norm, ly.k_norm, c->rope_cos,
-                   c->rope_sin, cf.rotary_dim, cf.rms_eps, nq, L.qbuf, M};
+  if (!fused) {
+    for (int j = 0; j < ly.nqkv; ++j) {
+      ifrk::QGemmArgs a{L.aq, L.as, L.gs, L.qkv + ly.qkv_off[j], nullptr, M, qN + 2 * kvN};
+      Scope sc(c, L.st, "qgemm_qkv", (double)ly.qkv[j].bytes + (double)M * (H + 4) + (double)M * ly.qkv[j].N * 2,
+               2.0 * M * ly.qkv[j].N * H);
+      HIPCHK(ifrk::launch_qgemm(ly.qkv[j], a, L.st));
+    }
     Scope sc(c, L.st, "qk_rope_kv", (double)M * (qN + 2 * kvN) * 2 * 2);
-    HIPCHK(ifrk::launch_qk_rope_kv(a, kv, L.st));
+    HIPCHK(ifrk::launch_qk_rope_kv(qka, kv, L.st));
   }
   // (4) attention + combine (emits the O-proj int8 input)
   {

@@ -132,6 +132,13 @@ struct QKArgs {
   int M;
 };
 hipError_t launch_qk_rope_kv(const QKArgs& a, const KVLayout& kv, hipStream_t st);
+// The QKV projection with the q/k norm + RoPE + KV append as its epilogue
+// (launch_qgemm followed by launch_qk_rope_kv, bit-identical, without the
+// fp16 QKV buffer).  variant < 0: the default launch shape.  Returns
+// hipErrorInvalidValue where that shape is not a one-head-per-workgroup row
+// block (then run the two passes).
+hipError_t launch_qgemm_qkrope(const DLin& w, const QGemmArgs& a, const QKArgs& qa, const KVLayout& kv, int variant,
+                               hipStream_t st);
 
 // ---- KV page copy (prefix reuse) ----------------------------------------------
 // Copies n pages, sp[i] -> dp[i] (device page indices), in each of npools

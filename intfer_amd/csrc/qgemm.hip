@@ -50,6 +50,11 @@ struct KParams {
   // of rows and columns exchanged (activation rows kept, for a larger A).
   // The owned dimension is padded to a multiple of 8; padding blocks exit.
   int nbx, nby, swz;
+  // EPI 2 (QKV projection with the q/k norm + RoPE + KV append epilogue):
+  // the arguments of the separate pass (row maps, norms, RoPE tables, q
+  // output, paged KV)
+  QKArgs qa;
+  KVLayout kv;
 };
 
 // One compilation of this file per code width (IFR_QGEMM_BITS = 2, 4, 8)
@@ -217,6 +222,174 @@ __device__ __forceinline__ void stage_fold_operands(const KParams& p, int bm0, i
   }
 }
 
+// ---- QKV epilogue: q/k RMSNorm(1 + w) + RoPE + KV append ----------------------
+// For a block of BM rows x one 128-column head (BN = 128): the fp16-rounded
+// outputs y = fp16(ascale * post * acc) -- the values the separate
+// qk_rope_kv_kernel reads back -- are staged in LDS, then each wave takes 8
+// rows with 8 lanes per row.  Lane s of a row owns dims 8 s .. 8 s + 7 and
+// their rotate-half partners 64 + 8 s .. + 7, so RoPE needs no exchange; the
+// RMS sum runs the reference's eight chains (chain s over dims s + 8 n), and
+// every value is formed as in qk_rope_kv_kernel, so the results are
+// bit-identical.  Requires hd = 128 and rotary = 128.
+template <int BM, int BN, int WM, int WN, int MW>
+__device__ __forceinline__ void qk_epilogue(const KParams& p, float* lds, const v4f (&acc)[WM][WN],
+                                            const float (&asr)[WM][4], int bm0, int bt0, int wave, int lane) {
+  static_assert(BN == 128 && BM == 32, "one 128-column head of 32 rows per workgroup");
+  constexpr int NW = 4 / MW, YS = BN + 4;  // padded LDS row
+  const QKArgs& qa = p.qa;
+  const KVLayout& kv = p.kv;
+  const int nq = qa.nq, nkv = kv.nkv;
+  const int h = (bt0 * 16) / 128;
+  const int kind = h < nq ? 0 : (h < nq + nkv ? 1 : 2);  // q, k, v
+  const int hh = kind == 0 ? h : (kind == 1 ? h - nq : h - nq - nkv);
+  const int rr = lane >> 3, sub = lane & 7;
+  const int row_l = 8 * wave + rr, m = bm0 + row_l;
+  const int mc = min(m, p.M - 1);
+  const int d0 = 8 * sub;
+  // stage y (the fold-operand LDS is free once every wave has folded)
+  float* Y = lds;
+  float* red = lds + BM * YS;
+  __syncthreads();
+  {
+    const int lrow = lane & 15, lgrp = lane >> 4;
+    const int wm = wave % MW, wn = wave / MW;
+#pragma unroll
+    for (int i = 0; i < WM; ++i)
+#pragma unroll
+      for (int j = 0; j < WN; ++j)
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+          Y[(16 * WM * wm + 16 * i + 4 * lgrp + r) * YS + 16 * (WN * wn + j) + lrow] =
+              ifrd::fp16r(asr[i][r] * acc[i][j][r]);
+  }
+  (void)NW;
+  // then the row record, RoPE entries, norm weights and block table (issued
+  // once the accumulators are dead, so they do not raise the register peak)
+  const int pos = qa.row_pos[mc], seq = qa.row_seq[mc];
+  float cs[8], sn[8], nwa[8], nwb[8];
+  {
+    const float4* cp = reinterpret_cast<const float4*>(qa.rope_cos + (size_t)pos * 64 + d0);
+    const float4* sp = reinterpret_cast<const float4*>(qa.rope_sin + (size_t)pos * 64 + d0);
+    const float* nw = kind == 0 ? qa.q_norm : (kind == 1 ? qa.k_norm : qa.rope_cos);
+    const float4* na = reinterpret_cast<const float4*>(nw + d0);
+    const float4* nb = reinterpret_cast<const float4*>(nw + 64 + d0);
+#pragma unroll
+    for (int q = 0; q < 2; ++q) {
+      const float4 c4 = cp[q], s4 = sp[q], a4 = na[q], b4 = nb[q];
+      cs[4 * q] = c4.x; cs[4 * q + 1] = c4.y; cs[4 * q + 2] = c4.z; cs[4 * q + 3] = c4.w;
+      sn[4 * q] = s4.x; sn[4 * q + 1] = s4.y; sn[4 * q + 2] = s4.z; sn[4 * q + 3] = s4.w;
+      nwa[4 * q] = a4.x; nwa[4 * q + 1] = a4.y; nwa[4 * q + 2] = a4.z; nwa[4 * q + 3] = a4.w;
+      nwb[4 * q] = b4.x; nwb[4 * q + 1] = b4.y; nwb[4 * q + 2] = b4.z; nwb[4 * q + 3] = b4.w;
+    }
+  }
+  const int page = kv.block_table[(size_t)seq * kv.max_pages + pos / kv.page];
+  __syncthreads();
+  if (m >= p.M) return;  // after the last workgroup barrier
+  const float* y = Y + row_l * YS;
+  float xa[8], xb[8];
+#pragma unroll
+  for (int k = 0; k < 8; ++k) {
+    xa[k] = y[d0 + k];
+    xb[k] = y[64 + d0 + k];
+  }
+  // RMSNorm(1+w) of the head: chain `sub` over dims sub + 8 n (reference
+  // AVX2 order, main.cpp:306-351)
+  {
+    float t[16];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) t[i] = y[sub + 8 * i];
+    float accn = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) accn = fmaf(t[i], t[i], accn);
+    red[row_l * 8 + sub] = accn;
+  }
+  ifrd::wave_sync();
+  const float* rd = red + row_l * 8;
+  const float s0 = rd[0] + rd[4], s1 = rd[1] + rd[5];
+  const float s2 = rd[2] + rd[6], s3 = rd[3] + rd[7];
+  const float tot = (s0 + s1) + (s2 + s3);
+  const float f = 1.0f / sqrtf(tot / 128.0f + qa.eps);
+  float oa[8], ob[8];
+#pragma unroll
+  for (int k = 0; k < 8; ++k) {
+    if (kind < 2) {
+      const float va = (xa[k] * f) * (1.0f + nwa[k]), vb = (xb[k] * f) * (1.0f + nwb[k]);
+      // rotate-half RoPE (main.cpp:365-373): dims d and d + 64 share entry d
+      oa[k] = va * cs[k] - vb * sn[k];
+      ob[k] = va * sn[k] + vb * cs[k];
+    } else {
+      oa[k] = xa[k];
+      ob[k] = xb[k];
+    }
+    oa[k] = ifrd::fp16r(oa[k]);
+    ob[k] = ifrd::fp16r(ob[k]);
+  }
+  auto pack8 = [&](const float (&v)[8]) {
+    uint32_t w4[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) w4[k] = (uint32_t)ifrd::f2h(v[2 * k]) | ((uint32_t)ifrd::f2h(v[2 * k + 1]) << 16);
+    return make_uint4(w4[0], w4[1], w4[2], w4[3]);
+  };
+  if (kind == 0) {
+    uint16_t* dst = qa.qout + ((size_t)m * nq + hh) * 128;
+    *reinterpret_cast<uint4*>(dst + d0) = pack8(oa);
+    *reinterpret_cast<uint4*>(dst + 64 + d0) = pack8(ob);
+    return;
+  }
+  const int tok = pos % kv.page;
+  const size_t base = (size_t)page * nkv + hh;
+  if (!kv.kv_int8) {
+    if (kind == 1) {  // 8 consecutive dims of one token are 16 contiguous bytes
+      uint16_t* kp = reinterpret_cast<uint16_t*>(kv.kpool) + base * kv.page * 128;
+      *reinterpret_cast<uint4*>(kp + kv_koff(tok, d0)) = pack8(oa);
+      *reinterpret_cast<uint4*>(kp + kv_koff(tok, 64 + d0)) = pack8(ob);
+    } else {
+      uint16_t* vp = reinterpret_cast<uint16_t*>(kv.vpool) + base * 128 * kv.page;
+#pragma unroll
+      for (int k = 0; k < 8; ++k) {
+        vp[kv_voff(tok, d0 + k)] = ifrd::f2h(oa[k]);
+        vp[kv_voff(tok, 64 + d0 + k)] = ifrd::f2h(ob[k]);
+      }
+    }
+  } else {
+    float mx = 0.0f;
+#pragma unroll
+    for (int k = 0; k < 8; ++k) mx = fmaxf(mx, fmaxf(fabsf(oa[k]), fabsf(ob[k])));
+    // the row's 8 lanes: max is order-free
+    mx = fmaxf(mx, ifrd::lane_xor<1>(mx));
+    mx = fmaxf(mx, ifrd::lane_xor<2>(mx));
+    mx = fmaxf(mx, ifrd::lane_xor<4>(mx));
+    const uint16_t sh16 = ifrd::f2h(mx > 0.0f ? mx / 127.0f : 1.0f);
+    const float sc = ifrd::h2f(sh16);
+    const float inv = 1.0f / sc;
+    auto code = [&](float v) {
+      const float t = v * inv;
+      int q = (int)(t >= 0.0f ? t + 0.5f : t - 0.5f);
+      return (uint32_t)(min(127, max(-127, q)) & 0xFF);
+    };
+    if (kind == 1) {
+      int8_t* kp = reinterpret_cast<int8_t*>(kv.kpool) + base * kv.page * 128;
+      uint32_t la[2] = {0u, 0u}, lb[2] = {0u, 0u};
+#pragma unroll
+      for (int k = 0; k < 8; ++k) {
+        la[k >> 2] |= code(oa[k]) << (8 * (k & 3));
+        lb[k >> 2] |= code(ob[k]) << (8 * (k & 3));
+      }
+      *reinterpret_cast<uint2*>(kp + kv_koff(tok, d0)) = make_uint2(la[0], la[1]);
+      *reinterpret_cast<uint2*>(kp + kv_koff(tok, 64 + d0)) = make_uint2(lb[0], lb[1]);
+      if (sub == 0) kv.kscale[base * kv.page + tok] = sh16;
+    } else {
+      int8_t* vp = reinterpret_cast<int8_t*>(kv.vpool) + base * 128 * kv.page;
+#pragma unroll
+      for (int k = 0; k < 8; ++k) {
+        vp[kv_voff(tok, d0 + k)] = (int8_t)code(oa[k]);
+        vp[kv_voff(tok, 64 + d0 + k)] = (int8_t)code(ob[k]);
+      }
+      if (sub == 0) kv.vscale[base * kv.page + tok] = sh16;
+    }
+  }
+}
+
 // ---- larger M: a workgroup computes a BM x BN block, its 4 waves arranged
 // MW x (4/MW); each wave owns WM x WN 16x16 tiles and folds its own
 // accumulators group by group while the next R groups are in flight.  The
@@ -313,6 +486,10 @@ __global__ __launch_bounds__(256) void qgemm_rows(KParams p) {
     fold(g + d);
   }
 
+  if constexpr (EPI == 2) {
+    qk_epilogue<BM, BN, WM, WN, MW>(p, lds_f, acc, asr, bm0, bt0, wave, lane);
+    return;
+  }
 #pragma unroll
   for (int i = 0; i < WM; ++i)
 #pragma unroll
@@ -600,7 +777,12 @@ hipError_t launch_rows(const KParams& p, hipStream_t st) {
   constexpr int NW = 4 / MW;
   constexpr int BM = 16 * WM * MW, BN = 16 * WN * NW;
   if (p.ng % R != 0) return hipErrorInvalidValue;
-  const size_t lds = (size_t)p.ng * (BM + BN) * sizeof(float);
+  size_t lds = (size_t)p.ng * (BM + BN) * sizeof(float);
+  if constexpr (EPI == 2) {
+    // the staged y tile (padded rows) and the RMS partial sums
+    if (BM != 32 || BN != 128 || p.qa.rotary != 128 || p.kv.hd != 128) return hipErrorInvalidValue;
+    lds = std::max(lds, (size_t)(BM * (BN + 4) + BM * 8) * sizeof(float));
+  }
   if (lds > 160 * 1024) return hipErrorInvalidValue;
   static bool attr_set = false;
   if (!attr_set) {
@@ -728,6 +910,29 @@ hipError_t launch_rows_r(const KParams& p, hipStream_t st) {
 // Launch-shape table.  Every variant computes identical bits; the choice is
 // a pure performance decision (variant < 0: the default heuristic).
 template <int BITS, int EPI>
+hipError_t launch_bits(const KParams& p, int variant, hipStream_t st);
+
+// The QKV projection with the q/k epilogue: the default shape when it is a
+// 32 x 128 row block (one head per workgroup), else declined (the caller
+// runs the GEMM and the separate q/k pass).
+template <int BITS>
+hipError_t launch_bits_qk(const KParams& p, int variant, hipStream_t st) {
+  if (variant < 0) {
+    const int ng = p.ng;
+    // the plain-GEMM heuristic of launch_bits for these shapes
+    variant = (ng <= 24 && p.M <= 128) ? 0 : 5;
+    if (p.K >= 4096 && p.M > 256 && (ng >= 96 || p.M >= 1024 || p.N >= 6144)) variant = -1;
+    if (p.K >= 4096 && p.M <= 16) variant = -1;
+  }
+  switch (variant) {
+    case 4: return launch_rows_r<BITS, 2, 2, 1, 4, 2>(p, st);
+    case 5: return launch_rows_r<BITS, 2, 2, 1, 2, 2>(p, st);
+    case 12: return launch_rows_r<BITS, 2, 2, 1, 8, 2>(p, st);
+    default: return hipErrorInvalidValue;
+  }
+}
+
+template <int BITS, int EPI>
 hipError_t launch_bits(const KParams& p, int variant, hipStream_t st) {
   constexpr int WNs = EPI == 0 ? 1 : 2;
   if (variant < 0) {
@@ -791,6 +996,7 @@ hipError_t launch_bits(const KParams& p, int variant, hipStream_t st) {
 #define IFR_QG_CAT2(a, b) a##b
 #define IFR_QG_CAT(a, b) IFR_QG_CAT2(a, b)
 hipError_t IFR_QG_CAT(launch_b, IFR_QGEMM_BITS)(const KParams& p, int epi, int variant, hipStream_t st) {
+  if (epi == 2) return launch_bits_qk<IFR_QGEMM_BITS>(p, variant, st);
   return epi ? launch_bits<IFR_QGEMM_BITS, 1>(p, variant, st) : launch_bits<IFR_QGEMM_BITS, 0>(p, variant, st);
 }
 
@@ -850,13 +1056,30 @@ hipError_t launch_qgemm(const DLin& w, const QGemmArgs& a, hipStream_t st) {
   return launch_qgemm_variant(w, a, -1, st);
 }
 
+hipError_t launch_qgemm_qkrope(const DLin& w, const QGemmArgs& a, const QKArgs& qa, const KVLayout& kv, int variant,
+                               hipStream_t st) {
+  if (a.M <= 0) return hipSuccess;
+  if (w.pair || w.K % kG != 0 || w.N % 128 != 0 || !w.codes || !a.a || !a.as || !a.gs || qa.M != a.M ||
+      w.N != (qa.nq + 2 * kv.nkv) * kv.hd || !qa.qout || !kv.kpool || !kv.vpool || !kv.block_table ||
+      (kv.kv_int8 && (!kv.kscale || !kv.vscale)))
+    return hipErrorInvalidValue;
+  qg::KParams p{a.a, a.as, a.gs, w.codes, w.sz, nullptr, nullptr, a.M, w.N, w.K, w.ng, w.nsteps, w.N,
+                w.post, 0, 0, 0, qa, kv};
+  switch (w.bits) {
+    case 2: return qg::launch_b2(p, 2, variant, st);
+    case 4: return qg::launch_b4(p, 2, variant, st);
+    case 8: return qg::launch_b8(p, 2, variant, st);
+    default: return hipErrorInvalidValue;
+  }
+}
+
 hipError_t launch_qgemm_variant(const DLin& w, const QGemmArgs& a, int variant, hipStream_t st) {
   if (a.M <= 0) return hipSuccess;
   if (w.K % kG != 0 || w.N % 16 != 0 || !w.codes || !a.a || !a.as || !a.gs || !a.out)
     return hipErrorInvalidValue;
   if (w.pair && (w.N % 32 != 0 || a.tdump)) return hipErrorInvalidValue;
   qg::KParams p{a.a, a.as, a.gs, w.codes, w.sz, a.out, a.tdump, a.M, w.N, w.K, w.ng, w.nsteps, a.ldo,
-                w.post, 0, 0, 0};
+                w.post, 0, 0, 0, {}, {}};
   const int epi = w.pair ? 1 : 0;
   switch (w.bits) {
     case 2: return qg::launch_b2(p, epi, variant, st);

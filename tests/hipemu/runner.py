@@ -352,6 +352,38 @@ def attention_ragged_g5():
 
 
 @scenario
+def forward_fused_qk():
+    """The QKV GEMM with the q/k norm + RoPE + KV append epilogue (M > 128,
+    one head per workgroup) against the two separate passes: logits and the
+    following decode step bit-identical, fp16 and int8 KV."""
+    import intfer_amd as ia
+    cfg = ia.default_cfg(layers=1, vocab=2048)
+    model = ia.SynthModel(cfg, seed=6, bits=2)
+    dev = ia.Device(0)
+    rng = np.random.default_rng(12)
+    prompt = rng.integers(0, cfg.vocab, size=150).tolist()
+    for kv8 in (0, 1):
+        outs = []
+        for sep in (0, 1):
+            eng = ia.Engine(dev, model, max_seqs=4, max_seq_tokens=512, pool_tokens=4 * 512, kv_int8=kv8,
+                            max_rows=192, separate_qk=sep)
+            s = eng.seq_open()
+            eng.set_timing(True)
+            b, lg = eng.forward([(s, p, t, ia.ROW_PREFILL, int(p % 50 == 49)) for p, t in enumerate(prompt)],
+                                logits=True)
+            # the 150-row forward ran the separate q/k pass only when asked to
+            assert (eng.timing("qk_rope_kv")[1] > 0) == bool(sep), (sep, eng.timing("qk_rope_kv"))
+            eng.set_timing(False)
+            _, lg2 = eng.forward([(s, 150, int(b[-1]), ia.ROW_DECODE, 1)], logits=True)
+            outs.append((lg, lg2))
+            del eng
+        assert np.array_equal(outs[0][0], outs[1][0]) and np.array_equal(outs[0][1], outs[1][1]), kv8
+        say(f"fused q/k epilogue kv_int8={kv8}: logits and next step bit-identical to the two passes")
+    dev.close()
+    model.close()
+
+
+@scenario
 def prefix_copy():
     """ifr_seq_copy_prefix (the prefix cache's page copy) with fp16 and int8
     KV: a copied prefix plus the recomputed rest gives the same logits, bit
