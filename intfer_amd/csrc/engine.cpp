@@ -823,7 +823,15 @@ int ifr_model_load(ifr_ctx* c, const ifr_host_model* m, const ifr_kv_cfg* kvc) {
   if (!c || !m || !kvc) return fail(IFR_EINVAL, "null arg");
   HIPCHK(hipSetDevice(c->device));
   const ifr_model_cfg& cf = m->cfg;
+  if (cf.layers <= 0 || cf.n_heads <= 0 || cf.n_kv <= 0 || cf.vocab <= 0 || cf.hidden <= 0 || cf.inter <= 0 ||
+      !m->layers || !m->embed || !m->final_norm)
+    return fail(IFR_EINVAL, "model cfg / buffers");
   if (cf.head_dim != 128) return fail(IFR_EDECLINE, "head_dim %d != 128", cf.head_dim);
+  // every per-kernel shape limit is checked here, so no forward can fail
+  // part-way through a layer because of the model's shape: the attention
+  // combine holds one row of n_heads * head_dim <= 8192 in a workgroup
+  if (cf.n_heads * cf.head_dim > 8192)
+    return fail(IFR_EDECLINE, "n_heads * head_dim = %d > 8192", cf.n_heads * cf.head_dim);
   if (cf.n_heads % cf.n_kv != 0 || cf.n_heads / cf.n_kv > 8)
     return fail(IFR_EDECLINE, "GQA group %d/%d unsupported", cf.n_heads, cf.n_kv);
   if (cf.hidden % 256 || cf.hidden > 8192 || (cf.n_heads * cf.head_dim) % 256 ||
@@ -1301,14 +1309,14 @@ int ifr_forward(ifr_ctx* c, const ifr_row* rows, int32_t M, int32_t* best_out, f
   return IFR_OK;
 }
 
-int ifr_attention(ifr_ctx* c, int32_t layer, const ifr_row* rows, int32_t M, const uint16_t* q_h,
-                  float* out_h) {
-  if (!c || !rows || !q_h || !out_h) return fail(IFR_EINVAL, "null arg");
-  if (!c->loaded) return fail(IFR_ESTATE, "no model loaded");
-  if (M <= 0 || M > c->maxM) return fail(IFR_EINVAL, "M=%d outside [1, %d]", M, c->maxM);
-  if (layer < 0 || layer >= c->cfg.layers) return fail(IFR_EINVAL, "layer %d", layer);
-  const int nq = c->cfg.n_heads, nkv = c->cfg.n_kv, hd = c->cfg.head_dim;
-  std::vector<int> g_len, g_pos0, g_seq;
+}  // extern "C"
+
+namespace {
+
+// Rows of an attention-only call: open sequences whose KV already holds every
+// row's position, one contiguous run of consecutive positions per sequence.
+int attn_groups(ifr_ctx* c, const ifr_row* rows, int M, std::vector<int>& g_len, std::vector<int>& g_pos0) {
+  std::vector<int> g_seq;
   for (int m = 0; m < M; ++m) {
     const ifr_row& r = rows[m];
     if (r.seq < 0 || r.seq >= (int)c->seqs.size() || !c->seqs[r.seq].open)
@@ -1327,6 +1335,22 @@ int ifr_attention(ifr_ctx* c, int32_t layer, const ifr_row* rows, int32_t M, con
       g_len.back() += 1;
     }
   }
+  return IFR_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int ifr_attention(ifr_ctx* c, int32_t layer, const ifr_row* rows, int32_t M, const uint16_t* q_h,
+                  float* out_h) {
+  if (!c || !rows || !q_h || !out_h) return fail(IFR_EINVAL, "null arg");
+  if (!c->loaded) return fail(IFR_ESTATE, "no model loaded");
+  if (M <= 0 || M > c->maxM) return fail(IFR_EINVAL, "M=%d outside [1, %d]", M, c->maxM);
+  if (layer < 0 || layer >= c->cfg.layers) return fail(IFR_EINVAL, "layer %d", layer);
+  const int nq = c->cfg.n_heads, nkv = c->cfg.n_kv, hd = c->cfg.head_dim;
+  std::vector<int> g_len, g_pos0;
+  if (int r = attn_groups(c, rows, M, g_len, g_pos0)) return r;
   int split = c->kv.attn_split > 0 ? c->kv.attn_split : kSplit;
   long nunits = count_units(g_pos0, g_len, nkv, split, c->qb);
   while (nunits > c->max_units) {

@@ -270,7 +270,10 @@ __device__ __forceinline__ void qk_epilogue(const KParams& p, float* lds, const 
   {
     const float4* cp = reinterpret_cast<const float4*>(qa.rope_cos + (size_t)pos * 64 + d0);
     const float4* sp = reinterpret_cast<const float4*>(qa.rope_sin + (size_t)pos * 64 + d0);
-    const float* nw = kind == 0 ? qa.q_norm : (kind == 1 ? qa.k_norm : qa.rope_cos);
+    // a model without q/k norm (or a v head) reads the RoPE table in its place
+    // and ignores it, so the loads stay unconditional
+    const float* nwh = kind == 0 ? qa.q_norm : (kind == 1 ? qa.k_norm : nullptr);
+    const float* nw = nwh ? nwh : qa.rope_cos;
     const float4* na = reinterpret_cast<const float4*>(nw + d0);
     const float4* nb = reinterpret_cast<const float4*>(nw + 64 + d0);
 #pragma unroll
@@ -282,6 +285,7 @@ __device__ __forceinline__ void qk_epilogue(const KParams& p, float* lds, const 
       nwb[4 * q] = b4.x; nwb[4 * q + 1] = b4.y; nwb[4 * q + 2] = b4.z; nwb[4 * q + 3] = b4.w;
     }
   }
+  const bool has_norm = (kind == 0 ? qa.q_norm : qa.k_norm) != nullptr;
   const int page = kv.block_table[(size_t)seq * kv.max_pages + pos / kv.page];
   __syncthreads();
   if (m >= p.M) return;  // after the last workgroup barrier
@@ -313,7 +317,10 @@ __device__ __forceinline__ void qk_epilogue(const KParams& p, float* lds, const 
 #pragma unroll
   for (int k = 0; k < 8; ++k) {
     if (kind < 2) {
-      const float va = (xa[k] * f) * (1.0f + nwa[k]), vb = (xb[k] * f) * (1.0f + nwb[k]);
+      // RMSNorm(1+w) only where the model has q/k norm weights (the separate
+      // pass, qk_rope_kv_kernel, makes the same choice)
+      const float va = has_norm ? (xa[k] * f) * (1.0f + nwa[k]) : xa[k];
+      const float vb = has_norm ? (xb[k] * f) * (1.0f + nwb[k]) : xb[k];
       // rotate-half RoPE (main.cpp:365-373): dims d and d + 64 share entry d
       oa[k] = va * cs[k] - vb * sn[k];
       ob[k] = va * sn[k] + vb * cs[k];

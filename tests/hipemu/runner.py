@@ -355,14 +355,17 @@ def attention_ragged_g5():
 def forward_fused_qk():
     """The QKV GEMM with the q/k norm + RoPE + KV append epilogue (M > 128,
     one head per workgroup) against the two separate passes: logits and the
-    following decode step bit-identical, fp16 and int8 KV."""
+    following decode step bit-identical, fp16 and int8 KV.  A model without
+    q/k norm weights (qk_norm = 0) takes the same epilogue without the norm,
+    bit-identical to the separate pass and token-equal to the oracle."""
     import intfer_amd as ia
-    cfg = ia.default_cfg(layers=1, vocab=2048)
-    model = ia.SynthModel(cfg, seed=6, bits=2)
+    from oracle import pyoracle as po
     dev = ia.Device(0)
     rng = np.random.default_rng(12)
-    prompt = rng.integers(0, cfg.vocab, size=150).tolist()
-    for kv8 in (0, 1):
+    prompt = rng.integers(0, 2048, size=150).tolist()
+    for qkn, kv8 in ((1, 0), (1, 1), (0, 0)):
+        cfg = ia.default_cfg(layers=1, vocab=2048, qk_norm=qkn)
+        model = ia.SynthModel(cfg, seed=6, bits=2)
         outs = []
         for sep in (0, 1):
             eng = ia.Engine(dev, model, max_seqs=4, max_seq_tokens=512, pool_tokens=4 * 512, kv_int8=kv8,
@@ -375,12 +378,19 @@ def forward_fused_qk():
             assert (eng.timing("qk_rope_kv")[1] > 0) == bool(sep), (sep, eng.timing("qk_rope_kv"))
             eng.set_timing(False)
             _, lg2 = eng.forward([(s, 150, int(b[-1]), ia.ROW_DECODE, 1)], logits=True)
-            outs.append((lg, lg2))
+            outs.append((lg, lg2, b))
             del eng
         assert np.array_equal(outs[0][0], outs[1][0]) and np.array_equal(outs[0][1], outs[1][1]), kv8
-        say(f"fused q/k epilogue kv_int8={kv8}: logits and next step bit-identical to the two passes")
+        if not qkn:
+            ora = po.OracleEngine(model, kv_int8=kv8, mode=0, max_seqs=4)
+            so = ora.seq_open()
+            bo, lo = ora.forward([(so, p, t, ia.ROW_PREFILL, int(p % 50 == 49)) for p, t in enumerate(prompt)],
+                                 logits=True)
+            assert np.array_equal(bo, outs[0][2]), (bo, outs[0][2])
+            assert float(np.abs(outs[0][0] - lo).max()) <= 0.05 * float(lo.std())
+        say(f"fused q/k epilogue qk_norm={qkn} kv_int8={kv8}: logits and next step bit-identical to the two passes")
+        model.close()
     dev.close()
-    model.close()
 
 
 @scenario

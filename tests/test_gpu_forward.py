@@ -6,20 +6,25 @@ against the oracle except attention (fp32-accurate, not bit-identical), so:
   * a 1-layer model gives the same tokens and logits within 2e-3 sigma (most
     rows bit-identical; a rare int8 activation-code flip moves the rest);
   * the full 28-layer model drifts by such code flips, amplified layer by
-    layer: logits must stay within rms <= RMS_TOL * sigma and
-    corr >= CORR_MIN of the oracle's (sigma = the oracle row's logit std).
-    RMS_TOL is set just above the measured spread between the oracle's own
-    a8 contract and its f32 reference path on this workload (0.05-0.21 sigma
-    per row, corr >= 0.978): int8 activations turn any ulp-level difference
-    into discrete code flips that compound through 28 layers;
-  * greedy decode is checked teacher-forced for 64 steps (both sides fed the
-    oracle's token): every step's logits must meet the bounds above (plus
-    max |dlogit| <= MAX_TOL * sigma), and the device argmax must agree with
-    the oracle's on at least MIN_AGREE of the 320 row-steps.  A disagreement
-    can only happen where the oracle's top-2 margin is below the two logits'
-    error difference, which the bounds already limit; the count is reported.
+    layer: logits must stay within rms <= RMS_TOL * sigma, max <= MAX_TOL *
+    sigma and corr >= CORR_MIN of the oracle's (sigma = the oracle row's
+    logit std), bounds set just above the spread measured between the device
+    and the oracle on this workload;
+  * greedy decode runs 64 steps free-running, each side feeding its own
+    argmax (the reference's token KATs, scripts/gates/test_cpu_parity.sh:
+    53-63).  A sequence's streams must stay identical until a step where the
+    two argmaxes differ, and every such divergence must be a documented tie:
+    the oracle's margin between its token and the device's token is below
+    TIE_TOL * sigma.  A divergence with a larger margin fails the test.  The
+    same 64 steps then run teacher-forced (both sides fed the oracle's
+    token), so every step compares the same distribution: each disagreement
+    there must be a tie by the same rule, and the agreement rate is reported.
+  Measured figures are printed, and written as JSON to $IFR_PARITY_OUT when
+  that directory is set.
 """
 import ctypes as C
+import json
+import os
 
 import numpy as np
 import pytest
@@ -31,10 +36,15 @@ from tests.conftest import announce
 
 pytestmark = pytest.mark.gpu
 
-RMS_TOL = 0.25
-CORR_MIN = 0.97
-MAX_TOL = 1.5
-MIN_AGREE = 0.70
+# measured on this workload (fp16 / int8 KV): logit rms 0.175 / 0.200 sigma
+# at worst, max |dlogit| 0.92 / 0.94 sigma, corr >= 0.985 / 0.980
+RMS_TOL = 0.22
+CORR_MIN = 0.975
+MAX_TOL = 1.0
+# a divergence of the greedy streams is a tie when the oracle's margin
+# between its token and the device's is below this many sigma (measured
+# margins at divergences: at most 0.50 sigma)
+TIE_TOL = 0.6
 
 
 @pytest.fixture(scope="module")
@@ -161,6 +171,24 @@ def test_intfer_file_load_one_layer(dev, tmp_path):
         m.close()
 
 
+def _row_err(lg, lo):
+    """(rms / sigma, max / sigma, corr) of one logit row against the oracle's."""
+    sd = float(lo.std())
+    d = lg.astype(np.float64) - lo
+    return (float(np.sqrt((d * d).mean())) / sd, float(np.abs(d).max()) / sd,
+            float(np.corrcoef(lg, lo)[0, 1]))
+
+
+def _tie(lg, lo, t_e, t_o):
+    """The divergence record of one row where the device chose t_e and the
+    oracle t_o: the oracle's margin lo[t_o] - lo[t_e] and the device's
+    lg[t_e] - lg[t_o], with the two tokens' logit errors, all in sigma."""
+    sd = float(lo.std())
+    return {"oracle_margin": float(lo[t_o] - lo[t_e]) / sd, "device_margin": float(lg[t_e] - lg[t_o]) / sd,
+            "err_dev_token": float(lg[t_e] - lo[t_e]) / sd, "err_oracle_token": float(lg[t_o] - lo[t_o]) / sd,
+            "token_device": int(t_e), "token_oracle": int(t_o)}
+
+
 @pytest.mark.parametrize("kv_int8", [0, 1])
 def test_cfg1_mixed_iteration_and_greedy64(dev, model, kv_int8):
     w, eng, ora, dec_e, dec_o, pe, pq = _setup(dev, model, kv_int8)
@@ -173,29 +201,78 @@ def test_cfg1_mixed_iteration_and_greedy64(dev, model, kv_int8):
     assert len(want) == 5
     stats = []
     _check_logits(lg, lo, "cfg1", stats)
-    ties = sum(1 for i in want if be[i] != bo[i])
-    # 64 teacher-forced greedy steps for the 5 sequences: both sides are fed
-    # the oracle's token, so every step compares the same distribution.
+    rec = {"kv_int8": kv_int8, "cfg1_tokens_equal": int(sum(be[i] == bo[i] for i in want)),
+           "cfg1_row_err": [_row_err(lg[j], lo[j]) for j in range(5)], "ties": []}
+    for j, i in enumerate(want):
+        if be[i] != bo[i]:
+            rec["ties"].append({"phase": "cfg1", "step": -1, "seq": j, **_tie(lg[j], lo[j], be[i], bo[i])})
     seq_e, seq_o = dec_e + [pe], dec_o + [pq]
-    pos = [n + 1 for n in w.contexts] + [len(w.pre_tokens)]
-    tok = [int(bo[i]) for i in want]
-    stream, agree = [list(tok)], 0
+    pos0 = [n + 1 for n in w.contexts] + [len(w.pre_tokens)]
+    tok_e0 = [int(be[i]) for i in want]
+    tok_o0 = [int(bo[i]) for i in want]
+    errs = []
+    # (1) free-running: each side feeds its own argmax; a sequence is compared
+    # while its two streams are identical, and its first divergence must be a tie
+    synced = [a == b for a, b in zip(tok_e0, tok_o0)]
+    matched = [0 if not s else 64 for s in synced]
+    tok_e, tok_o, pos = list(tok_e0), list(tok_o0), list(pos0)
     for step in range(64):
-        announce(f"cfg1 greedy step {step} kv_int8={kv_int8}")
-        be2, lg2 = eng.forward([(s, p, t, 0, 1) for s, p, t in zip(seq_e, pos, tok)], logits=True)
-        bo2, lo2 = ora.forward([(s, p, t, 0, 1) for s, p, t in zip(seq_o, pos, tok)], logits=True)
-        _check_logits(lg2, lo2, f"step {step}", stats)
+        announce(f"cfg1 free-running step {step} kv_int8={kv_int8}")
+        b_e, l_e = eng.forward([(s, p, t, 0, 1) for s, p, t in zip(seq_e, pos, tok_e)], logits=True)
+        b_o, l_o = ora.forward([(s, p, t, 0, 1) for s, p, t in zip(seq_o, pos, tok_o)], logits=True)
         for j in range(5):
-            if be2[j] == bo2[j]:
+            if not synced[j]:
+                continue
+            errs.append(_row_err(l_e[j], l_o[j]))
+            _check_logits(l_e[j:j + 1], l_o[j:j + 1], f"free step {step} seq {j}", stats)
+            if b_e[j] != b_o[j]:
+                rec["ties"].append({"phase": "free", "step": step, "seq": j,
+                                    **_tie(l_e[j], l_o[j], b_e[j], b_o[j])})
+                synced[j] = False
+                matched[j] = step
+        tok_e, tok_o = [int(x) for x in b_e], [int(x) for x in b_o]
+        pos = [p + 1 for p in pos]
+    rec["free_steps_identical"] = matched
+    # (2) the same 64 steps teacher-forced from the cfg1 iteration's state
+    for s, n in zip(seq_e, pos0):
+        eng.seq_truncate(s, n)
+    for s, n in zip(seq_o, pos0):
+        ora.seq_truncate(s, n)
+    tok, pos, agree, stream = list(tok_o0), list(pos0), 0, [list(tok_o0)]
+    for step in range(64):
+        announce(f"cfg1 teacher-forced step {step} kv_int8={kv_int8}")
+        b_e, l_e = eng.forward([(s, p, t, 0, 1) for s, p, t in zip(seq_e, pos, tok)], logits=True)
+        b_o, l_o = ora.forward([(s, p, t, 0, 1) for s, p, t in zip(seq_o, pos, tok)], logits=True)
+        _check_logits(l_e, l_o, f"teacher-forced step {step}", stats)
+        for j in range(5):
+            errs.append(_row_err(l_e[j], l_o[j]))
+            if b_e[j] == b_o[j]:
                 agree += 1
             else:
-                ties += 1
-        tok = [int(x) for x in bo2]
+                rec["ties"].append({"phase": "forced", "step": step, "seq": j,
+                                    **_tie(l_e[j], l_o[j], b_e[j], b_o[j])})
+        tok = [int(x) for x in b_o]
         stream.append(tok)
         pos = [p + 1 for p in pos]
-    print(f"[cfg1 kv_int8={kv_int8}] greedy argmax agreement {agree}/320, disagreements {ties}, "
-          f"logit rms/sigma mean {np.mean(stats):.4f} max {np.max(stats):.4f}")
-    assert agree >= MIN_AGREE * 320
+    e = np.array(errs)
+    rec.update({"forced_agree": agree, "forced_rows": 320,
+                "rms_sigma_mean": float(e[:, 0].mean()), "rms_sigma_max": float(e[:, 0].max()),
+                "max_sigma_max": float(e[:, 1].max()), "corr_min": float(e[:, 2].min())})
+    print(f"[cfg1 kv_int8={kv_int8}] free-running steps identical per sequence {matched}; "
+          f"teacher-forced argmax agreement {agree}/320; logit rms/sigma mean {rec['rms_sigma_mean']:.4f} "
+          f"max {rec['rms_sigma_max']:.4f}, max|d|/sigma {rec['max_sigma_max']:.4f}, corr min {rec['corr_min']:.5f}")
+    for t in rec["ties"]:
+        print(f"  tie {t['phase']} step {t['step']} seq {t['seq']}: oracle margin {t['oracle_margin']:.4f} sigma, "
+              f"device margin {t['device_margin']:.4f}, token errors {t['err_dev_token']:+.4f} / "
+              f"{t['err_oracle_token']:+.4f}")
+    out = os.environ.get("IFR_PARITY_OUT")
+    if out:
+        os.makedirs(out, exist_ok=True)
+        with open(os.path.join(out, f"parity_cfg1_kv{kv_int8}.json"), "w") as f:
+            json.dump(rec, f, indent=1)
+    # every divergence, free-running or forced, is a documented near-tie
+    for t in rec["ties"]:
+        assert 0 <= t["oracle_margin"] < TIE_TOL, t
     # a non-degenerate stream: the model does not just repeat a few tokens
     assert len(set(np.array(stream).reshape(-1).tolist())) > 20
 
@@ -289,3 +366,18 @@ def test_spec_verify_rows_keep_greedy_stream(dev, model):
         out.append([sch.result(i)[0] for i in ids])
         sch.close()
     assert out[0] == out[1]
+
+
+def test_model_load_declines_shapes_the_kernels_cannot_run(dev):
+    """ifr_model_load checks every per-kernel shape limit up front: a model
+    whose attention row (n_heads * head_dim = 10240) exceeds the combine
+    kernel's 8192 is declined at load, not part-way through a forward."""
+    cfg = ia.default_cfg(layers=1, n_heads=80, n_kv=10, inter=384, vocab=512)
+    m = ia.SynthModel(cfg, seed=1, bits=2)
+    try:
+        announce("model load declines n_heads * head_dim > 8192")
+        with pytest.raises(ia.IfrError) as e:
+            ia.Engine(dev, m, max_seqs=2, max_seq_tokens=64, max_rows=16)
+        assert e.value.code == ia.IFR_EDECLINE
+    finally:
+        m.close()

@@ -2,7 +2,9 @@
 (one launch where the GEMM's launch shape holds one head per workgroup)
 against the two separate passes (ifr_kv_cfg.separate_qk = 1), on the 0.8B
 shape: the logits of a 300-row prefill and of the decode steps after it are
-bit-identical, with fp16 and with int8 KV."""
+bit-identical, with fp16 and with int8 KV.  A model without q/k norm
+weights (qk_norm = 0) runs the epilogue without the norm, bit-identical to
+the separate pass (regression: the epilogue once read the absent weights)."""
 import numpy as np
 import pytest
 
@@ -12,16 +14,16 @@ from tests.conftest import announce
 pytestmark = pytest.mark.gpu
 
 
-@pytest.mark.parametrize("kv8", [0, 1])
-def test_fused_qk_epilogue_bit_identical(dev, kv8):
-    cfg = ia.default_cfg(layers=2)
+@pytest.mark.parametrize("kv8,qkn", [(0, 1), (1, 1), (0, 0)])
+def test_fused_qk_epilogue_bit_identical(dev, kv8, qkn):
+    cfg = ia.default_cfg(layers=2, qk_norm=qkn)
     m = ia.SynthModel(cfg, seed=17, bits=2)
     try:
         rng = np.random.default_rng(31)
         prompt = rng.integers(0, cfg.vocab, size=300).tolist()
         outs = []
         for sep in (0, 1):
-            announce(f"fused q/k epilogue kv_int8={kv8} separate={sep}: 300-row prefill + 2 decode steps")
+            announce(f"fused q/k epilogue kv_int8={kv8} qk_norm={qkn} separate={sep}: 300-row prefill + 2 decode steps")
             eng = ia.Engine(dev, m, max_seqs=4, max_seq_tokens=1024, pool_tokens=4 * 1024, kv_int8=kv8,
                             max_rows=320, separate_qk=sep)
             s = eng.seq_open()
