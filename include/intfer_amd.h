@@ -292,6 +292,23 @@ int ifr_forward(ifr_ctx* ctx, const ifr_row* rows, int32_t M, int32_t* best_out,
 int ifr_attention(ifr_ctx* ctx, int32_t layer, const ifr_row* rows, int32_t M,
                   const uint16_t* q_h, float* out_h);
 
+/* No counterpart in the reference.  For callers that cannot allocate device
+ * memory (code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc): ifr_attention with device buffers q_d (fp16 bits
+ * [M][n_heads][head_dim]) and out_d (fp32 [M][n_heads*head_dim]), and every
+ * intermediate (row maps, attention units, split-KV partials, the combine's
+ * int8 codes) in a fixed per-GPU device array of the library (about 37 MB,
+ * held by each GPU the library runs on until the process ends).  The call
+ * makes no hipMalloc / hipFree.  Limits: M <= 512 rows, n_heads * head_dim <=
+ * 8192, and at most 4096 attention units (one per q-block of 16 / GQA-group
+ * tokens, kv head and 256-token KV split); beyond them it returns IFR_EINVAL
+ * with a message and does nothing.  Results are bit-identical to
+ * ifr_attention's.  Every call on one GPU shares that array: calls that
+ * overlap on one GPU (other threads or contexts) race.  Returns after out_d
+ * is written. */
+int ifr_attention_noalloc(ifr_ctx* ctx, int32_t layer, const ifr_row* rows, int32_t M,
+                          const uint16_t* q_d, float* out_d);
+
 /* Per-kernel device timing of ifr_forward calls since ifr_set_timing(ctx, 1)
  * (HIP events on the launching stream; while it is on, every forward runs
  * on one stream so each kernel is timed alone), for the bench.  Names:

@@ -156,6 +156,7 @@ _PROTOS = {
     "ifr_seq_load_kv": (C.c_int, [P, i32, i32, pf32, pf32]),
     "ifr_forward": (C.c_int, [P, C.POINTER(Row), i32, pi32, pf32]),
     "ifr_attention": (C.c_int, [P, i32, C.POINTER(Row), i32, P, pf32]),
+    "ifr_attention_noalloc": (C.c_int, [P, i32, C.POINTER(Row), i32, P, P]),
     "ifr_set_timing": (C.c_int, [P, i32]),
     "ifr_get_timing": (C.c_int, [P, C.c_char_p, C.POINTER(C.c_double), C.POINTER(i64),
                                  C.POINTER(C.c_double), C.POINTER(C.c_double)]),

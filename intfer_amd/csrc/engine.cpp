@@ -56,6 +56,26 @@ constexpr int kPage = 32;
 constexpr int kSplit = 256;  // default KV tokens per attention unit
 constexpr int kAttnTiles = 1;  // 16-column MFMA tiles per attention unit (q-block = 16 / G tokens)
 
+// ---- the no-allocation attention entry point's scratch (ifr_attention_noalloc)
+// Limits of one call: rows, attention units (one per (q-block, kv head,
+// 256-token KV split)) and the attention row width n_heads * head_dim.
+constexpr int kNaRows = 512;
+constexpr int kNaUnits = 4096;
+constexpr int kNaRowWidth = 8192;
+constexpr size_t na_align(size_t x) { return (x + 255) & ~(size_t)255; }
+// byte offsets of each region inside the array
+constexpr size_t kNaRowsOff = 0;                                                    // ifr_row[kNaRows]
+constexpr size_t kNaMapsOff = na_align(kNaRowsOff + (size_t)kNaRows * 5 * 4);      // 9 int32 maps
+constexpr size_t kNaMapLen = na_align((size_t)(kNaRows + 1) * 4);
+constexpr size_t kNaUnitsOff = kNaMapsOff + 9 * kNaMapLen;                          // AttnUnit[kNaUnits]
+constexpr size_t kNaOrderOff = na_align(kNaUnitsOff + (size_t)kNaUnits * 32);      // int32[4 * kNaUnits]
+constexpr size_t kNaPartOOff = na_align(kNaOrderOff + (size_t)kNaUnits * 4 * 4);   // fp32 partial O
+constexpr size_t kNaPartMLOff = na_align(kNaPartOOff + (size_t)kNaUnits * 16 * kAttnTiles * 128 * 4);
+constexpr size_t kNaAqOff = na_align(kNaPartMLOff + (size_t)kNaUnits * 16 * kAttnTiles * 2 * 4);
+constexpr size_t kNaAsOff = na_align(kNaAqOff + (size_t)kNaRows * kNaRowWidth);    // combine's int8 codes
+constexpr size_t kNaGsOff = na_align(kNaAsOff + (size_t)kNaRows * 4);
+constexpr size_t kNaScratchBytes = na_align(kNaGsOff + (size_t)kNaRows * (kNaRowWidth / 128) * 4);
+
 struct Layer {
   DLin qkv[3];     // fused QKV in qkv[0] when all widths match (nqkv = 1)
   int nqkv = 1;
@@ -117,6 +137,11 @@ struct Lane {
 
 }  // namespace
 
+// Device memory of ifr_attention_noalloc: one copy per GPU, held until the
+// process ends.  Host code uses the address hipGetSymbolAddress gives for the
+// current device (ifr_ctx::scratch), never this name.
+static __device__ __align__(256) uint8_t scratch[kNaScratchBytes];
+
 struct ifr_dlinear {
   DLin d;
 };
@@ -159,6 +184,7 @@ struct ifr_ctx {
   // last forward's split (for tests / bench notes)
   int last_split = 0, last_units = 0;
   int qb = 8;  // q-block tokens per attention unit: 16 MFMA columns / GQA group
+  uint8_t* scratch = nullptr;  // this device's copy of `scratch` (resolved at ifr_ctx_create)
 
   void* dalloc(size_t bytes) {
     void* p = nullptr;
@@ -649,6 +675,17 @@ int ifr_ctx_create(int32_t device, ifr_ctx** out) {
     return fail(IFR_EDEVICE, "hipStreamCreate (lane 1)");
   }
   c->lane[0].st = c->st;
+  // the device's copy of the no-allocation scratch array, with the device current
+  void* sp = nullptr;
+  const hipError_t es = hipGetSymbolAddress(&sp, HIP_SYMBOL(scratch));
+  if (es != hipSuccess || !sp) {
+    hipEventDestroy(c->ev_bt);
+    hipStreamDestroy(c->lane[1].st);
+    hipStreamDestroy(c->st);
+    delete c;
+    return fail(IFR_EDEVICE, "hipGetSymbolAddress(scratch): %s", hipGetErrorString(es));
+  }
+  c->scratch = static_cast<uint8_t*>(sp);
   *out = c;
   return IFR_OK;
 }
@@ -1391,6 +1428,63 @@ int ifr_attention(ifr_ctx* c, int32_t layer, const ifr_row* rows, int32_t M, con
   hipFree(out_d);
   HIPCHK(e);
   if (c->timing) flush_timers(c);
+  return IFR_OK;
+}
+
+int ifr_attention_noalloc(ifr_ctx* c, int32_t layer, const ifr_row* rows, int32_t M, const uint16_t* q_d,
+                          float* out_d) {
+  if (!c || !rows || !q_d || !out_d) return fail(IFR_EINVAL, "null arg");
+  if (!c->loaded) return fail(IFR_ESTATE, "no model loaded");
+  if (!c->scratch) return fail(IFR_ESTATE, "scratch address not resolved");
+  if (M <= 0 || M > kNaRows) return fail(IFR_EINVAL, "M=%d outside [1, %d] (no-allocation limit)", M, kNaRows);
+  if (layer < 0 || layer >= c->cfg.layers) return fail(IFR_EINVAL, "layer %d", layer);
+  const int nq = c->cfg.n_heads, nkv = c->cfg.n_kv, hd = c->cfg.head_dim;
+  if (nq * hd > kNaRowWidth) return fail(IFR_EINVAL, "n_heads * head_dim %d > %d", nq * hd, kNaRowWidth);
+  std::vector<int> g_len, g_pos0;
+  if (int r = attn_groups(c, rows, M, g_len, g_pos0)) return r;
+  // the engine's split, never widened here: a batch that needs more units
+  // than the scratch holds is refused instead
+  const int split = c->kv.attn_split > 0 ? c->kv.attn_split : kSplit;
+  const long nunits = count_units(g_pos0, g_len, nkv, split, c->qb);
+  long nchunked = 0;
+  const long nslots = ifrk::attn_slot_count(g_pos0.data(), g_len.data(), (int)g_len.size(), nkv, split, c->qb,
+                                            &nchunked);
+  if (nunits > kNaUnits || nslots > 4L * kNaUnits)
+    return fail(IFR_EINVAL, "%ld attention units (%ld slots) > %d (no-allocation limit)", nunits, nslots, kNaUnits);
+  HIPCHK(hipSetDevice(c->device));
+  uint8_t* S = c->scratch;
+  int32_t* rows_d = reinterpret_cast<int32_t*>(S + kNaRowsOff);
+  auto map = [&](int i) { return reinterpret_cast<int32_t*>(S + kNaMapsOff + (size_t)i * kNaMapLen); };
+  ifrk::PackOut pk{};
+  pk.cu_seqlens = map(0);
+  pk.row_grp = map(1);
+  pk.row_seq = map(2);
+  pk.row_pos = map(3);
+  pk.row_kind = map(4);
+  pk.comb_base = map(5);
+  pk.comb_nsplit = map(6);
+  pk.comb_tok = map(7);
+  pk.want_rows = map(8);
+  pk.units = reinterpret_cast<ifrk::AttnUnit*>(S + kNaUnitsOff);
+  pk.order = reinterpret_cast<int32_t*>(S + kNaOrderOff);
+  float* part_o = reinterpret_cast<float*>(S + kNaPartOOff);
+  float* part_ml = reinterpret_cast<float*>(S + kNaPartMLOff);
+  // every region is fully written by the kernel that produces it before it
+  // is read (the pack maps, each unit's partials, the combine outputs), so
+  // nothing is cleared between calls
+  HIPCHK(hipMemcpyAsync(rows_d, rows, (size_t)M * sizeof(ifr_row), hipMemcpyHostToDevice, c->st));
+  HIPCHK(ifrk::launch_pack(rows_d, M, nkv, c->qb, split, pk, c->st));
+  ifrk::KVLayout kv{nkv, hd, kPage, c->max_pages, c->kv.kv_int8, c->kpool[layer], c->vpool[layer],
+                    c->kscale[layer], c->vscale[layer], c->bt_d};
+  ifrk::AttnArgs a{pk.units, (int)nunits, pk.order, (int)nslots, c->kv.kv_int8 ? 0 : (int)nchunked, q_d, nq,
+                   1.4426950408889634f / std::sqrt((float)hd), part_o, part_ml, kAttnTiles};
+  HIPCHK(ifrk::launch_attention(a, kv, c->st));
+  ifrk::CombineArgs cb{part_o, part_ml, pk.comb_base, pk.comb_nsplit, pk.comb_tok, M, nq, nkv, hd, out_d,
+                       reinterpret_cast<int8_t*>(S + kNaAqOff), reinterpret_cast<float*>(S + kNaAsOff),
+                       reinterpret_cast<float*>(S + kNaGsOff), 16 * kAttnTiles};
+  HIPCHK(ifrk::launch_combine(cb, c->st));
+  // the rows copy read the caller's host array; return once out_d is written
+  HIPCHK(hipStreamSynchronize(c->st));
   return IFR_OK;
 }
 

@@ -26,6 +26,8 @@
 #define __launch_bounds__(...)
 #define __restrict__ __restrict
 #define __shared__ static
+#define __align__(n) __attribute__((aligned(n)))
+#define HIP_SYMBOL(x) (&(x))
 
 typedef int hipError_t;
 enum {
@@ -274,4 +276,9 @@ hipError_t hipEventElapsedTime(float* ms, hipEvent_t a, hipEvent_t b);
 hipError_t hipFuncSetAttribute(const void* f, hipFuncAttribute a, int v);
 hipError_t hipGetLastError();
 hipError_t hipPeekAtLastError();
+// a file-scope device array is ordinary host memory here: its address is itself
+inline hipError_t hipGetSymbolAddress(void** p, const void* sym) {
+  *p = const_cast<void*>(sym);
+  return hipSuccess;
+}
 const char* hipGetErrorString(hipError_t e);
