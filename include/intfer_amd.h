@@ -242,6 +242,9 @@ typedef struct ifr_kv_cfg {
  * afterwards. */
 int ifr_model_load(ifr_ctx* ctx, const ifr_host_model* m, const ifr_kv_cfg* kv);
 
+/* No reference counterpart: the configuration of the loaded model. */
+int ifr_model_info(ifr_ctx* ctx, ifr_model_cfg* out);
+
 /* Sequence slots over the paged KV pool.  truncate = speculative rollback
  * (main.cpp:11896-11915) and prefix reuse: KV beyond len is dropped. */
 int ifr_seq_open(ifr_ctx* ctx, int32_t* slot);
@@ -272,14 +275,16 @@ typedef struct ifr_row {
   int32_t pos;   /* absolute position of this row's token */
   int32_t token; /* input token id */
   int32_t kind;  /* IFR_ROW_* */
-  int32_t want;  /* 1: score this row (argmax, optional logits) */
+  int32_t want;  /* 0: not scored; 1: scored (argmax); 2: scored, and its
+                  * logits returned (rows the caller samples from) */
 } ifr_row;
 
 /* One mixed iteration (replaces step_batch main.cpp:7519-8320 and the
  * LinearBackend calls it makes).  best_out[M]: argmax (first max wins) for
- * rows with want=1, -1 otherwise.  logits_out, if non-NULL, receives fp32
- * [n_want][vocab] logits of the scored rows in row order.  The call appends
- * every row's K/V to its sequence. */
+ * scored rows (want >= 1), -1 otherwise.  logits_out, if non-NULL, receives
+ * fp32 [n][vocab] logits in row order: of the rows with want = 2 when there
+ * are any, else of every scored row.  The call appends every row's K/V to
+ * its sequence. */
 int ifr_forward(ifr_ctx* ctx, const ifr_row* rows, int32_t M, int32_t* best_out,
                 float* logits_out);
 
@@ -468,6 +473,9 @@ typedef struct ifr_sched_cfg {
                          * (LRU); an admitted prompt sharing a prefix with a
                          * cached stream copies that KV and prefills only the
                          * rest.  Token streams are unchanged. */
+  uint32_t seed;        /* base seed of the requests' samplers: a request
+                         * without its own seed draws from mt19937(seed + id)
+                         * (run_serve admission, main.cpp:9305) */
 } ifr_sched_cfg;
 
 int ifr_sched_create(ifr_ctx* ctx, const ifr_sched_cfg* cfg, ifr_sched** out);
@@ -485,6 +493,11 @@ typedef struct ifr_sched_backend {
   int32_t kv_capacity;
   /* ifr_seq_copy_prefix; may be NULL (no prefix cache) */
   int (*seq_copy_prefix)(void* user, int32_t dst, int32_t src, int32_t len);
+  /* the forward that also returns the logits of the rows with want = 2
+   * (ifr_forward's logits_out), [n][vocab] in row order; may be NULL (then
+   * only greedy requests are accepted) */
+  int (*forward_logits)(void* user, const ifr_row* rows, int32_t M, int32_t* best, float* logits);
+  int32_t vocab;
 } ifr_sched_backend;
 int ifr_sched_create_backend(const ifr_sched_backend* be, const ifr_sched_cfg* cfg,
                              ifr_sched** out);
@@ -492,6 +505,43 @@ int ifr_sched_destroy(ifr_sched* s);
 /* Admit a request (prompt token ids, max_new).  Returns its id. */
 int ifr_sched_submit(ifr_sched* s, const int32_t* prompt, int32_t n, int32_t max_new,
                      int64_t* id);
+
+/* Per-request sampling (Request::temperature / top_k / top_p / rng,
+ * main.cpp:4812-4815).  A request is greedy when temperature <= 0, top_k
+ * == 0 and top_p <= 0 (main.cpp:8401, :8505): its decode tokens are the
+ * device argmax.  Otherwise each decode row's token is ifr_sample over the
+ * row's logits with the request's own mt19937, seeded with `seed` when
+ * has_seed, else with the scheduler's seed + the request id
+ * (main.cpp:9305).  The token that completes a prompt is the argmax in
+ * either case (main.cpp:8522-8523, :8366), and a sampling request gets no
+ * n-gram verify rows (their acceptance is greedy, main.cpp:11869-11883). */
+typedef struct ifr_sample_params {
+  float temperature;
+  int32_t top_k;
+  float top_p;
+  uint32_t seed;
+  int32_t has_seed;
+} ifr_sample_params;
+/* ifr_sched_submit with sampling parameters (NULL: greedy).  IFR_EDECLINE
+ * for a sampling request when the backend has no forward_logits. */
+int ifr_sched_submit_sampled(ifr_sched* s, const int32_t* prompt, int32_t n, int32_t max_new,
+                             const ifr_sample_params* sp, int64_t* id);
+
+/* The sampler itself (sample, main.cpp:8674-8764), for one row of logits:
+ * temperature <= 0 is read as 1e-5; p = softmax((l - max) / T) with a
+ * sequential sum; top_k > 0 keeps the p >= the k-th largest and
+ * renormalises; 0 < top_p < 1 keeps the shortest most-probable prefix
+ * whose sum reaches top_p and renormalises; the token is the first whose
+ * running sum reaches r = U[0,1) (std::uniform_real_distribution<float> of
+ * the mt19937: float(x) * 2^-32 below 1), else the last.  ifr_rng is the
+ * request's std::mt19937 (the C++ standard's engine, seeded with `seed`). */
+typedef struct ifr_rng ifr_rng;
+int ifr_rng_create(uint32_t seed, ifr_rng** out);
+void ifr_rng_free(ifr_rng* r);
+/* The next U[0,1) draw of the generator (the sampler's r). */
+int ifr_rng_uniform(ifr_rng* r, float* u);
+int ifr_sample(const float* logits, int32_t vocab, int32_t top_k, float top_p, float temperature,
+               ifr_rng* rng, int32_t* token);
 /* Run one serve iteration (serve_iteration, main.cpp:9203-9259).  Returns
  * the number of rows in the forward(s) it ran, 0 when idle. */
 int ifr_sched_step(ifr_sched* s, int32_t* rows_run);
@@ -525,12 +575,15 @@ int ifr_sched_info(ifr_sched* s, int32_t* live, int32_t* prefill, int32_t* pendi
 
 /* The --serve JSON-lines loop (run_serve, main.cpp:9260-9377), over file
  * descriptors.  Each input line is one request,
- *   {"prompt_ids":[t0,t1,...], "max_new":N, "id":K}
+ *   {"prompt_ids":[t0,t1,...], "max_new":N, "id":K,
+ *    "temperature":T, "top_k":K, "top_p":P, "seed":S}
  * (max_new defaults to cfg->default_max_new and is clamped to [1, 4096]; a
- * missing id takes the next free one, main.cpp:9329-9342).  Token ids stand
- * in for the reference's "prompt" text: this build has no tokenizer, so a
- * line with only "prompt" is answered with an error, as are sampling keys
- * asking for more than greedy decoding.  Output lines, flushed per
+ * missing id takes the next free one, main.cpp:9329-9342; the sampling keys
+ * default to cfg's, top_k is clamped to >= 0 and top_p to [0, 1], and a
+ * seed makes the request's sampler independent of its id,
+ * parse_serve_line main.cpp:8646-8668).  Token ids stand in for the
+ * reference's "prompt" text: this build has no tokenizer, so a line with
+ * only "prompt" is answered with an error.  Output lines, flushed per
  * iteration: {"id":K,"token":T} per streamed token, {"id":K,"done":true,
  * "generated":n} when a request finishes, {"error":"..."} (with "id" when
  * known) for a line that is refused.  Input is polled between iterations
@@ -540,6 +593,11 @@ int ifr_sched_info(ifr_sched* s, int32_t* live, int32_t* prefill, int32_t* pendi
 typedef struct ifr_serve_cfg {
   int32_t default_max_new; /* 0: 64 (ServeOpts, main.cpp:8563-8568) */
   int32_t vocab;           /* token ids must be below it (0: checked by the forward) */
+  /* defaults of the sampling keys (the CLI's -t / -k / -T, main.cpp:10555-10557) */
+  float temperature;
+  int32_t top_k;
+  float top_p;
+  uint32_t seed;           /* a line without "seed" samples from mt19937(seed + its id) (-S) */
 } ifr_serve_cfg;
 int ifr_serve(ifr_sched* s, int32_t in_fd, int32_t out_fd, const ifr_serve_cfg* cfg);
 

@@ -18,7 +18,7 @@ from ._abi import (KVCfg, Linear, ModelCfg, Row, SchedBackend, SchedCfg, ROW_DEC
                    ROW_VERIFY, IFR_OK, IFR_EDECLINE, IFR_EINVAL, IFR_ENOMEM, IFR_EDEVICE, IFR_ESTATE,
                    IfrError, check, lib)
 
-__all__ = ["Device", "Engine", "Scheduler", "SynthModel", "HostModelHandle", "IntferFile", "default_cfg", "make_linear", "rows_array",
+__all__ = ["Device", "Engine", "Scheduler", "Rng", "sample", "SynthModel", "HostModelHandle", "IntferFile", "default_cfg", "make_linear", "rows_array",
            "atile", "untile",
            "ROW_DECODE", "ROW_PREFILL", "ROW_VERIFY", "IfrError", "ModelCfg", "KVCfg", "SchedCfg",
            "Row", "Linear", "lib"]
@@ -361,7 +361,9 @@ class Engine:
         arr = rows if isinstance(rows, C.Array) else rows_array(rows)
         M = len(arr)
         best = np.full(M, -1, dtype=np.int32)
-        nwant = sum(1 for r in arr if r.want)
+        # logits of the want = 2 rows when there are any, else of every scored row
+        n2 = sum(1 for r in arr if r.want == 2)
+        nwant = n2 if n2 else sum(1 for r in arr if r.want)
         lg = np.empty((nwant, self.cfg.vocab), dtype=np.float32) if logits else None
         check(lib().ifr_forward(self.dev.ctx, arr, M, best.ctypes.data_as(_abi.pi32),
                                 lg.ctypes.data_as(_abi.pf32) if logits else None), "ifr_forward")
@@ -394,11 +396,11 @@ class Scheduler:
 
     def __init__(self, engine: Engine | None = None, chunk_m=128, live_cap=64, split_iter=0,
                  round_robin=1, spec_k=0, backend: SchedBackend | None = None, pack_prefill=0,
-                 prefix_cache=0):
+                 prefix_cache=0, seed=0):
         cfg = SchedCfg()
         cfg.chunk_m, cfg.live_cap, cfg.split_iter = chunk_m, live_cap, split_iter
         cfg.round_robin, cfg.spec_k, cfg.pack_prefill = round_robin, spec_k, pack_prefill
-        cfg.prefix_cache = prefix_cache
+        cfg.prefix_cache, cfg.seed = prefix_cache, seed & 0xFFFFFFFF
         self.h = C.c_void_p()
         self._keep = backend
         if backend is not None:
@@ -408,11 +410,15 @@ class Scheduler:
             check(lib().ifr_sched_create(engine.dev.ctx, C.byref(cfg), C.byref(self.h)),
                   "ifr_sched_create")
 
-    def submit(self, prompt: Sequence[int], max_new: int) -> int:
+    def submit(self, prompt: Sequence[int], max_new: int, temperature: float = 0.0, top_k: int = 0,
+               top_p: float = 0.0, seed: int | None = None) -> int:
+        """Queue a request; greedy unless a sampling parameter is set."""
         p = np.ascontiguousarray(prompt, dtype=np.int32)
         rid = C.c_int64()
-        check(lib().ifr_sched_submit(self.h, p.ctypes.data_as(_abi.pi32), len(p), max_new,
-                                     C.byref(rid)), "ifr_sched_submit")
+        sp = _abi.SampleParams(temperature, top_k, top_p, 0 if seed is None else seed & 0xFFFFFFFF,
+                               0 if seed is None else 1)
+        check(lib().ifr_sched_submit_sampled(self.h, p.ctypes.data_as(_abi.pi32), len(p), max_new,
+                                             C.byref(sp), C.byref(rid)), "ifr_sched_submit_sampled")
         return rid.value
 
     def step(self) -> int:
@@ -442,7 +448,8 @@ class Scheduler:
         check(lib().ifr_sched_info(self.h, *[C.byref(x) for x in v]), "ifr_sched_info")
         return tuple(x.value for x in v)
 
-    def serve(self, lines, vocab: int = 0, default_max_new: int = 64):
+    def serve(self, lines, vocab: int = 0, default_max_new: int = 64, temperature: float = 0.0,
+              top_k: int = 0, top_p: float = 0.0, seed: int = 0):
         """Run the JSON-lines serve loop (ifr_serve) over pipes on `lines`
         (one request per string); returns (output events as dicts, status)."""
         import json
@@ -450,7 +457,7 @@ class Scheduler:
         import threading
         rin, win = os.pipe()
         rout, wout = os.pipe()
-        cfg = _abi.ServeCfg(default_max_new, vocab)
+        cfg = _abi.ServeCfg(default_max_new, vocab, temperature, top_k, top_p, seed & 0xFFFFFFFF)
         res = {}
 
         def run():
@@ -477,3 +484,36 @@ class Scheduler:
         if self.h:
             lib().ifr_sched_destroy(self.h)
             self.h = C.c_void_p()
+
+
+class Rng:
+    """A request's sampler state: the library's std::mt19937 (ifr_rng)."""
+
+    def __init__(self, seed: int):
+        self.h = C.c_void_p()
+        check(lib().ifr_rng_create(seed & 0xFFFFFFFF, C.byref(self.h)), "ifr_rng_create")
+
+    def uniform(self) -> float:
+        u = C.c_float()
+        check(lib().ifr_rng_uniform(self.h, C.byref(u)), "ifr_rng_uniform")
+        return u.value
+
+    def close(self):
+        if self.h:
+            lib().ifr_rng_free(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+def sample(logits: np.ndarray, rng: Rng, temperature: float = 0.0, top_k: int = 0, top_p: float = 0.0) -> int:
+    """ifr_sample over one row of logits (the reference's sample())."""
+    lg = np.ascontiguousarray(logits, dtype=np.float32)
+    t = C.c_int32()
+    check(lib().ifr_sample(lg.ctypes.data_as(_abi.pf32), lg.size, top_k, top_p, temperature, rng.h,
+                           C.byref(t)), "ifr_sample")
+    return t.value

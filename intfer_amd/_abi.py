@@ -77,7 +77,7 @@ class Row(C.Structure):
 class SchedCfg(C.Structure):
     _fields_ = [("chunk_m", C.c_int32), ("live_cap", C.c_int32), ("split_iter", C.c_int32),
                 ("round_robin", C.c_int32), ("spec_k", C.c_int32), ("pack_prefill", C.c_int32),
-                ("prefix_cache", C.c_int32)]
+                ("prefix_cache", C.c_int32), ("seed", C.c_uint32)]
 
 
 SEQ_OPEN = C.CFUNCTYPE(C.c_int, C.c_void_p, C.POINTER(C.c_int32))
@@ -85,6 +85,13 @@ SEQ_CLOSE = C.CFUNCTYPE(C.c_int, C.c_void_p, C.c_int32)
 SEQ_TRUNC = C.CFUNCTYPE(C.c_int, C.c_void_p, C.c_int32, C.c_int32)
 FORWARD = C.CFUNCTYPE(C.c_int, C.c_void_p, C.POINTER(Row), C.c_int32, C.POINTER(C.c_int32))
 SEQ_COPY = C.CFUNCTYPE(C.c_int, C.c_void_p, C.c_int32, C.c_int32, C.c_int32)
+FORWARD_LOGITS = C.CFUNCTYPE(C.c_int, C.c_void_p, C.POINTER(Row), C.c_int32, C.POINTER(C.c_int32),
+                             C.POINTER(C.c_float))
+
+
+class SampleParams(C.Structure):
+    _fields_ = [("temperature", C.c_float), ("top_k", C.c_int32), ("top_p", C.c_float),
+                ("seed", C.c_uint32), ("has_seed", C.c_int32)]
 
 
 class SchedEvent(C.Structure):
@@ -93,13 +100,14 @@ class SchedEvent(C.Structure):
 
 
 class ServeCfg(C.Structure):
-    _fields_ = [("default_max_new", C.c_int32), ("vocab", C.c_int32)]
+    _fields_ = [("default_max_new", C.c_int32), ("vocab", C.c_int32), ("temperature", C.c_float),
+                ("top_k", C.c_int32), ("top_p", C.c_float), ("seed", C.c_uint32)]
 
 
 class SchedBackend(C.Structure):
     _fields_ = [("user", C.c_void_p), ("seq_open", SEQ_OPEN), ("seq_close", SEQ_CLOSE),
                 ("seq_truncate", SEQ_TRUNC), ("forward", FORWARD), ("kv_capacity", C.c_int32),
-                ("seq_copy_prefix", SEQ_COPY)]
+                ("seq_copy_prefix", SEQ_COPY), ("forward_logits", FORWARD_LOGITS), ("vocab", C.c_int32)]
 
 
 P = C.c_void_p
@@ -148,6 +156,12 @@ _PROTOS = {
     "ifr_quant_gemm_variant": (C.c_int, [P, P, P, P, P, i32, P, i32]),
     "ifr_model_load": (C.c_int, [P, C.POINTER(HostModel), C.POINTER(KVCfg)]),
     "ifr_seq_open": (C.c_int, [P, pi32]),
+    "ifr_model_info": (C.c_int, [P, C.POINTER(ModelCfg)]),
+    "ifr_sched_submit_sampled": (C.c_int, [P, pi32, i32, i32, C.POINTER(SampleParams), C.POINTER(i64)]),
+    "ifr_rng_create": (C.c_int, [C.c_uint32, C.POINTER(P)]),
+    "ifr_rng_free": (None, [P]),
+    "ifr_rng_uniform": (C.c_int, [P, pf32]),
+    "ifr_sample": (C.c_int, [pf32, i32, i32, f32, f32, P, pi32]),
     "ifr_seq_close": (C.c_int, [P, i32]),
     "ifr_seq_truncate": (C.c_int, [P, i32, i32]),
     "ifr_seq_len": (C.c_int, [P, i32, pi32]),

@@ -28,7 +28,8 @@ SOURCES = [("qgemm.hip", [], "qgemm"),
            ("qgemm.hip", ["-DIFR_QGEMM_BITS=8"], "qgemm_b8"),
            ("rows.hip", [], "rows"), ("attn.hip", [], "attn"), ("lmhead.hip", [], "lmhead"),
            ("engine.cpp", [], "engine"), ("sched.cpp", [], "sched"), ("synth.cpp", [], "synth"),
-           ("intfer_file.cpp", [], "intfer_file"), ("serve.cpp", [], "serve")]
+           ("intfer_file.cpp", [], "intfer_file"), ("serve.cpp", [], "serve"),
+           ("sample.cpp", [], "sample")]
 SERVE_BIN = HERE / "intfer_serve"  # the --serve command line (serve_main.cpp)
 
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")

@@ -209,8 +209,10 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs p, KVLayout kv) {
           sv[2 * r + h] = v;
           mt = fmaxf(mt, v);
         }
-      mt = fmaxf(mt, __shfl_xor(mt, 16, 64));
-      mt = fmaxf(mt, __shfl_xor(mt, 32, 64));
+      // the 4 lane groups hold the page's other tokens: exchange through the
+      // gfx950 lane swaps (VALU), not the LDS crossbar; same partner values
+      mt = fmaxf(mt, ifrd::lane_xor<16>(mt));
+      mt = fmaxf(mt, ifrd::lane_xor<32>(mt));
       const float m_new = fmaxf(m_run[t], mt);
       const float m_use = (m_new == -INFINITY) ? 0.0f : m_new;
       alpha[t] = __builtin_amdgcn_exp2f(m_run[t] - m_use);
@@ -227,8 +229,8 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs p, KVLayout kv) {
         phi[t][j] = hh;
         plo[t][j] = (_Float16)(pv - (float)hh);
       }
-      rs += __shfl_xor(rs, 16, 64);
-      rs += __shfl_xor(rs, 32, 64);
+      rs += ifrd::lane_xor<16>(rs);
+      rs += ifrd::lane_xor<32>(rs);
       l_run[t] = l_run[t] * alpha[t] + rs;
       m_run[t] = m_new;
     }
@@ -339,9 +341,9 @@ __device__ __forceinline__ int group_sum_int(int v) {
   if constexpr (CS == 8) {
     return ifrd::row16_sum_int(v);
   } else {
-    v += __shfl_xor(v, 1, 64);
-    v += __shfl_xor(v, 2, 64);
-    if constexpr (CS == 16) v += __shfl_xor(v, 4, 64);
+    v += __builtin_bit_cast(int, ifrd::lane_xor<1>(__builtin_bit_cast(float, v)));
+    v += __builtin_bit_cast(int, ifrd::lane_xor<2>(__builtin_bit_cast(float, v)));
+    if constexpr (CS == 16) v += __builtin_bit_cast(int, ifrd::lane_xor<4>(__builtin_bit_cast(float, v)));
     return v;
   }
 }

@@ -410,6 +410,7 @@ struct SubBatch {
   int row0 = 0, M = 0;             // rows [row0, row0 + M) of the call
   std::vector<int> g_pos0, g_len;  // its sequence groups
   std::vector<int> want;           // scored rows (local indices, ascending)
+  std::vector<int> want_logits;    // positions in `want` of the rows with want = 2
   int split = 0, nslots = 0;
   long nunits = 0, nchunked = 0;
   double attn_bytes = 0, attn_flops = 0;
@@ -418,7 +419,10 @@ struct SubBatch {
 int prep_sub(ifr_ctx* c, const ifr_row* rows, SubBatch& sb) {
   const ifr_row* r = rows + sb.row0;
   for (int m = 0; m < sb.M; ++m)
-    if (r[m].want) sb.want.push_back(m);
+    if (r[m].want) {
+      if (r[m].want == 2) sb.want_logits.push_back((int)sb.want.size());
+      sb.want.push_back(m);
+    }
   const int nkv = c->cfg.n_kv;
   // fixed KV split: each row's partial decomposition depends only on its own
   // sequence (batch-invariant results: split == joint, solo == loaded)
@@ -586,8 +590,9 @@ int launch_layer(ifr_ctx* c, const SubBatch& sb, int l) {
 }
 
 // Final residual, norm, lm_head + argmax on the scored rows; the tokens (and
-// logits, into logits_out when given) come back on the lane's stream.
-int launch_tail(ifr_ctx* c, const SubBatch& sb, float* logits_out) {
+// logits, into logits_out when given: every scored row's, or with only_2 the
+// rows with want = 2) come back on the lane's stream.
+int launch_tail(ifr_ctx* c, const SubBatch& sb, float* logits_out, bool only_2) {
   const ifr_model_cfg& cf = c->cfg;
   Lane& L = c->lane[sb.lane];
   const int nwant = (int)sb.want.size();
@@ -637,9 +642,13 @@ int launch_tail(ifr_ctx* c, const SubBatch& sb, float* logits_out) {
     HIPCHK(ifrk::launch_lmhead(a, L.st));
   }
   HIPCHK(hipMemcpyAsync(L.best_h, L.best_d, nwant * sizeof(int32_t), hipMemcpyDeviceToHost, L.st));
-  if (logits_out)
+  if (logits_out && !only_2)
     HIPCHK(hipMemcpyAsync(logits_out, L.logits_d, (size_t)nwant * V * sizeof(float), hipMemcpyDeviceToHost,
                           L.st));
+  if (logits_out && only_2)
+    for (size_t j = 0; j < sb.want_logits.size(); ++j)
+      HIPCHK(hipMemcpyAsync(logits_out + j * V, L.logits_d + (size_t)sb.want_logits[j] * V, (size_t)V * sizeof(float),
+                            hipMemcpyDeviceToHost, L.st));
   return IFR_OK;
 }
 
@@ -1136,6 +1145,13 @@ int ifr_seq_len(ifr_ctx* c, int32_t slot, int32_t* len) {
   return IFR_OK;
 }
 
+int ifr_model_info(ifr_ctx* c, ifr_model_cfg* out) {
+  if (!c || !out) return fail(IFR_EINVAL, "null arg");
+  if (!c->loaded) return fail(IFR_ESTATE, "no model loaded");
+  *out = c->cfg;
+  return IFR_OK;
+}
+
 int ifr_kv_capacity(ifr_ctx* c, int32_t* tokens) {
   if (!c || !c->loaded || !tokens) return fail(IFR_ESTATE, "no model loaded");
   *tokens = c->kv.max_seq_tokens;
@@ -1232,12 +1248,15 @@ int ifr_forward(ifr_ctx* c, const ifr_row* rows, int32_t M, int32_t* best_out, f
   const int V = c->cfg.vocab;
   // ---- validate rows (BatchItem rules: one contiguous run per sequence)
   std::vector<int> g_start, g_len, g_pos0, g_seq;
+  bool any_logit_rows = false;  // logits_out then holds only the want = 2 rows
   for (int m = 0; m < M; ++m) {
     const ifr_row& r = rows[m];
     if (r.seq < 0 || r.seq >= (int)c->seqs.size() || !c->seqs[r.seq].open)
       return fail(IFR_EINVAL, "row %d: sequence slot %d not open", m, r.seq);
     if (r.token < 0 || r.token >= V) return fail(IFR_EINVAL, "row %d: token %d", m, r.token);
     if (r.kind < IFR_ROW_DECODE || r.kind > IFR_ROW_VERIFY) return fail(IFR_EINVAL, "row %d: kind", m);
+    if (r.want < 0 || r.want > 2) return fail(IFR_EINVAL, "row %d: want %d", m, r.want);
+    if (r.want == 2) any_logit_rows = true;
     if (r.pos < 0 || r.pos >= c->kv.max_seq_tokens)
       return fail(IFR_EINVAL, "row %d: pos %d >= KV capacity %d", m, r.pos, c->kv.max_seq_tokens);
     const bool first = (m == 0 || rows[m - 1].seq != r.seq);
@@ -1328,8 +1347,9 @@ int ifr_forward(ifr_ctx* c, const ifr_row* rows, int32_t M, int32_t* best_out, f
       if (int r = launch_layer(c, sb, l)) return r;
   int want_off = 0;
   for (SubBatch& sb : sbs) {
-    if (int r = launch_tail(c, sb, logits_out ? logits_out + (size_t)want_off * V : nullptr)) return r;
-    want_off += (int)sb.want.size();
+    if (int r = launch_tail(c, sb, logits_out ? logits_out + (size_t)want_off * V : nullptr, any_logit_rows))
+      return r;
+    want_off += (int)(any_logit_rows ? sb.want_logits.size() : sb.want.size());
   }
   const auto t_sub = std::chrono::steady_clock::now();
   for (SubBatch& sb : sbs) HIPCHK(hipStreamSynchronize(c->lane[sb.lane].st));

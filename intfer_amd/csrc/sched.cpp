@@ -13,11 +13,15 @@
 // plus n-gram speculative verify rows (main.cpp:11522-11550 ngram_from,
 // :11842-11931 verify / accept / rollback) as a third row kind: a speculating
 // request contributes its token and K drafts as one causal verify group.
+// Per-request sampling (sched_iteration_joint's qgreedy / sample choice,
+// main.cpp:8505-8508): a non-greedy request's decode rows ask the forward for
+// their logits (want = 2) and draw the token with ifr_sample.
 #include <algorithm>
 #include <deque>
 #include <iterator>
 #include <map>
 #include <memory>
+#include <random>
 #include <string>
 #include <vector>
 
@@ -33,6 +37,12 @@ struct Req {
   int token = -1, pos = 0, fill = 0, max_new = 0;
   bool finished = false;
   int slot = -1;
+  // sampling (Request :4812-4815); greedy when all three are off (:8401)
+  float temperature = 0.f, top_p = 0.f;
+  int top_k = 0;
+  ifr_rng* rng = nullptr;
+  bool greedy() const { return temperature <= 0.f && top_k == 0 && top_p <= 0.f; }
+  ~Req() { ifr_rng_free(rng); }
 };
 
 // Drafts: tokens following the last occurrence of `tok` in generated (stops
@@ -87,6 +97,7 @@ struct ifr_sched {
   std::vector<ifr_row> last_rows;
   std::vector<ifr_row> rows;
   std::vector<int32_t> best;
+  std::vector<float> logits;           // [rows with want = 2][vocab] of the last forward
   bool record = false;                 // ifr_sched_record_events
   std::deque<ifr_sched_event> events;
   std::deque<CacheEntry> cache;        // most recently used first
@@ -186,25 +197,39 @@ struct ifr_sched {
     Req* r;
     int row0;
     std::vector<int32_t> drafts;
+    int lrow;  // its row among the want = 2 rows (sampling requests), else -1
   };
 
   int forward() {
     best.assign(rows.size(), -1);
     last_rows = rows;
+    size_t nl = 0;
+    for (const ifr_row& rw : rows) nl += rw.want == 2;
+    if (nl) logits.resize(nl * (size_t)be.vocab);
     int r;
     // a refused forward (KV pages exhausted) changed nothing: cached
     // prefixes give their pages back first
-    while ((r = be.forward(be.user, rows.data(), (int32_t)rows.size(), best.data())) == IFR_ENOMEM)
-      if (!evict_lru()) break;
+    for (;;) {
+      r = nl ? be.forward_logits(be.user, rows.data(), (int32_t)rows.size(), best.data(), logits.data())
+             : be.forward(be.user, rows.data(), (int32_t)rows.size(), best.data());
+      if (r != IFR_ENOMEM || !evict_lru()) break;
+    }
     return r;
   }
 
   // Decode (or verify) rows for every live request (main.cpp:8438-8446).
   void build_decode(std::vector<DecodeItem>& items) {
+    int nl = 0;
     for (Req* q : live) {
       if (q->finished) continue;
       if ((int)q->generated.size() >= q->max_new + 1) { q->finished = true; continue; }
-      DecodeItem it{q, (int)rows.size(), {}};
+      DecodeItem it{q, (int)rows.size(), {}, -1};
+      if (!q->greedy()) {  // one decode row whose logits come back
+        it.lrow = nl++;
+        rows.push_back({q->slot, q->pos, q->token, IFR_ROW_DECODE, 2});
+        items.push_back(std::move(it));
+        continue;
+      }
       if (cfg.spec_k > 0) {
         it.drafts = ngram_from(q->generated, q->prompt, q->token, cfg.spec_k);
         while (!it.drafts.empty() && q->pos + (int)it.drafts.size() >= max_seq_tokens) it.drafts.pop_back();
@@ -223,7 +248,12 @@ struct ifr_sched {
     for (const DecodeItem& it : items) {
       Req& q = *it.r;
       if (it.drafts.empty()) {
-        const int next = best[(size_t)it.row0];
+        int next = best[(size_t)it.row0];
+        if (it.lrow >= 0) {
+          if (int r = ifr_sample(logits.data() + (size_t)it.lrow * be.vocab, be.vocab, q.top_k, q.top_p,
+                                 q.temperature, q.rng, &next))
+            return r;
+        }
         q.generated.push_back(next);
         q.pos++;
         emit(q, next);
@@ -361,6 +391,9 @@ int eng_trunc(void* u, int32_t slot, int32_t len) {
 int eng_fwd(void* u, const ifr_row* rows, int32_t M, int32_t* best) {
   return ifr_forward(static_cast<ifr_ctx*>(u), rows, M, best, nullptr);
 }
+int eng_fwd_logits(void* u, const ifr_row* rows, int32_t M, int32_t* best, float* logits) {
+  return ifr_forward(static_cast<ifr_ctx*>(u), rows, M, best, logits);
+}
 int eng_copy(void* u, int32_t dst, int32_t src, int32_t len) {
   return ifr_seq_copy_prefix(static_cast<ifr_ctx*>(u), dst, src, len);
 }
@@ -371,7 +404,7 @@ int ifr_sched_create_backend(const ifr_sched_backend* be, const ifr_sched_cfg* c
     return IFR_EINVAL;
   if (cfg->chunk_m < 1 || cfg->chunk_m > 4096 || cfg->live_cap < 1 || cfg->spec_k < 0 ||
       cfg->spec_k > 15 || cfg->pack_prefill < 0 || cfg->pack_prefill > 1 || cfg->prefix_cache < 0 ||
-      cfg->prefix_cache > 16 || be->kv_capacity <= 0)
+      cfg->prefix_cache > 16 || be->kv_capacity <= 0 || (be->forward_logits && be->vocab <= 0))
     return IFR_EINVAL;
   auto* s = new ifr_sched();
   s->be = *be;
@@ -390,6 +423,10 @@ int ifr_sched_create(ifr_ctx* ctx, const ifr_sched_cfg* cfg, ifr_sched** out) {
   be.seq_truncate = eng_trunc;
   be.forward = eng_fwd;
   be.seq_copy_prefix = eng_copy;
+  be.forward_logits = eng_fwd_logits;
+  ifr_model_cfg mc{};
+  if (int r = ifr_model_info(ctx, &mc)) return r;
+  be.vocab = mc.vocab;
   if (int r = ifr_kv_capacity(ctx, &be.kv_capacity)) return r;
   return ifr_sched_create_backend(&be, cfg, out);
 }
@@ -404,9 +441,25 @@ int ifr_sched_destroy(ifr_sched* s) {
 }
 
 int ifr_sched_submit(ifr_sched* s, const int32_t* prompt, int32_t n, int32_t max_new, int64_t* id) {
+  return ifr_sched_submit_sampled(s, prompt, n, max_new, nullptr, id);
+}
+
+int ifr_sched_submit_sampled(ifr_sched* s, const int32_t* prompt, int32_t n, int32_t max_new,
+                             const ifr_sample_params* sp, int64_t* id) {
   if (!s || !prompt || n <= 0 || max_new < 0) return IFR_EINVAL;
   auto r = std::make_unique<Req>();
-  r->id = s->next_id++;
+  if (sp) {
+    r->temperature = sp->temperature;
+    r->top_k = sp->top_k < 0 ? 0 : sp->top_k;
+    r->top_p = sp->top_p < 0.f ? 0.f : (sp->top_p > 1.f ? 1.f : sp->top_p);
+  }
+  r->id = s->next_id;
+  if (!r->greedy()) {
+    if (!s->be.forward_logits) return IFR_EDECLINE;
+    // the request's generator (main.cpp:9305)
+    if (int e = ifr_rng_create(sp->has_seed ? sp->seed : s->cfg.seed + (uint32_t)r->id, &r->rng)) return e;
+  }
+  s->next_id++;
   r->prompt.assign(prompt, prompt + n);
   r->max_new = max_new;
   if (id) *id = r->id;

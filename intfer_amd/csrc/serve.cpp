@@ -90,6 +90,7 @@ struct Request {
   int max_new = 64;
   bool has_id = false;
   int64_t id = 0;
+  ifr_sample_params sp{};
 };
 
 // Parse one request line (parse_serve_line, main.cpp:8595-8676, with token
@@ -108,8 +109,21 @@ std::string parse_line(const std::string& line, const ifr_serve_cfg& cfg, int32_
   if (as_int(root.at("max_new"), &v)) r.max_new = (int)std::max<int64_t>(std::min<int64_t>(v, 1 << 30), -1);
   if (r.max_new < 1) r.max_new = 1;
   if (r.max_new > 4096) r.max_new = 4096;
-  if (as_real(root.at("temperature")) > 0 || as_real(root.at("top_k")) > 0 || as_real(root.at("top_p")) > 0)
-    return "only greedy decoding (temperature 0) is served";
+  // sampling keys over the serve defaults; top_k >= 0, top_p in [0, 1]
+  // (parse_serve_line, main.cpp:8646-8668)
+  r.sp.temperature = cfg.temperature;
+  r.sp.top_k = cfg.top_k;
+  r.sp.top_p = cfg.top_p;
+  if (const JNode* t = root.at("temperature")) r.sp.temperature = (float)as_real(t);
+  if (as_int(root.at("top_k"), &v)) r.sp.top_k = (int32_t)std::max<int64_t>(std::min<int64_t>(v, INT32_MAX), 0);
+  if (const JNode* t = root.at("top_p")) r.sp.top_p = (float)as_real(t);
+  if (r.sp.top_k < 0) r.sp.top_k = 0;
+  if (r.sp.top_p < 0.f) r.sp.top_p = 0.f;
+  if (r.sp.top_p > 1.f) r.sp.top_p = 1.f;
+  if (as_int(root.at("seed"), &v)) {
+    r.sp.seed = (uint32_t)v;
+    r.sp.has_seed = 1;
+  }
   const JNode* ids = root.at("prompt_ids");
   if (!ids) {
     if (root.at("prompt")) return "text prompts need a tokenizer: send prompt_ids";
@@ -185,8 +199,14 @@ extern "C" int ifr_serve(ifr_sched* s, int32_t in_fd, int32_t out_fd, const ifr_
       }
       if (!r.has_id) r.id = next_id++;
       else if (r.id >= next_id) next_id = r.id + 1;
+      // a request without a seed draws from mt19937(seed + its id) (main.cpp:9305)
+      if (!r.sp.has_seed) {
+        r.sp.seed = cfg.seed + (uint32_t)r.id;
+        r.sp.has_seed = 1;
+      }
       int64_t sid = 0;
-      if (ifr_sched_submit(s, r.prompt.data(), (int32_t)r.prompt.size(), r.max_new, &sid) != IFR_OK) {
+      if (ifr_sched_submit_sampled(s, r.prompt.data(), (int32_t)r.prompt.size(), r.max_new, &r.sp, &sid) !=
+          IFR_OK) {
         out += "{\"id\":" + std::to_string(r.id) + ",\"error\":\"request refused by the scheduler\"}\n";
         continue;
       }

@@ -6,6 +6,7 @@
 // INTFER_PREFILL_CHUNK_M, INTFER_SERVE_MAX, INTFER_SPLIT_ITER, INTFER_PREFILL_RR.
 #include <unistd.h>
 
+#include <chrono>
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
@@ -21,7 +22,7 @@ void usage() {
                "  [--hidden H --layers L --heads NQ --kv-heads NKV --inter F --vocab V]\n"
                "  [--kv-int8] [--max-new N] [--chunk-m N] [--live-cap N] [--split-iter] [--no-rr]\n"
                "  [--spec-k K] [--pack-prefill] [--prefix-cache N] [--max-seq-tokens N] [--max-seqs N]\n"
-               "  [--pool-tokens N] [--device D]\n");
+               "  [--pool-tokens N] [--device D] [-t TEMP] [-k TOP_K] [-T TOP_P] [-S SEED]\n");
 }
 
 int env_int(const char* name, int dflt, int lo, int hi) {
@@ -45,6 +46,9 @@ int main(int argc, char** argv) {
   int rr = (std::getenv("INTFER_PREFILL_RR") && std::string(std::getenv("INTFER_PREFILL_RR")) == "0") ? 0 : 1;
   int max_seq_tokens = 4096, max_seqs = 0, pack = 0, pcache = 0;
   long long pool_tokens = 0;
+  float temperature = 0.f, top_p = 0.f;
+  int top_k = 0;
+  uint32_t seed = 0;
   for (int i = 1; i < argc; ++i) {
     const std::string a = argv[i];
     auto next = [&]() -> const char* {
@@ -77,6 +81,10 @@ int main(int argc, char** argv) {
     else if (a == "--max-seqs") max_seqs = std::atoi(next());
     else if (a == "--pool-tokens") pool_tokens = std::atoll(next());
     else if (a == "--device") device = std::atoi(next());
+    else if (a == "-t") temperature = (float)std::atof(next());
+    else if (a == "-k") top_k = std::atoi(next());
+    else if (a == "-T") top_p = (float)std::atof(next());
+    else if (a == "-S") seed = (uint32_t)std::atoi(next());
     else {
       usage();
       return 2;
@@ -134,9 +142,19 @@ int main(int argc, char** argv) {
                "[intfer] serve: live cap %d, chunk %d, %s, spec_k %d, KV %s, %d x %d tokens, prefix cache %d\n",
                live_cap, chunk_m, split_iter ? "split" : "joint", spec_k, kv_int8 ? "int8" : "fp16",
                max_seqs, max_seq_tokens, pcache);
+  // the reference's sampling defaults (-t / -k / -T) and base seed (-S; 0
+  // picks one from the clock, main.cpp:10590-10591, printed to reproduce)
+  if (seed == 0) {
+    seed = (uint32_t)std::chrono::high_resolution_clock::now().time_since_epoch().count();
+    if (temperature > 0.f || top_k > 0 || top_p > 0.f) std::fprintf(stderr, "[intfer] serve: seed %u\n", seed);
+  }
   ifr_serve_cfg scfg{};
   scfg.default_max_new = max_new;
   scfg.vocab = cfg.vocab;
+  scfg.temperature = temperature;
+  scfg.top_k = top_k;
+  scfg.top_p = top_p;
+  scfg.seed = seed;
   rc = ifr_serve(s, STDIN_FILENO, STDOUT_FILENO, &scfg);
   if (rc != IFR_OK) std::fprintf(stderr, "FAIL: serve: %s\n", ifr_last_error());
   ifr_sched_destroy(s);

@@ -22,6 +22,7 @@
 #include <cstdint>
 #include <cstdlib>
 #include <cstring>
+#include <random>
 #include <vector>
 
 #include "intfer_amd.h"
@@ -675,6 +676,67 @@ void or_attention_row(const float* q, const float* k, const float* v, int pos, i
 }
 
 void or_kv_int8_round(float* x, int hd) { kv_int8_round(x, hd); }
+
+// ---- sampling: the reference's sample() (main.cpp:8674-8764, default path;
+// the INTFER_SAMPLE_TOPK_DIRECT variant :8695-8724 is opt-in) over the
+// request's std::mt19937 (main.cpp:4815, seeded :9305), with the draw taken
+// by std::uniform_real_distribution<float>(0, 1) of the standard library,
+// exactly as the reference takes it.
+void* or_rng_create(uint32_t seed) { return new std::mt19937(seed); }
+void or_rng_free(void* g) { delete static_cast<std::mt19937*>(g); }
+uint32_t or_rng_next(void* g) { return (uint32_t)(*static_cast<std::mt19937*>(g))(); }
+float or_rng_uniform(void* g) {
+  std::uniform_real_distribution<float> U(0.f, 1.f);
+  return U(*static_cast<std::mt19937*>(g));
+}
+int or_sample(const float* logits, int V, int top_k, float top_p, float temperature, void* g) {
+  std::mt19937& rng = *static_cast<std::mt19937*>(g);
+  if (temperature <= 0.f) temperature = 1e-5f;                     // :8676
+  float mx = -1e30f;                                                // :8725-8726
+  for (int i = 0; i < V; ++i)
+    if (logits[i] > mx) mx = logits[i];
+  std::vector<float> probs((size_t)V);
+  float sum = 0.f;                                                  // :8730-8735
+  for (int i = 0; i < V; ++i) {
+    probs[(size_t)i] = expf((logits[i] - mx) / temperature);
+    sum += probs[(size_t)i];
+  }
+  for (float& q : probs) q /= sum;                                  // :8736
+  auto renorm = [&]() {
+    sum = 0.f;
+    for (float q : probs) sum += q;
+    for (float& q : probs) q /= sum;
+  };
+  if (top_k > 0 && V > top_k) {                                     // :8737-8743
+    std::vector<float> sorted = probs;
+    std::nth_element(sorted.begin(), sorted.end() - top_k, sorted.end());
+    const float kth = sorted[sorted.size() - (size_t)top_k];
+    for (float& q : probs)
+      if (q < kth) q = 0.f;
+    renorm();
+  }
+  if (top_p > 0.f && top_p < 1.f) {                                 // :8744-8756
+    std::vector<int> idx((size_t)V);
+    for (int i = 0; i < V; ++i) idx[(size_t)i] = i;
+    std::sort(idx.begin(), idx.end(), [&](int a, int b) { return probs[(size_t)a] > probs[(size_t)b]; });
+    float cum = 0.f;
+    int cutoff = V;
+    for (int i = 0; i < V; ++i) {
+      cum += probs[(size_t)idx[(size_t)i]];
+      if (cum >= top_p) { cutoff = i + 1; break; }
+    }
+    for (int i = cutoff; i < V; ++i) probs[(size_t)idx[(size_t)i]] = 0.f;
+    renorm();
+  }
+  std::uniform_real_distribution<float> U(0.f, 1.f);               // :8757-8763
+  const float r = U(rng);
+  float acc = 0.f;
+  for (int i = 0; i < V; ++i) {
+    acc += probs[(size_t)i];
+    if (r <= acc) return i;
+  }
+  return V - 1;
+}
 
 void* or_engine_create(const ifr_host_model* m, int kv_int8, int mode, int max_seqs) {
   if (!m || (mode != 0 && mode != 1)) return nullptr;

@@ -57,6 +57,11 @@ def oracle() -> C.CDLL:
             "or_seq_truncate": (C.c_int, [P, C.c_int, C.c_int]),
             "or_seq_set_kv": (C.c_int, [P, C.c_int, C.c_int, P, P]),
             "or_forward": (C.c_int, [P, P, C.c_int, P, P]),
+            "or_rng_create": (P, [C.c_uint32]),
+            "or_rng_free": (None, [P]),
+            "or_rng_next": (C.c_uint32, [P]),
+            "or_rng_uniform": (f32, [P]),
+            "or_sample": (C.c_int, [P, C.c_int, C.c_int, f32, f32, P]),
         }
         for n, (res, args) in protos.items():
             fn = getattr(L, n)

@@ -34,7 +34,8 @@ UNITS = [("qgemm.hip", [], "qgemm"),
          ("qgemm.hip", ["-DIFR_QGEMM_BITS=8"], "qgemm_b8"),
          ("rows.hip", [], "rows"), ("attn.hip", [], "attn"), ("lmhead.hip", [], "lmhead"),
          ("engine.cpp", [], "engine"), ("sched.cpp", [], "sched"), ("synth.cpp", [], "synth"),
-         ("intfer_file.cpp", [], "intfer_file"), ("serve.cpp", [], "serve")]
+         ("intfer_file.cpp", [], "intfer_file"), ("serve.cpp", [], "serve"),
+         ("sample.cpp", [], "sample")]
 
 FLAGS = ["-O1", "-g", "-fPIC", "-std=c++17", "-fsanitize=address", "-fno-omit-frame-pointer",
          "-ffp-contract=off", "-Wno-unused-command-line-argument", "-w",

@@ -47,7 +47,8 @@ class MockLM:
         self._cb = (_abi.SEQ_OPEN(self._open), _abi.SEQ_CLOSE(self._close),
                     _abi.SEQ_TRUNC(self._trunc), _abi.FORWARD(self._fwd))
         self._copy_cb = _abi.SEQ_COPY(self._copy) if copy else _abi.SEQ_COPY()
-        self.table = _abi.SchedBackend(None, *self._cb, cap, self._copy_cb)
+        self._logits_cb = _abi.FORWARD_LOGITS(self._fwd_logits)
+        self.table = _abi.SchedBackend(None, *self._cb, cap, self._copy_cb, self._logits_cb, V)
 
     def used(self):
         return sum(len(h) for h in self.hist.values())
@@ -85,6 +86,23 @@ class MockLM:
         for t in h:
             x = ((x ^ t) * 1099511) % 4294967291
         return x % V
+
+    @staticmethod
+    def logits_of(h):
+        """The mock's logits after history h (returned for want = 2 rows)."""
+        return (np.random.default_rng(MockLM.next_token(h) * 7919 + len(h)).standard_normal(V) * 2).astype(
+            np.float32)
+
+    def _fwd_logits(self, user, rows, M, best, logits):
+        r = self._fwd(user, rows, M, best)
+        if r == 0:
+            k = 0
+            for i, (s, p, t, kind, w) in enumerate(self.forwards[-1]):
+                if w == 2:
+                    lg = self.logits_of(self.hist[s][:p + 1])
+                    C.memmove(C.addressof(logits.contents) + k * V * 4, lg.ctypes.data, V * 4)
+                    k += 1
+        return r
 
     def _fwd(self, user, rows, M, best):
         rs = [(rows[i].seq, rows[i].pos, rows[i].token, rows[i].kind, rows[i].want) for i in range(M)]
@@ -219,6 +237,76 @@ def test_spec_verify_rows_keep_stream_and_accept():
     assert spec == plain
     ver = [r for f in lm.forwards for r in f if r[3] == ia.ROW_VERIFY]
     assert ver, "no verify rows were scheduled"
+
+
+def expected_sampled(prompt, max_new, seed, T, k, p):
+    """A sampling request's stream: the prompt's last row scores the argmax
+    (main.cpp:8522-8523), then every decode token is the oracle's sample()
+    over the mock's logits with the request's mt19937."""
+    from oracle import pyoracle as po
+    from oracle.pyoracle import ptr
+    O = po.oracle()
+    g = O.or_rng_create(seed)
+    try:
+        h = list(prompt)
+        out = [MockLM.next_token(h)]
+        while len(out) < max_new + 1:
+            h.append(out[-1])
+            out.append(O.or_sample(ptr(MockLM.logits_of(h)), V, k, p, T, g))
+    finally:
+        O.or_rng_free(g)
+    return out
+
+
+@pytest.mark.parametrize("split,spec_k", [(0, 0), (1, 0), (0, 3)])
+def test_sampled_requests_follow_the_reference_sampler(split, spec_k):
+    """Per-request temperature / top_k / top_p with the request's own
+    mt19937 (its seed, else the scheduler's seed + id, main.cpp:9305) beside
+    greedy requests, in joint, split and speculating schedulers: every stream
+    is the oracle sampler's, whatever the batching; sampled requests get no
+    verify rows."""
+    ps = prompts_of(5, 21)
+    params = [(0.8, 0, 0.0, None), (1.2, 10, 0.0, 77), (0.7, 0, 0.9, None), None, (1.0, 5, 0.8, 5)]
+    lm = MockLM()
+    sch = ia.Scheduler(backend=lm.table, chunk_m=16, live_cap=8, split_iter=split, spec_k=spec_k, seed=1000)
+    ids = []
+    for pr, pa in zip(ps, params):
+        if pa is None:
+            ids.append(sch.submit(pr, 9))
+        else:
+            T, k, pp, sd = pa
+            ids.append(sch.submit(pr, 9, temperature=T, top_k=k, top_p=pp, seed=sd))
+    for _ in range(2000):
+        if sch.step() == 0 and all(sch.result(i)[1] for i in ids):
+            break
+    for rid, pr, pa in zip(ids, ps, params):
+        got = sch.result(rid)[0]
+        if pa is None:
+            assert got == expected_stream(pr, 9)
+        else:
+            T, k, pp, sd = pa
+            assert got == expected_sampled(pr, 9, 1000 + rid if sd is None else sd, T, k, pp), rid
+    sch.close()
+    sampled_slots = set()
+    for f in lm.forwards:
+        for r in f:
+            if r[4] == 2:
+                sampled_slots.add(r[0])
+                assert r[3] == ia.ROW_DECODE
+    assert sampled_slots
+
+
+def test_sampling_needs_a_logits_forward():
+    lm = MockLM()
+    lm.table.forward_logits = _abi.FORWARD_LOGITS()
+    sch = ia.Scheduler(backend=lm.table, chunk_m=16, live_cap=8)
+    try:
+        with pytest.raises(ia.IfrError) as e:
+            sch.submit([1, 2, 3], 4, temperature=0.9)
+        assert e.value.code == ia.IFR_EDECLINE
+        sch.submit([1, 2, 3], 4)  # greedy is still accepted
+    finally:
+        sch.close()
 
 
 def test_oracle_backend_split_equals_joint():

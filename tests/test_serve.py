@@ -94,7 +94,7 @@ def test_ids_defaults_and_clamps():
 
 def test_refusals_keep_serving():
     p = prompts_of(1, 14)[0]
-    lines = ["not json", '{"prompt":"hello"}', line(p, 2, temperature=0.7), '{"max_new":3}',
+    lines = ["not json", '{"prompt":"hello"}', '{"max_new":3}',
              line([5, V + 1000], 2, rid=9), '{"prompt_ids":[1,"x"]}', line(p, 2, rid=3),
              line(list(range(10)) * 500, 64, rid=11)]
     out, rc, _, _ = serve(lines, vocab=V + 10, chunk_m=64, live_cap=8)
@@ -103,11 +103,33 @@ def test_refusals_keep_serving():
     msgs = [e["error"] for e in errs]
     assert msgs.count("malformed request line") == 3
     assert any("tokenizer" in m for m in msgs)
-    assert any("greedy" in m for m in msgs)
     assert any("out of range" in m and e.get("id") == 9 for m, e in zip(msgs, errs))
     assert any("KV capacity" in m and e.get("id") == 11 for m, e in zip(msgs, errs))
     toks, done = streams_of(out)
     assert done == {3: 3} and toks[3] == expected_stream(p, 2)[1:]
+
+
+def test_sampling_keys_are_served():
+    """temperature / top_k / top_p / seed per line (parse_serve_line,
+    main.cpp:8646-8668) over the serve defaults; a line without a seed draws
+    from mt19937(serve seed + its id) (main.cpp:9305); top_k < 0 reads as 0
+    and top_p is clamped to [0, 1]."""
+    from tests.test_sched import expected_sampled
+    ps = prompts_of(4, 31)
+    lines = [line(ps[0], 6, temperature=0.8, seed=42), line(ps[1], 6, rid=20, temperature=1.1, top_k=7),
+             line(ps[2], 6, top_p=0.9, top_k=-3), line(ps[3], 6)]
+    lm = MockLM(slots=32)
+    sch = ia.Scheduler(backend=lm.table, chunk_m=64, live_cap=8)
+    try:
+        out, rc = sch.serve(lines, default_max_new=64, temperature=0.5, seed=900)
+    finally:
+        sch.close()
+    toks, done = streams_of(out)
+    assert rc == 0 and done == {1: 7, 20: 7, 21: 7, 22: 7}
+    assert toks[1] == expected_sampled(ps[0], 6, 42, 0.8, 0, 0.0)[1:]
+    assert toks[20] == expected_sampled(ps[1], 6, 920, 1.1, 7, 0.0)[1:]
+    assert toks[21] == expected_sampled(ps[2], 6, 921, 0.5, 0, 0.9)[1:]
+    assert toks[22] == expected_sampled(ps[3], 6, 922, 0.5, 0, 0.0)[1:]
 
 
 def test_empty_prompt_uses_reference_fallback():
