@@ -293,6 +293,16 @@ int upload_group(ifr_ctx* c, const ifr_linear* const* ws, int count, int pair, D
   d.nsteps = K / 64;
   d.pair = pair;
   d.post = post_of(*ws[0]);
+  // codebook zeros (C/2 everywhere, C = 2^bits - 1: 1.5 or 7.5 in fp16) take
+  // the GEMM's two-operation fold, which gives the same bits
+  d.ff = 0;
+  if (bits == 2 || bits == 4) {
+    const uint16_t zc = bits == 2 ? 0x3E00 : 0x4780;
+    d.ff = 1;
+    for (int i = 0; i < count && d.ff; ++i)
+      for (size_t e = 0; e < (size_t)ws[i]->N * (K / 128); ++e)
+        if (ws[i]->zero[e] != zc) { d.ff = 0; break; }
+  }
   const size_t cb = code_bytes(N, K, bits), sb = sz_bytes(N, K);
   std::vector<uint32_t> hc(cb / 4), hs(sb / 4);
   int tile_off = 0;

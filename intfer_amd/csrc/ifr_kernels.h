@@ -34,6 +34,7 @@ struct DLin {
   int nsteps = 0;  // K / 64
   int pair = 0;    // 1: tiles alternate gate / up (SwiGLU epilogue)
   float post = 1.0f;  // factor on every output: y = fp16((ascale * post) * acc)
+  int ff = 0;  // 1: every zero is the codebook midpoint, so the folded integer path applies
   uint32_t* codes = nullptr;
   uint32_t* sz = nullptr;
   size_t bytes = 0;

@@ -12,6 +12,19 @@
 // element: split-K variants exchange the int32 T through LDS and fold them in
 // group order, so every launch shape produces the same bits.
 //
+// Codebook linears (every zero(n,g) = C/2, C = 2^bits - 1: the reference's
+// canonical codebook, dashq.cpp:405-417) take a two-operation fold with the
+// same bits.  The MFMA runs over the doubled codes 2c and starts each group's
+// accumulator at the integer 0x4B400000, whose bits read as the float
+// 1.5 * 2^23: the accumulator's bits then read as the float 1.5 * 2^23 + 2T
+// exactly (|2T| < 2^22).  With Y(m,g) = 1.5 * 2^23 + C * S(m,g) (an exact
+// integer below 2^24) and h(n,g) = scale(n,g) / 2 (exact),
+//     d2  = T_float - Y          = 2T - C S = 2 (T - zero S)   exact
+//     acc = fma(h, d2, acc)
+// and fma(h, d2, acc) == fma(scale, d, acc) because both products are the
+// same real number and d = fma(-zero, S, T) is exact for these codes (a
+// multiple of 1/2 below 2^20).  No int->float conversion, one subtract.
+//
 // Tiling: a workgroup is 4 waves (256 lanes).  Each wave owns WM x WN tiles of
 // 16x16 outputs (MFMA 16x16x64).  The fold-side operands (S, scale/zero) are
 // staged in LDS once per workgroup so the K loop carries only the A and B
@@ -50,6 +63,8 @@ struct KParams {
   // of rows and columns exchanged (activation rows kept, for a larger A).
   // The owned dimension is padded to a multiple of 8; padding blocks exit.
   int nbx, nby, swz;
+  // 1: every zero of the linear is C/2 (the codebook fold applies)
+  int ff;
   // EPI 2 (QKV projection with the q/k norm + RoPE + KV append epilogue):
   // the arguments of the separate pass (row maps, norms, RoPE tables, q
   // output, paged KV)
@@ -93,10 +108,20 @@ __device__ __forceinline__ void load_raw(const uint32_t* __restrict__ base, int 
     w[3] = (uint32_t)x.w;
   }
 }
-template <int BITS>
+template <int BITS, bool DBL = false>
 __device__ __forceinline__ v4i unpack_b(const uint32_t (&w)[BITS / 2]) {
   v4i r;
-  if constexpr (BITS == 2) {
+  if constexpr (DBL && BITS == 2) {  // 2c: the same fields, one bit higher
+    r.x = (int)((w[0] << 1) & 0x06060606u);
+    r.y = (int)((w[0] >> 1) & 0x06060606u);
+    r.z = (int)((w[0] >> 3) & 0x06060606u);
+    r.w = (int)((w[0] >> 5) & 0x06060606u);
+  } else if constexpr (DBL && BITS == 4) {
+    r.x = (int)((w[0] << 1) & 0x1E1E1E1Eu);
+    r.y = (int)((w[0] >> 3) & 0x1E1E1E1Eu);
+    r.z = (int)((w[1] << 1) & 0x1E1E1E1Eu);
+    r.w = (int)((w[1] >> 3) & 0x1E1E1E1Eu);
+  } else if constexpr (BITS == 2) {
     r.x = (int)(w[0] & 0x03030303u);
     r.y = (int)((w[0] >> 2) & 0x03030303u);
     r.z = (int)((w[0] >> 4) & 0x03030303u);
@@ -163,18 +188,23 @@ __device__ __forceinline__ void load_ops(const KParams& p, const uint32_t (&aoff
   }
 }
 
-template <int BITS, int WM, int WN>
+// The bits of the float 1.5 * 2^23 (the codebook fold's accumulator start).
+constexpr int kFoldBias = 0x4B400000;
+constexpr float kFoldBiasF = 12582912.0f;
+
+template <int BITS, int WM, int WN, bool FF = false>
 __device__ __forceinline__ void mma_group(const GroupOps<BITS, WM, WN>& b, v4i (&T)[WM][WN]) {
+  constexpr int c0 = FF ? kFoldBias : 0;
 #pragma unroll
   for (int h = 0; h < 2; ++h) {
     v4i B[WN];
 #pragma unroll
-    for (int j = 0; j < WN; ++j) B[j] = unpack_b<BITS>(b.B[h][j]);
+    for (int j = 0; j < WN; ++j) B[j] = unpack_b<BITS, FF>(b.B[h][j]);
 #pragma unroll
     for (int i = 0; i < WM; ++i)
 #pragma unroll
       for (int j = 0; j < WN; ++j)
-        T[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(b.A[h][i], B[j], h ? T[i][j] : (v4i){0, 0, 0, 0},
+        T[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(b.A[h][i], B[j], h ? T[i][j] : (v4i){c0, c0, c0, c0},
                                                         0, 0, 0);
   }
 }
@@ -185,9 +215,16 @@ __device__ __forceinline__ void mma_group(const GroupOps<BITS, WM, WN>& b, v4i (
 // and columns past N read the last tile; their outputs are never stored.
 // Up to NQ elements per thread are fetched with all loads in flight at once;
 // larger blocks (K > 128 * NQ * 256 / max(BM, BN)) take a plain loop.
-template <int BM, int BN, int NQ>
+// FF (codebook fold): S_l holds Y = 1.5 * 2^23 + C * S and Z_l the fp32
+// scale / 2 instead (see the header).
+template <int BM, int BN, int NQ, int BITS = 2, bool FF = false>
 __device__ __forceinline__ void stage_fold_operands(const KParams& p, int bm0, int bt0, float* S_l,
                                                     uint32_t* Z_l) {
+  constexpr float C = (float)((1 << BITS) - 1);
+  auto sval = [&](float sv) { return FF ? kFoldBiasF + C * sv : sv; };
+  auto zval = [&](uint32_t zw) {
+    return FF ? __float_as_uint(0.5f * ifrd::h2f((uint16_t)(zw & 0xFFFFu))) : zw;
+  };
   const int ng = p.ng, ntiles = p.N >> 4;
   constexpr int TB = BN / 16;
   auto s_src = [&](int t) {  // t = g * BM + r
@@ -213,12 +250,12 @@ __device__ __forceinline__ void stage_fold_operands(const KParams& p, int bm0, i
 #pragma unroll
     for (int q = 0; q < NQ; ++q) {
       const int t = threadIdx.x + 256 * q;
-      if (t < BM * ng) S_l[t] = sv[q];
-      if (t < BN * ng) Z_l[z_dst(t)] = zv[q];
+      if (t < BM * ng) S_l[t] = sval(sv[q]);
+      if (t < BN * ng) Z_l[z_dst(t)] = zval(zv[q]);
     }
   } else {
-    for (int t = threadIdx.x; t < BM * ng; t += 256) S_l[t] = *s_src(t);
-    for (int t = threadIdx.x; t < BN * ng; t += 256) Z_l[z_dst(t)] = *z_src(t);
+    for (int t = threadIdx.x; t < BM * ng; t += 256) S_l[t] = sval(*s_src(t));
+    for (int t = threadIdx.x; t < BN * ng; t += 256) Z_l[z_dst(t)] = zval(*z_src(t));
   }
 }
 
@@ -402,8 +439,10 @@ __device__ __forceinline__ void qk_epilogue(const KParams& p, float* lds, const 
 // accumulators group by group while the next R groups are in flight.  The
 // loads are unconditional (R divides ng; the last R groups are peeled), so the
 // wait before each group only covers that group's operands.
-template <int BITS, int WM, int WN, int MW, int R, int EPI, bool DUMP>
+// MODE 0: the general fold; 1: the general fold, T dumped; 2: the codebook fold.
+template <int BITS, int WM, int WN, int MW, int R, int EPI, int MODE>
 __global__ __launch_bounds__(256) void qgemm_rows(KParams p) {
+  constexpr bool DUMP = MODE == 1, FF = MODE == 2;
   constexpr int NW = 4 / MW;
   constexpr int BM = 16 * WM * MW, BN = 16 * WN * NW;
   extern __shared__ float lds_f[];
@@ -441,7 +480,7 @@ __global__ __launch_bounds__(256) void qgemm_rows(KParams p) {
   Ops ring[R];
 #pragma unroll
   for (int d = 0; d < R; ++d) load_ops<BITS, WM, WN>(p, aoff, tl, lane, d, ring[d]);
-  stage_fold_operands<BM, BN, 12>(p, bm0, bt0, S_l, Z_l);
+  stage_fold_operands<BM, BN, 12, BITS, FF>(p, bm0, bt0, S_l, Z_l);
   float asr[WM][4];
 #pragma unroll
   for (int i = 0; i < WM; ++i)
@@ -464,6 +503,15 @@ __global__ __launch_bounds__(256) void qgemm_rows(KParams p) {
 #pragma unroll
     for (int j = 0; j < WN; ++j) {
       const uint32_t zw = Z_l[g * BN + 16 * (WN * wn + j) + lrow];
+      if constexpr (FF) {  // S holds Y, zw the scale / 2
+        const float h = __uint_as_float(zw);
+#pragma unroll
+        for (int i = 0; i < WM; ++i)
+#pragma unroll
+          for (int r = 0; r < 4; ++r)
+            acc[i][j][r] = fmaf(h, __int_as_float(T[i][j][r]) - S[i][r], acc[i][j][r]);
+        continue;
+      }
       const float sc = ifrd::h2f((uint16_t)(zw & 0xFFFFu));
       const float ze = ifrd::h2f((uint16_t)(zw >> 16));
 #pragma unroll
@@ -482,14 +530,14 @@ __global__ __launch_bounds__(256) void qgemm_rows(KParams p) {
   for (; g + R < ng; g += R) {
 #pragma unroll
     for (int d = 0; d < R; ++d) {
-      mma_group<BITS, WM, WN>(ring[d], T);
+      mma_group<BITS, WM, WN, FF>(ring[d], T);
       load_ops<BITS, WM, WN>(p, aoff, tl, lane, g + d + R, ring[d]);
       fold(g + d);
     }
   }
 #pragma unroll
   for (int d = 0; d < R; ++d) {
-    mma_group<BITS, WM, WN>(ring[d], T);
+    mma_group<BITS, WM, WN, FF>(ring[d], T);
     fold(g + d);
   }
 
@@ -521,8 +569,9 @@ __global__ __launch_bounds__(256) void qgemm_rows(KParams p) {
 // of one WM x WN tile block.  Each wave issues the loads of all its groups
 // (at most NGW) at entry, runs the MFMAs, and parks its int32 T in LDS; after
 // one barrier all 256 lanes fold every group in ascending order.
-template <int BITS, int WM, int WN, int NGW, int EPI, bool DUMP>
+template <int BITS, int WM, int WN, int NGW, int EPI, int MODE>
 __global__ __launch_bounds__(256) void qgemm_splitk(KParams p) {
+  constexpr bool DUMP = MODE == 1, FF = MODE == 2;
   extern __shared__ int32_t lds[];
   constexpr int BM = 16 * WM, BN = 16 * WN;
   const int lane = threadIdx.x & 63;
@@ -548,7 +597,7 @@ __global__ __launch_bounds__(256) void qgemm_splitk(KParams p) {
   const int glast = max(g1 - 1, 0);
 #pragma unroll
   for (int d = 0; d < NGW; ++d) load_ops<BITS, WM, WN>(p, aoff, tl, lane, min(g0 + d, glast), ops[d]);
-  stage_fold_operands<BM, BN, 6>(p, row0, tile0, S_l, Z_l);
+  stage_fold_operands<BM, BN, 6, BITS, FF>(p, row0, tile0, S_l, Z_l);
   constexpr int JS = (EPI == 0) ? 1 : 2;  // swiglu: one thread folds the pair
   constexpr int NOUT = WM * (WN / JS) * 256;
   constexpr int NO = (NOUT + 255) / 256;
@@ -563,7 +612,7 @@ __global__ __launch_bounds__(256) void qgemm_splitk(KParams p) {
 #pragma unroll
   for (int d = 0; d < NGW; ++d) {
     if (g0 + d < g1) {
-      mma_group<BITS, WM, WN>(ops[d], T);
+      mma_group<BITS, WM, WN, FF>(ops[d], T);
 #pragma unroll
       for (int i = 0; i < WM; ++i)
 #pragma unroll
@@ -588,8 +637,14 @@ __global__ __launch_bounds__(256) void qgemm_splitk(KParams p) {
 #pragma unroll
       for (int q = 0; q < JS; ++q) {
         const int j = jj + q;
-        const int32_t Tv = true_t<BITS>(lds[(((size_t)g * WM + i) * WN + j) * 256 + ln * 4 + r], S);
+        const int32_t Tr = lds[(((size_t)g * WM + i) * WN + j) * 256 + ln * 4 + r];
         const uint32_t szw = Z_l[g * BN + 16 * j + c];
+        if constexpr (FF) {  // S holds Y, szw the scale / 2
+          const float d2 = __int_as_float(Tr) - S;
+          if (q == 0) a0 = fmaf(__uint_as_float(szw), d2, a0); else a1 = fmaf(__uint_as_float(szw), d2, a1);
+          continue;
+        }
+        const int32_t Tv = true_t<BITS>(Tr, S);
         const float sc = ifrd::h2f((uint16_t)(szw & 0xFFFFu));
         const float ze = ifrd::h2f((uint16_t)(szw >> 16));
         const float d = fmaf(-ze, S, (float)Tv);
@@ -791,11 +846,14 @@ hipError_t launch_rows(const KParams& p, hipStream_t st) {
     lds = std::max(lds, (size_t)(BM * (BN + 4) + BM * 8) * sizeof(float));
   }
   if (lds > 160 * 1024) return hipErrorInvalidValue;
+  constexpr bool kFF = BITS != 8;  // the codebook fold needs 2c in int8
   static bool attr_set = false;
   if (!attr_set) {
-    hipError_t e = set_lds_limit(qgemm_rows<BITS, WM, WN, MW, R, EPI, false>);
+    hipError_t e = set_lds_limit(qgemm_rows<BITS, WM, WN, MW, R, EPI, 0>);
     if constexpr (EPI == 0)
-      if (e == hipSuccess) e = set_lds_limit(qgemm_rows<BITS, WM, WN, MW, R, EPI, true>);
+      if (e == hipSuccess) e = set_lds_limit(qgemm_rows<BITS, WM, WN, MW, R, EPI, 1>);
+    if constexpr (kFF)
+      if (e == hipSuccess) e = set_lds_limit(qgemm_rows<BITS, WM, WN, MW, R, EPI, 2>);
     if (e != hipSuccess) return e;
     attr_set = true;
   }
@@ -817,10 +875,15 @@ hipError_t launch_rows(const KParams& p, hipStream_t st) {
                     : q.swz < 0 ? dim3((q.nby + 7) / 8 * 8 * q.nbx) : dim3(q.nbx, q.nby);
   if constexpr (EPI == 0)
     if (p.tdump) {
-      hipLaunchKernelGGL((qgemm_rows<BITS, WM, WN, MW, R, EPI, true>), grid, dim3(256), lds, st, q);
+      hipLaunchKernelGGL((qgemm_rows<BITS, WM, WN, MW, R, EPI, 1>), grid, dim3(256), lds, st, q);
       return hipGetLastError();
     }
-  hipLaunchKernelGGL((qgemm_rows<BITS, WM, WN, MW, R, EPI, false>), grid, dim3(256), lds, st, q);
+  if constexpr (kFF)
+    if (p.ff) {
+      hipLaunchKernelGGL((qgemm_rows<BITS, WM, WN, MW, R, EPI, 2>), grid, dim3(256), lds, st, q);
+      return hipGetLastError();
+    }
+  hipLaunchKernelGGL((qgemm_rows<BITS, WM, WN, MW, R, EPI, 0>), grid, dim3(256), lds, st, q);
   return hipGetLastError();
 }
 
@@ -830,20 +893,28 @@ hipError_t launch_splitk(const KParams& p, hipStream_t st) {
   const dim3 grid((ntiles + WN - 1) / WN, (p.M + 16 * WM - 1) / (16 * WM));
   const size_t lds = ((size_t)p.ng * WM * WN * 256 + (size_t)16 * (WM + WN) * p.ng) * sizeof(int32_t);
   if ((p.ng + 3) / 4 > NGW || lds > 160 * 1024) return hipErrorInvalidValue;
+  constexpr bool kFF = BITS != 8;
   static bool attr_set = false;
   if (!attr_set) {
-    hipError_t e = set_lds_limit(qgemm_splitk<BITS, WM, WN, NGW, EPI, false>);
+    hipError_t e = set_lds_limit(qgemm_splitk<BITS, WM, WN, NGW, EPI, 0>);
     if constexpr (EPI == 0)
-      if (e == hipSuccess) e = set_lds_limit(qgemm_splitk<BITS, WM, WN, NGW, EPI, true>);
+      if (e == hipSuccess) e = set_lds_limit(qgemm_splitk<BITS, WM, WN, NGW, EPI, 1>);
+    if constexpr (kFF)
+      if (e == hipSuccess) e = set_lds_limit(qgemm_splitk<BITS, WM, WN, NGW, EPI, 2>);
     if (e != hipSuccess) return e;
     attr_set = true;
   }
   if constexpr (EPI == 0)
     if (p.tdump) {
-      hipLaunchKernelGGL((qgemm_splitk<BITS, WM, WN, NGW, EPI, true>), grid, dim3(256), lds, st, p);
+      hipLaunchKernelGGL((qgemm_splitk<BITS, WM, WN, NGW, EPI, 1>), grid, dim3(256), lds, st, p);
       return hipGetLastError();
     }
-  hipLaunchKernelGGL((qgemm_splitk<BITS, WM, WN, NGW, EPI, false>), grid, dim3(256), lds, st, p);
+  if constexpr (kFF)
+    if (p.ff) {
+      hipLaunchKernelGGL((qgemm_splitk<BITS, WM, WN, NGW, EPI, 2>), grid, dim3(256), lds, st, p);
+      return hipGetLastError();
+    }
+  hipLaunchKernelGGL((qgemm_splitk<BITS, WM, WN, NGW, EPI, 0>), grid, dim3(256), lds, st, p);
   return hipGetLastError();
 }
 
@@ -1071,7 +1142,7 @@ hipError_t launch_qgemm_qkrope(const DLin& w, const QGemmArgs& a, const QKArgs& 
       (kv.kv_int8 && (!kv.kscale || !kv.vscale)))
     return hipErrorInvalidValue;
   qg::KParams p{a.a, a.as, a.gs, w.codes, w.sz, nullptr, nullptr, a.M, w.N, w.K, w.ng, w.nsteps, w.N,
-                w.post, 0, 0, 0, qa, kv};
+                w.post, 0, 0, 0, w.ff, qa, kv};
   switch (w.bits) {
     case 2: return qg::launch_b2(p, 2, variant, st);
     case 4: return qg::launch_b4(p, 2, variant, st);
@@ -1086,7 +1157,7 @@ hipError_t launch_qgemm_variant(const DLin& w, const QGemmArgs& a, int variant, 
     return hipErrorInvalidValue;
   if (w.pair && (w.N % 32 != 0 || a.tdump)) return hipErrorInvalidValue;
   qg::KParams p{a.a, a.as, a.gs, w.codes, w.sz, a.out, a.tdump, a.M, w.N, w.K, w.ng, w.nsteps, a.ldo,
-                w.post, 0, 0, 0, {}, {}};
+                w.post, 0, 0, 0, w.ff, {}, {}};
   const int epi = w.pair ? 1 : 0;
   switch (w.bits) {
     case 2: return qg::launch_b2(p, epi, variant, st);

@@ -109,10 +109,14 @@ def _gemm_shapes(bits_list, shapes, Ms=(1, 17, 70), pair_check=False):
     dev = ia.Device(0)
     rng = np.random.default_rng(5)
     nv = L.ifr_quant_gemm_variants()
-    for bits in bits_list:
-        for (N, K) in shapes:
-            lin = ia.make_linear(N, K, bits, rng)
-            gate, up = ia.make_linear(N, K, bits, rng), ia.make_linear(N, K, bits, rng)
+    # each shape with codebook zeros (C/2: the two-operation fold) and with
+    # general fp16 zeros (the three-operation fold)
+    for bits, (N, K), zmode in [(b, s, z) for b in bits_list for s in shapes for z in ("codebook", "general")]:
+        if True:
+            zero = None if zmode == "codebook" else rng.uniform(0, (1 << bits) - 1, size=(N, K // 128))
+            lin = ia.make_linear(N, K, bits, rng, zero=zero)
+            gate = ia.make_linear(N, K, bits, rng, zero=zero)
+            up = ia.make_linear(N, K, bits, rng, zero=zero)
             dl, dp = C.c_void_p(), C.c_void_p()
             ia.check(L.ifr_linear_upload(dev.ctx, C.byref(lin.struct), C.byref(dl)), "upload")
             ia.check(L.ifr_linear_upload_pair(dev.ctx, C.byref(gate.struct), C.byref(up.struct),
@@ -130,7 +134,7 @@ def _gemm_shapes(bits_list, shapes, Ms=(1, 17, 70), pair_check=False):
                         continue
                     ia.check(rc, f"variant {v}")
                     out = dev.download(od, np.uint16, (M, N))
-                    assert np.array_equal(out, ref), f"bits {bits} N {N} K {K} M {M} variant {v}"
+                    assert np.array_equal(out, ref), f"bits {bits} N {N} K {K} M {M} variant {v} {zmode}"
                     rc = L.ifr_quant_gemm_variant(dev.ctx, dp, qd.p, sd.p, gd.p, M, od.p, v)
                     if rc != ia.IFR_EDECLINE:
                         ia.check(rc, f"pair variant {v}")
@@ -141,7 +145,7 @@ def _gemm_shapes(bits_list, shapes, Ms=(1, 17, 70), pair_check=False):
                             assert np.array_equal(po_, pair_ref), f"pair variant {v} N {N} K {K} M {M}"
                 for b in (qd, sd, gd, od):
                     b.free()
-                say(f"gemm bits={bits} N={N} K={K} M={M} ok")
+                say(f"gemm bits={bits} N={N} K={K} M={M} zeros={zmode} ok")
             L.ifr_linear_free(dev.ctx, dl)
             L.ifr_linear_free(dev.ctx, dp)
     dev.close()

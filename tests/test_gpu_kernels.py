@@ -119,17 +119,20 @@ def test_qgemm_swiglu_pair(dev, M):
     assert (out == ref).mean() > 0.99
 
 
-@pytest.mark.parametrize("bits", [2, 4, 8])
-def test_qgemm_every_launch_shape_bitexact(dev, bits):
+@pytest.mark.parametrize("bits,zmode", [(2, "codebook"), (4, "codebook"), (8, "codebook"), (2, "general"),
+                                        (4, "general")])
+def test_qgemm_every_launch_shape_bitexact(dev, bits, zmode):
     """Every launch shape of the table gives the oracle's bits (plain), and
     the same bits as every other shape (SwiGLU pair); shapes that do not
-    apply decline with IFR_EDECLINE."""
+    apply decline with IFR_EDECLINE.  Codebook zeros (C/2) run the
+    two-operation fold, general fp16 zeros the three-operation one."""
     rng = np.random.default_rng(900 + bits)
     nv = L.ifr_quant_gemm_variants()
     assert nv >= 2
     for (N, K) in ((512, 1024), (256, 3072), (384, 2048)):
-        lin = ia.make_linear(N, K, bits, rng)
-        gate, up = ia.make_linear(N, K, bits, rng), ia.make_linear(N, K, bits, rng)
+        zero = None if zmode == "codebook" else rng.uniform(0, (1 << bits) - 1, size=(N, K // 128))
+        lin = ia.make_linear(N, K, bits, rng, zero=zero)
+        gate, up = ia.make_linear(N, K, bits, rng, zero=zero), ia.make_linear(N, K, bits, rng, zero=zero)
         dl, dp = C.c_void_p(), C.c_void_p()
         ia.check(L.ifr_linear_upload(dev.ctx, C.byref(lin.struct), C.byref(dl)), "upload")
         ia.check(L.ifr_linear_upload_pair(dev.ctx, C.byref(gate.struct), C.byref(up.struct),
