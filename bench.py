@@ -70,6 +70,12 @@ def parse():
                     help="run only 8 device copies of 1 GiB (HBM traffic counter calibration)")
     ap.add_argument("--cfg5", action="store_true",
                     help="run only the cfg5 27B-class mixed iteration (M ~ 2160) and print its JSON line")
+    ap.add_argument("--cpu-full", action="store_true",
+                    help="run only the full CPU-baseline plan (cfg1 iteration, cfg2 fp32 GEMMs, cfg4 "
+                         "decode windows at C=1 / 4 and the extrapolated loads) and print its JSON line")
+    ap.add_argument("--gemm-case", default="",
+                    help="NAME:M[:REPS] (qkv, o, gate_up, down, c5gu, c5down): repeat one cache-cold "
+                         "GEMM launch shape (for counter collection) and print its JSON line")
     return ap.parse_args()
 
 
@@ -144,7 +150,7 @@ KERNELS = GEMMS + ["attention", "row_quant", "qk_rope_kv", "combine", "quant_pla
 # the rocprofv3 kernel names each timing category covers (each GEMM category:
 # qgemm_splitk<...> for M <= 64, qgemm_rows<...> above)
 ROCPROF_NAMES = {"attention": "attn_kernel<{kv}, 1>",
-                 "combine": "combine_kernel", "row_quant": "row_quant1024_kernel",
+                 "combine": "combine_kernel<8>", "row_quant": "row_quant1024_kernel",
                  "quant_plain": "quant_plain8<384>", "qk_rope_kv": "qk_rope_kv_kernel",
                  "lmhead": "lmhead_kernel<...> + argmax_final_kernel", "pack": "pack_kernel"}
 PEAK_FLOPS = {"qgemm": INT8_PEAK, "attention": FP16_PEAK, "lmhead": INT8_PEAK, **{g: INT8_PEAK for g in GEMMS}}
@@ -159,6 +165,22 @@ def traffic_from_profile(kernel, kv_int8):
     for line in f.read_text().splitlines():
         if line.startswith("hbm_bytes_per_launch:"):
             return float(line.split(":", 1)[1])
+    return None
+
+
+def rocprof_avg_us(rocprof_kernel):
+    """Average duration of one kernel in the committed rocprofv3 kernel-trace
+    summary of the same load (profiles/serve_load_cfg4_c64_kernel_stats.md)."""
+    f = ROOT / "profiles" / "serve_load_cfg4_c64_kernel_stats.md"
+    if not f.exists():
+        return None
+    for line in f.read_text().splitlines():
+        cells = [c.strip().strip("`") for c in line.split("|")]
+        if len(cells) > 4 and cells[1].replace("void ", "") == rocprof_kernel:
+            try:
+                return float(cells[4])
+            except ValueError:
+                return None
     return None
 
 
@@ -183,8 +205,16 @@ def kernel_roofline(name, st, kv_int8, brief=False):
         return r
     tr = traffic_from_profile(name, kv_int8)
     r["traffic"] = round(tr) if tr is not None else None
-    r.update({"kernel": name, "rocprof_kernel": ROCPROF_NAMES.get(name, name).format(
-                  kv="true" if kv_int8 else "false"),
+    rk = ROCPROF_NAMES.get(name, name).format(kv="true" if kv_int8 else "false")
+    ra = rocprof_avg_us(rk)
+    r["basis"] = ("avg_us: HIP events around every launch of this kind on the engine stream in a "
+                  "separate timing pass of the same load (the event pairs add gaps between launches); "
+                  "rocprof_avg_us: the committed rocprofv3 kernel-trace average of the same kernel")
+    r["rocprof_avg_us"] = ra
+    if ra and n:
+        per = (f if r["bound"] == "mfma" else b) / n
+        r["frac_rocprof"] = round(per / (ra * 1e-6) / (pk if r["bound"] == "mfma" else HBM_PEAK), 4)
+    r.update({"kernel": name, "rocprof_kernel": rk,
               "bytes_per_launch": round(b / n) if n else None,
               "flops_per_launch": round(f / n) if n else None,
               "peak_time_us": {"hbm": round(t_hbm / n * 1e6, 2) if n else None,
@@ -297,6 +327,59 @@ SHAPES_27B = [("qkv", 5120, 7168, False), ("o", 5120, 5120, False), ("gate_up", 
               ("down", 17408, 5120, False)]
 
 
+GEMM_CASES = {"qkv": SHAPES_08B[0], "o": SHAPES_08B[1], "gate_up": SHAPES_08B[2], "down": SHAPES_08B[3],
+              "c5gu": SHAPES_27B[2], "c5down": SHAPES_27B[3]}
+
+
+def gemm_case(ia, dev, spec, reps=20):
+    """One W2A8 projection (codebook zeros, as the synthetic model) at one M
+    through the engine's default launch shape, cache-cold (rotating weight
+    copies over > 320 MB), `reps` passes: the workload of the counter runs
+    under rocprofv3 --pmc."""
+    import ctypes as C
+    parts = spec.split(":")
+    name, M = parts[0], int(parts[1])
+    if len(parts) > 2:
+        reps = int(parts[2])
+    _, K, N, pair = GEMM_CASES[name]
+    L = ia.lib()
+    rng = np.random.default_rng(0)
+    lins = [ia.make_linear(N, K, 2, rng) for _ in range(2 if pair else 1)]
+    wb = sum(l.N * K * 2 // 8 + l.N * (K // 128) * 4 for l in lins)
+    R = int(np.ceil(320e6 / wb))
+    dls = []
+    for _ in range(R):
+        d = C.c_void_p()
+        if pair:
+            ia.check(L.ifr_linear_upload_pair(dev.ctx, C.byref(lins[0].struct), C.byref(lins[1].struct),
+                                              C.byref(d)), "upload")
+        else:
+            ia.check(L.ifr_linear_upload(dev.ctx, C.byref(lins[0].struct), C.byref(d)), "upload")
+        dls.append(d)
+    q = dev.upload(rng.integers(-127, 128, size=((M + 15) // 16 * 16) * K, dtype=np.int8))
+    asc = dev.upload(np.full(M, 1e-3, dtype=np.float32))
+    gs = dev.upload(rng.integers(-2000, 2000, size=M * (K // 128)).astype(np.float32))
+    out = dev.alloc(M * N * 2 * 2)
+    fn = L.ifr_quant_gemm_swiglu if pair else L.ifr_quant_gemm
+    extra = () if pair else (None,)
+    dev.timer_begin()
+    for _ in range(reps):
+        for d in dls:
+            ia.check(fn(dev.ctx, d, q.p, asc.p, gs.p, M, out.p, *extra), "gemm")
+    ms = dev.timer_end()
+    us = ms * 1e3 / (reps * R)
+    ops = 2.0 * M * N * len(lins) * K
+    byts = wb + M * K + M * 4 + M * N * len(lins) * 2
+    for b in (q, asc, gs, out):
+        b.free()
+    for d in dls:
+        L.ifr_linear_free(dev.ctx, d)
+    return {"metric": "quant-GEMM case (cache-cold, default launch shape)", "shape": name, "M": M, "N": N,
+            "K": K, "pair": pair, "launches": reps * R, "us": round(us, 2), "TOPS": round(ops / us / 1e6, 1),
+            "mfma_frac": round(ops / us / 1e6 / 5000, 4), "GBps": round(byts / us / 1e3, 1),
+            "hbm_frac": round(byts / us / 1e3 / 8000, 4)}
+
+
 def gemm_variants(ia, dev, Ms=(128, 256, 576, 1024), bits=2, reps=3, shapes=SHAPES_08B):
     """Every launch shape of the quant GEMM on the four projection shapes
     (gate_up as the interleaved SwiGLU pair the forward runs), cache-cold as
@@ -402,13 +485,76 @@ def decode_gemm_brief(ia, dev, reps=3):
     return res
 
 
+def _read(path, default=""):
+    try:
+        with open(path) as f:
+            return f.read().strip()
+    except OSError:
+        return default
+
+
+def _cpulist(text):
+    cpus = set()
+    for part in text.split(","):
+        if "-" in part:
+            lo, hi = part.split("-")
+            cpus.update(range(int(lo), int(hi) + 1))
+        elif part.strip():
+            cpus.add(int(part))
+    return cpus
+
+
+def gpu_numa_node():
+    """NUMA node of the GPU this process sees: the render node under /dev/dri
+    (the container shows only its own card) mapped to its PCI device."""
+    try:
+        nodes = sorted(n for n in os.listdir("/dev/dri") if n.startswith("renderD"))
+    except OSError:
+        return None
+    found = set()
+    for n in nodes:
+        dev = f"/sys/class/drm/{n}/device"
+        if _read(dev + "/vendor") != "0x1002":
+            continue
+        v = _read(dev + "/numa_node", "-1")
+        if v.lstrip("-").isdigit():
+            found.add(int(v))
+    # -1: the platform reports no NUMA locality for the device
+    return found.pop() if len(found) == 1 else None
+
+
+def bind_host_cpus():
+    """Pin this process (and the CPU path's OpenMP threads it starts later) to
+    the CPUs of the GPU's NUMA node that it may use, and describe the host:
+    CPU model, nproc, the CPU set, its physical cores and the thread count."""
+    allowed = os.sched_getaffinity(0)
+    node = gpu_numa_node()
+    bound = False
+    if node is not None and node >= 0:
+        mine = _cpulist(_read(f"/sys/devices/system/node/node{node}/cpulist")) & allowed
+        if mine:
+            os.sched_setaffinity(0, mine)
+            allowed, bound = mine, True
+    cores = {(_read(f"/sys/devices/system/cpu/cpu{c}/topology/physical_package_id"),
+              _read(f"/sys/devices/system/cpu/cpu{c}/topology/core_id")) for c in allowed}
+    model_name = ""
+    for ln in _read("/proc/cpuinfo").splitlines():
+        if ln.startswith("model name"):
+            model_name = ln.split(":", 1)[1].strip()
+            break
+    threads = int(os.environ.get("OMP_NUM_THREADS", len(allowed)))
+    return {"host_cpu": model_name, "host_nproc": os.cpu_count(), "gpu_numa_node": node,
+            "numa_bound": bound, "cpus": len(allowed), "physical_cores": len(cores),
+            "omp_threads": threads, "cores": min(threads, len(allowed))}
+
+
 def cpu_baseline(ia, model, cfg):
     """Reference CPU path on a bounded sample with the load's per-output-token
     mix: 4 decode rows at the load's mean context (1088) + one 66-row prefill
     chunk at offset 512 (each request of the load prefills ~16.5 tokens per
     output token).  cpu tok/s = decode rows / iteration time."""
     from oracle import pyoracle as po
-    threads = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
+    host = bind_host_cpus()
     ora = po.OracleEngine(model, mode=1, max_seqs=8)
     rng = np.random.default_rng(0)
     ctx, D, P, off = 1088, 4, 66, 512
@@ -427,17 +573,111 @@ def cpu_baseline(ia, model, cfg):
     ora.forward(rows)
     dt = time.perf_counter() - t0
     ora.close()
-    model_name = ""
-    try:
-        with open("/proc/cpuinfo") as f:
-            model_name = next((ln.split(":", 1)[1].strip() for ln in f if ln.startswith("model name")), "")
-    except OSError:
-        pass
-    return {"value": D / dt, "unit": "tok/s", "cores": threads, "kind": "port",
-            "host_cpu": model_name, "host_nproc": os.cpu_count(),
+    return {"value": D / dt, "unit": "tok/s", "cores": host["cores"], "kind": "port", **host,
             "sample": f"one mixed iteration of the 28-layer f32 CPU path: {D} decode rows at "
                       f"context {ctx} + a {P}-row prefill chunk at offset {off} "
-                      f"(the load's ~16.5 prefill tokens per output token); {dt:.1f} s"}
+                      f"(the load's ~16.5 prefill tokens per output token); {dt:.1f} s; "
+                      "the full plan (bench.py --cpu-full) times cfg1, cfg2 and cfg4 C=1 / 4"}
+
+
+def cpu_full(ia, wl):
+    """The CPU-baseline plan on the host cores: the reference CpuBackend path
+    restated (oracle f32 mode: weights dequantized once to fp32, OpenMP row
+    dot above M*N >= 2048, single-threaded host attention, fp32 tied lm_head).
+      cfg1  one mixed iteration (4 decode rows at contexts 17 / 133 / 512 /
+            1000 + a 60-row prefill chunk), best of 2
+      cfg2  the fp32-dequant dot of every 0.8B GEMM shape at M = 1 .. 1024
+      cfg4  decode iterations at C = 1 and C = 4 (each sequence's context
+            = its cfg4 prompt, KV seeded N(0,1), one row per sequence per
+            iteration, argmax fed back), 8 iterations each
+      load  C = 1, 4, 64 loads extrapolated from those: prompt tokens x the
+            prefill cost per row (cfg1 minus its decode rows) + C x 64 decode
+            rows x the decode cost per row at C = 4"""
+    from oracle import pyoracle as po
+    host = bind_host_cpus()
+    cfg = ia.default_cfg()
+    log("cpu-full: building the synthetic 0.8B-class INT2 model")
+    model = ia.SynthModel(cfg, seed=11, bits=2)
+    out = {"metric": "reference CPU path (f32 CpuBackend restatement) on the host cores", "kind": "port",
+           **host}
+    ora = po.OracleEngine(model, mode=1, max_seqs=8)
+    # cfg1
+    w = wl.cfg1(cfg, seed=1)
+    times = []
+    for _ in range(2):
+        dec = []
+        for (k, v) in w.kv:
+            s = ora.seq_open()
+            ora.set_kv(s, k.reshape(cfg.layers, k.shape[1], -1), v.reshape(cfg.layers, v.shape[1], -1))
+            dec.append(s)
+        pre = ora.seq_open()
+        t0 = time.perf_counter()
+        ora.forward(wl.cfg1_rows(w, dec, pre))
+        times.append(time.perf_counter() - t0)
+        for s in dec + [pre]:
+            ora.seq_close(s)
+    t_cfg1 = min(times)
+    out["cfg1"] = {"iteration_s": [round(t, 3) for t in times], "rows": 64}
+    log(f"cpu-full: cfg1 iteration {t_cfg1:.2f} s")
+    # cfg2: fp32-dequant dot per shape and M (weights dequantized beforehand)
+    O = po.oracle()
+    rng = np.random.default_rng(2)
+    g2 = []
+    for name, K, N in (("qkv", 1024, 4096), ("o", 2048, 1024), ("gate_up", 1024, 6144), ("down", 3072, 1024)):
+        W = rng.standard_normal((N, K), dtype=np.float32)
+        for M in (1, 8, 16, 64, 256, 1024):
+            X = rng.standard_normal((M, K), dtype=np.float32)
+            Y = np.empty((M, N), np.float32)
+            t0 = time.perf_counter()
+            O.or_gemm_f32(po.ptr(W), po.ptr(X), po.ptr(Y), M, N, K)
+            dt = time.perf_counter() - t0
+            g2.append({"shape": name, "M": M, "N": N, "K": K, "ms": round(1e3 * dt, 3),
+                       "GFLOPs": round(2.0 * M * N * K / dt / 1e9, 2),
+                       "weight_GBps": round(4.0 * N * K / dt / 1e9, 2)})
+    out["cfg2"] = g2
+    log("cpu-full: cfg2 done")
+    # cfg4 decode windows
+    dec_row = {}
+    for C in (1, 4):
+        prompts = wl.cfg4_requests(C, seed=4, vocab=cfg.vocab)
+        seqs, pos, tok = [], [], []
+        for p in prompts:
+            s = ora.seq_open()
+            k = rng.standard_normal((cfg.layers, len(p), cfg.n_kv * cfg.head_dim), dtype=np.float32)
+            ora.set_kv(s, k, k)
+            seqs.append(s)
+            pos.append(len(p))
+            tok.append(int(p[-1]))
+        it = []
+        for _ in range(8):
+            rows = [(s, q, t, 0, 1) for s, q, t in zip(seqs, pos, tok)]
+            t0 = time.perf_counter()
+            best = ora.forward(rows)
+            it.append(time.perf_counter() - t0)
+            pos = [q + 1 for q in pos]
+            tok = [int(b) for b in best]
+        for s in seqs:
+            ora.seq_close(s)
+        t_it = sum(it) / len(it)
+        dec_row[C] = t_it / C
+        out[f"cfg4_c{C}_decode"] = {"iterations": len(it), "iteration_s_mean": round(t_it, 4),
+                                    "tok_s": round(C / t_it, 3),
+                                    "contexts": [len(p) for p in prompts]}
+        log(f"cpu-full: C={C} decode {t_it:.3f} s per iteration")
+    ora.close()
+    # extrapolated loads
+    pre_row = max(t_cfg1 - 4 * dec_row[4], 0.0) / 60
+    loads = {}
+    for C in (1, 4, 64):
+        ptoks = sum(len(p) for p in wl.cfg4_requests(C, seed=4, vocab=cfg.vocab))
+        t = ptoks * pre_row + C * 64 * dec_row[4 if C >= 4 else 1]
+        loads[f"c{C}"] = {"prompt_tokens": ptoks, "load_s": round(t, 1), "tok_s": round(C * 64 / t, 4)}
+    out["cfg4_loads_extrapolated"] = {"prefill_s_per_row": round(pre_row, 5),
+                                      "decode_s_per_row": {str(k): round(v, 5) for k, v in dec_row.items()},
+                                      **loads}
+    model.close()
+    print(json.dumps(out))
+    return 0
 
 
 def cfg5_bench(ia, a):
@@ -577,6 +817,14 @@ def main():
         return 0
     if a.cfg5:
         return cfg5_bench(ia, a)
+    if a.cpu_full:
+        return cpu_full(ia, wl)
+    if a.gemm_case:
+        dev = ia.Device(0)
+        res = gemm_case(ia, dev, a.gemm_case)
+        print(json.dumps(res))
+        dev.close()
+        return 0
     if a.attn_sweep:
         dev = ia.Device(0)
         res = attn_sweep(ia, dev, splits=tuple(int(x) for x in a.attn_splits.split(",")))
@@ -653,12 +901,10 @@ def main():
         dt, toks, iters, rows, _ = run_load(ia, eng, prompts, max_new, chunk, record=rec)
         stats = {k: eng.timing(k) for k in KERNELS}
         eng.set_timing(False)
-        busy = sum(v[0] for v in stats.values())
         dom = max(KERNELS, key=lambda k: stats[k][0])
         out["roofline"] = kernel_roofline(dom, stats[dom], a.kv_int8)
         out["kernels"] = {k: kernel_roofline(k, v, a.kv_int8, brief=True)
                           for k, v in stats.items() if v[1]}
-        out["gpu_busy_frac"] = round(busy / (dt * 1e3), 3)
         g = [stats[k] for k in GEMMS]
         out["quant_gemm"] = kernel_roofline("qgemm", tuple(sum(x[i] for x in g) for i in range(4)),
                                             a.kv_int8, brief=True)

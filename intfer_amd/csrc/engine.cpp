@@ -408,6 +408,28 @@ void attn_work(const ifr_ctx* c, const ifr_row* rows, int M, const std::vector<i
   *flops = f;
 }
 
+// Bytes the combine pass moves: each row's fp32 partial (O, m, l) of every
+// q head over its splits (a q-block's split count is ceil(kv_hi / split)),
+// and the int8 row, its scale and group sums out.
+double combine_work(const ifr_ctx* c, int M, const std::vector<int>& g_pos0, const std::vector<int>& g_len,
+                    int split, int qb) {
+  const int nq = c->cfg.n_heads, hd = c->cfg.head_dim;
+  double b = (double)M * (nq * hd + 4 + nq * hd / 128 * 4);
+  for (size_t g = 0; g < g_len.size(); ++g)
+    for (int t = 0; t < g_len[g]; ++t) {
+      const int kvhi = g_pos0[g] + std::min((t / qb + 1) * qb, g_len[g]);
+      b += (double)nq * ((kvhi + split - 1) / split) * (hd * 4 + 8);
+    }
+  return b;
+}
+
+// Bytes the pack pass moves: the rows in, the per-row maps, the group
+// offsets, the units and the dispatch order out.
+double pack_work(int M, size_t ngroups, long nunits, int nslots) {
+  return (double)M * (5 + 7) * 4 + (double)(ngroups + 1) * 4 + (double)nunits * sizeof(ifrk::AttnUnit) +
+         (double)nslots * 4;
+}
+
 // Groups of at least this many rows are prefill chunks: ifr_forward runs them
 // on lane 1 while the decode / verify rows run on lane 0.
 constexpr int kChunkRows = 32;
@@ -423,7 +445,7 @@ struct SubBatch {
   std::vector<int> want_logits;    // positions in `want` of the rows with want = 2
   int split = 0, nslots = 0;
   long nunits = 0, nchunked = 0;
-  double attn_bytes = 0, attn_flops = 0;
+  double attn_bytes = 0, attn_flops = 0, comb_bytes = 0, pack_bytes = 0;
 };
 
 int prep_sub(ifr_ctx* c, const ifr_row* rows, SubBatch& sb) {
@@ -445,6 +467,8 @@ int prep_sub(ifr_ctx* c, const ifr_row* rows, SubBatch& sb) {
   sb.nslots = (int)ifrk::attn_slot_count(sb.g_pos0.data(), sb.g_len.data(), (int)sb.g_len.size(), nkv,
                                          sb.split, c->qb, &sb.nchunked);
   attn_work(c, r, sb.M, sb.g_pos0, sb.g_len, &sb.attn_bytes, &sb.attn_flops);
+  sb.comb_bytes = combine_work(c, sb.M, sb.g_pos0, sb.g_len, sb.split, c->qb);
+  sb.pack_bytes = pack_work(sb.M, sb.g_len.size(), sb.nunits, sb.nslots);
   if (sb.lane == 0) {
     c->last_split = sb.split;
     c->last_units = (int)sb.nunits;
@@ -460,7 +484,7 @@ int launch_head(ifr_ctx* c, const ifr_row* rows, const SubBatch& sb) {
   std::memcpy(L.rows_h, r, (size_t)sb.M * sizeof(ifr_row));
   HIPCHK(hipMemcpyAsync(L.rows_d, L.rows_h, (size_t)sb.M * sizeof(ifr_row), hipMemcpyHostToDevice, L.st));
   {
-    Scope sc(c, L.st, "pack", 0);
+    Scope sc(c, L.st, "pack", sb.pack_bytes);
     HIPCHK(ifrk::launch_pack(L.rows_d, sb.M, c->cfg.n_kv, c->qb, sb.split, L.pk, L.st));
   }
   for (int m = 0; m < sb.M; ++m) L.tok_h[m] = r[m].token;
@@ -542,7 +566,7 @@ int launch_layer(ifr_ctx* c, const SubBatch& sb, int l) {
   {
     ifrk::CombineArgs a{L.part_o, L.part_ml, L.pk.comb_base, L.pk.comb_nsplit, L.pk.comb_tok,
                         M, nq, nkv, hd, nullptr, L.aq, L.as, L.gs, 16 * kAttnTiles};
-    Scope sc(c, L.st, "combine", 0);
+    Scope sc(c, L.st, "combine", sb.comb_bytes);
     HIPCHK(ifrk::launch_combine(a, L.st));
   }
   // (5) O projection
@@ -1450,7 +1474,7 @@ int ifr_attention(ifr_ctx* c, int32_t layer, const ifr_row* rows, int32_t M, con
                        M, nq, nkv, hd, out_d, c->lane[0].aq, c->lane[0].as, c->lane[0].gs, 16 * kAttnTiles};
   hipError_t e;
   {
-    Scope sc(c, c->st, "combine", 0);
+    Scope sc(c, c->st, "combine", combine_work(c, M, g_pos0, g_len, split, c->qb));
     e = ifrk::launch_combine(cb, c->st);
   }
   if (e == hipSuccess) e = hipMemcpyAsync(out_h, out_d, (size_t)M * nq * hd * sizeof(float), hipMemcpyDeviceToHost, c->st);
