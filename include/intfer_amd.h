@@ -57,6 +57,13 @@ typedef struct ifr_model_cfg {
   int32_t group_size; /* weight K-group (128) */
   int32_t qk_norm;    /* 1: per-head RMSNorm(1+w) on q and k (main.cpp:7641-7650) */
   int32_t rotate;     /* 1: online Hadamard at the QKV/O/FFN_IN/FFN_OUT sites */
+  int32_t attn_gate;  /* 1: attention output gate (ModelConfig::attn_output_gate,
+                       * main.cpp:108): q_proj has 2 * n_heads * head_dim rows,
+                       * head h's q rows [2h*hd, 2h*hd + hd) followed by its gate
+                       * rows [2h*hd + hd, 2h*hd + 2hd) (main.cpp:7625-7640), and
+                       * the attention output is scaled by sigmoid(gate) before
+                       * the O projection (:7697-7698); 0: q_proj has
+                       * n_heads * head_dim rows, no gate */
 } ifr_model_cfg;
 
 /* One quantized linear y = W x, W is [N][K].  Logical (load) layout:
@@ -426,9 +433,11 @@ int ifr_intfer_dequant(const ifr_intfer* f, int32_t i, float* out);
  * dequantized to fp32.  cfg->rotate is set from the file: 1 when every
  * linear's rotation (looked up by rotation_id, main.cpp:839-850) is the
  * canonical Hadamard of the hidden size, 0 when none has one.
+ * cfg->attn_gate is set from the file as well: 1 when q_proj has
+ * 2 * n_heads * head_dim rows ([q, gate] per head, main.cpp:7624-7640).
  * IFR_EDECLINE for content this engine does not run: FP16 / FP8-scale /
- * non-128-group linears, gated q_proj (2 * n_heads * head_dim rows), dense
- * rotations, or a mix of rotated and unrotated linears.  Free the model
+ * non-128-group linears, dense rotations, or a mix of rotated and
+ * unrotated linears.  Free the model
  * with ifr_host_model_free; it does not borrow the file. */
 int ifr_intfer_host_model(const ifr_intfer* f, const ifr_model_cfg* cfg, ifr_host_model** out);
 

@@ -23,7 +23,7 @@ class ModelCfg(C.Structure):
                 ("n_kv", C.c_int32), ("head_dim", C.c_int32), ("inter", C.c_int32),
                 ("vocab", C.c_int32), ("rotary_dim", C.c_int32), ("rms_eps", C.c_float),
                 ("rope_theta", C.c_float), ("group_size", C.c_int32), ("qk_norm", C.c_int32),
-                ("rotate", C.c_int32)]
+                ("rotate", C.c_int32), ("attn_gate", C.c_int32)]
 
 
 class Linear(C.Structure):

@@ -360,6 +360,16 @@ __global__ __launch_bounds__(256) void combine_kernel(CombineArgs a) {
   const int ns = a.comb_nsplit[m];
   const int base = a.comb_base[m] + kvh * ns;
   const int col = a.comb_tok[m] * G + j;
+  // the output gate's CS fp16 values (issued first; used after the merge)
+  uint32_t gw[CS / 2];
+  if (a.gate) {
+    const uint4* gp = reinterpret_cast<const uint4*>(a.gate + (size_t)m * N + e0);
+#pragma unroll
+    for (int r = 0; r < CS / 8; ++r) {
+      const uint4 x = gp[r];
+      gw[4 * r] = x.x; gw[4 * r + 1] = x.y; gw[4 * r + 2] = x.z; gw[4 * r + 3] = x.w;
+    }
+  }
   float mx = -INFINITY;
   float L = 0.0f;
   float acc[CS];
@@ -434,7 +444,12 @@ __global__ __launch_bounds__(256) void combine_kernel(CombineArgs a) {
   float amax = 0.0f;
 #pragma unroll
   for (int i = 0; i < CS; ++i) {
-    const float v = acc[i] * invL;
+    float v = acc[i] * invL;
+    if (a.gate) {  // attn *= sigmoid(gate) (main.cpp:7697-7698, sigmoidf of :294)
+      const float g = ifrd::h2f((uint16_t)(gw[i >> 1] >> (16 * (i & 1))));
+      v *= 1.0f / (1.0f + expf(-g));
+    }
+    acc[i] = v;
     amax = fmaxf(amax, fabsf(v));
     if (own && a.attn_out) a.attn_out[(size_t)m * N + e0 + i] = v;
   }
@@ -453,7 +468,7 @@ __global__ __launch_bounds__(256) void combine_kernel(CombineArgs a) {
   for (int i = 0; i < CS / 4; ++i) w[i] = 0u;
 #pragma unroll
   for (int i = 0; i < CS; ++i) {
-    const int c = ifrd::quant_half_away(acc[i] * invL, inv);
+    const int c = ifrd::quant_half_away(acc[i], inv);
     w[i >> 2] |= (uint32_t)(c & 0xFF) << (8 * (i & 3));
     csum += c;
   }

@@ -118,6 +118,7 @@ struct Lane {
   float* gs = nullptr;
   uint16_t* qkv = nullptr;
   uint16_t* qbuf = nullptr;
+  uint16_t* gate = nullptr;   // [M][n_heads * head_dim] attention output gate (gated models)
   uint16_t* y = nullptr;
   uint16_t* mg = nullptr;
   uint16_t* gu = nullptr;
@@ -499,6 +500,7 @@ int launch_layer(ifr_ctx* c, const SubBatch& sb, int l) {
   const int M = sb.M;
   const int H = cf.hidden, hd = cf.head_dim, nq = cf.n_heads, nkv = cf.n_kv;
   const int qN = nq * hd, kvN = nkv * hd, F = cf.inter;
+  const int qkvN = (cf.attn_gate ? 2 * qN : qN) + 2 * kvN;  // QKV output width
   Layer& ly = c->layers[l];
   ifrk::KVLayout kv{nkv, hd, kPage, c->max_pages, c->kv.kv_int8, c->kpool[l], c->vpool[l],
                     c->kscale[l], c->vscale[l], c->bt_d};
@@ -531,10 +533,10 @@ int launch_layer(ifr_ctx* c, const SubBatch& sb, int l) {
   // (2) QKV and (3) q/k norm + RoPE + KV append: one launch when the QKV
   // GEMM's launch shape holds one head per workgroup, else two passes
   const ifrk::QKArgs qka{L.qkv, L.pk.row_seq, L.pk.row_pos, ly.q_norm, ly.k_norm, c->rope_cos,
-                         c->rope_sin, cf.rotary_dim, cf.rms_eps, nq, L.qbuf, M};
+                         c->rope_sin, cf.rotary_dim, cf.rms_eps, nq, L.qbuf, M, cf.attn_gate, L.gate};
   bool fused = false;
   if (!c->kv.separate_qk && ly.nqkv == 1) {
-    ifrk::QGemmArgs a{L.aq, L.as, L.gs, nullptr, nullptr, M, qN + 2 * kvN};
+    ifrk::QGemmArgs a{L.aq, L.as, L.gs, nullptr, nullptr, M, qkvN};
     Scope sc(c, L.st, "qgemm_qkv", (double)ly.qkv[0].bytes + (double)M * (H + 4) + (double)M * ly.qkv[0].N * 2,
              2.0 * M * ly.qkv[0].N * H);
     const hipError_t e = ifrk::launch_qgemm_qkrope(ly.qkv[0], a, qka, kv, -1, L.st);
@@ -548,12 +550,12 @@ int launch_layer(ifr_ctx* c, const SubBatch& sb, int l) {
   }
   if (!fused) {
     for (int j = 0; j < ly.nqkv; ++j) {
-      ifrk::QGemmArgs a{L.aq, L.as, L.gs, L.qkv + ly.qkv_off[j], nullptr, M, qN + 2 * kvN};
+      ifrk::QGemmArgs a{L.aq, L.as, L.gs, L.qkv + ly.qkv_off[j], nullptr, M, qkvN};
       Scope sc(c, L.st, "qgemm_qkv", (double)ly.qkv[j].bytes + (double)M * (H + 4) + (double)M * ly.qkv[j].N * 2,
                2.0 * M * ly.qkv[j].N * H);
       HIPCHK(ifrk::launch_qgemm(ly.qkv[j], a, L.st));
     }
-    Scope sc(c, L.st, "qk_rope_kv", (double)M * (qN + 2 * kvN) * 2 * 2);
+    Scope sc(c, L.st, "qk_rope_kv", (double)M * qkvN * 2 * 2);
     HIPCHK(ifrk::launch_qk_rope_kv(qka, kv, L.st));
   }
   // (4) attention + combine (emits the O-proj int8 input)
@@ -565,7 +567,8 @@ int launch_layer(ifr_ctx* c, const SubBatch& sb, int l) {
   }
   {
     ifrk::CombineArgs a{L.part_o, L.part_ml, L.pk.comb_base, L.pk.comb_nsplit, L.pk.comb_tok,
-                        M, nq, nkv, hd, nullptr, L.aq, L.as, L.gs, 16 * kAttnTiles};
+                        M, nq, nkv, hd, nullptr, L.aq, L.as, L.gs, 16 * kAttnTiles,
+                        cf.attn_gate ? L.gate : nullptr};
     Scope sc(c, L.st, "combine", sb.comb_bytes);
     HIPCHK(ifrk::launch_combine(a, L.st));
   }
@@ -933,7 +936,7 @@ int ifr_model_load(ifr_ctx* c, const ifr_host_model* m, const ifr_kv_cfg* kvc) {
   for (int l = 0; l < L; ++l) {
     const ifr_layer_w& lw = m->layers[l];
     Layer& ly = c->layers[l];
-    if (lw.q.N != qN || lw.k.N != kvN || lw.v.N != kvN || lw.o.N != H || lw.o.K != qN ||
+    if (lw.q.N != (cf.attn_gate ? 2 * qN : qN) || lw.k.N != kvN || lw.v.N != kvN || lw.o.N != H || lw.o.K != qN ||
         lw.gate.N != F || lw.up.N != F || lw.down.N != H || lw.down.K != F || lw.q.K != H)
       return fail(IFR_EINVAL, "layer %d: linear shapes do not match the config", l);
     if (lw.q.bits == lw.k.bits && lw.q.bits == lw.v.bits && post_of(lw.q) == post_of(lw.k) &&
@@ -1072,7 +1075,8 @@ int ifr_model_load(ifr_ctx* c, const ifr_host_model* m, const ifr_kv_cfg* kvc) {
     if ((r = walloc(c, &L.rows_d, (size_t)Mx * 5)) || (r = walloc(c, &L.resid, (size_t)Mx * H)) ||
         (r = walloc(c, &L.aq, ifrk::atile_bytes(Mx, Kmax))) || (r = walloc(c, &L.as, (size_t)Mx)) ||
         (r = walloc(c, &L.gs, (size_t)Mx * (Kmax / 128))) ||
-        (r = walloc(c, &L.qkv, (size_t)Mx * (qN + 2 * kvN))) ||
+        (r = walloc(c, &L.qkv, (size_t)Mx * ((cf.attn_gate ? 2 * qN : qN) + 2 * kvN))) ||
+        (cf.attn_gate && (r = walloc(c, &L.gate, (size_t)Mx * qN))) ||
         (r = walloc(c, &L.qbuf, (size_t)Mx * qN)) || (r = walloc(c, &L.y, (size_t)Mx * H)) ||
         (r = walloc(c, &L.mg, (size_t)Mx * F)) || (r = walloc(c, &L.gu, (size_t)Mx * 2 * F)) ||
         (r = walloc(c, &L.pk.cu_seqlens, (size_t)Mx + 1)) || (r = walloc(c, &L.pk.row_grp, Mx)) ||

@@ -119,7 +119,7 @@ struct KVLayout {
   const int32_t* block_table; // [max_seqs][max_pages]
 };
 struct QKArgs {
-  const uint16_t* qkv;        // [M][nq*hd + 2*nkv*hd] fp16
+  const uint16_t* qkv;        // [M][nqb*hd + 2*nkv*hd] fp16, nqb = nq (2 nq gated)
   const int32_t* row_seq;     // [M]
   const int32_t* row_pos;     // [M]
   const float* q_norm;        // [hd] or null
@@ -131,7 +131,27 @@ struct QKArgs {
   int nq;
   uint16_t* qout;             // [M][nq][hd] fp16
   int M;
+  // 1: the q heads of the QKV output are [q | gate] pairs (head-sized column
+  // block 2h is q head h, 2h + 1 its gate), and the gate is copied, as the
+  // fp16 GEMM output, to gout [M][nq][hd]
+  int gated;
+  uint16_t* gout;
 };
+// Head-sized column block b of the QKV output: its kind (0 q, 1 k, 2 v,
+// 3 gate) and head index within that kind.
+__host__ __device__ inline void qkv_block(int b, int nq, int nkv, int gated, int& kind, int& hh) {
+  const int nqb = gated ? 2 * nq : nq;
+  if (b < nqb) {
+    kind = gated && (b & 1) ? 3 : 0;
+    hh = gated ? b >> 1 : b;
+  } else if (b < nqb + nkv) {
+    kind = 1;
+    hh = b - nqb;
+  } else {
+    kind = 2;
+    hh = b - nqb - nkv;
+  }
+}
 hipError_t launch_qk_rope_kv(const QKArgs& a, const KVLayout& kv, hipStream_t st);
 // The QKV projection with the q/k norm + RoPE + KV append as its epilogue
 // (launch_qgemm followed by launch_qk_rope_kv, bit-identical, without the
@@ -214,6 +234,9 @@ struct CombineArgs {
   float* qscale;           // [M]
   float* gsum;             // [M][nq*hd/128]
   int ucols;               // partial columns per unit (16 * col_tiles)
+  // optional fp16 [M][nq*hd] attention output gate: the merged row is scaled
+  // by sigmoid(gate) = 1 / (1 + exp(-gate)) before it is quantized
+  const uint16_t* gate;
 };
 hipError_t launch_combine(const CombineArgs& a, hipStream_t st);
 

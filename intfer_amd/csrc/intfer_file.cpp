@@ -350,8 +350,6 @@ struct Mapper {
     if (t.scale_dtype != 0) return fail(IFR_EDECLINE, "intfer: %s has FP8 scales", t.name.c_str());
     const uint32_t G = t.group > 0 ? t.group : t.K;
     if (G != 128) return fail(IFR_EDECLINE, "intfer: %s group %u, the GEMM needs 128", t.name.c_str(), G);
-    if ((int)t.N == 2 * N && (int)t.K == K && t.role == IFR_ROLE_ATTN_Q)
-      return fail(IFR_EDECLINE, "intfer: %s carries the attention output gate (2x rows)", t.name.c_str());
     if ((int)t.N != N || (int)t.K != K)
       return fail(IFR_EINVAL, "intfer: %s is %ux%u, the config needs %dx%d", t.name.c_str(), t.N, t.K, N, K);
     const int bits = scheme_bits(t.scheme), C = (1 << bits) - 1, ng = K / 128;
@@ -425,9 +423,18 @@ int build_host(const ifr_intfer& f, const ifr_model_cfg& cfg_in, ifr_host_model*
   static const char* const kLin[7] = {"self_attn.q_proj", "self_attn.k_proj", "self_attn.v_proj",
                                       "self_attn.o_proj", "mlp.gate_proj",    "mlp.up_proj",
                                       "mlp.down_proj"};
-  const int Ns[7] = {qN, kvN, kvN, H, F, F, H};
+  int Ns[7] = {qN, kvN, kvN, H, F, F, H};
   const int Ks[7] = {H, H, H, qN, H, H, F};
   const bool left[7] = {false, false, false, true, false, false, true};
+  // the attention output gate is set from the file, as the reference decides
+  // packed_gate from the q projection's size (main.cpp:7624): q_proj with
+  // 2 * n_heads * head_dim rows carries [q, gate] per head
+  cfg.attn_gate = 0;
+  {
+    if (int r = mp.need(pre + "layers.0.self_attn.q_proj.weight", &t)) return r;
+    if ((int)t->N == 2 * qN) cfg.attn_gate = 1;
+    Ns[0] = cfg.attn_gate ? 2 * qN : qN;
+  }
   for (int l = 0; l < Lc; ++l) {
     const std::string lp = pre + "layers." + std::to_string(l) + ".";
     for (int j = 0; j < 4; ++j) {

@@ -276,9 +276,8 @@ __device__ __forceinline__ void qk_epilogue(const KParams& p, float* lds, const 
   const QKArgs& qa = p.qa;
   const KVLayout& kv = p.kv;
   const int nq = qa.nq, nkv = kv.nkv;
-  const int h = (bt0 * 16) / 128;
-  const int kind = h < nq ? 0 : (h < nq + nkv ? 1 : 2);  // q, k, v
-  const int hh = kind == 0 ? h : (kind == 1 ? h - nq : h - nq - nkv);
+  int kind, hh;  // q, k, v or gate
+  qkv_block((bt0 * 16) / 128, nq, nkv, qa.gated, kind, hh);
   const int rr = lane >> 3, sub = lane & 7;
   const int row_l = 8 * wave + rr, m = bm0 + row_l;
   const int mc = min(m, p.M - 1);
@@ -374,8 +373,8 @@ __device__ __forceinline__ void qk_epilogue(const KParams& p, float* lds, const 
     for (int k = 0; k < 4; ++k) w4[k] = (uint32_t)ifrd::f2h(v[2 * k]) | ((uint32_t)ifrd::f2h(v[2 * k + 1]) << 16);
     return make_uint4(w4[0], w4[1], w4[2], w4[3]);
   };
-  if (kind == 0) {
-    uint16_t* dst = qa.qout + ((size_t)m * nq + hh) * 128;
+  if (kind == 0 || kind == 3) {  // q after norm + RoPE; the gate as computed
+    uint16_t* dst = (kind == 0 ? qa.qout : qa.gout) + ((size_t)m * nq + hh) * 128;
     *reinterpret_cast<uint4*>(dst + d0) = pack8(oa);
     *reinterpret_cast<uint4*>(dst + 64 + d0) = pack8(ob);
     return;
@@ -1138,7 +1137,8 @@ hipError_t launch_qgemm_qkrope(const DLin& w, const QGemmArgs& a, const QKArgs& 
                                hipStream_t st) {
   if (a.M <= 0) return hipSuccess;
   if (w.pair || w.K % kG != 0 || w.N % 128 != 0 || !w.codes || !a.a || !a.as || !a.gs || qa.M != a.M ||
-      w.N != (qa.nq + 2 * kv.nkv) * kv.hd || !qa.qout || !kv.kpool || !kv.vpool || !kv.block_table ||
+      w.N != ((qa.gated ? 2 : 1) * qa.nq + 2 * kv.nkv) * kv.hd || !qa.qout || (qa.gated && !qa.gout) ||
+      !kv.kpool || !kv.vpool || !kv.block_table ||
       (kv.kv_int8 && (!kv.kscale || !kv.vscale)))
     return hipErrorInvalidValue;
   qg::KParams p{a.a, a.as, a.gs, w.codes, w.sz, nullptr, nullptr, a.M, w.N, w.K, w.ng, w.nsteps, w.N,

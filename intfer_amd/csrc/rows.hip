@@ -694,13 +694,14 @@ __global__ __launch_bounds__(256) void qk_rope_kv_kernel(QKArgs a, KVLayout kv) 
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int hd = kv.hd, nq = a.nq, nkv = kv.nkv;
   const int h = blockIdx.y * 4 + w;
-  if (h >= nq + 2 * nkv) return;  // no block-wide barrier below
-  const int ncols = (nq + 2 * nkv) * hd;
+  const int nhead = (a.gated ? 2 * nq : nq) + 2 * nkv;  // head-sized column blocks
+  if (h >= nhead) return;  // no block-wide barrier below
+  const int ncols = nhead * hd;
   const int pos = a.row_pos[m], seq = a.row_seq[m];
   const int half = a.rotary / 2;
   float* x = hx[w];
-  const int kind = h < nq ? 0 : (h < nq + nkv ? 1 : 2);  // q, k, v
-  const int hh = kind == 0 ? h : (kind == 1 ? h - nq : h - nq - nkv);
+  int kind, hh;  // q, k, v or gate
+  qkv_block(h, nq, nkv, a.gated, kind, hh);
   // every global load of this wave is issued here, before any use
   const uint32_t y2 = *reinterpret_cast<const uint32_t*>(a.qkv + (size_t)m * ncols + (size_t)h * hd + 2 * lane);
   // (unconditional: loads that a head kind does not need read valid memory
@@ -762,8 +763,8 @@ __global__ __launch_bounds__(256) void qk_rope_kv_kernel(QKArgs a, KVLayout kv) 
   v1 = kind < 2 ? o[1] : r1;
   v0 = ifrd::fp16r(v0);
   v1 = ifrd::fp16r(v1);
-  if (kind == 0) {
-    uint16_t* dst = a.qout + ((size_t)m * nq + hh) * hd;
+  if (kind == 0 || kind == 3) {  // q after norm + RoPE; the gate as computed
+    uint16_t* dst = (kind == 0 ? a.qout : a.gout) + ((size_t)m * nq + hh) * hd;
     *reinterpret_cast<uint32_t*>(dst + 2 * lane) = (uint32_t)ifrd::f2h(v0) | ((uint32_t)ifrd::f2h(v1) << 16);
     return;
   }
@@ -1122,10 +1123,10 @@ hipError_t launch_quant_plain(const float* xf, const uint16_t* xh, int M, int K,
 hipError_t launch_qk_rope_kv(const QKArgs& a, const KVLayout& kv, hipStream_t st) {
   if (a.M <= 0) return hipSuccess;
   if (kv.hd != 128 || a.rotary <= 0 || a.rotary > kv.hd || a.rotary % 2 != 0 || kv.page <= 0 ||
-      !a.qkv || !a.qout || !kv.kpool || !kv.vpool || !kv.block_table)
+      !a.qkv || !a.qout || !kv.kpool || !kv.vpool || !kv.block_table || (a.gated && !a.gout))
     return hipErrorInvalidValue;
   if (kv.kv_int8 && (!kv.kscale || !kv.vscale)) return hipErrorInvalidValue;
-  const int heads = a.nq + 2 * kv.nkv;
+  const int heads = (a.gated ? 2 * a.nq : a.nq) + 2 * kv.nkv;
   hipLaunchKernelGGL(qk_rope_kv_kernel, dim3(a.M, (heads + 3) / 4), dim3(256), 0, st, a, kv);
   return hipGetLastError();
 }

@@ -140,6 +140,39 @@ void make_linear(OwnedLinear& o, ifr_linear& L, int N, int K, int bits, int grou
   L.post = intfer_form ? 2.0f / (float)C : 0.0f;
 }
 
+// The attention output gate: the gate rows are drawn as a linear of their own
+// (stream `tid`), so every other weight of a gated model equals the ungated
+// model of the same seed, and interleaved per head into q_proj: head h's q
+// rows, then its gate rows.  In the .intfer form both halves share the q
+// linear's K-group scales (one scale per group for the whole tensor).
+bool add_gate_rows(OwnedLinear& q, ifr_linear& L, int nh, int hd, int bits, int group, uint64_t seed,
+                   uint64_t tid, bool intfer_form) {
+  const int K = L.K, ng = K / group;
+  if ((size_t)K * bits % 8 || L.N != nh * hd) return false;
+  OwnedLinear g;
+  ifr_linear gl;
+  make_linear(g, gl, nh * hd, K, bits, group, seed, tid, intfer_form);
+  const size_t rb = (size_t)K * bits / 8;
+  OwnedLinear o;
+  o.codes.resize(2 * q.codes.size());
+  o.scale.resize(2 * q.scale.size());
+  o.zero.resize(2 * q.zero.size());
+  for (int h = 0; h < nh; ++h)
+    for (int half = 0; half < 2; ++half) {
+      const OwnedLinear& src = half ? g : q;
+      const size_t r0 = (size_t)h * hd, d0 = (size_t)(2 * h + half) * hd;
+      std::memcpy(&o.codes[d0 * rb], &src.codes[r0 * rb], hd * rb);
+      for (size_t r = 0; r < (size_t)hd; ++r)
+        for (int gi = 0; gi < ng; ++gi) {
+          o.scale[(d0 + r) * ng + gi] = intfer_form ? q.scale[(r0 + r) * ng + gi] : src.scale[(r0 + r) * ng + gi];
+          o.zero[(d0 + r) * ng + gi] = src.zero[(r0 + r) * ng + gi];
+        }
+    }
+  q = std::move(o);
+  L.N = 2 * nh * hd;
+  return true;
+}
+
 void round_fp16(std::vector<float>& v) {
   for (float& x : v) x = ifr::h2f(ifr::f2h(x));
 }
@@ -198,6 +231,12 @@ extern "C" ifr_host_model* ifr_synth_model(const ifr_model_cfg* cfg, uint64_t se
       if (bits_mode == 0) bits = ((splitmix64(split) >> 11) % 10 < 7) ? 2 : 4;
       make_linear(m->lin[(size_t)l * 7 + j], *slots[j], Ns[j], Ks[j], bits, G, seed,
                   1000 + (uint64_t)l * 16 + j, intfer_form);
+      if (j == 0 && cfg->attn_gate)
+        if (!add_gate_rows(m->lin[(size_t)l * 7], *slots[0], cfg->n_heads, hd, bits, G, seed,
+                           1000 + (uint64_t)l * 16 + 7, intfer_form)) {
+          delete m;
+          return nullptr;
+        }
     }
   }
   if (intfer_form) {

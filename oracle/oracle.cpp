@@ -365,6 +365,8 @@ int forward(Engine& e, const ifr_row* rows, int M, int32_t* best, float* logits_
     std::memcpy(&Hs[(size_t)m * H], e.m->embed + (size_t)rows[m].token * H, H * sizeof(float));
   std::vector<float> normed((size_t)M * H), rin((size_t)M * H), qkv((size_t)M * (qN + 2 * kvN));
   std::vector<float> qb((size_t)M * qN), kb((size_t)M * kvN), vb((size_t)M * kvN);
+  // gated q_proj output [M][2 qN] (per head: q rows, then gate rows) and the gate
+  std::vector<float> qg(c.attn_gate ? (size_t)M * 2 * qN : 0), gate(c.attn_gate ? (size_t)M * qN : 0);
   std::vector<float> attn((size_t)M * qN), y((size_t)M * H), tmp(H);
   std::vector<float> g((size_t)M * F), u((size_t)M * F);
   // grow KV
@@ -382,7 +384,18 @@ int forward(Engine& e, const ifr_row* rows, int M, int32_t* best, float* logits_
       if (c.rotate) rot(&normed[(size_t)m * H], &rin[(size_t)m * H], H);
       else std::memcpy(&rin[(size_t)m * H], &normed[(size_t)m * H], H * sizeof(float));
     }
-    linear(e, l, 0, rin.data(), M, qb.data());
+    if (c.attn_gate) {
+      // [q, gate] interleaved per head (main.cpp:7625-7640)
+      linear(e, l, 0, rin.data(), M, qg.data());
+      for (int m = 0; m < M; ++m)
+        for (int h = 0; h < nq; ++h)
+          for (int d = 0; d < hd; ++d) {
+            qb[(size_t)m * qN + h * hd + d] = qg[(size_t)m * 2 * qN + 2 * h * hd + d];
+            gate[(size_t)m * qN + h * hd + d] = qg[(size_t)m * 2 * qN + 2 * h * hd + hd + d];
+          }
+    } else {
+      linear(e, l, 0, rin.data(), M, qb.data());
+    }
     linear(e, l, 1, rin.data(), M, kb.data());
     linear(e, l, 2, rin.data(), M, vb.data());
     // q/k norm, RoPE, KV append: all rows first (main.cpp:7625-7656)
@@ -450,6 +463,9 @@ int forward(Engine& e, const ifr_row* rows, int M, int32_t* best, float* logits_
           }
         }
       }
+      // output gate (main.cpp:7697-7698; sigmoidf of main.cpp:294)
+      if (c.attn_gate)
+        for (int i = 0; i < qN; ++i) at[i] *= 1.0f / (1.0f + std::exp(-gate[(size_t)m * qN + i]));
     }
     // o-proj, rot_left, residual (main.cpp:7702-7727)
     linear(e, l, 3, attn.data(), M, y.data());

@@ -398,6 +398,56 @@ def forward_fused_qk():
 
 
 @scenario
+def forward_gated():
+    """The attention output gate: a gated one-layer model through the fused
+    QKV epilogue (150 prefill rows) and the separate q/k pass (the decode
+    row, and a separate_qk engine): fused == separate bit for bit, tokens
+    equal to the oracle's; and zero gate rows (sigmoid = 1/2) give the
+    ungated model with its O projection halved, bit for bit."""
+    import intfer_amd as ia
+    from oracle import pyoracle as po
+    dev = ia.Device(0)
+    rng = np.random.default_rng(13)
+    prompt = rng.integers(0, 2048, size=150).tolist()
+
+    def run(model, sep):
+        eng = ia.Engine(dev, model, max_seqs=4, max_seq_tokens=512, pool_tokens=4 * 512, max_rows=192,
+                        separate_qk=sep)
+        s = eng.seq_open()
+        b, lg = eng.forward([(s, p, t, ia.ROW_PREFILL, int(p % 50 == 49)) for p, t in enumerate(prompt)],
+                            logits=True)
+        _, lg2 = eng.forward([(s, 150, int(b[-1]), ia.ROW_DECODE, 1)], logits=True)
+        del eng
+        return b, lg, lg2
+
+    cfg = ia.default_cfg(layers=1, vocab=2048, attn_gate=1)
+    model = ia.SynthModel(cfg, seed=6, bits=2)
+    outs = [run(model, sep) for sep in (0, 1)]
+    assert all(np.array_equal(outs[0][i], outs[1][i]) for i in range(3))
+    ora = po.OracleEngine(model, mode=0, max_seqs=4)
+    so = ora.seq_open()
+    bo, lo = ora.forward([(so, p, t, ia.ROW_PREFILL, int(p % 50 == 49)) for p, t in enumerate(prompt)], logits=True)
+    assert np.array_equal(bo, outs[0][0]), (bo, outs[0][0])
+    err = float(np.abs(outs[0][1] - lo).max() / lo.std())
+    assert err <= 0.05, err
+    say(f"gated forward: fused == separate, tokens equal to the oracle, max|dlogit|/std {err:.3g}")
+    model.close()
+    gated = ia.SynthModel(cfg, seed=6, bits=2)
+    plain = ia.SynthModel(ia.default_cfg(layers=1, vocab=2048), seed=6, bits=2)
+    q = gated.layer(0).q
+    sc = np.ctypeslib.as_array(q.scale, shape=(q.N, q.K // 128))
+    for h in range(cfg.n_heads):
+        sc[(2 * h + 1) * 128:(2 * h + 2) * 128] = 0
+    plain.ptr.contents.layers[0].o.post = 0.5
+    a, b = run(gated, 0), run(plain, 0)
+    assert all(np.array_equal(a[i], b[i]) for i in range(3))
+    say("zero gate == ungated with the O projection halved, bit for bit")
+    gated.close()
+    plain.close()
+    dev.close()
+
+
+@scenario
 def prefix_copy():
     """ifr_seq_copy_prefix (the prefix cache's page copy) with fp16 and int8
     KV: a copied prefix plus the recomputed rest gives the same logits, bit

@@ -56,3 +56,7 @@ def test_prefix_copy_and_cache_in_bounds(emu_lib):
 
 def test_fused_qk_epilogue_in_bounds_and_bit_identical(emu_lib):
     assert runner.run_scenarios(["forward_fused_qk"], timeout=900) == 0
+
+
+def test_attention_output_gate_in_bounds(emu_lib):
+    assert runner.run_scenarios(["forward_gated"], timeout=900) == 0

@@ -211,14 +211,15 @@ def numpy_dequant(t: dict) -> np.ndarray:
 
 # ---- writer -> reader -> host model ----------------------------------------------
 
-@pytest.mark.parametrize("bits", [2, 4, 8, 0])
-def test_roundtrip_reproduces_synthetic_model(bits):
-    cfg = small_cfg()
+@pytest.mark.parametrize("bits,gate", [(2, 0), (4, 0), (8, 0), (0, 0), (2, 1), (0, 1)])
+def test_roundtrip_reproduces_synthetic_model(bits, gate):
+    cfg = small_cfg(attn_gate=gate)
     m = ia.SynthModel(cfg, 7, bits, intfer_form=True)
     f = ia.IntferFile(m.write_intfer("rt"))
     assert f.counts() == (2 + 2 * 11, 4, 2) and f.model_id() == "rt"
-    h = f.host_model(cfg)
+    h = f.host_model(small_cfg())  # the gate is read from the file
     assert h.cfg.rotate == 1 and h.cfg.group_size == 128 and not h.ptr.contents.lm_head
+    assert h.cfg.attn_gate == gate
     H, V = cfg.hidden, cfg.vocab
     for l in range(cfg.layers):
         A, B = m.layer(l), h.ptr.contents.layers[l]
@@ -326,11 +327,14 @@ def test_rotation_matrices_are_canonical():
         assert np.allclose(hh, np.eye(256), atol=1e-6)  # symmetric orthogonal: H H = I
 
 
-@pytest.mark.parametrize("variant", ["base", "alpha", "int8q", "int4q"])
+@pytest.mark.parametrize("variant", ["base", "alpha", "int8q", "int4q", "gated"])
 def test_host_linears_dequantize_to_file_values(variant):
-    """scale = s_g, zero = C/2, post = 2*alpha/C reproduces (s_g*alpha)*cb[c]."""
+    """scale = s_g, zero = C/2, post = 2*alpha/C reproduces (s_g*alpha)*cb[c];
+    a q_proj of 2 * n_heads * head_dim rows (the attention output gate) is
+    taken whole and sets attn_gate."""
     rng = np.random.default_rng(77 + len(variant))
-    kw = dict(base={}, alpha=dict(alpha=0.37), int8q=dict(q_bits=8, alpha=2.5), int4q=dict(q_bits=4))[variant]
+    kw = dict(base={}, alpha=dict(alpha=0.37), int8q=dict(q_bits=8, alpha=2.5), int4q=dict(q_bits=4),
+              gated=dict(q_override="gated"))[variant]
     b, ts = crafted_model(rng, **kw)
     f = ia.IntferFile(b)
     cfg = ia.default_cfg(**CRAFT_CFG)
@@ -351,6 +355,8 @@ def test_host_linears_dequantize_to_file_values(variant):
     lm = arr(h.ptr.contents.lm_head, V * H, C.c_float).reshape(V, H)
     assert np.array_equal(lm, f.dequant(f.find("lm_head.weight")))
     assert h.cfg.rotate == 1
+    assert h.cfg.attn_gate == (variant == "gated")
+    assert L.q.N == (2 if variant == "gated" else 1) * cfg.n_heads * cfg.head_dim
 
 
 def test_forward_of_parsed_model_equals_synthetic(tmp_path):
@@ -374,7 +380,6 @@ def test_forward_of_parsed_model_equals_synthetic(tmp_path):
 
 @pytest.mark.parametrize("kw,code", [
     (dict(q_override="fp16"), _abi.IFR_EDECLINE),
-    (dict(q_override="gated"), _abi.IFR_EDECLINE),
     (dict(group=64), _abi.IFR_EDECLINE),
     (dict(rotations="partial"), _abi.IFR_EDECLINE),
 ])

@@ -18,8 +18,13 @@ Each oracle function is checked against something other than itself:
   or_attention_row       float64 softmax attention
   or_rope                float64 cos/sin of the float32 angle
   forward (a8 / f32)     chunk invariance (M=1 == M=8 rows), f32 ~ a8 agreement
-Parity unpinned: none of the oracle functions above; the composition of the
-forward is pinned by its parts plus the invariants in the last tests.
+  forward (f32), whole   a float64 numpy restatement of the layer (norms,
+                         rotation as the dense Hadamard, q/k norm, RoPE,
+                         causal GQA attention, output gate, SwiGLU, tied
+                         lm_head) from the model's own tensors: 1e-4 sigma
+  output gate            zero gate rows == the ungated model with its O
+                         projection halved, bit for bit, a8 and f32
+Parity unpinned: none of the oracle functions above.
 """
 import ctypes as C
 
@@ -392,3 +397,135 @@ def test_attn_dispatch_order_invariants():
         single = [u for u, x in enumerate(units) if sum(1 for r in rows if r[0] == x[0]) <= qb]
         tail = [u for u in order[len(order) - len(single):]] if single else []
         assert tail == single
+
+
+# ---- the forward as a whole, and the attention output gate ---------------------------------------
+
+def _dequant(O, lin):
+    w = np.empty(lin.N * lin.K, np.float32)
+    O.or_dequant(C.byref(lin), ptr(w))
+    return w.reshape(lin.N, lin.K).astype(np.float64)
+
+
+def _vec(p, n):
+    return np.ctypeslib.as_array(p, shape=(n,)).astype(np.float64)
+
+
+def _np_forward_f32(O, m, toks):
+    """float64 restatement of the reference CPU path (step_batch's full-attention
+    branch, main.cpp:7519-7772; tied lm_head :8302-8307) for one sequence's
+    prompt rows at positions 0..M-1, from the model's own tensors: weights
+    dequantized by or_dequant, the rotation as the dense Sylvester Hadamard
+    over sqrt(n), RoPE angles in float32 as the oracle forms them, the output
+    gate as sigmoid of the gate rows [2h hd + hd, 2h hd + 2 hd) of q_proj."""
+    from scipy.linalg import hadamard
+    c = m.cfg
+    H, hd, nq, nkv, F = c.hidden, c.head_dim, c.n_heads, c.n_kv, c.inter
+    G = nq // nkv
+    R = hadamard(H).astype(np.float64) / np.sqrt(H)
+    rot = (lambda x: x @ R.T) if c.rotate else (lambda x: x)
+
+    def rms(x, w):
+        return x / np.sqrt((x * x).mean(axis=-1, keepdims=True) + np.float64(np.float32(c.rms_eps))) * (1.0 + w)
+
+    half = c.rotary_dim // 2
+    pw = np.array([np.float32(float(np.float32(c.rope_theta)) ** (2.0 * d / c.rotary_dim)) for d in range(half)],
+                  np.float32)
+    inv = (np.float32(1.0) / pw).astype(np.float32)
+
+    def rope(x, pos):  # x [..., hd]
+        f = (inv * np.float32(pos)).astype(np.float32).astype(np.float64)
+        a, b = x[..., :half].copy(), x[..., half:2 * half].copy()
+        y = x.copy()
+        y[..., :half] = a * np.cos(f) - b * np.sin(f)
+        y[..., half:2 * half] = a * np.sin(f) + b * np.cos(f)
+        return y
+
+    emb = m.embed().astype(np.float64)
+    M = len(toks)
+    x = emb[toks]
+    for l in range(c.layers):
+        L = m.layer(l)
+        W = {nm: _dequant(O, getattr(L, nm)) for nm in ("q", "k", "v", "o", "gate", "up", "down")}
+        r = rot(rms(x, _vec(L.in_ln, H)))
+        qo = r @ W["q"].T
+        if c.attn_gate:
+            qo = qo.reshape(M, nq, 2, hd)
+            q, gate = qo[:, :, 0], qo[:, :, 1]
+        else:
+            q, gate = qo.reshape(M, nq, hd), None
+        k = (r @ W["k"].T).reshape(M, nkv, hd)
+        v = (r @ W["v"].T).reshape(M, nkv, hd)
+        if c.qk_norm:
+            q = rms(q, _vec(L.q_norm, hd))
+            k = rms(k, _vec(L.k_norm, hd))
+        q = np.stack([rope(q[p], p) for p in range(M)])
+        k = np.stack([rope(k[p], p) for p in range(M)])
+        att = np.zeros((M, nq, hd))
+        for p in range(M):
+            for h in range(nq):
+                s = k[:p + 1, h // G] @ q[p, h] / np.sqrt(hd)
+                e = np.exp(s - s.max())
+                att[p, h] = (e / e.sum()) @ v[:p + 1, h // G]
+        if gate is not None:
+            att = att / (1.0 + np.exp(-gate))
+        x = x + rot(att.reshape(M, nq * hd) @ W["o"].T)
+        r2 = rot(rms(x, _vec(L.post_ln, H)))
+        g, u = r2 @ W["gate"].T, r2 @ W["up"].T
+        x = x + rot((g / (1.0 + np.exp(-g)) * u) @ W["down"].T)
+    return rms(x, _vec(m.model.final_norm, H)) @ emb.T
+
+
+@pytest.mark.parametrize("gate", [0, 1])
+def test_forward_f32_matches_float64_restatement(O, gate):
+    """The f32 (reference CpuBackend) forward, composed, against float64:
+    a wrong head / gate index, a dropped norm or rotation, a sign in the gate
+    or a transposed operand moves the logits far beyond fp32 rounding."""
+    m = ia.SynthModel(tiny_cfg(attn_gate=gate), seed=24)
+    toks = np.random.default_rng(24).integers(0, 512, size=7).tolist()
+    e = po.OracleEngine(m, mode=1)
+    s = e.seq_open()
+    _, lg = e.forward([(s, p, t, 1, 1) for p, t in enumerate(toks)], logits=True)
+    ref = _np_forward_f32(O, m, toks)
+    for r in range(len(toks)):
+        sd = ref[r].std()
+        assert np.abs(lg[r] - ref[r]).max() < 1e-4 * sd, (r, np.abs(lg[r] - ref[r]).max() / sd)
+    e.close()
+
+
+def _zero_gate_pair(cfg_kw, seed):
+    """A gated model whose gate rows all have scale 0 (gate = 0, sigmoid = 1/2
+    exactly) and the ungated model of the same seed with its O projection's
+    post factor 1/2: the same forward, bit for bit, in every path (the
+    per-token quantization of x / 2 gives the codes of x and half the scale)."""
+    gated = ia.SynthModel(tiny_cfg(attn_gate=1, **cfg_kw), seed=seed)
+    plain = ia.SynthModel(tiny_cfg(**cfg_kw), seed=seed)
+    c = gated.cfg
+    hd, nq = c.head_dim, c.n_heads
+    for l in range(c.layers):
+        q = gated.layer(l).q
+        ng = q.K // 128
+        sc = np.ctypeslib.as_array(q.scale, shape=(q.N, ng))
+        for h in range(nq):
+            sc[(2 * h + 1) * hd:(2 * h + 2) * hd] = 0
+        plain.ptr.contents.layers[l].o.post = 0.5
+    return gated, plain
+
+
+@pytest.mark.parametrize("mode", [0, 1])
+def test_zero_gate_is_half_the_attention_output(mode):
+    gated, plain = _zero_gate_pair({}, 25)
+    toks = np.random.default_rng(25).integers(0, 512, size=9).tolist()
+    out = []
+    for m in (gated, plain):
+        e = po.OracleEngine(m, mode=mode)
+        s = e.seq_open()
+        _, lg = e.forward([(s, p, t, 1, 1) for p, t in enumerate(toks)], logits=True)
+        out.append(lg)
+        e.close()
+    assert np.array_equal(out[0].view(np.uint32), out[1].view(np.uint32))
+    # and the gate matters: with its real rows the outputs differ
+    e = po.OracleEngine(ia.SynthModel(tiny_cfg(attn_gate=1), seed=25), mode=mode)
+    s = e.seq_open()
+    _, lg = e.forward([(s, p, t, 1, 1) for p, t in enumerate(toks)], logits=True)
+    assert not np.array_equal(lg, out[1])
