@@ -65,6 +65,9 @@ struct KParams {
   int nbx, nby, swz;
   // 1: every zero of the linear is C/2 (the codebook fold applies)
   int ff;
+  // 1: out is 16-byte aligned and ldo a multiple of 8, so qgemm_rows stores
+  // its output tile as 16-byte row chunks
+  int vst;
   // EPI 2 (QKV projection with the q/k norm + RoPE + KV append epilogue):
   // the arguments of the separate pass (row maps, norms, RoPE tables, q
   // output, paged KV)
@@ -544,6 +547,44 @@ __global__ __launch_bounds__(256) void qgemm_rows(KParams p) {
     qk_epilogue<BM, BN, WM, WN, MW>(p, lds_f, acc, asr, bm0, bt0, wave, lane);
     return;
   }
+  if (!DUMP && p.vst) {
+    // The wave's output tile (16 WM rows x TC columns of fp16) is staged in
+    // its own LDS slice and stored as 16-byte row chunks: the MFMA layout
+    // (a lane holds one column of 4 rows) would write each row in 32-byte
+    // pieces of 2-byte stores, which cost 2.5-4.6 us of a 9-12 us launch at
+    // M = 576..1024.  Same values as store_plain / store_swiglu.
+    constexpr int TR = 16 * WM, TC = EPI == 0 ? 16 * WN : 8 * WN, CPR = TC / 8, NCH = TR * CPR;
+    uint16_t* yt = reinterpret_cast<uint16_t*>(lds_f + ng * (BM + BN)) + wave * TR * TC;
+#pragma unroll
+    for (int i = 0; i < WM; ++i)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int rl = 16 * i + 4 * lgrp + r;
+        if constexpr (EPI == 0) {
+#pragma unroll
+          for (int j = 0; j < WN; ++j) yt[rl * TC + 16 * j + lrow] = ifrd::f2h(asr[i][r] * acc[i][j][r]);
+        } else {
+#pragma unroll
+          for (int j = 0; j < WN; j += 2) {
+            const float g = ifrd::fp16r(asr[i][r] * acc[i][j][r]);
+            const float u = ifrd::fp16r(asr[i][r] * acc[i][j + 1][r]);
+            yt[rl * TC + 8 * j + lrow] = ifrd::f2h(silu_f(g) * u);
+          }
+        }
+      }
+    ifrd::wave_sync();
+    const int col0 = EPI == 0 ? 16 * tile0 : 8 * tile0;
+#pragma unroll
+    for (int q = 0; q < (NCH + 63) / 64; ++q) {
+      const int ch = lane + 64 * q;
+      if (NCH % 64 != 0 && ch >= NCH) break;
+      const int rr = ch / CPR, cc = (ch % CPR) * 8, row = row0 + rr;
+      const bool colv = EPI == 0 ? tile0 + cc / 16 < ntiles : tile0 + 2 * (cc / 16) + 1 < ntiles;
+      const uint4 v = *reinterpret_cast<const uint4*>(yt + rr * TC + cc);
+      if (row < p.M && colv) *reinterpret_cast<uint4*>(p.out + (size_t)row * p.ldo + col0 + cc) = v;
+    }
+    return;
+  }
 #pragma unroll
   for (int i = 0; i < WM; ++i)
 #pragma unroll
@@ -839,6 +880,8 @@ hipError_t launch_rows(const KParams& p, hipStream_t st) {
   constexpr int BM = 16 * WM * MW, BN = 16 * WN * NW;
   if (p.ng % R != 0) return hipErrorInvalidValue;
   size_t lds = (size_t)p.ng * (BM + BN) * sizeof(float);
+  // the output tiles of the 4 waves (16-byte stores)
+  if constexpr (EPI != 2) lds += (size_t)4 * 16 * WM * (EPI == 0 ? 16 * WN : 8 * WN) * sizeof(uint16_t);
   if constexpr (EPI == 2) {
     // the staged y tile (padded rows) and the RMS partial sums
     if (BM != 32 || BN != 128 || p.qa.rotary != 128 || p.kv.hd != 128) return hipErrorInvalidValue;
@@ -858,6 +901,7 @@ hipError_t launch_rows(const KParams& p, hipStream_t st) {
   }
   const int ntiles = p.N / 16;
   KParams q = p;
+  q.vst = EPI != 2 && !p.tdump && reinterpret_cast<uintptr_t>(p.out) % 16 == 0 && p.ldo % 8 == 0;
   q.nbx = (ntiles + BN / 16 - 1) / (BN / 16);
   q.nby = (p.M + BM - 1) / BM;
   // XCD-grouped order by weight columns when an XCD's share of the weights
@@ -1142,7 +1186,7 @@ hipError_t launch_qgemm_qkrope(const DLin& w, const QGemmArgs& a, const QKArgs& 
       (kv.kv_int8 && (!kv.kscale || !kv.vscale)))
     return hipErrorInvalidValue;
   qg::KParams p{a.a, a.as, a.gs, w.codes, w.sz, nullptr, nullptr, a.M, w.N, w.K, w.ng, w.nsteps, w.N,
-                w.post, 0, 0, 0, w.ff, qa, kv};
+                w.post, 0, 0, 0, w.ff, 0, qa, kv};
   switch (w.bits) {
     case 2: return qg::launch_b2(p, 2, variant, st);
     case 4: return qg::launch_b4(p, 2, variant, st);
@@ -1157,7 +1201,7 @@ hipError_t launch_qgemm_variant(const DLin& w, const QGemmArgs& a, int variant, 
     return hipErrorInvalidValue;
   if (w.pair && (w.N % 32 != 0 || a.tdump)) return hipErrorInvalidValue;
   qg::KParams p{a.a, a.as, a.gs, w.codes, w.sz, a.out, a.tdump, a.M, w.N, w.K, w.ng, w.nsteps, a.ldo,
-                w.post, 0, 0, 0, w.ff, {}, {}};
+                w.post, 0, 0, 0, w.ff, 0, {}, {}};
   const int epi = w.pair ? 1 : 0;
   switch (w.bits) {
     case 2: return qg::launch_b2(p, epi, variant, st);

@@ -125,7 +125,9 @@ def test_qgemm_every_launch_shape_bitexact(dev, bits, zmode):
     """Every launch shape of the table gives the oracle's bits (plain), and
     the same bits as every other shape (SwiGLU pair); shapes that do not
     apply decline with IFR_EDECLINE.  Codebook zeros (C/2) run the
-    two-operation fold, general fp16 zeros the three-operation one."""
+    two-operation fold, general fp16 zeros the three-operation one.  An
+    output that is not 16-byte aligned takes the per-element stores instead
+    of the 16-byte row chunks, with the same bits."""
     rng = np.random.default_rng(900 + bits)
     nv = L.ifr_quant_gemm_variants()
     assert nv >= 2
@@ -142,7 +144,8 @@ def test_qgemm_every_launch_shape_bitexact(dev, bits, zmode):
                 x = rng.standard_normal((M, K), dtype=np.float32)
                 q, sc, g = po.act_quant(x)
                 qd, sd, gd = dev.upload(ia.atile(q)), dev.upload(sc[:, 0].copy()), dev.upload(g)
-                od = dev.alloc(M * N * 2)
+                od = dev.alloc(M * N * 2 + 16)
+                od2 = C.c_void_p(od.p.value + 2)  # 2-byte aligned only
                 ref = po.qgemm(q, sc[:, 0], lin)
                 pair_out, ran = None, 0
                 for v in range(nv):
@@ -153,6 +156,9 @@ def test_qgemm_every_launch_shape_bitexact(dev, bits, zmode):
                     ia.check(rc, f"variant {v}")
                     out = dev.download(od, np.uint16, (M, N))
                     assert np.array_equal(out, ref), f"variant {v} N={N} K={K} M={M}"
+                    ia.check(L.ifr_quant_gemm_variant(dev.ctx, dl, qd.p, sd.p, gd.p, M, od2, v), "unaligned")
+                    raw = dev.download(od, np.uint16, (M * N + 8,))
+                    assert np.array_equal(raw[1:1 + M * N].reshape(M, N), ref), f"unaligned variant {v}"
                     ran += 1
                     rc = L.ifr_quant_gemm_variant(dev.ctx, dp, qd.p, sd.p, gd.p, M, od.p, v)
                     if rc == ia.IFR_EDECLINE:
