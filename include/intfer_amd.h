@@ -221,6 +221,21 @@ int ifr_quant_gemm_variant(ifr_ctx* ctx, const ifr_dlinear* w, const int8_t* a_d
                            const float* ascale_d, const float* gsum_d, int32_t M,
                            uint16_t* out_d, int32_t variant);
 
+/* FP16-activation dequant GEMM (replaces quant_gemm_forward_usm, the
+ * reference's default GPU linear, quant_gemm.cpp:359-2153):
+ *   out(m,n) = fp16_rne( sum_k a(m,k) * w(n,k) ), fp32, k ascending
+ *   w(n,k)   = (scale(n,k/128) * alpha) * cb(code(n,k)),
+ * cb the canonical codebook (2c - C)/C as fp32 ({-1, -1/3, 1/3, 1} for
+ * INT2; canon_value :139-144).  M == 1 keeps w in fp32 and accumulates
+ * acc = fma(a, w, acc) (the decode kernels :1026-1080, :2022-2066); M > 1
+ * rounds w to fp16 as the tiled kernel stages it (:2069-2150).  a_d fp16
+ * [M][K] row-major, out_d fp16 [M][N]; alpha is the tensor's global factor
+ * (1 when it has none).  IFR_EDECLINE for a gate/up pair, a linear whose
+ * zeros are not all C/2 (the reference path knows only the codebook), or
+ * K > 32768 at M == 1. */
+int ifr_quant_gemm_f16(ifr_ctx* ctx, const ifr_dlinear* w, const uint16_t* a_d, int32_t M,
+                       float alpha, uint16_t* out_d);
+
 /* ------------------------------------------------------------------------
  * Engine: model load, paged KV, one mixed iteration.
  * ---------------------------------------------------------------------- */

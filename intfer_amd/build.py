@@ -29,7 +29,7 @@ SOURCES = [("qgemm.hip", [], "qgemm"),
            ("rows.hip", [], "rows"), ("attn.hip", [], "attn"), ("lmhead.hip", [], "lmhead"),
            ("engine.cpp", [], "engine"), ("sched.cpp", [], "sched"), ("synth.cpp", [], "synth"),
            ("intfer_file.cpp", [], "intfer_file"), ("serve.cpp", [], "serve"),
-           ("sample.cpp", [], "sample")]
+           ("sample.cpp", [], "sample"), ("qgemm_f16.hip", [], "qgemm_f16")]
 SERVE_BIN = HERE / "intfer_serve"  # the --serve command line (serve_main.cpp)
 
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")

@@ -294,16 +294,15 @@ int upload_group(ifr_ctx* c, const ifr_linear* const* ws, int count, int pair, D
   d.nsteps = K / 64;
   d.pair = pair;
   d.post = post_of(*ws[0]);
-  // codebook zeros (C/2 everywhere, C = 2^bits - 1: 1.5 or 7.5 in fp16) take
-  // the GEMM's two-operation fold, which gives the same bits
-  d.ff = 0;
-  if (bits == 2 || bits == 4) {
-    const uint16_t zc = bits == 2 ? 0x3E00 : 0x4780;
-    d.ff = 1;
-    for (int i = 0; i < count && d.ff; ++i)
-      for (size_t e = 0; e < (size_t)ws[i]->N * (K / 128); ++e)
-        if (ws[i]->zero[e] != zc) { d.ff = 0; break; }
-  }
+  // codebook zeros (C/2 everywhere, C = 2^bits - 1: 1.5, 7.5 or 127.5 in
+  // fp16): the reference's canonical codebook.  INT2 / INT4 ones take the
+  // GEMM's two-operation fold, which gives the same bits.
+  const uint16_t zc = bits == 2 ? 0x3E00 : bits == 4 ? 0x4780 : 0x57F8;
+  d.cb = 1;
+  for (int i = 0; i < count && d.cb; ++i)
+    for (size_t e = 0; e < (size_t)ws[i]->N * (K / 128); ++e)
+      if (ws[i]->zero[e] != zc) { d.cb = 0; break; }
+  d.ff = d.cb && bits != 8;
   const size_t cb = code_bytes(N, K, bits), sb = sz_bytes(N, K);
   std::vector<uint32_t> hc(cb / 4), hs(sb / 4);
   int tile_off = 0;
@@ -880,6 +879,18 @@ int ifr_quant_gemm_swiglu(ifr_ctx* c, const ifr_dlinear* w, const int8_t* a_d,
   if (!w->d.pair) return fail(IFR_EINVAL, "linear is not a gate/up pair");
   ifrk::QGemmArgs a{a_d, ascale_d, gsum_d, out_d, nullptr, M, w->d.N / 2};
   HIPCHK(ifrk::launch_qgemm(w->d, a, c->st));
+  return IFR_OK;
+}
+
+int ifr_quant_gemm_f16(ifr_ctx* c, const ifr_dlinear* w, const uint16_t* a_d, int32_t M, float alpha,
+                       uint16_t* out_d) {
+  if (!c || !w || !a_d || !out_d) return fail(IFR_EINVAL, "null arg");
+  if (w->d.pair) return fail(IFR_EDECLINE, "fp16 GEMM: gate/up pairs are not supported");
+  if (!w->d.cb) return fail(IFR_EDECLINE, "fp16 GEMM: needs the canonical codebook (zero = C/2 in every group)");
+  if (M <= 0) return fail(IFR_EINVAL, "M=%d", M);
+  if (M == 1 && w->d.K > 32768) return fail(IFR_EDECLINE, "fp16 GEMM: K=%d above 32768 at M = 1", w->d.K);
+  const ifrk::F16Args p{a_d, w->d.codes, w->d.sz, out_d, M, w->d.N, w->d.K, w->d.bits, w->d.nsteps, w->d.ng, alpha};
+  HIPCHK(ifrk::launch_qgemm_f16(p, c->st));
   return IFR_OK;
 }
 

@@ -34,7 +34,8 @@ struct DLin {
   int nsteps = 0;  // K / 64
   int pair = 0;    // 1: tiles alternate gate / up (SwiGLU epilogue)
   float post = 1.0f;  // factor on every output: y = fp16((ascale * post) * acc)
-  int ff = 0;  // 1: every zero is the codebook midpoint, so the folded integer path applies
+  int cb = 0;  // 1: every zero is the codebook midpoint C/2 (the reference's canonical codebook)
+  int ff = 0;  // 1: cb at 2 or 4 bits, so the folded integer path applies
   uint32_t* codes = nullptr;
   uint32_t* sz = nullptr;
   size_t bytes = 0;
@@ -62,6 +63,19 @@ hipError_t launch_qgemm(const DLin& w, const QGemmArgs& a, hipStream_t st);
 // bits.  Returns hipErrorInvalidValue where a shape does not apply.
 constexpr int kQGemmVariants = 16;
 hipError_t launch_qgemm_variant(const DLin& w, const QGemmArgs& a, int variant, hipStream_t st);
+
+// FP16-activation dequant GEMM (qgemm_f16.hip): out = fp16(sum_k a * w) with
+// w = (scale * alpha) * canonical codebook value, fp32 accumulation in
+// ascending k (the weight rounded to fp16 for M > 1).  Codebook linears only.
+struct F16Args {
+  const uint16_t* a;      // fp16 [M][K], row-major
+  const uint32_t* codes;  // a DLin's codes (not a gate/up pair)
+  const uint32_t* sz;
+  uint16_t* out;          // fp16 [M][N]
+  int M, N, K, bits, nsteps, ng;
+  float alpha;
+};
+hipError_t launch_qgemm_f16(const F16Args& p, hipStream_t st);
 
 // ---- row kernels -----------------------------------------------------------
 enum { SRC_X = 0, SRC_EMBED = 1, SRC_RESID = 2 };

@@ -617,6 +617,39 @@ void or_swiglu(const uint16_t* g, const uint16_t* u, uint16_t* out, size_t n) {
   for (size_t i = 0; i < n; ++i) out[i] = f2h(silu(h2f(g[i])) * h2f(u[i]));
 }
 
+// FP16-activation dequant GEMM (quant_gemm_forward_usm,
+// src/gemm/quant_gemm.cpp:359-2153): w(n,k) = (half(scale) * alpha) *
+// canon_value(bits, code) (:139-144, fp32), out = fp16(sum_k a * w) with an
+// fp32 accumulator in ascending k.  M == 1 (decode1 kernels :1026-1080,
+// :2022-2066): w in fp32 and `acc += av * w` taken as one fused
+// multiply-add; M > 1 (tiled kernel :2069-2150): w rounded to fp16 as staged,
+// so a * w is exact and the step is one rounded add.
+void or_qgemm_f16(const uint16_t* a, int M, const ifr_linear* w, float alpha, uint16_t* out) {
+  Unpacked u;
+  unpack(*w, u);
+  const int N = u.N, K = u.K, G = u.G, bits = w->bits;
+  const float Cf = (float)((1 << bits) - 1);
+  auto canon = [&](int c) -> float {
+    if (bits >= 8) return (2.0f * (float)c - 255.0f) / 255.0f;
+    if (bits == 4) return (2.0f * (float)c - 15.0f) / 15.0f;
+    static const float c2[4] = {-1.0f, -1.0f / 3.0f, 1.0f / 3.0f, 1.0f};
+    return c2[c & 3];
+  };
+  (void)Cf;
+#pragma omp parallel for schedule(static) if ((long)M * N >= 2048)
+  for (long r = 0; r < (long)M * N; ++r) {
+    const int m = (int)(r / N), n = (int)(r % N);
+    float acc = 0.0f;
+    for (int k = 0; k < K; ++k) {
+      const float s = u.s[(size_t)n * (K / G) + k / G] * alpha;
+      float wv = s * canon(u.c[(size_t)n * K + k]);
+      if (M > 1) wv = h2f(f2h(wv));
+      acc = std::fmaf(h2f(a[(size_t)m * K + k]), wv, acc);
+    }
+    out[r] = f2h(acc);
+  }
+}
+
 void or_dequant(const ifr_linear* w, float* out) {
   Unpacked u;
   unpack(*w, u);

@@ -398,6 +398,36 @@ def forward_fused_qk():
 
 
 @scenario
+def gemm_f16():
+    """The FP16-activation dequant GEMM (both kernels: M == 1 and tiled) in
+    bounds and bit-exact against the oracle, INT2 / INT4 / INT8."""
+    import intfer_amd as ia
+    from oracle import pyoracle as po
+    L = ia.lib()
+    dev = ia.Device(0)
+    rng = np.random.default_rng(17)
+    for bits in (2, 4, 8):
+        N, K = 80, 256
+        lin = ia.make_linear(N, K, bits, rng)
+        dl = C.c_void_p()
+        ia.check(L.ifr_linear_upload(dev.ctx, C.byref(lin.struct), C.byref(dl)), "upload")
+        for M in (1, 3, 70):
+            a = (rng.standard_normal((M, K)) * 2).astype(np.float16)
+            ad, od = dev.upload(a.view(np.uint16)), dev.alloc(M * N * 2)
+            ia.check(L.ifr_quant_gemm_f16(dev.ctx, dl, ad.p, M, C.c_float(0.5), od.p), "f16")
+            got = dev.download(od, np.uint16, (M, N))
+            ref = np.empty((M, N), np.uint16)
+            po.oracle().or_qgemm_f16(po.ptr(a.view(np.uint16)), M, C.byref(lin.struct), np.float32(0.5),
+                                     po.ptr(ref))
+            assert np.array_equal(got, ref), (bits, M)
+            ad.free()
+            od.free()
+        L.ifr_linear_free(dev.ctx, dl)
+        say(f"fp16 GEMM bits={bits}: M = 1, 3, 70 bit-exact")
+    dev.close()
+
+
+@scenario
 def forward_gated():
     """The attention output gate: a gated one-layer model through the fused
     QKV epilogue (150 prefill rows) and the separate q/k pass (the decode

@@ -529,3 +529,83 @@ def test_zero_gate_is_half_the_attention_output(mode):
     s = e.seq_open()
     _, lg = e.forward([(s, p, t, 1, 1) for p, t in enumerate(toks)], logits=True)
     assert not np.array_equal(lg, out[1])
+
+
+# ---- FP16-activation dequant GEMM (the reference's default GPU linear) ----------------------------
+
+def _f32_round(x):
+    """The float32 nearest to the exact rational x (ties to even; normal range)."""
+    from fractions import Fraction
+    if x == 0:
+        return np.float32(0.0)
+    sgn = -1 if x < 0 else 1
+    mag = abs(x)
+    e = mag.numerator.bit_length() - mag.denominator.bit_length()
+    if Fraction(2) ** e > mag:
+        e -= 1
+    ulp = Fraction(2) ** (e - 23)
+    q = mag / ulp
+    fl = q.numerator // q.denominator
+    rem = q - fl
+    if rem > Fraction(1, 2) or (rem == Fraction(1, 2) and fl % 2 == 1):
+        fl += 1
+    return np.float32(sgn * float(fl * ulp))
+
+
+def _f16_case(O, bits, M, N, K, alpha, seed):
+    rng = np.random.default_rng(seed)
+    lin = ia.make_linear(N, K, bits, rng)
+    a = (rng.standard_normal((M, K)) * 2).astype(np.float16)
+    out = np.empty((M, N), np.uint16)
+    O.or_qgemm_f16(ptr(a.view(np.uint16)), M, C.byref(lin.struct), np.float32(alpha), ptr(out))
+    Cb = (1 << bits) - 1
+    if bits == 2:
+        cb = np.array([-1.0, np.float32(-1.0) / np.float32(3.0), np.float32(1.0) / np.float32(3.0), 1.0],
+                      np.float32)
+    else:
+        cb = ((np.float32(2) * np.arange(Cb + 1, dtype=np.float32) - np.float32(Cb)) / np.float32(Cb)).astype(np.float32)
+    s = lin.scale.view(np.float16).astype(np.float32).reshape(N, K // 128)
+    w = (np.repeat(s, 128, axis=1) * np.float32(alpha)).astype(np.float32) * cb[lin.values]
+    return a, w.astype(np.float32), out
+
+
+@pytest.mark.parametrize("bits", [2, 4, 8])
+def test_qgemm_f16_tiled_is_sequential_fp32(O, bits):
+    """M > 1: w rounded to fp16, products exact in fp32, one rounded add per k
+    in ascending order -- numpy float32, step by step."""
+    M, N, K = 3, 48, 256
+    a, w, out = _f16_case(O, bits, M, N, K, 0.37, 40 + bits)
+    wh = w.astype(np.float16).astype(np.float32)
+    acc = np.zeros((M, N), np.float32)
+    af = a.astype(np.float32)
+    for k in range(K):
+        acc = (acc + af[:, k, None] * wh[None, :, k]).astype(np.float32)
+    assert np.array_equal(out, acc.astype(np.float16).view(np.uint16))
+
+
+@pytest.mark.parametrize("bits", [2, 4, 8])
+def test_qgemm_f16_decode_is_fused_fp32(O, bits):
+    """M == 1: w kept in fp32 and acc = fma(a, w, acc) exactly (rational
+    arithmetic rounded once per step); the unfused `acc + a * w` differs."""
+    from fractions import Fraction
+    N, K = 16, 256
+    a, w, out = _f16_case(O, bits, 1, N, K, 1.0, 50 + bits)
+    af = a.astype(np.float32)
+    ref = np.empty(N, np.uint16)
+    unfused_differs = False
+    for n in range(N):
+        acc, acc2 = np.float32(0), np.float32(0)
+        for k in range(K):
+            acc = _f32_round(Fraction(float(af[0, k])) * Fraction(float(w[n, k])) + Fraction(float(acc)))
+            acc2 = np.float32(acc2 + np.float32(af[0, k] * w[n, k]))
+        ref[n] = np.float16(acc).view(np.uint16)
+        unfused_differs |= acc2 != acc
+    assert np.array_equal(out[0], ref)
+    assert unfused_differs
+
+
+def test_qgemm_f16_tracks_float64(O):
+    a, w, out = _f16_case(O, 2, 5, 64, 1024, 1.0, 60)
+    ref = a.astype(np.float64) @ w.astype(np.float16).astype(np.float64).T
+    got = out.view(np.float16).astype(np.float64)
+    assert np.allclose(got, ref, rtol=2e-3, atol=2e-3 * np.abs(ref).max())
