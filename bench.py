@@ -73,6 +73,9 @@ def parse():
     ap.add_argument("--cpu-full", action="store_true",
                     help="run only the full CPU-baseline plan (cfg1 iteration, cfg2 fp32 GEMMs, cfg4 "
                          "decode windows at C=1 / 4 and the extrapolated loads) and print its JSON line")
+    ap.add_argument("--f16-gemm", action="store_true",
+                    help="time the FP16-activation dequant GEMM (the reference's default linear) on the 0.8B "
+                         "projections at M = 1, 16, 576 and print its JSON line")
     ap.add_argument("--gemm-case", default="",
                     help="NAME:M[:REPS] (qkv, o, gate_up, down, c5gu, c5down): repeat one cache-cold "
                          "GEMM launch shape (for counter collection) and print its JSON line")
@@ -378,6 +381,47 @@ def gemm_case(ia, dev, spec, reps=20):
             "K": K, "pair": pair, "launches": reps * R, "us": round(us, 2), "TOPS": round(ops / us / 1e6, 1),
             "mfma_frac": round(ops / us / 1e6 / 5000, 4), "GBps": round(byts / us / 1e3, 1),
             "hbm_frac": round(byts / us / 1e3 / 8000, 4)}
+
+
+def f16_gemm(ia, dev, Ms=(1, 16, 576), reps=3):
+    """The FP16-activation dequant GEMM (ifr_quant_gemm_f16) on the plain 0.8B
+    projections, cache-cold as in gemm_sweep (rotating weight copies over
+    > 320 MB), HIP events around back-to-back launches, best of `reps`."""
+    import ctypes as C
+    L = ia.lib()
+    rng = np.random.default_rng(0)
+    res = []
+    for name, K, N, pair in SHAPES_08B:
+        if pair:
+            continue
+        lin = ia.make_linear(N, K, 2, rng)
+        wb = lin.N * K * 2 // 8 + lin.N * (K // 128) * 4
+        R = int(np.ceil(320e6 / wb))
+        dls = []
+        for _ in range(R):
+            d = C.c_void_p()
+            ia.check(L.ifr_linear_upload(dev.ctx, C.byref(lin.struct), C.byref(d)), "upload")
+            dls.append(d)
+        for M in Ms:
+            a = dev.upload((rng.standard_normal((M, K)) * 2).astype(np.float16).view(np.uint16))
+            out = dev.alloc(M * N * 2)
+            best = None
+            for _ in range(reps + 1):
+                dev.timer_begin()
+                for d in dls:
+                    ia.check(L.ifr_quant_gemm_f16(dev.ctx, d, a.p, M, C.c_float(1.0), out.p), "f16 gemm")
+                ms = dev.timer_end()
+                best = ms if best is None else min(best, ms)
+            us = best * 1e3 / R
+            byts = wb + M * K * 2 + M * N * 2
+            res.append({"shape": name, "M": M, "us": round(us, 2), "GBps": round(byts / us / 1e3, 1),
+                        "hbm_frac": round(byts / us / 1e3 / 8000, 4),
+                        "TFLOPs": round(2.0 * M * N * K / us / 1e6, 2)})
+            a.free()
+            out.free()
+        for d in dls:
+            L.ifr_linear_free(dev.ctx, d)
+    return res
 
 
 def gemm_variants(ia, dev, Ms=(128, 256, 576, 1024), bits=2, reps=3, shapes=SHAPES_08B):
@@ -819,6 +863,12 @@ def main():
         return cfg5_bench(ia, a)
     if a.cpu_full:
         return cpu_full(ia, wl)
+    if a.f16_gemm:
+        dev = ia.Device(0)
+        print(json.dumps({"metric": "FP16-activation dequant GEMM (reference default linear), cache-cold",
+                          "unit": "us", "results": f16_gemm(ia, dev)}))
+        dev.close()
+        return 0
     if a.gemm_case:
         dev = ia.Device(0)
         res = gemm_case(ia, dev, a.gemm_case)

@@ -24,18 +24,9 @@
 namespace ifrk {
 namespace {
 
-// Code (n, k) of a linear in the fragment-major layout (pack_linear_host):
-// column tile n / 16, K step k / 64, lane 16 (k % 64 / 16) + n % 16, code
-// j = k % 16 of that lane, operand dword j / 4, byte j % 4.
-template <int BITS>
-__device__ __forceinline__ int code_at(const uint32_t* codes, int nsteps, int n, int k) {
-  const int t = n >> 4, c = n & 15, s = k >> 6, kk = k & 63;
-  const int l = 16 * (kk >> 4) + c, j = kk & 15, d = j >> 2, b = j & 3;
-  const size_t lane = ((size_t)t * nsteps + s) * 64 + l;
-  if constexpr (BITS == 2) return (int)((codes[lane] >> (8 * b + 2 * d)) & 3u);
-  else if constexpr (BITS == 4) return (int)((codes[lane * 2 + (d >> 1)] >> (8 * b + 4 * (d & 1))) & 15u);
-  else return (int)(((codes[lane * 4 + d] >> (8 * b)) & 0xFFu) ^ 0x80u);  // stored c ^ 0x80
-}
+// Codes in the fragment-major layout (pack_linear_host): column tile n / 16,
+// K step k / 64, lane 16 (k % 64 / 16) + n % 16, code j = k % 16 of that
+// lane in operand dword j / 4, byte j % 4 (INT8 stored as c ^ 0x80).
 
 template <int BITS>
 __device__ __forceinline__ float canon(int c) {
@@ -47,23 +38,81 @@ __device__ __forceinline__ float canon(int c) {
   }
 }
 
+// scale(n, g) * alpha, the reference's `s` (fp32)
+__device__ __forceinline__ float group_scale(const F16Args& p, int n, int g) {
+  const uint32_t zw = p.sz[((size_t)(n >> 4) * p.ng + g) * 16 + (n & 15)];
+  return ifrd::h2f((uint16_t)(zw & 0xFFFFu)) * p.alpha;
+}
+
+// The operand dwords of column n at k = 16 q0 .. 16 q0 + 15 (q0 = k / 16):
+// one lane's share of the fragment-major layout, and its 16 codes.
 template <int BITS>
-__device__ __forceinline__ float weight(const F16Args& p, int n, int k) {
-  const uint32_t zw = p.sz[((size_t)(n >> 4) * p.ng + (k >> 7)) * 16 + (n & 15)];
-  const float s = ifrd::h2f((uint16_t)(zw & 0xFFFFu)) * p.alpha;
-  return s * canon<BITS>(code_at<BITS>(p.codes, p.nsteps, n, k));
+__device__ __forceinline__ void raw16(const F16Args& p, int n, int q0, uint32_t (&w)[BITS / 2]) {
+  const int t = n >> 4, s = q0 >> 2, l = 16 * (q0 & 3) + (n & 15);
+  const uint32_t* src = p.codes + (((size_t)t * p.nsteps + s) * 64 + l) * (BITS / 2);
+#pragma unroll
+  for (int i = 0; i < BITS / 2; ++i) w[i] = src[i];
+}
+template <int BITS>
+__device__ __forceinline__ void decode16(const uint32_t (&w)[BITS / 2], int (&c)[16]) {
+#pragma unroll
+  for (int j = 0; j < 16; ++j) {
+    const int d = j >> 2, b = j & 3;
+    if constexpr (BITS == 2) c[j] = (int)((w[0] >> (8 * b + 2 * d)) & 3u);
+    else if constexpr (BITS == 4) c[j] = (int)((w[d >> 1] >> (8 * b + 4 * (d & 1))) & 15u);
+    else c[j] = (int)(((w[d] >> (8 * b)) & 0xFFu) ^ 0x80u);
+  }
+}
+template <int BITS>
+__device__ __forceinline__ void codes16(const F16Args& p, int n, int q0, int (&c)[16]) {
+  uint32_t w[BITS / 2];
+  raw16<BITS>(p, n, q0, w);
+  decode16<BITS>(w, c);
 }
 
 // M == 1: one thread per output column; the activation row is staged in LDS.
+// The 2^BITS codebook values, computed once per workgroup into LDS (the
+// same fp32 values canon() gives per element).
+template <int BITS>
+__device__ __forceinline__ void canon_table(float* tab) {
+  for (int c = threadIdx.x; c < (1 << BITS); c += blockDim.x) tab[c] = canon<BITS>(c);
+}
+
 template <int BITS>
 __global__ __launch_bounds__(256) void qgemm_f16_m1(F16Args p) {
   extern __shared__ uint16_t arow[];
+  __shared__ float tab[1 << BITS];
   for (int k = threadIdx.x; k < p.K; k += 256) arow[k] = p.a[k];
+  canon_table<BITS>(tab);
   __syncthreads();
   const int n = blockIdx.x * 256 + threadIdx.x;
   if (n >= p.N) return;  // (after the only barrier)
+  // k ascending, one 128-wide group (8 operand chunks of 16 codes) at a
+  // time; the next group's codes and scale are loaded while this one runs
   float acc = 0.0f;
-  for (int k = 0; k < p.K; ++k) acc = fmaf(ifrd::h2f(arow[k]), weight<BITS>(p, n, k), acc);
+  const int ng = p.K / 128;
+  uint32_t cur[8][BITS / 2], nxt[8][BITS / 2];
+  float sc = group_scale(p, n, 0), sn = sc;
+#pragma unroll
+  for (int q = 0; q < 8; ++q) raw16<BITS>(p, n, q, cur[q]);
+  for (int g = 0; g < ng; ++g) {
+    const int gn = min(g + 1, ng - 1);
+#pragma unroll
+    for (int q = 0; q < 8; ++q) raw16<BITS>(p, n, 8 * gn + q, nxt[q]);
+    sn = group_scale(p, n, gn);
+#pragma unroll
+    for (int q = 0; q < 8; ++q) {
+      int c[16];
+      decode16<BITS>(cur[q], c);
+#pragma unroll
+      for (int j = 0; j < 16; ++j) acc = fmaf(ifrd::h2f(arow[128 * g + 16 * q + j]), sc * tab[c[j]], acc);
+    }
+#pragma unroll
+    for (int q = 0; q < 8; ++q)
+#pragma unroll
+      for (int i = 0; i < BITS / 2; ++i) cur[q][i] = nxt[q][i];
+    sc = sn;
+  }
   p.out[n] = ifrd::f2h(acc);
 }
 
@@ -84,9 +133,22 @@ __global__ __launch_bounds__(256) void qgemm_f16_tiled(F16Args p) {
     for (int j = 0; j < 4; ++j) acc[i][j] = 0.0f;
   for (int k0 = 0; k0 < p.K; k0 += BK) {
     for (int e = threadIdx.x; e < BM * BK; e += 256) {
-      const int r = e / BK, c = e % BK, m = m0 + r, n = n0 + r;
+      const int r = e / BK, c = e % BK, m = m0 + r;
       sA[r][c] = m < p.M ? p.a[(size_t)m * p.K + k0 + c] : (uint16_t)0;
-      sW[r][c] = n < p.N ? ifrd::f2h(weight<BITS>(p, n, k0 + c)) : (uint16_t)0;
+    }
+    if (threadIdx.x < BN * BK / 16) {  // one 16-code chunk of one column each
+      const int r = threadIdx.x >> 1, h = threadIdx.x & 1, n = n0 + r;
+      if (n < p.N) {
+        const int q0 = k0 / 16 + h;
+        const float sc = group_scale(p, n, q0 >> 3);
+        int c[16];
+        codes16<BITS>(p, n, q0, c);
+#pragma unroll
+        for (int j = 0; j < 16; ++j) sW[r][16 * h + j] = ifrd::f2h(sc * canon<BITS>(c[j]));
+      } else {
+#pragma unroll
+        for (int j = 0; j < 16; ++j) sW[r][16 * h + j] = 0;
+      }
     }
     __syncthreads();
     for (int kk = 0; kk < BK; ++kk) {
