@@ -276,9 +276,9 @@ def gemm_sweep(ia, dev, bits_list=(2, 4), Ms=(1, 8, 16, 64, 256, 1024), reps=3):
 
 def attn_sweep(ia, dev, reps=10, splits=(0,)):
     """Joint ragged attention on one layer at the serve shapes: cfg3 (64
-    decode rows, lognormal lengths, + two 512-row causal chunks), C=64
-    decode-only rows at the cfg4 context mix, and the same rows plus one
-    512-row prefill chunk at offset 1024.  Durations come from HIP events on
+    decode rows, lognormal lengths, + two 512-row causal chunks), one
+    512-row prefill chunk at offset 1024 alone, C=64 decode-only rows at the
+    cfg4 context mix, and the same rows plus that chunk.  Durations come from HIP events on
     the engine stream around each launch (attention and combine separately)."""
     from intfer_amd import workloads as wl
     cfg = ia.default_cfg(layers=1, vocab=1024)
@@ -286,6 +286,7 @@ def attn_sweep(ia, dev, reps=10, splits=(0,)):
     rng = np.random.default_rng(21)
     dec4 = [len(p) + 32 for p in wl.cfg4_requests(64, seed=4, vocab=cfg.vocab)]
     cases = [("cfg3", wl.cfg3_lengths(seed=3), [(0, 512), (1536, 512)]),
+             ("prefill", [], [(1024, 512)]),
              ("c64_decode", dec4, []),
              ("c64_mixed", dec4, [(1024, 512)])]
     res = []

@@ -257,6 +257,11 @@ typedef struct ifr_kv_cfg {
                            * QKV GEMM's epilogue where the launch shape is one
                            * head per workgroup (bit-identical); 1: always as
                            * its own pass */
+  int32_t dense_attention; /* 0: the q-blocks of a prefill chunk that share a
+                            * kv head and KV split run in one workgroup that
+                            * copies each K/V page once into LDS for all of
+                            * them (fp16 KV); 1: every attention unit runs on
+                            * its own (bit-identical; a check of the first) */
 } ifr_kv_cfg;
 
 /* Upload + repack a model (replaces Engine::load, build_shards,

@@ -309,7 +309,8 @@ class Engine:
     """The device forward over one loaded model."""
 
     def __init__(self, dev: Device, model: HostModelHandle, max_seqs=8, max_seq_tokens=4096,
-                 pool_tokens=None, kv_int8=0, max_rows=640, attn_split=0, lanes=0, intfer=None, separate_qk=0):
+                 pool_tokens=None, kv_int8=0, max_rows=640, attn_split=0, lanes=0, intfer=None, separate_qk=0,
+                 dense_attention=0):
         """Load `model` (a host model), or with intfer= an .intfer file path
         or image for the architecture `model` (a ModelCfg)."""
         self.dev = dev
@@ -319,6 +320,7 @@ class Engine:
         kv.pool_tokens = pool_tokens or max_seqs * max_seq_tokens
         kv.kv_int8, kv.max_rows, kv.attn_split, kv.lanes = kv_int8, max_rows, attn_split, lanes
         kv.separate_qk = separate_qk
+        kv.dense_attention = dense_attention
         self.kv = kv
         if intfer is None:
             check(lib().ifr_model_load(dev.ctx, model.ptr, C.byref(kv)), "ifr_model_load")

@@ -66,7 +66,8 @@ class IntferRotation(C.Structure):
 class KVCfg(C.Structure):
     _fields_ = [("max_seqs", C.c_int32), ("max_seq_tokens", C.c_int32),
                 ("pool_tokens", C.c_int32), ("kv_int8", C.c_int32), ("max_rows", C.c_int32),
-                ("attn_split", C.c_int32), ("lanes", C.c_int32), ("separate_qk", C.c_int32)]
+                ("attn_split", C.c_int32), ("lanes", C.c_int32), ("separate_qk", C.c_int32),
+                ("dense_attention", C.c_int32)]
 
 
 class Row(C.Structure):

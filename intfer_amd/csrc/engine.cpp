@@ -423,6 +423,13 @@ double combine_work(const ifr_ctx* c, int M, const std::vector<int>& g_pos0, con
   return b;
 }
 
+// Slots of the chunked region whose workgroups share K/V pages through LDS
+// (the q-blocks of prefill chunks; fp16 KV); otherwise every slot runs as an
+// independent unit, with the same results.
+int shared_slots(const ifr_ctx* c, long nchunked) {
+  return c->kv.kv_int8 || c->kv.dense_attention ? 0 : (int)nchunked;
+}
+
 // Bytes the pack pass moves: the rows in, the per-row maps, the group
 // offsets, the units and the dispatch order out.
 double pack_work(int M, size_t ngroups, long nunits, int nslots) {
@@ -559,7 +566,7 @@ int launch_layer(ifr_ctx* c, const SubBatch& sb, int l) {
   }
   // (4) attention + combine (emits the O-proj int8 input)
   {
-    ifrk::AttnArgs a{L.pk.units, (int)sb.nunits, L.pk.order, sb.nslots, c->kv.kv_int8 ? 0 : (int)sb.nchunked,
+    ifrk::AttnArgs a{L.pk.units, (int)sb.nunits, L.pk.order, sb.nslots, shared_slots(c, sb.nchunked),
                      L.qbuf, nq, 1.4426950408889634f / std::sqrt((float)hd), L.part_o, L.part_ml, kAttnTiles};
     Scope sc(c, L.st, "attention", sb.attn_bytes, sb.attn_flops);
     HIPCHK(ifrk::launch_attention(a, kv, L.st));
@@ -935,7 +942,8 @@ int ifr_model_load(ifr_ctx* c, const ifr_host_model* m, const ifr_kv_cfg* kvc) {
     return fail(IFR_EINVAL, "rotary_dim");
   if (kvc->max_seqs <= 0 || kvc->max_seq_tokens <= 0 || kvc->pool_tokens < kPage ||
       kvc->max_rows <= 0 || kvc->max_rows > 6144 || kvc->attn_split < 0 || kvc->attn_split % kPage ||
-      kvc->attn_split > 65536 || kvc->lanes < 0 || kvc->lanes > 2)
+      kvc->attn_split > 65536 || kvc->lanes < 0 || kvc->lanes > 2 || kvc->dense_attention < 0 ||
+      kvc->dense_attention > 1)
     return fail(IFR_EINVAL, "kv cfg");
   release_model(c);
   c->cfg = cf;
@@ -1475,7 +1483,7 @@ int ifr_attention(ifr_ctx* c, int32_t layer, const ifr_row* rows, int32_t M, con
   HIPCHK(hipMemcpyAsync(c->lane[0].qbuf, q_h, (size_t)M * nq * hd * 2, hipMemcpyHostToDevice, c->st));
   ifrk::KVLayout kv{nkv, hd, kPage, c->max_pages, c->kv.kv_int8, c->kpool[layer], c->vpool[layer],
                     c->kscale[layer], c->vscale[layer], c->bt_d};
-  ifrk::AttnArgs a{c->lane[0].pk.units, (int)nunits, c->lane[0].pk.order, nslots, c->kv.kv_int8 ? 0 : (int)nchunked, c->lane[0].qbuf, nq, 1.4426950408889634f / std::sqrt((float)hd),
+  ifrk::AttnArgs a{c->lane[0].pk.units, (int)nunits, c->lane[0].pk.order, nslots, shared_slots(c, nchunked), c->lane[0].qbuf, nq, 1.4426950408889634f / std::sqrt((float)hd),
                    c->lane[0].part_o, c->lane[0].part_ml, kAttnTiles};
   double attn_bytes = 0, attn_flops = 0;
   attn_work(c, rows, M, g_pos0, g_len, &attn_bytes, &attn_flops);
@@ -1545,7 +1553,7 @@ int ifr_attention_noalloc(ifr_ctx* c, int32_t layer, const ifr_row* rows, int32_
   HIPCHK(ifrk::launch_pack(rows_d, M, nkv, c->qb, split, pk, c->st));
   ifrk::KVLayout kv{nkv, hd, kPage, c->max_pages, c->kv.kv_int8, c->kpool[layer], c->vpool[layer],
                     c->kscale[layer], c->vscale[layer], c->bt_d};
-  ifrk::AttnArgs a{pk.units, (int)nunits, pk.order, (int)nslots, c->kv.kv_int8 ? 0 : (int)nchunked, q_d, nq,
+  ifrk::AttnArgs a{pk.units, (int)nunits, pk.order, (int)nslots, shared_slots(c, nchunked), q_d, nq,
                    1.4426950408889634f / std::sqrt((float)hd), part_o, part_ml, kAttnTiles};
   HIPCHK(ifrk::launch_attention(a, kv, c->st));
   ifrk::CombineArgs cb{part_o, part_ml, pk.comb_base, pk.comb_nsplit, pk.comb_tok, M, nq, nkv, hd, out_d,

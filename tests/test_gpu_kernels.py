@@ -290,13 +290,45 @@ def test_act_quant_bitexact(dev, K, norm, rot, rnd, ga):
     assert np.array_equal(gg, g)
 
 
-def _attn_engine(dev, kv_int8, lens, chunks):
+def _attn_engine(dev, kv_int8, lens, chunks, dense_attention=0, model=None):
     cfg = ia.default_cfg(layers=1, vocab=1024)
-    model = ia.SynthModel(cfg, seed=5)
+    model = model or ia.SynthModel(cfg, seed=5)
     total = sum(lens) + sum(o + n for o, n in chunks)
     eng = ia.Engine(dev, model, max_seqs=len(lens) + len(chunks) + 1, max_seq_tokens=8192,
-                    pool_tokens=total + 64 * (len(lens) + 4), kv_int8=kv_int8, max_rows=1200)
+                    pool_tokens=total + 64 * (len(lens) + 4), kv_int8=kv_int8, max_rows=1200,
+                    dense_attention=dense_attention)
     return cfg, model, eng
+
+
+def test_chunked_region_matches_dense_units(dev):
+    """The chunked region (4 q-blocks of a prefill chunk per workgroup, each
+    K/V page staged once in LDS for all of them) gives the same bits as
+    running every unit on its own: decode rows, full and ragged chunk groups
+    (idle waves), chunks from offset 0 and at long offsets (up to 15 KV
+    splits)."""
+    lens = wl.cfg3_lengths(seed=3)[:24]
+    chunks = [(0, 512), (1536, 200), (100, 37), (3500, 300), (31, 9), (7000, 64)]
+    rng = np.random.default_rng(44)
+    cfg = ia.default_cfg(layers=1, vocab=1024)
+    nkv, hd, nq = cfg.n_kv, cfg.head_dim, cfg.n_heads
+    all_lens = lens + [o + n for o, n in chunks]
+    kvs = [(rng.standard_normal((1, n, nkv, hd), dtype=np.float32),
+            rng.standard_normal((1, n, nkv, hd), dtype=np.float32)) for n in all_lens]
+    outs, model = [], None
+    for dense in (0, 1):
+        cfg, model, eng = _attn_engine(dev, 0, lens, chunks, dense_attention=dense, model=model)
+        seqs = []
+        for k, v in kvs:
+            s = eng.seq_open()
+            eng.load_kv(s, k, v)
+            seqs.append(s)
+        rows = [(seqs[i], n - 1, 0, 0, 1) for i, n in enumerate(lens)]
+        for j, (o, n) in enumerate(chunks):
+            rows += [(seqs[len(lens) + j], o + p, 0, 1, 1) for p in range(n)]
+        q = np.random.default_rng(45).standard_normal((len(rows), nq, hd), dtype=np.float32).astype(np.float16)
+        announce(f"attention chunked region vs dense units: dense_attention={dense} M={len(rows)}")
+        outs.append(eng.attention(0, rows, q))
+    assert np.array_equal(outs[0], outs[1])
 
 
 @pytest.mark.parametrize("kv_int8", [0, 1])
