@@ -76,6 +76,9 @@ def parse():
     ap.add_argument("--f16-gemm", action="store_true",
                     help="time the FP16-activation dequant GEMM (the reference's default linear) on the 0.8B "
                          "projections at M = 1, 16, 576 and print its JSON line")
+    ap.add_argument("--ga-gemm", action="store_true",
+                    help="time the grouped-activation DPAS-fold GEMM (64-wide activation slices) on the 0.8B "
+                         "projections at M = 1, 16, 576 and print its JSON line")
     ap.add_argument("--gemm-case", default="",
                     help="NAME:M[:REPS] (qkv, o, gate_up, down, c5gu, c5down): repeat one cache-cold "
                          "GEMM launch shape (for counter collection) and print its JSON line")
@@ -384,10 +387,12 @@ def gemm_case(ia, dev, spec, reps=20):
             "hbm_frac": round(byts / us / 1e3 / 8000, 4)}
 
 
-def f16_gemm(ia, dev, Ms=(1, 16, 576), reps=3):
-    """The FP16-activation dequant GEMM (ifr_quant_gemm_f16) on the plain 0.8B
-    projections, cache-cold as in gemm_sweep (rotating weight copies over
-    > 320 MB), HIP events around back-to-back launches, best of `reps`."""
+def f16_gemm(ia, dev, Ms=(1, 16, 576), reps=3, kind="f16"):
+    """The FP16-activation dequant GEMM (ifr_quant_gemm_f16; kind "ga": the
+    grouped-activation DPAS fold, ifr_quant_gemm_ga with 64-wide slices) on
+    the plain 0.8B projections, cache-cold as in gemm_sweep (rotating weight
+    copies over > 320 MB), HIP events around back-to-back launches, best of
+    `reps`."""
     import ctypes as C
     L = ia.lib()
     rng = np.random.default_rng(0)
@@ -404,22 +409,32 @@ def f16_gemm(ia, dev, Ms=(1, 16, 576), reps=3):
             ia.check(L.ifr_linear_upload(dev.ctx, C.byref(lin.struct), C.byref(d)), "upload")
             dls.append(d)
         for M in Ms:
-            a = dev.upload((rng.standard_normal((M, K)) * 2).astype(np.float16).view(np.uint16))
+            if kind == "ga":
+                a = dev.upload(ia.atile(rng.integers(-127, 128, size=(M, K), dtype=np.int8)))
+                asc = dev.upload((rng.random((M, K // 64)) * 0.05 + 1e-4).astype(np.float32))
+                run = lambda d: L.ifr_quant_gemm_ga(dev.ctx, d, a.p, asc.p, M, 64, C.c_float(1.0), out.p)
+                abytes = M * K + M * (K // 64) * 4
+            else:
+                a = dev.upload((rng.standard_normal((M, K)) * 2).astype(np.float16).view(np.uint16))
+                run = lambda d: L.ifr_quant_gemm_f16(dev.ctx, d, a.p, M, C.c_float(1.0), out.p)
+                abytes = M * K * 2
             out = dev.alloc(M * N * 2)
             best = None
             for _ in range(reps + 1):
                 dev.timer_begin()
                 for d in dls:
-                    ia.check(L.ifr_quant_gemm_f16(dev.ctx, d, a.p, M, C.c_float(1.0), out.p), "f16 gemm")
+                    ia.check(run(d), kind + " gemm")
                 ms = dev.timer_end()
                 best = ms if best is None else min(best, ms)
             us = best * 1e3 / R
-            byts = wb + M * K * 2 + M * N * 2
+            byts = wb + abytes + M * N * 2
             res.append({"shape": name, "M": M, "us": round(us, 2), "GBps": round(byts / us / 1e3, 1),
                         "hbm_frac": round(byts / us / 1e3 / 8000, 4),
                         "TFLOPs": round(2.0 * M * N * K / us / 1e6, 2)})
             a.free()
             out.free()
+            if kind == "ga":
+                asc.free()
         for d in dls:
             L.ifr_linear_free(dev.ctx, d)
     return res
@@ -868,6 +883,12 @@ def main():
         dev = ia.Device(0)
         print(json.dumps({"metric": "FP16-activation dequant GEMM (reference default linear), cache-cold",
                           "unit": "us", "results": f16_gemm(ia, dev)}))
+        dev.close()
+        return 0
+    if a.ga_gemm:
+        dev = ia.Device(0)
+        print(json.dumps({"metric": "grouped-activation (GA64) DPAS-fold GEMM, cache-cold",
+                          "unit": "us", "results": f16_gemm(ia, dev, kind="ga")}))
         dev.close()
         return 0
     if a.gemm_case:

@@ -236,6 +236,23 @@ int ifr_quant_gemm_variant(ifr_ctx* ctx, const ifr_dlinear* w, const int8_t* a_d
 int ifr_quant_gemm_f16(ifr_ctx* ctx, const ifr_dlinear* w, const uint16_t* a_d, int32_t M,
                        float alpha, uint16_t* out_d);
 
+/* W2A8 / W4A8 / W8A8 GEMM with grouped activation scales: the reference's
+ * DPAS fold as written (dpas48_tiled, quant_gemm.cpp:3492-3791; per-op math
+ * :3602-3736; act_group GA, As[r][k0/GA] :3502, :3614; Dpas48Params
+ * quant_gemm.hpp:522-558).  For each 32-wide K op o, ascending (k0 = 32 o):
+ *   T = sum a_q(m,k) c(n,k),  S = sum a_q(m,k)            (int32, exact)
+ *   acc += as(m, k0/ga) * ws(n, k0/128) * alpha * (2T - C S) * (1/C)
+ *   out(m,n) = fp16_rne(acc)
+ * left to right in fp32, each product and the add rounded (no contraction:
+ * the reference's device compiler may fuse the last step, which this does
+ * not).  a_d: int8 activations in the A-tile layout (IFR_ATILE_OFF), as
+ * ifr_act_quant writes them with the same ga; ascale_d fp32 [M][K/ga];
+ * ga a multiple of 64 dividing K (64 the reference's default, 0 = K: one
+ * scale per row); out_d fp16 [M][N].  IFR_EDECLINE for a gate/up pair or a
+ * linear whose zeros are not all C/2 (the fold has no zero term). */
+int ifr_quant_gemm_ga(ifr_ctx* ctx, const ifr_dlinear* w, const int8_t* a_d, const float* ascale_d,
+                      int32_t M, int32_t ga, float alpha, uint16_t* out_d);
+
 /* ------------------------------------------------------------------------
  * Engine: model load, paged KV, one mixed iteration.
  * ---------------------------------------------------------------------- */

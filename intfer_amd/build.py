@@ -29,7 +29,8 @@ SOURCES = [("qgemm.hip", [], "qgemm"),
            ("rows.hip", [], "rows"), ("attn.hip", [], "attn"), ("lmhead.hip", [], "lmhead"),
            ("engine.cpp", [], "engine"), ("sched.cpp", [], "sched"), ("synth.cpp", [], "synth"),
            ("intfer_file.cpp", [], "intfer_file"), ("serve.cpp", [], "serve"),
-           ("sample.cpp", [], "sample"), ("qgemm_f16.hip", [], "qgemm_f16")]
+           ("sample.cpp", [], "sample"), ("qgemm_f16.hip", [], "qgemm_f16"),
+           ("qgemm_ga.hip", [], "qgemm_ga")]
 SERVE_BIN = HERE / "intfer_serve"  # the --serve command line (serve_main.cpp)
 
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")

@@ -901,6 +901,22 @@ int ifr_quant_gemm_f16(ifr_ctx* c, const ifr_dlinear* w, const uint16_t* a_d, in
   return IFR_OK;
 }
 
+int ifr_quant_gemm_ga(ifr_ctx* c, const ifr_dlinear* w, const int8_t* a_d, const float* ascale_d, int32_t M,
+                      int32_t ga, float alpha, uint16_t* out_d) {
+  if (!c || !w || !a_d || !ascale_d || !out_d) return fail(IFR_EINVAL, "null arg");
+  if (w->d.pair) return fail(IFR_EDECLINE, "grouped-activation GEMM: gate/up pairs are not supported");
+  if (!w->d.cb)
+    return fail(IFR_EDECLINE, "grouped-activation GEMM: needs the canonical codebook (zero = C/2 in every group)");
+  if (M <= 0) return fail(IFR_EINVAL, "M=%d", M);
+  if (ga == 0) ga = w->d.K;
+  if (ga < 0 || ga % 64 != 0 || w->d.K % ga != 0)
+    return fail(IFR_EINVAL, "ga=%d: a multiple of 64 dividing K=%d (0: K)", ga, w->d.K);
+  const ifrk::GaArgs p{a_d, ascale_d, w->d.codes, w->d.sz, out_d, M, w->d.N, w->d.K, w->d.bits,
+                       w->d.nsteps, w->d.ng, ga, alpha};
+  HIPCHK(ifrk::launch_qgemm_ga(p, c->st));
+  return IFR_OK;
+}
+
 int ifr_quant_gemm_variants(void) { return ifrk::kQGemmVariants; }
 
 int ifr_quant_gemm_variant(ifr_ctx* c, const ifr_dlinear* w, const int8_t* a_d,

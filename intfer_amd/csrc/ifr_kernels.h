@@ -77,6 +77,19 @@ struct F16Args {
 };
 hipError_t launch_qgemm_f16(const F16Args& p, hipStream_t st);
 
+// Grouped-activation DPAS fold (qgemm_ga.hip): per 32-wide K op,
+// acc += as(m, k0/ga) * ws * alpha * (2T - C S) * (1/C), out = fp16(acc).
+struct GaArgs {
+  const int8_t* a;        // int8 activations, A-tile layout (ceil(M/16)*16 rows)
+  const float* as;        // fp32 [M][K / ga]
+  const uint32_t* codes;  // a DLin's codes (not a gate/up pair)
+  const uint32_t* sz;
+  uint16_t* out;          // fp16 [M][N]
+  int M, N, K, bits, nsteps, ng, ga;
+  float alpha;
+};
+hipError_t launch_qgemm_ga(const GaArgs& p, hipStream_t st);
+
 // ---- row kernels -----------------------------------------------------------
 enum { SRC_X = 0, SRC_EMBED = 1, SRC_RESID = 2 };
 struct RowQuantArgs {

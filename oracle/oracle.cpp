@@ -612,6 +612,47 @@ void or_qgemm(const int8_t* a, const float* as, int M, const ifr_linear* w, uint
   for (size_t i = 0; i < y.size(); ++i) out[i] = f2h(y[i]);
 }
 
+// The reference's DPAS fold with grouped activation scales (dpas48_tiled,
+// src/gemm/quant_gemm.cpp:3492-3791; the per-op math :3602-3736, act_group
+// GA :3502, As[r][k0 / GA] :3614).  For each 32-wide K op o in ascending
+// order (k0 = 32 o): T = sum a_q c and S = sum a_q over the op (exact int32,
+// c the code 0..C), and
+//     acc += as[m][k0 / GA] * ws[n][k0 / G] * alpha * (2T - C S) * (1 / C)
+// evaluated in the source's left-to-right order in fp32, every product and
+// the add rounded (no contraction); out = fp16_rne(acc) (to_half_bits :84).
+// 2T - C S is an integer below 2^24, exact in fp32 however it is formed.
+// a: int8 [M][K] row-major, as: fp32 [M][K / GA].
+void or_qgemm_ga(const int8_t* a, const float* as, int M, int ga, const ifr_linear* w, float alpha,
+                 uint16_t* out) {
+  Unpacked u;
+  unpack(*w, u);
+  const int N = u.N, K = u.K, G = u.G;
+  const float C = (float)((1 << w->bits) - 1);
+  const float Cinv = 1.0f / C;
+#pragma omp parallel for schedule(static) if ((long)M * N >= 2048)
+  for (long r = 0; r < (long)M * N; ++r) {
+    const int m = (int)(r / N), n = (int)(r % N);
+    float acc = 0.0f;
+    for (int k0 = 0; k0 < K; k0 += 32) {
+      int32_t T = 0, S = 0;
+      for (int k = k0; k < k0 + 32; ++k) {
+        const int32_t av = a[(size_t)m * K + k];
+        T += av * (int32_t)u.c[(size_t)n * K + k];
+        S += av;
+      }
+      const float asv = as[(size_t)m * (K / ga) + k0 / ga];
+      const float ws = u.s[(size_t)n * (K / G) + k0 / G];
+      const float d = 2.0f * (float)T - C * (float)S;
+      float x = asv * ws;
+      x = x * alpha;
+      x = x * d;
+      x = x * Cinv;
+      acc = acc + x;
+    }
+    out[r] = f2h(acc);
+  }
+}
+
 // SwiGLU over two fp16 GEMM outputs: fp16(silu(g) * u).
 void or_swiglu(const uint16_t* g, const uint16_t* u, uint16_t* out, size_t n) {
   for (size_t i = 0; i < n; ++i) out[i] = f2h(silu(h2f(g[i])) * h2f(u[i]));

@@ -42,6 +42,7 @@ def oracle() -> C.CDLL:
             "or_qgemm_ts": (None, [P, C.c_int, P, P, P]),
             "or_qgemm": (None, [P, P, C.c_int, P, P]),
             "or_qgemm_f16": (None, [P, C.c_int, P, f32, P]),
+            "or_qgemm_ga": (None, [P, P, C.c_int, C.c_int, P, f32, P]),
             "or_swiglu": (None, [P, P, P, sz]),
             "or_dequant": (None, [P, P]),
             "or_gemm_f32": (None, [P, P, P, C.c_int, C.c_int, C.c_int]),

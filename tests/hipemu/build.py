@@ -35,7 +35,8 @@ UNITS = [("qgemm.hip", [], "qgemm"),
          ("rows.hip", [], "rows"), ("attn.hip", [], "attn"), ("lmhead.hip", [], "lmhead"),
          ("engine.cpp", [], "engine"), ("sched.cpp", [], "sched"), ("synth.cpp", [], "synth"),
          ("intfer_file.cpp", [], "intfer_file"), ("serve.cpp", [], "serve"),
-         ("sample.cpp", [], "sample"), ("qgemm_f16.hip", [], "qgemm_f16")]
+         ("sample.cpp", [], "sample"), ("qgemm_f16.hip", [], "qgemm_f16"),
+           ("qgemm_ga.hip", [], "qgemm_ga")]
 
 FLAGS = ["-O1", "-g", "-fPIC", "-std=c++17", "-fsanitize=address", "-fno-omit-frame-pointer",
          "-ffp-contract=off", "-Wno-unused-command-line-argument", "-w",

@@ -428,6 +428,38 @@ def gemm_f16():
 
 
 @scenario
+def gemm_ga():
+    """The grouped-activation GEMM in bounds and bit-exact against the
+    oracle, INT2 / INT4 / INT8, ga = 64 and K, ragged M."""
+    import intfer_amd as ia
+    from oracle import pyoracle as po
+    L = ia.lib()
+    dev = ia.Device(0)
+    rng = np.random.default_rng(19)
+    for bits in (2, 4, 8):
+        N, K = 80, 256
+        lin = ia.make_linear(N, K, bits, rng)
+        dl = C.c_void_p()
+        ia.check(L.ifr_linear_upload(dev.ctx, C.byref(lin.struct), C.byref(dl)), "upload")
+        for M, ga in ((1, 64), (21, 0)):
+            g = ga or K
+            a = rng.integers(-127, 128, size=(M, K), dtype=np.int8)
+            asc = (rng.random((M, K // g)) * 0.05 + 1e-4).astype(np.float32)
+            ad, sd, od = dev.upload(ia.atile(a)), dev.upload(asc), dev.alloc(M * N * 2)
+            ia.check(L.ifr_quant_gemm_ga(dev.ctx, dl, ad.p, sd.p, M, ga, C.c_float(0.5), od.p), "ga")
+            got = dev.download(od, np.uint16, (M, N))
+            ref = np.empty((M, N), np.uint16)
+            po.oracle().or_qgemm_ga(po.ptr(a), po.ptr(asc), M, g, C.byref(lin.struct), np.float32(0.5),
+                                    po.ptr(ref))
+            assert np.array_equal(got, ref), (bits, M, ga)
+            for b in (ad, sd, od):
+                b.free()
+        L.ifr_linear_free(dev.ctx, dl)
+        say(f"grouped-activation GEMM bits={bits}: M = 1, 21 bit-exact")
+    dev.close()
+
+
+@scenario
 def forward_gated():
     """The attention output gate: a gated one-layer model through the fused
     QKV epilogue (150 prefill rows) and the separate q/k pass (the decode

@@ -13,6 +13,14 @@ Each oracle function is checked against something other than itself:
                          bit-exactly against the GPU kernel, not here
   or_qgemm_ts            int64 brute force
   or_qgemm (fold)        float64 dequant GEMM
+  or_qgemm_f16           numpy float32 step by step (M > 1); exact rational
+                         fma per step, the unfused form differing (M == 1);
+                         float64 dequant GEMM
+  or_qgemm_ga            one-hot activations naming the slice, group and code
+                         used (exact powers of two); exact rational
+                         arithmetic rounded per op (unit scales); GA = K
+                         equal to GA = 64 with equal slices; float64 dequant
+                         GEMM
   or_lmhead_quant        numpy float32 closed form of main.cpp:1745-1761
   or_lmhead / or_argmax  float64 logits; first-max-wins on planted ties
   or_attention_row       float64 softmax attention
@@ -609,3 +617,92 @@ def test_qgemm_f16_tracks_float64(O):
     ref = a.astype(np.float64) @ w.astype(np.float16).astype(np.float64).T
     got = out.view(np.float16).astype(np.float64)
     assert np.allclose(got, ref, rtol=2e-3, atol=2e-3 * np.abs(ref).max())
+
+# ---- W2A8 DPAS fold with grouped activation scales (the reference's act_group) -----------
+
+def _ga_case(O, bits, M, N, K, ga, alpha, seed, a=None, asc=None, lin=None):
+    rng = np.random.default_rng(seed)
+    lin = lin or ia.make_linear(N, K, bits, rng)
+    if a is None:
+        a = rng.integers(-127, 128, size=(M, K), dtype=np.int8)
+    if asc is None:
+        asc = (rng.random((M, K // ga)) * 0.02 + 1e-3).astype(np.float32)
+    out = np.empty((M, N), np.uint16)
+    O.or_qgemm_ga(ptr(np.ascontiguousarray(a)), ptr(np.ascontiguousarray(asc, np.float32)), M, ga,
+                  C.byref(lin.struct), np.float32(alpha), ptr(out))
+    return a, asc, lin, out
+
+
+@pytest.mark.parametrize("bits", [2, 4, 8])
+def test_qgemm_ga_one_hot_reads_the_right_slice_and_group(O, bits):
+    """One nonzero activation at column k: every op but k's has T = S = 0, so
+    out = fp16(((as[k / 64] * ws[k / 128]) * alpha) * (2c - C) * (1/C)) with
+    slice scales 2^-j and group scales 2^-g (exact products): the output
+    names the slice, the group and the code the fold used."""
+    N, K, ga, C_ = 16, 512, 64, (1 << bits) - 1
+    rng = np.random.default_rng(7)
+    lin = ia.make_linear(N, K, bits, rng)
+    sc = np.array([2.0 ** -g for g in range(K // 128)], np.float16)
+    lin.scale[:] = np.tile(sc.view(np.uint16), (N, 1))
+    asc = np.array([[2.0 ** -(j + 1) for j in range(K // ga)]], np.float32)
+    for k in (0, 63, 64, 200, 511):
+        a = np.zeros((1, K), np.int8)
+        a[0, k] = 3
+        _, _, _, out = _ga_case(O, bits, 1, N, K, ga, 1.0, 0, a=a, asc=asc, lin=lin)
+        c = lin.values[:, k].astype(np.float64)
+        x = (2.0 ** -(k // ga + 1)) * (2.0 ** -(k // 128)) * (2 * 3 * c - C_ * 3)
+        ref = (x.astype(np.float32) * np.float32(1.0 / C_)).astype(np.float16)
+        assert np.array_equal(out[0], ref.view(np.uint16)), (bits, k)
+
+
+def test_qgemm_ga_unit_scales_round_each_op(O):
+    """Unit scales: each op adds x = fl(d * fl(1/3)) (d = 2T - 3S, exact) to
+    the fp32 accumulator with one rounding, ops ascending -- exact rational
+    arithmetic rounded per step, T and S summed in int64 over each 32-wide
+    op."""
+    from fractions import Fraction
+    M, N, K, ga = 2, 16, 256, 64
+    rng = np.random.default_rng(11)
+    lin = ia.make_linear(N, K, 2, rng)
+    lin.scale[:] = np.float16(1.0).view(np.uint16)
+    a = rng.integers(-127, 128, size=(M, K), dtype=np.int8)
+    asc = np.ones((M, K // ga), np.float32)
+    _, _, _, out = _ga_case(O, 2, M, N, K, ga, 1.0, 0, a=a, asc=asc, lin=lin)
+    third = Fraction(float(np.float32(1.0) / np.float32(3.0)))
+    for m in range(M):
+        for n in range(N):
+            acc = np.float32(0)
+            for o in range(K // 32):
+                sl = slice(32 * o, 32 * o + 32)
+                T = int(np.dot(a[m, sl].astype(np.int64), lin.values[n, sl].astype(np.int64)))
+                S = int(a[m, sl].astype(np.int64).sum())
+                x = _f32_round(Fraction(2 * T - 3 * S) * third)
+                acc = _f32_round(Fraction(float(acc)) + Fraction(float(x)))
+            assert out[m, n] == np.float16(acc).view(np.uint16), (m, n)
+
+
+@pytest.mark.parametrize("bits", [2, 4, 8])
+def test_qgemm_ga_equal_slices_match_per_row_scale(O, bits):
+    """GA = K (one scale per row) equals GA = 64 with that scale in every
+    slice, bit for bit."""
+    M, N, K = 3, 32, 384
+    a, asc, lin, out64 = _ga_case(O, bits, M, N, K, 64, 0.73, 20 + bits,
+                                  asc=np.repeat(np.float32([[0.011], [0.02], [0.0037]]), 384 // 64, axis=1))
+    _, _, _, outK = _ga_case(O, bits, M, N, K, K, 0.73, 0, a=a, asc=np.float32([[0.011], [0.02], [0.0037]]),
+                             lin=lin)
+    assert np.array_equal(out64, outK)
+
+
+@pytest.mark.parametrize("bits", [2, 4, 8])
+def test_qgemm_ga_tracks_float64(O, bits):
+    """The dequantized product in float64, sum_k as[m][k/64] a(m,k) ws
+    alpha (2c - C)/C, within fp16 output rounding."""
+    M, N, K, ga = 4, 64, 1024, 64
+    a, asc, lin, out = _ga_case(O, bits, M, N, K, ga, 0.5, 30 + bits)
+    C_ = (1 << bits) - 1
+    s = lin.scale.view(np.float16).astype(np.float64).reshape(N, K // 128)
+    w = np.repeat(s, 128, axis=1) * 0.5 * (2.0 * lin.values - C_) / C_
+    ar = a.astype(np.float64) * np.repeat(asc.astype(np.float64), ga, axis=1)
+    ref = ar @ w.T
+    got = out.view(np.float16).astype(np.float64)
+    assert np.allclose(got, ref, rtol=2e-3, atol=1e-3 * np.abs(ref).max())
