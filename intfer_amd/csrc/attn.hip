@@ -116,13 +116,15 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs p, KVLayout kv) {
   };
   // pages are [kv_lo + 32 i, +32); a shared workgroup walks its widest range
   const int last = ((shared ? upg.kv_hi : un.kv_hi) - 1 - un.kv_lo) / kPage;
-  auto load = [&](PageBuf& b, int i) {
+  // fragment-major pages: fragment f is 64 lanes x 8 elements, lane at 8 * lane
+  constexpr int W = KV8 ? 2 : 4;
+  auto page_of = [&](int i) {
     const int t0 = un.kv_lo + kPage * min(i, last);
-    const size_t pb = (size_t)bt[t0 / kPage] * kv.nkv + un.kvh;
-    constexpr int W = KV8 ? 2 : 4;
+    return (size_t)bt[t0 / kPage] * kv.nkv + un.kvh;
+  };
+  auto load_k = [&](PageBuf& b, int i) {
+    const size_t pb = page_of(i);
     const uint8_t* kp = reinterpret_cast<const uint8_t*>(kv.kpool) + pb * kPage * kHD * (KV8 ? 1 : 2);
-    const uint8_t* vp = reinterpret_cast<const uint8_t*>(kv.vpool) + pb * kHD * kPage * (KV8 ? 1 : 2);
-    // fragment-major pages: fragment f is 64 lanes x 8 elements, lane at 8 * lane
 #pragma unroll
     for (int h = 0; h < 2; ++h)
 #pragma unroll
@@ -131,6 +133,17 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs p, KVLayout kv) {
         const uint32_t* src = reinterpret_cast<const uint32_t*>(kp + e * (KV8 ? 1 : 2));
         load_frag<W>(src, b.k[h][i4]);
       }
+    if constexpr (KV8) {
+      const uint16_t* ksc = kv.kscale + pb * kPage;
+#pragma unroll
+      for (int h = 0; h < 2; ++h)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) b.ks[h][r] = ksc[8 * g + 2 * r + h];
+    }
+  };
+  auto load_v = [&](PageBuf& b, int i) {
+    const size_t pb = page_of(i);
+    const uint8_t* vp = reinterpret_cast<const uint8_t*>(kv.vpool) + pb * kHD * kPage * (KV8 ? 1 : 2);
 #pragma unroll
     for (int d = 0; d < 8; ++d) {
       const size_t e = (size_t)(d * 64 + lane) * 8;
@@ -138,12 +151,7 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs p, KVLayout kv) {
       load_frag<W>(src, b.v[d]);
     }
     if constexpr (KV8) {
-      const uint16_t* ksc = kv.kscale + pb * kPage;
       const uint16_t* vsc = kv.vscale + pb * kPage;
-#pragma unroll
-      for (int h = 0; h < 2; ++h)
-#pragma unroll
-        for (int r = 0; r < 4; ++r) b.ks[h][r] = ksc[8 * g + 2 * r + h];
 #pragma unroll
       for (int j = 0; j < 8; ++j) b.vs[j] = vsc[8 * g + j];
     }
@@ -170,14 +178,15 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs p, KVLayout kv) {
     }
     return f;
   };
-  auto step = [&](const PageBuf& b, int i) {
+  // K fragments and scales from kb, V fragments and scales from vb
+  auto step = [&](const PageBuf& kb, const PageBuf& vb, int i) {
     const int t0 = un.kv_lo + kPage * i;
     // ---- S^T: K tile h covers tokens 2c' + h; lane (c, g) reg r -> token 8g + 2r + h.
     v8h kf[2][4];
 #pragma unroll
     for (int h = 0; h < 2; ++h)
 #pragma unroll
-      for (int i4 = 0; i4 < 4; ++i4) kf[h][i4] = frag(b.k[h][i4]);
+      for (int i4 = 0; i4 < 4; ++i4) kf[h][i4] = frag(kb.k[h][i4]);
     v8h phi[NT], plo[NT];
     float alpha[NT];
     // A page wholly below the unit's first query position and its KV end
@@ -203,7 +212,7 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs p, KVLayout kv) {
         for (int h = 0; h < 2; ++h) {
           const int tk = t0 + 8 * g + 2 * r + h;
           float v = s[h][r];
-          if constexpr (KV8) v *= ifrd::h2f(b.ks[h][r]);
+          if constexpr (KV8) v *= ifrd::h2f(kb.ks[h][r]);
           v *= p.scale_log2;
           if (!interior && (!colv[t] || tk > qpos[t] || tk >= un.kv_hi)) v = -INFINITY;
           sv[2 * r + h] = v;
@@ -224,7 +233,7 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs p, KVLayout kv) {
       for (int j = 0; j < 8; ++j) {
         const float pf = __builtin_amdgcn_exp2f(sv[j] - m_use);
         rs += pf;
-        const float pv = KV8 ? pf * ifrd::h2f(b.vs[j]) : pf;
+        const float pv = KV8 ? pf * ifrd::h2f(vb.vs[j]) : pf;
         const _Float16 hh = (_Float16)pv;
         phi[t][j] = hh;
         plo[t][j] = (_Float16)(pv - (float)hh);
@@ -242,7 +251,7 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs p, KVLayout kv) {
         for (int d = 0; d < 8; ++d) o[t][d] *= alpha[t];
 #pragma unroll
     for (int d = 0; d < 8; ++d) {
-      const v8h vf = frag(b.v[d]);
+      const v8h vf = frag(vb.v[d]);
 #pragma unroll
       for (int t = 0; t < NT; ++t) {
         o[t][d] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vf, phi[t], o[t][d], 0, 0, 0);
@@ -294,20 +303,26 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs p, KVLayout kv) {
           const uint4 x = kvs[i & 1][8 + d][lane];
           b.v[d][0] = x.x; b.v[d][1] = x.y; b.v[d][2] = x.z; b.v[d][3] = x.w;
         }
-        step(b, i);
+        step(b, b, i);
       }
       if (i >= last) break;
     }
    }
   } else {
-    PageBuf bA, bB;
-    load(bA, 0);
+    // K double-buffered, V single: page i + 1's K loads are in flight
+    // while page i is computed, its V loads once page i's PV product has
+    // read V(i) (during page i + 1's scores and softmax)
+    PageBuf kA, kB, vb;
+    load_k(kA, 0);
+    load_v(vb, 0);
     for (int i = 0;; i += 2) {
-      load(bB, i + 1);
-      step(bA, i);
+      load_k(kB, i + 1);
+      step(kA, vb, i);
+      load_v(vb, i + 1);
       if (i + 1 > last) break;
-      load(bA, i + 2);
-      step(bB, i + 1);
+      load_k(kA, i + 2);
+      step(kB, vb, i + 1);
+      load_v(vb, i + 2);
       if (i + 2 > last) break;
     }
   }
