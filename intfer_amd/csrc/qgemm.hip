@@ -488,7 +488,7 @@ __global__ __launch_bounds__(256) void qgemm_rows(KParams p) {
   for (int i = 0; i < WM; ++i)
 #pragma unroll
     for (int r = 0; r < 4; ++r) asr[i][r] = p.as[min(row0 + 16 * i + 4 * lgrp + r, p.M - 1)] * p.post;
-  __syncthreads();  // the only barrier
+  __syncthreads();  // the operands' barrier (the 16-byte store path has one more)
 
   v4i T[WM][WN];
   v4f acc[WM][WN];
@@ -553,8 +553,13 @@ __global__ __launch_bounds__(256) void qgemm_rows(KParams p) {
     // (a lane holds one column of 4 rows) would write each row in 32-byte
     // pieces of 2-byte stores, which cost 2.5-4.6 us of a 9-12 us launch at
     // M = 576..1024.  Same values as store_plain / store_swiglu.
+    // (The tiles reuse the fold operands' LDS, so the launch needs no more
+    // than the larger of the two: at the 27B-class shapes that keeps 3
+    // workgroups per CU instead of 2.  Every wave has read its last fold
+    // operand before any wave passes this barrier.)
     constexpr int TR = 16 * WM, TC = EPI == 0 ? 16 * WN : 8 * WN, CPR = TC / 8, NCH = TR * CPR;
-    uint16_t* yt = reinterpret_cast<uint16_t*>(lds_f + ng * (BM + BN)) + wave * TR * TC;
+    __syncthreads();
+    uint16_t* yt = reinterpret_cast<uint16_t*>(lds_f) + wave * TR * TC;
 #pragma unroll
     for (int i = 0; i < WM; ++i)
 #pragma unroll
@@ -880,8 +885,8 @@ hipError_t launch_rows(const KParams& p, hipStream_t st) {
   constexpr int BM = 16 * WM * MW, BN = 16 * WN * NW;
   if (p.ng % R != 0) return hipErrorInvalidValue;
   size_t lds = (size_t)p.ng * (BM + BN) * sizeof(float);
-  // the output tiles of the 4 waves (16-byte stores)
-  if constexpr (EPI != 2) lds += (size_t)4 * 16 * WM * (EPI == 0 ? 16 * WN : 8 * WN) * sizeof(uint16_t);
+  // the output tiles of the 4 waves (16-byte stores), in the same space
+  if constexpr (EPI != 2) lds = std::max(lds, (size_t)4 * 16 * WM * (EPI == 0 ? 16 * WN : 8 * WN) * sizeof(uint16_t));
   if constexpr (EPI == 2) {
     // the staged y tile (padded rows) and the RMS partial sums
     if (BM != 32 || BN != 128 || p.qa.rotary != 128 || p.kv.hd != 128) return hipErrorInvalidValue;
