@@ -314,6 +314,11 @@ __device__ __forceinline__ void bfly_lanes(float (&v)[E]) {
   for (int e = 0; e < E; ++e) v[e] = bfly_lane<M>(v[e]);
 }
 
+// LDS index of row element i with one pad float per 32: lanes that hold E
+// consecutive elements each (E a power of two) then hit 32 distinct banks
+// instead of a few.
+__device__ __forceinline__ int pad32(int i) { return i + (i >> 5); }
+
 template <int E>
 __device__ void fwht_regs(float (&v)[E], float* xs) {
   constexpr int P = 256 * E;
@@ -334,14 +339,15 @@ __device__ void fwht_regs(float (&v)[E], float* xs) {
   bfly_lanes<32>(v);
   __syncthreads();
 #pragma unroll
-  for (int e = 0; e < E; ++e) xs[E * threadIdx.x + e] = v[e];
+  for (int e = 0; e < E; ++e) xs[pad32(E * threadIdx.x + e)] = v[e];
   __syncthreads();
   const int q = threadIdx.x >> 6;  // quarter of the P head elements
   const float inv = 1.0f / sqrtf((float)P);
 #pragma unroll
   for (int e = 0; e < E; ++e) {
     const int base = (E * threadIdx.x + e) & (P / 4 - 1);
-    const float a0 = xs[base], a1 = xs[base + P / 4], a2 = xs[base + P / 2], a3 = xs[base + 3 * P / 4];
+    const float a0 = xs[pad32(base)], a1 = xs[pad32(base + P / 4)], a2 = xs[pad32(base + P / 2)],
+                a3 = xs[pad32(base + 3 * P / 4)];
     const float b0 = a0 + a1, b1 = a0 - a1, b2 = a2 + a3, b3 = a2 - a3;
     const float c = q == 0 ? b0 + b2 : q == 1 ? b1 + b3 : q == 2 ? b0 - b2 : b1 - b3;
     v[e] = c * inv;
@@ -427,7 +433,8 @@ __device__ __forceinline__ void store_codes(int8_t* q, int m, int k0, int K, con
 
 template <int E>
 __global__ __launch_bounds__(256) void row_quant_wide(RowQuantArgs a) {
-  __shared__ float xs[8192];
+  // the padded FWHT exchange (P + P / 32) or the chain-major row (K + 32)
+  __shared__ __attribute__((aligned(16))) float xs[8192 + 256];
   __shared__ float red[16];
   constexpr int P = 256 * E;
   const int K = a.K, ET = (K - P) / 256;
@@ -462,23 +469,38 @@ __global__ __launch_bounds__(256) void row_quant_wide(RowQuantArgs a) {
     st_f32<E>(a.resid + t0, w, ET);
   }
   if (a.norm_w) {
-    // the row in LDS for the eight sequential chains (rms_factor's order)
+    // The row in LDS chain-major for the eight sequential chains
+    // (rms_factor's order): chain j = i % 8 holds x[j + 8 n] at j * CS + n,
+    // so each chain reads its values 4 at a time in order.  K / 8 is a
+    // multiple of 32 (K a multiple of 256), CS a multiple of 4.
+    const int CS = K / 8 + 4;
     __syncthreads();
 #pragma unroll
-    for (int e = 0; e < E; ++e) xs[E * t + e] = v[e];
+    for (int e = 0; e < E; ++e) {
+      const int i = E * t + e;
+      xs[(i & 7) * CS + (i >> 3)] = v[e];
+    }
 #pragma unroll
     for (int e = 0; e < E; ++e)
-      if (e < ET) xs[P + ET * t + e] = w[e];
+      if (e < ET) {
+        const int i = P + ET * t + e;
+        xs[(i & 7) * CS + (i >> 3)] = w[e];
+      }
     __syncthreads();
     if (t < 8) {
       float acc = 0.0f;
-      for (int n0 = 0; n0 < K / 8; n0 += 16) {
-        float x16[16];
+      const float4* xc = reinterpret_cast<const float4*>(xs + t * CS);
+      for (int n4 = 0; n4 < K / 32; n4 += 8) {
+        float4 x8[8];
 #pragma unroll
-        for (int i = 0; i < 16; ++i) x16[i] = (n0 + i < K / 8) ? xs[t + 8 * (n0 + i)] : 0.0f;
+        for (int i = 0; i < 8; ++i) x8[i] = xc[n4 + i];
 #pragma unroll
-        for (int i = 0; i < 16; ++i)
-          if (n0 + i < K / 8) acc = fmaf(x16[i], x16[i], acc);
+        for (int i = 0; i < 8; ++i) {
+          acc = fmaf(x8[i].x, x8[i].x, acc);
+          acc = fmaf(x8[i].y, x8[i].y, acc);
+          acc = fmaf(x8[i].z, x8[i].z, acc);
+          acc = fmaf(x8[i].w, x8[i].w, acc);
+        }
       }
       red[t] = acc;
     }
