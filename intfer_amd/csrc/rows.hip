@@ -202,20 +202,33 @@ __device__ void fwht1024(float (&v)[4], float* xs) {
 
 // RMSNorm factor of the 1024 values held 4 per thread, reference order: eight
 // sequential fused chains over x[j + 8n], folded (j, j+4) then two horizontal
-// adds.  The chains read LDS in batches of 16 so loads overlap.
+// adds.  The row is stored chain-major (chain j = i % 8 holds x[j + 8n] at
+// 132 j + n; the stride 132 keeps the stores on distinct banks), so each
+// chain reads its 128 values 4 at a time, in batches that overlap.
+constexpr int kRms1024Lds = 8 * 132;  // floats of xs the chain-major copy uses
 __device__ float rms1024(const float (&v)[4], float* xs, float* red, float eps) {
   __syncthreads();
 #pragma unroll
-  for (int e = 0; e < 4; ++e) xs[4 * threadIdx.x + e] = v[e];
+  for (int e = 0; e < 4; ++e) {
+    const int i = 4 * threadIdx.x + e;
+    xs[(i & 7) * 132 + (i >> 3)] = v[e];
+  }
   __syncthreads();
   if (threadIdx.x < 8) {
     float acc = 0.0f;
-    for (int n0 = 0; n0 < 128; n0 += 16) {
-      float t[16];
+    const float4* xc = reinterpret_cast<const float4*>(xs + threadIdx.x * 132);
 #pragma unroll
-      for (int i = 0; i < 16; ++i) t[i] = xs[threadIdx.x + 8 * (n0 + i)];
+    for (int n4 = 0; n4 < 32; n4 += 8) {
+      float4 x8[8];
 #pragma unroll
-      for (int i = 0; i < 16; ++i) acc = fmaf(t[i], t[i], acc);
+      for (int i = 0; i < 8; ++i) x8[i] = xc[n4 + i];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        acc = fmaf(x8[i].x, x8[i].x, acc);
+        acc = fmaf(x8[i].y, x8[i].y, acc);
+        acc = fmaf(x8[i].z, x8[i].z, acc);
+        acc = fmaf(x8[i].w, x8[i].w, acc);
+      }
     }
     red[threadIdx.x] = acc;
   }
@@ -226,7 +239,7 @@ __device__ float rms1024(const float (&v)[4], float* xs, float* red, float eps) 
 }
 
 __global__ __launch_bounds__(256) void row_quant1024_kernel(RowQuantArgs a) {
-  __shared__ float xs[1024];
+  __shared__ __attribute__((aligned(16))) float xs[kRms1024Lds];  // fwht1024 uses the first 1024
   __shared__ float red[16];
   const int m = blockIdx.x, t = threadIdx.x, lane = t & 63;
   const int src = a.rowmap ? a.rowmap[m] : m;
