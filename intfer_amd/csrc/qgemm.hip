@@ -447,7 +447,10 @@ __global__ __launch_bounds__(256) void qgemm_rows(KParams p) {
   constexpr bool DUMP = MODE == 1, FF = MODE == 2;
   constexpr int NW = 4 / MW;
   constexpr int BM = 16 * WM * MW, BN = 16 * WN * NW;
-  extern __shared__ float lds_f[];
+  // (declared as 16-byte vectors so the dynamic LDS is 16-byte aligned and
+  // the compiler may use 128-bit LDS accesses)
+  extern __shared__ v4f lds_f4[];
+  float* const lds_f = reinterpret_cast<float*>(lds_f4);
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int lrow = lane & 15, lgrp = lane >> 4;
@@ -617,7 +620,8 @@ __global__ __launch_bounds__(256) void qgemm_rows(KParams p) {
 template <int BITS, int WM, int WN, int NGW, int EPI, int MODE>
 __global__ __launch_bounds__(256) void qgemm_splitk(KParams p) {
   constexpr bool DUMP = MODE == 1, FF = MODE == 2;
-  extern __shared__ int32_t lds[];
+  extern __shared__ v4i lds4[];  // 16-byte aligned: T parks as 128-bit stores
+  int32_t* const lds = reinterpret_cast<int32_t*>(lds4);
   constexpr int BM = 16 * WM, BN = 16 * WN;
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -716,7 +720,8 @@ __global__ __launch_bounds__(256) void qgemm_splitk(KParams p) {
 // one barrier each output's groups fold in ascending order, as everywhere.
 template <int BITS, int WN, int NWV, int NGW, int EPI, bool ALDS, bool DUMP>
 __global__ __launch_bounds__(64 * NWV) void qgemm_stream(KParams p) {
-  extern __shared__ int32_t lds[];
+  extern __shared__ v4i lds4[];  // 16-byte aligned: T parks as 128-bit stores
+  int32_t* const lds = reinterpret_cast<int32_t*>(lds4);
   constexpr int BN = 16 * WN, NT = 64 * NWV;
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);

@@ -190,10 +190,16 @@ __device__ void fwht1024(float (&v)[4], float* xs) {
   __syncthreads();
   const int q = threadIdx.x >> 6;  // quarter of the 1024 elements
   const float inv = 1.0f / sqrtf(1024.0f);
+  // element (4 t + e) & 255 of each quarter: one 16-byte read per quarter
+  float aq[4][4];
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    const float4 x = *reinterpret_cast<const float4*>(xs + ((4 * threadIdx.x) & 255) + 256 * k);
+    aq[k][0] = x.x; aq[k][1] = x.y; aq[k][2] = x.z; aq[k][3] = x.w;
+  }
 #pragma unroll
   for (int e = 0; e < 4; ++e) {
-    const int base = (4 * threadIdx.x + e) & 255;
-    const float a0 = xs[base], a1 = xs[base + 256], a2 = xs[base + 512], a3 = xs[base + 768];
+    const float a0 = aq[0][e], a1 = aq[1][e], a2 = aq[2][e], a3 = aq[3][e];
     const float b0 = a0 + a1, b1 = a0 - a1, b2 = a2 + a3, b3 = a2 - a3;
     const float c = q == 0 ? b0 + b2 : q == 1 ? b1 + b3 : q == 2 ? b0 - b2 : b1 - b3;
     v[e] = c * inv;
