@@ -45,12 +45,20 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs p, KVLayout kv) {
   // wave-uniform unit index: the unit record and block-table entries become
   // scalar loads, which do not queue behind the vector K/V loads
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int slot = blockIdx.x * 4 + w;
+  // Dispatch order: the dense workgroups (slots [n_shared, n_slots)) take the
+  // first block ids, the chunked region the rest.  The dense units stream KV
+  // from HBM and the chunked ones are bound by MFMA / VALU issue; started
+  // first, the dense units keep HBM busy while the chunked workgroups fill
+  // the remaining slots, instead of queueing behind them (c64 decode rows +
+  // a 512-row chunk: 81.3 -> 73.6 us).  Only the order changes, not the work.
+  const int nsw = p.n_shared / 4, nwg = (int)gridDim.x, ndw = nwg - nsw;
+  const int bid = (int)blockIdx.x < ndw ? nsw + (int)blockIdx.x : (int)blockIdx.x - ndw;
+  const int slot = bid * 4 + w;
   // Workgroups of the chunked region serve 4 q-blocks of one sequence with the
   // same kv head and split: they stream each K/V page once into LDS and all 4
   // waves read it there.  Other workgroups run 4 independent units.
   // (fp16 pages only: the host rejects n_shared > 0 for int8 KV)
-  const bool shared = !KV8 && blockIdx.x * 4 < p.n_shared;  // workgroup-uniform
+  const bool shared = !KV8 && bid * 4 < p.n_shared;  // workgroup-uniform
   if (!shared && slot >= p.n_slots) return;         // (no barrier on this path)
   const int u = p.order[slot];
   if (!shared && u < 0) return;
@@ -61,7 +69,7 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs p, KVLayout kv) {
   if (shared) {
 #pragma unroll
     for (int q = 3; q >= 0; --q) {
-      const int uq = p.order[blockIdx.x * 4 + q];
+      const int uq = p.order[bid * 4 + q];
       if (uq >= 0) { u_pg = uq; break; }
     }
   }
