@@ -34,6 +34,7 @@ __device__ __forceinline__ bool better(float v, int i, float bv, int bi) {
 
 template <int WM>
 __global__ __launch_bounds__(256) void lmhead_kernel(LmP p) {
+  extern __shared__ float as_l[];  // [16 WM rows][nsteps] activation scales of the block
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int lrow = lane & 15, lgrp = lane >> 4;
   const int ntiles = p.V >> 4;
@@ -47,6 +48,13 @@ __global__ __launch_bounds__(256) void lmhead_kernel(LmP p) {
 #pragma unroll
   for (int i = 0; i < WM; ++i)
     arow[i] = p.a + ((size_t)(min(row0 + 16 * i, p.W - 1) >> 4) * p.nsteps << 10) + 16 * lane;
+  // the block's activation scales, staged once (rows past W read row W - 1):
+  // per K step a lane then reads its 4 WM scales from LDS instead of memory
+  for (int e = threadIdx.x; e < 16 * WM * p.nsteps; e += 256) {
+    const int r = e / p.nsteps, s = e - r * p.nsteps;
+    as_l[e] = p.as[(size_t)min(row0 + r, p.W - 1) * p.nsteps + s];
+  }
+  __syncthreads();
   v4f acc[WM][kWN];
 #pragma unroll
   for (int i = 0; i < WM; ++i)
@@ -64,11 +72,7 @@ __global__ __launch_bounds__(256) void lmhead_kernel(LmP p) {
     for (int i = 0; i < WM; ++i) {
       float asr[4];
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        int row = row0 + 16 * i + 4 * lgrp + r;
-        row = row < p.W ? row : p.W - 1;
-        asr[r] = p.as[(size_t)row * p.nsteps + s];
-      }
+      for (int r = 0; r < 4; ++r) asr[r] = as_l[(16 * i + 4 * lgrp + r) * p.nsteps + s];
 #pragma unroll
       for (int j = 0; j < kWN; ++j) {
         const v4i T = __builtin_amdgcn_mfma_i32_16x16x64_i8(A[i], B[j], (v4i){0, 0, 0, 0}, 0, 0, 0);
@@ -140,7 +144,9 @@ __global__ __launch_bounds__(256) void argmax_final_kernel(const float* pv, cons
 
 template <int WM>
 hipError_t launch_wm(const LmP& p, int nparts, int nrb, hipStream_t st) {
-  hipLaunchKernelGGL(lmhead_kernel<WM>, dim3(nparts / 4, nrb), dim3(256), 0, st, p);
+  const size_t lds = (size_t)16 * WM * p.nsteps * sizeof(float);
+  if (lds > 64 * 1024) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(lmhead_kernel<WM>, dim3(nparts / 4, nrb), dim3(256), lds, st, p);
   return hipGetLastError();
 }
 
