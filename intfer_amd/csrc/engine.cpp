@@ -111,7 +111,6 @@ struct Lane {
   hipStream_t st = nullptr;
   int32_t* rows_d = nullptr;
   int32_t* rows_h = nullptr;  // pinned
-  int32_t* tok_h = nullptr;   // pinned
   float* resid = nullptr;
   int8_t* aq = nullptr;
   float* as = nullptr;
@@ -359,7 +358,7 @@ void release_model(ifr_ctx* c) {
   if (c->bt_h) hipHostFree(c->bt_h);
   c->bt_h = nullptr;
   for (Lane& L : c->lane) {
-    for (int32_t** hp : {&L.rows_h, &L.tok_h, &L.best_h})
+    for (int32_t** hp : {&L.rows_h, &L.best_h})
       if (*hp) hipHostFree(*hp);
     if (L.logits_d) hipFree(L.logits_d);
     hipStream_t st = L.st;
@@ -484,18 +483,14 @@ int prep_sub(ifr_ctx* c, const ifr_row* rows, SubBatch& sb) {
   return IFR_OK;
 }
 
-// Rows up, packing maps, token column.
+// Rows up; the pack kernel writes the packing maps and the token column.
 int launch_head(ifr_ctx* c, const ifr_row* rows, const SubBatch& sb) {
   Lane& L = c->lane[sb.lane];
   const ifr_row* r = rows + sb.row0;
   std::memcpy(L.rows_h, r, (size_t)sb.M * sizeof(ifr_row));
   HIPCHK(hipMemcpyAsync(L.rows_d, L.rows_h, (size_t)sb.M * sizeof(ifr_row), hipMemcpyHostToDevice, L.st));
-  {
-    Scope sc(c, L.st, "pack", sb.pack_bytes);
-    HIPCHK(ifrk::launch_pack(L.rows_d, sb.M, c->cfg.n_kv, c->qb, sb.split, L.pk, L.st));
-  }
-  for (int m = 0; m < sb.M; ++m) L.tok_h[m] = r[m].token;
-  HIPCHK(hipMemcpyAsync(L.row_tok, L.tok_h, (size_t)sb.M * sizeof(int32_t), hipMemcpyHostToDevice, L.st));
+  Scope sc(c, L.st, "pack", sb.pack_bytes);
+  HIPCHK(ifrk::launch_pack(L.rows_d, sb.M, c->cfg.n_kv, c->qb, sb.split, L.pk, L.st));
   return IFR_OK;
 }
 
@@ -1104,7 +1099,6 @@ int ifr_model_load(ifr_ctx* c, const ifr_host_model* m, const ifr_kv_cfg* kvc) {
   const int nparts = ifrk::lmhead_nparts(V);
   for (Lane& L : c->lane) {
     HIPCHK(hipHostMalloc(reinterpret_cast<void**>(&L.rows_h), (size_t)Mx * 5 * sizeof(int32_t), hipHostMallocDefault));
-    HIPCHK(hipHostMalloc(reinterpret_cast<void**>(&L.tok_h), (size_t)Mx * sizeof(int32_t), hipHostMallocDefault));
     HIPCHK(hipHostMalloc(reinterpret_cast<void**>(&L.best_h), (size_t)Mx * sizeof(int32_t), hipHostMallocDefault));
     int r = 0;
     if ((r = walloc(c, &L.rows_d, (size_t)Mx * 5)) || (r = walloc(c, &L.resid, (size_t)Mx * H)) ||
@@ -1126,6 +1120,7 @@ int ifr_model_load(ifr_ctx* c, const ifr_host_model* m, const ifr_kv_cfg* kvc) {
         (r = walloc(c, &L.part_o, (size_t)c->max_units * 16 * kAttnTiles * hd)) ||
         (r = walloc(c, &L.part_ml, (size_t)c->max_units * 16 * kAttnTiles * 2)))
       return r;
+    L.pk.row_tok = L.row_tok;
   }
   HIPCHK(hipStreamSynchronize(c->st));
   c->loaded = true;

@@ -218,6 +218,7 @@ struct PackOut {
   AttnUnit* units;       // [n_units]
   int32_t* want_rows;    // [n_want] rows to score, in row order
   int32_t* order;        // [n_slots] attention dispatch slot -> unit (-1: idle)
+  int32_t* row_tok = nullptr;  // [M] the rows' token ids (optional)
 };
 // Attention dispatch order (4 slots = the 4 waves of one workgroup).  A
 // sequence group with several q-blocks is cut into chunks of 4 consecutive

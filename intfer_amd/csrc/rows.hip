@@ -894,6 +894,7 @@ __global__ __launch_bounds__(1024) void pack_kernel(const int32_t* rows, int M, 
     o.row_seq[m] = r[0];
     o.row_pos[m] = r[1];
     o.row_kind[m] = r[3];
+    if (o.row_tok) o.row_tok[m] = r[2];
   }
   __syncthreads();
   const int ngroups = block_exscan(grp_start, M, tmp);  // grp_start[m] = #starts before m
