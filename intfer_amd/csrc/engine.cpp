@@ -1354,22 +1354,25 @@ int ifr_forward(ifr_ctx* c, const ifr_row* rows, int32_t M, int32_t* best_out, f
     if (more > c->free_pages.size())
       return fail(IFR_ENOMEM, "KV pool exhausted (%zu pages needed, %zu free)", more, c->free_pages.size());
   }
+  // new pages go into the pinned host block table; the rows of the
+  // sequences that grew go up in one copy (their slot range)
+  int dlo = INT32_MAX, dhi = -1;
   for (size_t g = 0; g < g_seq.size(); ++g) {
     Seq& s = c->seqs[g_seq[g]];
     const int need = (g_pos0[g] + g_len[g] + kPage - 1) / kPage;
-    bool dirty = false;
     while ((int)s.pages.size() < need) {
       const int p = c->free_pages.back();
       c->free_pages.pop_back();
       c->bt_h[(size_t)g_seq[g] * c->max_pages + s.pages.size()] = p;
       s.pages.push_back(p);
-      dirty = true;
+      dlo = std::min(dlo, g_seq[g]);
+      dhi = std::max(dhi, g_seq[g]);
     }
-    if (dirty) {
-      const size_t off = (size_t)g_seq[g] * c->max_pages;
-      HIPCHK(hipMemcpyAsync(c->bt_d + off, c->bt_h + off, c->max_pages * sizeof(int32_t),
-                            hipMemcpyHostToDevice, c->lane[0].st));
-    }
+  }
+  if (dhi >= 0) {
+    const size_t off = (size_t)dlo * c->max_pages;
+    HIPCHK(hipMemcpyAsync(c->bt_d + off, c->bt_h + off, (size_t)(dhi - dlo + 1) * c->max_pages * sizeof(int32_t),
+                          hipMemcpyHostToDevice, c->lane[0].st));
   }
   // ---- cut into sub-batches: [decode / verify rows | prefill chunks], or
   // decode rows halved by KV length; one sub-batch when timing each kernel
