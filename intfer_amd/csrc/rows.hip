@@ -863,10 +863,16 @@ __device__ int block_exscan(int* v, int n, int* tmp) {
   }
   if (lane == 63) tmp[w] = incl;
   __syncthreads();
-  if (threadIdx.x == 0) {
-    int run = 0;
-    for (int i = 0; i < nw; ++i) { const int t = tmp[i]; tmp[i] = run; run += t; }
-    tmp[nw] = run;
+  if (w == 0) {  // the wave totals (nw <= 64), scanned by the first wave
+    const int t = lane < nw ? tmp[lane] : 0;
+    int x = t;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+      const int y = __shfl_up(x, o, 64);
+      if (lane >= o) x += y;
+    }
+    if (lane < nw) tmp[lane] = x - t;
+    if (lane == 63) tmp[nw] = x;
   }
   __syncthreads();
   int run = tmp[w] + incl - s;
@@ -1016,9 +1022,9 @@ __global__ __launch_bounds__(1024) void pack_kernel(const int32_t* rows, int M, 
         for (int k = 0; k < nkv * nsm; ++k) o.order[off + k * 4 + qq] = -1;
   }
   __syncthreads();
-  block_exscan(wnt, M, tmp);
-  for (int m = threadIdx.x; m < M; m += blockDim.x)
-    if (rows[5 * m + 4]) o.want_rows[wnt[m]] = m;
+  const int nwant = block_exscan(wnt, M, tmp);
+  for (int m = threadIdx.x; m < M; m += blockDim.x)  // row m is wanted if the scan steps at m
+    if ((m + 1 < M ? wnt[m + 1] : nwant) > wnt[m]) o.want_rows[wnt[m]] = m;
 }
 
 }  // namespace
