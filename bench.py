@@ -66,6 +66,8 @@ def parse():
                     help="the same on the 27B-class (cfg5) shapes at M = 512 and 2160")
     ap.add_argument("--attn-sweep", action="store_true",
                     help="run only the attention sweep (cfg3, C=64 decode, mixed) and print its JSON line")
+    ap.add_argument("--attn-case", default="",
+                    help="NAME[:KV8[:REPS]]: repeat one attention case of --attn-sweep (for rocprofv3)")
     ap.add_argument("--attn-splits", default="0",
                     help="comma-separated KV tokens per attention unit for --attn-sweep (0: default)")
     ap.add_argument("--copy-calib", action="store_true",
@@ -279,21 +281,57 @@ def gemm_sweep(ia, dev, bits_list=(2, 4), Ms=(1, 8, 16, 64, 256, 1024), reps=3):
     return res
 
 
+def attn_cases(ia, cfg):
+    """The attention sweep's cases: (name, decode-row KV lengths, prefill chunks (offset, rows))."""
+    from intfer_amd import workloads as wl
+    dec4 = [len(p) + 32 for p in wl.cfg4_requests(64, seed=4, vocab=cfg.vocab)]
+    return [("cfg3", wl.cfg3_lengths(seed=3), [(0, 512), (1536, 512)]),
+            ("prefill", [], [(1024, 512)]),
+            ("c64_decode", dec4, []),
+            ("c64_mixed", dec4, [(1024, 512)])]
+
+
+def attn_case(ia, dev, spec):
+    """One case of attn_sweep (NAME[:KV8[:REPS]]), launched REPS + 1 times
+    back to back: the workload of a rocprofv3 kernel-trace of that case."""
+    parts = spec.split(":")
+    name = parts[0]
+    kv_int8 = int(parts[1]) if len(parts) > 1 else 0
+    reps = int(parts[2]) if len(parts) > 2 else 20
+    cfg = ia.default_cfg(layers=1, vocab=1024)
+    model = ia.SynthModel(cfg, seed=5)
+    rng = np.random.default_rng(21)
+    _, lens, chunks = next(c for c in attn_cases(ia, cfg) if c[0] == name)
+    total = sum(lens) + sum(o + n for o, n in chunks)
+    eng = ia.Engine(dev, model, max_seqs=len(lens) + len(chunks) + 1, max_seq_tokens=8192,
+                    pool_tokens=total + 64 * (len(lens) + 4), kv_int8=kv_int8, max_rows=1200)
+    seqs = []
+    for n in lens + [o + m for o, m in chunks]:
+        s = eng.seq_open()
+        k = rng.standard_normal((1, n, cfg.n_kv, cfg.head_dim), dtype=np.float32)
+        eng.load_kv(s, k, k)
+        seqs.append(s)
+    rows = [(seqs[i], n - 1, 0, 0, 1) for i, n in enumerate(lens)]
+    for j, (o, m) in enumerate(chunks):
+        rows += [(seqs[len(lens) + j], o + p, 0, 1, 1) for p in range(m)]
+    q = rng.standard_normal((len(rows), cfg.n_heads, cfg.head_dim), dtype=np.float32).astype(np.float16)
+    for _ in range(reps + 1):
+        eng.attention(0, rows, q)
+    model.close()
+    return {"metric": "attention case (rocprofv3 workload)", "case": name, "kv_int8": kv_int8,
+            "rows": len(rows), "launches": reps + 1}
+
+
 def attn_sweep(ia, dev, reps=10, splits=(0,)):
     """Joint ragged attention on one layer at the serve shapes: cfg3 (64
     decode rows, lognormal lengths, + two 512-row causal chunks), one
     512-row prefill chunk at offset 1024 alone, C=64 decode-only rows at the
     cfg4 context mix, and the same rows plus that chunk.  Durations come from HIP events on
     the engine stream around each launch (attention and combine separately)."""
-    from intfer_amd import workloads as wl
     cfg = ia.default_cfg(layers=1, vocab=1024)
     model = ia.SynthModel(cfg, seed=5)
     rng = np.random.default_rng(21)
-    dec4 = [len(p) + 32 for p in wl.cfg4_requests(64, seed=4, vocab=cfg.vocab)]
-    cases = [("cfg3", wl.cfg3_lengths(seed=3), [(0, 512), (1536, 512)]),
-             ("prefill", [], [(1024, 512)]),
-             ("c64_decode", dec4, []),
-             ("c64_mixed", dec4, [(1024, 512)])]
+    cases = attn_cases(ia, cfg)
     res = []
     plan = [(kv, c, sp) for kv in (0, 1) for c in cases for sp in splits]
     for kv_int8, (name, lens, chunks), split in plan:
@@ -897,6 +935,11 @@ def main():
         dev = ia.Device(0)
         res = gemm_case(ia, dev, a.gemm_case)
         print(json.dumps(res))
+        dev.close()
+        return 0
+    if a.attn_case:
+        dev = ia.Device(0)
+        print(json.dumps(attn_case(ia, dev, a.attn_case)))
         dev.close()
         return 0
     if a.attn_sweep:
