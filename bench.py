@@ -48,6 +48,8 @@ def parse():
     ap.add_argument("--chunk", type=int, default=512)
     ap.add_argument("--kv-int8", type=int, default=0)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--lanes", type=int, default=0,
+                    help="concurrent sub-batches per forward (ifr_kv_cfg.lanes; 0: the engine default, 1)")
     ap.add_argument("--attn-split", type=int, default=0,
                     help="KV tokens per attention unit of the load's engine (0: the library default, 256)")
     ap.add_argument("--no-roofline", action="store_true")
@@ -979,7 +981,7 @@ def main():
     C, max_new, chunk = a.concurrency, a.max_new, a.chunk
     cap = 2176
     eng = ia.Engine(dev, model, max_seqs=C, max_seq_tokens=cap, pool_tokens=C * cap,
-                    kv_int8=a.kv_int8, max_rows=64 + chunk, attn_split=a.attn_split)
+                    kv_int8=a.kv_int8, max_rows=64 + chunk, attn_split=a.attn_split, lanes=a.lanes)
     prompts = wl.cfg4_requests(C, seed=4, vocab=cfg.vocab)
     log(f"C={C} prompts: mean {np.mean([len(p) for p in prompts]):.0f} tokens, max_new {max_new}")
     for w in range(a.warmup):
