@@ -934,8 +934,9 @@ __global__ __launch_bounds__(1024) void pack_kernel(const int32_t* rows, int M, 
   }
   __syncthreads();
   block_exscan(ucnt, nb, tmp);  // ucnt[b] = first unit of block b
-  // one thread per q-block: its units and its rows' combine map
-  for (int gb = threadIdx.x; gb < nb; gb += blockDim.x) {
+  // one thread per (q-block, kv head): that head's units of the q-block
+  for (int t = threadIdx.x; t < nb * nkv; t += blockDim.x) {
+    const int gb = t / nkv, kvh = t - gb * nkv;
     const int g = bgrp[gb], b = gb - nblk[g];
     const int r0 = grp_start[g], len = grp_start[g + 1] - r0;
     const int pos0 = rows[5 * r0 + 1], seq = rows[5 * r0];
@@ -943,25 +944,30 @@ __global__ __launch_bounds__(1024) void pack_kernel(const int32_t* rows, int M, 
     const int kvhi = pos0 + b * qb + qn;
     const int ns = (kvhi + split - 1) / split;
     const int base = ucnt[gb];
-    for (int kvh = 0; kvh < nkv; ++kvh)
-      for (int s = 0; s < ns; ++s) {
-        AttnUnit u;
-        u.seq = seq;
-        u.kvh = kvh;
-        u.row0 = r0 + b * qb;
-        u.qn = qn;
-        u.qpos0 = pos0 + b * qb;
-        u.kv_lo = s * split;
-        u.kv_hi = min((s + 1) * split, kvhi);
-        u.pad = 0;
-        o.units[base + kvh * ns + s] = u;
-      }
-    for (int i = 0; i < qn; ++i) {
-      const int m = r0 + b * qb + i;
-      o.comb_base[m] = base;
-      o.comb_nsplit[m] = ns;
-      o.comb_tok[m] = i;
+    for (int s = 0; s < ns; ++s) {
+      AttnUnit u;
+      u.seq = seq;
+      u.kvh = kvh;
+      u.row0 = r0 + b * qb;
+      u.qn = qn;
+      u.qpos0 = pos0 + b * qb;
+      u.kv_lo = s * split;
+      u.kv_hi = min((s + 1) * split, kvhi);
+      u.pad = 0;
+      o.units[base + kvh * ns + s] = u;
     }
+  }
+  // one thread per row: its combine map (q-block gb = its group's first
+  // block + (m - r0) / qb)
+  for (int m = threadIdx.x; m < M; m += blockDim.x) {
+    const int g = flag[m];  // the row's group
+    const int r0 = grp_start[g], len = grp_start[g + 1] - r0;
+    const int b = (m - r0) / qb, gb = nblk[g] + b;
+    const int pos0 = rows[5 * r0 + 1];
+    const int qn = min(qb, len - b * qb);
+    o.comb_base[m] = ucnt[gb];
+    o.comb_nsplit[m] = (pos0 + b * qb + qn + split - 1) / split;
+    o.comb_tok[m] = m - r0 - b * qb;
   }
   __syncthreads();
   // ---- dispatch order (see attn_slot_count): per-group slot counts of the
@@ -987,7 +993,9 @@ __global__ __launch_bounds__(1024) void pack_kernel(const int32_t* rows, int M, 
   __syncthreads();
   block_exscan(bgrp, ngroups, tmp);
   __syncthreads();
-  for (int gb = threadIdx.x; gb < nb; gb += blockDim.x) {
+  // one thread per (q-block, kv head): that head's slots of the q-block
+  for (int t = threadIdx.x; t < nb * nkv; t += blockDim.x) {
+    const int gb = t / nkv, kvh = t - gb * nkv;
     int g = 0;  // group of q-block gb (nblk[] holds first blocks, ascending)
     {
       int lo = 0, hi = ngroups - 1;
@@ -1003,7 +1011,7 @@ __global__ __launch_bounds__(1024) void pack_kernel(const int32_t* rows, int M, 
     const int ns = (pos0 + min((b + 1) * qb, len) + split - 1) / split;
     const int base = ucnt[gb];
     if (nbg == 1) {
-      for (int i = 0; i < nkv * ns; ++i) o.order[CS + bgrp[g] + i] = base + i;
+      for (int s = 0; s < ns; ++s) o.order[CS + bgrp[g] + kvh * ns + s] = base + kvh * ns + s;
       continue;
     }
     const int j = b >> 2, q = b & 3;
@@ -1014,12 +1022,11 @@ __global__ __launch_bounds__(1024) void pack_kernel(const int32_t* rows, int M, 
     }
     const int bl = min(4 * j + 3, nbg - 1);
     const int nsm = (pos0 + min((bl + 1) * qb, len) + split - 1) / split;
-    for (int kvh = 0; kvh < nkv; ++kvh)
-      for (int s = 0; s < nsm; ++s) o.order[off + (kvh * nsm + s) * 4 + q] = s < ns ? base + kvh * ns + s : -1;
+    for (int s = 0; s < nsm; ++s) o.order[off + (kvh * nsm + s) * 4 + q] = s < ns ? base + kvh * ns + s : -1;
     // slots of absent q-blocks in a short last chunk
     if (b == nbg - 1)
       for (int qq = q + 1; qq < 4; ++qq)
-        for (int k = 0; k < nkv * nsm; ++k) o.order[off + k * 4 + qq] = -1;
+        for (int s = 0; s < nsm; ++s) o.order[off + (kvh * nsm + s) * 4 + qq] = -1;
   }
   __syncthreads();
   const int nwant = block_exscan(wnt, M, tmp);
