@@ -383,21 +383,35 @@ def test_attention_cfg3(dev, kv_int8):
     assert np.sqrt((err ** 2).mean()) < 5e-4
 
 
-def test_pack_maps_match_restatement(dev):
+# (sequence lengths, rows as (sequence index, position, kind, want)):
+# decode, verify and a 3-q-block chunk in one quad; then several quads of a
+# chunk whose q-blocks span 3-4 KV splits, and a chunk that crosses a split
+# boundary inside a quad (q-blocks of one quad with different split counts)
+PACK_CASES = [
+    ([300, 40, 1000, 20],
+     [(0, 299, 0, 1), (1, 30, 2, 1), (1, 31, 2, 1), (1, 32, 2, 1), (2, 999, 0, 0)] +
+     [(3, p, 1, int(p == 19)) for p in range(20)]),
+    ([513, 900, 64, 280],
+     [(0, 512, 0, 1)] + [(1, 700 + p, 1, int(p == 199)) for p in range(200)] + [(2, 63, 0, 1)] +
+     [(3, 240 + p, 1, int(p == 39)) for p in range(40)]),
+]
+
+
+@pytest.mark.parametrize("case", range(len(PACK_CASES)))
+def test_pack_maps_match_restatement(dev, case):
     from oracle import pack as pk
-    cfg, model, eng = _attn_engine(dev, 0, [300, 40, 1000], [(0, 20)])
+    lens, spec = PACK_CASES[case]
+    cfg, model, eng = _attn_engine(dev, 0, lens, [])
     rng = np.random.default_rng(9)
-    lens = [300, 40, 1000, 20]
     seqs = []
     for n in lens:
         s = eng.seq_open()
         k = rng.standard_normal((1, n, cfg.n_kv, cfg.head_dim), dtype=np.float32)
         eng.load_kv(s, k, k)
         seqs.append(s)
-    rows = [(seqs[0], 299, 0, 0, 1), (seqs[1], 30, 0, 2, 1), (seqs[1], 31, 0, 2, 1),
-            (seqs[1], 32, 0, 2, 1), (seqs[2], 999, 0, 0, 0)] + \
-           [(seqs[3], p, 0, 1, int(p == 19)) for p in range(20)]
+    rows = [(seqs[i], pos, 0, kind, want) for i, pos, kind, want in spec]
     q = np.zeros((len(rows), cfg.n_heads, cfg.head_dim), np.float16)
+    announce(f"pack maps case {case}: M={len(rows)}")
     eng.attention(0, rows, q)
     M = len(rows)
     cu = np.zeros(M + 1, np.int32)
