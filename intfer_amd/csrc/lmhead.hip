@@ -106,8 +106,11 @@ __global__ __launch_bounds__(256) void lmhead_kernel(LmP p) {
         if (better(ov, oi, bv, bi)) { bv = ov; bi = oi; }
       }
       if (lrow == 0 && row < p.W) {
-        p.pv[(size_t)part * p.W + row] = bv;
-        p.pi[(size_t)part * p.W + row] = bi;
+        // row-major [row][part] (part count = 4 gridDim.x): the final
+        // reduce reads each row's partials contiguously
+        const size_t at = (size_t)row * (4 * gridDim.x) + part;
+        p.pv[at] = bv;
+        p.pi[at] = bi;
       }
     }
 }
@@ -119,8 +122,8 @@ __global__ __launch_bounds__(256) void argmax_final_kernel(const float* pv, cons
   float bv = -INFINITY;
   int bi = 0x7fffffff;
   for (int q = threadIdx.x; q < nparts; q += blockDim.x) {
-    const float v = pv[(size_t)q * W + row];
-    const int i = pi[(size_t)q * W + row];
+    const float v = pv[(size_t)row * nparts + q];
+    const int i = pi[(size_t)row * nparts + q];
     if (better(v, i, bv, bi)) { bv = v; bi = i; }
   }
   __shared__ float sv[256];
