@@ -64,6 +64,12 @@ typedef struct ifr_model_cfg {
                        * the attention output is scaled by sigmoid(gate) before
                        * the O projection (:7697-7698); 0: q_proj has
                        * n_heads * head_dim rows, no gate */
+  int32_t attn_gate_off; /* 1: a packed q_proj (attn_gate = 1) keeps its layout
+                          * but the gate is not applied, as the reference does
+                          * when config.json sets attn_output_gate false
+                          * (main.cpp:250, :7697: the sigmoid needs both
+                          * packed_gate and the flag); 0 (default, the
+                          * reference's default true): applied */
 } ifr_model_cfg;
 
 /* One quantized linear y = W x, W is [N][K].  Logical (load) layout:
@@ -522,6 +528,13 @@ typedef struct ifr_sched_cfg {
   uint32_t seed;        /* base seed of the requests' samplers: a request
                          * without its own seed draws from mt19937(seed + id)
                          * (run_serve admission, main.cpp:9305) */
+  int32_t spec_adapt;   /* adaptive draft width (SpecAdapt, main.cpp:
+                         * 11454-11511, INTFER_SPEC_ADAPT): 1 picks each
+                         * round's width per request as the w in 1..cap
+                         * maximising w * accept_ema / (w + 1), with
+                         * accept_ema an EMA (0.75 / 0.25, clamped to
+                         * [0.05, 0.95], start 0.5) of accepted / drafted;
+                         * cap = spec_k, or 8 when spec_k is 0 */
 } ifr_sched_cfg;
 
 int ifr_sched_create(ifr_ctx* ctx, const ifr_sched_cfg* cfg, ifr_sched** out);

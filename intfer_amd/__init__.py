@@ -398,11 +398,11 @@ class Scheduler:
 
     def __init__(self, engine: Engine | None = None, chunk_m=128, live_cap=64, split_iter=0,
                  round_robin=1, spec_k=0, backend: SchedBackend | None = None, pack_prefill=0,
-                 prefix_cache=0, seed=0):
+                 prefix_cache=0, seed=0, spec_adapt=0):
         cfg = SchedCfg()
         cfg.chunk_m, cfg.live_cap, cfg.split_iter = chunk_m, live_cap, split_iter
         cfg.round_robin, cfg.spec_k, cfg.pack_prefill = round_robin, spec_k, pack_prefill
-        cfg.prefix_cache, cfg.seed = prefix_cache, seed & 0xFFFFFFFF
+        cfg.prefix_cache, cfg.seed, cfg.spec_adapt = prefix_cache, seed & 0xFFFFFFFF, spec_adapt
         self.h = C.c_void_p()
         self._keep = backend
         if backend is not None:

@@ -23,7 +23,7 @@ class ModelCfg(C.Structure):
                 ("n_kv", C.c_int32), ("head_dim", C.c_int32), ("inter", C.c_int32),
                 ("vocab", C.c_int32), ("rotary_dim", C.c_int32), ("rms_eps", C.c_float),
                 ("rope_theta", C.c_float), ("group_size", C.c_int32), ("qk_norm", C.c_int32),
-                ("rotate", C.c_int32), ("attn_gate", C.c_int32)]
+                ("rotate", C.c_int32), ("attn_gate", C.c_int32), ("attn_gate_off", C.c_int32)]
 
 
 class Linear(C.Structure):
@@ -78,7 +78,7 @@ class Row(C.Structure):
 class SchedCfg(C.Structure):
     _fields_ = [("chunk_m", C.c_int32), ("live_cap", C.c_int32), ("split_iter", C.c_int32),
                 ("round_robin", C.c_int32), ("spec_k", C.c_int32), ("pack_prefill", C.c_int32),
-                ("prefix_cache", C.c_int32), ("seed", C.c_uint32)]
+                ("prefix_cache", C.c_int32), ("seed", C.c_uint32), ("spec_adapt", C.c_int32)]
 
 
 SEQ_OPEN = C.CFUNCTYPE(C.c_int, C.c_void_p, C.POINTER(C.c_int32))

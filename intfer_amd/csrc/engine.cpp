@@ -389,6 +389,22 @@ long count_units(const std::vector<int>& g_pos0, const std::vector<int>& g_len, 
   return n;
 }
 
+// Attention units the workspace is sized for: the most any admissible batch
+// can need.  M <= max_rows rows in at most min(M, max_seqs) sequence groups
+// make at most ceil(M / qb) + min(M, max_seqs) q-blocks (each group adds one
+// partial block), and a q-block's keys end at most at max_seq_tokens, so it
+// has at most ceil(max_seq_tokens / split) splits per kv head.  Capped at
+// kMaxUnits (partials of 8 KB each: about 4.4 GB); a capped engine declines
+// the batches beyond it.
+constexpr long kMaxUnits = 1L << 19;
+int max_units_for(const ifr_kv_cfg& kv, int nkv, int qb) {
+  const long split = kv.attn_split > 0 ? kv.attn_split : kSplit;
+  const long M = kv.max_rows;
+  const long qblocks = (M + qb - 1) / qb + std::min<long>(M, kv.max_seqs);
+  const long bound = (long)nkv * qblocks * ((kv.max_seq_tokens + split - 1) / split);
+  return (int)std::min(bound, kMaxUnits);
+}
+
 // Algorithmic work of one attention launch: K+V of every row's sequence
 // (plus int8 scales), Q in and O out; flops = QK^T + PV over each row's
 // visible keys (pos + 1).
@@ -463,13 +479,16 @@ int prep_sub(ifr_ctx* c, const ifr_row* rows, SubBatch& sb) {
     }
   const int nkv = c->cfg.n_kv;
   // fixed KV split: each row's partial decomposition depends only on its own
-  // sequence (batch-invariant results: split == joint, solo == loaded)
+  // sequence (batch-invariant results: split == joint, solo == loaded).  The
+  // unit workspace is sized at load for the largest batch the engine admits,
+  // so only an engine whose bound was capped can see more units; such a
+  // batch is declined (nothing enqueued) rather than run with a wider split,
+  // which would change every row's decomposition.
   sb.split = c->kv.attn_split > 0 ? c->kv.attn_split : kSplit;
   sb.nunits = count_units(sb.g_pos0, sb.g_len, nkv, sb.split, c->qb);
-  while (sb.nunits > c->max_units) {
-    sb.split *= 2;
-    sb.nunits = count_units(sb.g_pos0, sb.g_len, nkv, sb.split, c->qb);
-  }
+  if (sb.nunits > c->max_units)
+    return fail(IFR_EDECLINE, "batch needs %ld attention units, the workspace holds %d (KV split %d)",
+                sb.nunits, c->max_units, sb.split);
   sb.nslots = (int)ifrk::attn_slot_count(sb.g_pos0.data(), sb.g_len.data(), (int)sb.g_len.size(), nkv,
                                          sb.split, c->qb, &sb.nchunked);
   attn_work(c, r, sb.M, sb.g_pos0, sb.g_len, &sb.attn_bytes, &sb.attn_flops);
@@ -569,7 +588,7 @@ int launch_layer(ifr_ctx* c, const SubBatch& sb, int l) {
   {
     ifrk::CombineArgs a{L.part_o, L.part_ml, L.pk.comb_base, L.pk.comb_nsplit, L.pk.comb_tok,
                         M, nq, nkv, hd, nullptr, L.aq, L.as, L.gs, 16 * kAttnTiles,
-                        cf.attn_gate ? L.gate : nullptr};
+                        cf.attn_gate && !cf.attn_gate_off ? L.gate : nullptr};
     Scope sc(c, L.st, "combine", sb.comb_bytes);
     HIPCHK(ifrk::launch_combine(a, L.st));
   }
@@ -1094,10 +1113,12 @@ int ifr_model_load(ifr_ctx* c, const ifr_host_model* m, const ifr_kv_cfg* kvc) {
   // workspaces, one set per lane
   const int Mx = kvc->max_rows;
   c->maxM = Mx;
-  c->max_units = 65536;
+  c->max_units = max_units_for(*kvc, nkv, c->qb);
   const int Kmax = std::max(std::max(H, qN), F);
   const int nparts = ifrk::lmhead_nparts(V);
-  for (Lane& L : c->lane) {
+  // lane 1 runs only when two lanes are configured
+  for (int li = 0; li < (kvc->lanes == 2 ? 2 : 1); ++li) {
+    Lane& L = c->lane[li];
     HIPCHK(hipHostMalloc(reinterpret_cast<void**>(&L.rows_h), (size_t)Mx * 5 * sizeof(int32_t), hipHostMallocDefault));
     HIPCHK(hipHostMalloc(reinterpret_cast<void**>(&L.best_h), (size_t)Mx * sizeof(int32_t), hipHostMallocDefault));
     int r = 0;
@@ -1479,12 +1500,11 @@ int ifr_attention(ifr_ctx* c, int32_t layer, const ifr_row* rows, int32_t M, con
   const int nq = c->cfg.n_heads, nkv = c->cfg.n_kv, hd = c->cfg.head_dim;
   std::vector<int> g_len, g_pos0;
   if (int r = attn_groups(c, rows, M, g_len, g_pos0)) return r;
-  int split = c->kv.attn_split > 0 ? c->kv.attn_split : kSplit;
-  long nunits = count_units(g_pos0, g_len, nkv, split, c->qb);
-  while (nunits > c->max_units) {
-    split *= 2;
-    nunits = count_units(g_pos0, g_len, nkv, split, c->qb);
-  }
+  const int split = c->kv.attn_split > 0 ? c->kv.attn_split : kSplit;
+  const long nunits = count_units(g_pos0, g_len, nkv, split, c->qb);
+  if (nunits > c->max_units)
+    return fail(IFR_EDECLINE, "batch needs %ld attention units, the workspace holds %d (KV split %d)", nunits,
+                c->max_units, split);
   c->last_split = split;
   c->last_units = (int)nunits;
   long nchunked = 0;

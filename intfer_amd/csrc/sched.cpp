@@ -27,9 +27,46 @@
 
 #include "intfer_amd.h"
 
+namespace ifrh {
+// the library's error record (ifr_last_error): sets the message, returns code
+int fail(int code, const char* fmt, ...);
+}  // namespace ifrh
+
 namespace {
 
+using ifrh::fail;
+
 constexpr int kEos0 = 248044, kEos1 = 248046;
+
+// Adaptive draft width (SpecAdapt, main.cpp:11454-11511, restated without
+// the second-device producer scores, which this path does not have): the
+// width w in 1..cap maximising w * accept_ema / (w + 1), first maximum
+// kept; the EMA moves a quarter of the way to each round's accepted /
+// drafted ratio and stays inside [0.05, 0.95].  Scheduling only: it picks
+// how many drafts a round verifies, never which tokens.
+struct SpecAdapt {
+  double accept_ema = 0.5;
+  int choose(int cap) const {
+    if (cap < 1) return 1;
+    int best = 1;
+    double best_score = -1.0;
+    for (int w = 1; w <= cap; ++w) {
+      const double score = ((double)w * accept_ema) / ((double)w + 1.0);
+      if (score > best_score) {
+        best_score = score;
+        best = w;
+      }
+    }
+    return best;
+  }
+  void observe(int accepted, int tried) {
+    if (tried <= 0) return;
+    const double r = (double)accepted / (double)tried;
+    accept_ema = accept_ema * 0.75 + r * 0.25;
+    if (accept_ema < 0.05) accept_ema = 0.05;
+    if (accept_ema > 0.95) accept_ema = 0.95;
+  }
+};
 
 struct Req {
   int64_t id = 0;
@@ -41,6 +78,7 @@ struct Req {
   float temperature = 0.f, top_p = 0.f;
   int top_k = 0;
   ifr_rng* rng = nullptr;
+  SpecAdapt adapt;  // this request's draft-width controller (spec_adapt)
   bool greedy() const { return temperature <= 0.f && top_k == 0 && top_p <= 0.f; }
   ~Req() { ifr_rng_free(rng); }
 };
@@ -73,6 +111,7 @@ std::vector<int32_t> ngram_from(const std::vector<int32_t>& gen, const std::vect
 
 bool is_eos(int t) { return t == kEos0 || t == kEos1; }
 
+
 }  // namespace
 
 // A finished request kept for prefix reuse (PrefixCache::Entry,
@@ -103,6 +142,10 @@ struct ifr_sched {
   std::deque<CacheEntry> cache;        // most recently used first
 
   bool caching() const { return cfg.prefix_cache > 0 && be.seq_copy_prefix; }
+
+  // Draft width cap (main.cpp:11512-11514): spec_k, or 8 under spec_adapt
+  // when spec_k is 0; 0 = no speculation.
+  int spec_cap() const { return cfg.spec_adapt && cfg.spec_k < 1 ? 8 : cfg.spec_k; }
 
   // Drop the least recently used entry other than the one holding slot keep.
   bool evict_lru(int keep = -1) {
@@ -230,8 +273,9 @@ struct ifr_sched {
         items.push_back(std::move(it));
         continue;
       }
-      if (cfg.spec_k > 0) {
-        it.drafts = ngram_from(q->generated, q->prompt, q->token, cfg.spec_k);
+      if (spec_cap() > 0) {
+        const int width = cfg.spec_adapt ? q->adapt.choose(spec_cap()) : cfg.spec_k;
+        it.drafts = ngram_from(q->generated, q->prompt, q->token, width);
         while (!it.drafts.empty() && q->pos + (int)it.drafts.size() >= max_seq_tokens) it.drafts.pop_back();
       }
       const int kind = it.drafts.empty() ? IFR_ROW_DECODE : IFR_ROW_VERIFY;
@@ -265,6 +309,7 @@ struct ifr_sched {
       const int K = (int)it.drafts.size();
       int a = 0;
       while (a < K && best[(size_t)it.row0 + a] == it.drafts[(size_t)a]) a++;
+      if (cfg.spec_adapt) q.adapt.observe(a, K);
       const int corr = best[(size_t)it.row0 + a];
       std::vector<int32_t> acc;
       for (int i = 0; i < a; ++i) {
@@ -401,11 +446,12 @@ int eng_copy(void* u, int32_t dst, int32_t src, int32_t len) {
 
 int ifr_sched_create_backend(const ifr_sched_backend* be, const ifr_sched_cfg* cfg, ifr_sched** out) {
   if (!be || !cfg || !out || !be->seq_open || !be->seq_close || !be->seq_truncate || !be->forward)
-    return IFR_EINVAL;
+    return fail(IFR_EINVAL, "sched: null argument or backend entry");
   if (cfg->chunk_m < 1 || cfg->chunk_m > 4096 || cfg->live_cap < 1 || cfg->spec_k < 0 ||
       cfg->spec_k > 15 || cfg->pack_prefill < 0 || cfg->pack_prefill > 1 || cfg->prefix_cache < 0 ||
-      cfg->prefix_cache > 16 || be->kv_capacity <= 0 || (be->forward_logits && be->vocab <= 0))
-    return IFR_EINVAL;
+      cfg->prefix_cache > 16 || cfg->spec_adapt < 0 || cfg->spec_adapt > 1 || be->kv_capacity <= 0 ||
+      (be->forward_logits && be->vocab <= 0))
+    return fail(IFR_EINVAL, "sched: configuration out of range");
   auto* s = new ifr_sched();
   s->be = *be;
   s->cfg = *cfg;
@@ -415,7 +461,7 @@ int ifr_sched_create_backend(const ifr_sched_backend* be, const ifr_sched_cfg* c
 }
 
 int ifr_sched_create(ifr_ctx* ctx, const ifr_sched_cfg* cfg, ifr_sched** out) {
-  if (!ctx) return IFR_EINVAL;
+  if (!ctx) return fail(IFR_EINVAL, "sched: ctx is null");
   ifr_sched_backend be{};
   be.user = ctx;
   be.seq_open = eng_open;
@@ -446,7 +492,8 @@ int ifr_sched_submit(ifr_sched* s, const int32_t* prompt, int32_t n, int32_t max
 
 int ifr_sched_submit_sampled(ifr_sched* s, const int32_t* prompt, int32_t n, int32_t max_new,
                              const ifr_sample_params* sp, int64_t* id) {
-  if (!s || !prompt || n <= 0 || max_new < 0) return IFR_EINVAL;
+  if (!s || !prompt || n <= 0 || max_new < 0)
+    return fail(IFR_EINVAL, "sched_submit: null scheduler or prompt, n %d, max_new %d", n, max_new);
   auto r = std::make_unique<Req>();
   if (sp) {
     r->temperature = sp->temperature;
@@ -455,7 +502,7 @@ int ifr_sched_submit_sampled(ifr_sched* s, const int32_t* prompt, int32_t n, int
   }
   r->id = s->next_id;
   if (!r->greedy()) {
-    if (!s->be.forward_logits) return IFR_EDECLINE;
+    if (!s->be.forward_logits) return fail(IFR_EDECLINE, "sampling request needs a backend with forward_logits");
     // the request's generator (main.cpp:9305)
     if (int e = ifr_rng_create(sp->has_seed ? sp->seed : s->cfg.seed + (uint32_t)r->id, &r->rng)) return e;
   }
@@ -469,7 +516,7 @@ int ifr_sched_submit_sampled(ifr_sched* s, const int32_t* prompt, int32_t n, int
 }
 
 int ifr_sched_step(ifr_sched* s, int32_t* rows_run) {
-  if (!s) return IFR_EINVAL;
+  if (!s) return fail(IFR_EINVAL, "sched_step: scheduler is null");
   int32_t dummy = 0;
   if (!rows_run) rows_run = &dummy;
   *rows_run = 0;
@@ -481,6 +528,10 @@ int ifr_sched_step(ifr_sched* s, int32_t* rows_run) {
     s->prefill_q.push_back(q);
   }
   int r = s->cfg.split_iter ? s->split(rows_run) : s->joint(rows_run);
+  // A declined joint forward changed nothing: the same iteration runs the
+  // split path, the chunk then the decode rows (serve_iteration,
+  // main.cpp:9247-9256).
+  if (r == IFR_EDECLINE && !s->cfg.split_iter) r = s->split(rows_run);
   if (r) return r;
   // live compaction; finished requests release their KV and report done
   // (run_serve's {"done"} accounting, main.cpp:9349-9363)
@@ -498,9 +549,9 @@ int ifr_sched_step(ifr_sched* s, int32_t* rows_run) {
 }
 
 int ifr_sched_result(ifr_sched* s, int64_t id, int32_t* out, int32_t cap, int32_t* n, int32_t* done) {
-  if (!s) return IFR_EINVAL;
+  if (!s) return fail(IFR_EINVAL, "sched_result: scheduler is null");
   auto it = s->pool.find(id);
-  if (it == s->pool.end()) return IFR_EINVAL;
+  if (it == s->pool.end()) return fail(IFR_EINVAL, "sched_result: no request %lld", (long long)id);
   const Req& q = *it->second;
   const int k = std::min<int>(cap, (int)q.generated.size());
   for (int i = 0; i < k && out; ++i) out[i] = q.generated[(size_t)i];
@@ -510,14 +561,14 @@ int ifr_sched_result(ifr_sched* s, int64_t id, int32_t* out, int32_t cap, int32_
 }
 
 int ifr_sched_record_events(ifr_sched* s, int32_t on) {
-  if (!s) return IFR_EINVAL;
+  if (!s) return fail(IFR_EINVAL, "sched_record_events: scheduler is null");
   s->record = on != 0;
   if (!s->record) s->events.clear();
   return IFR_OK;
 }
 
 int ifr_sched_events(ifr_sched* s, ifr_sched_event* out, int32_t cap, int32_t* n) {
-  if (!s || (cap > 0 && !out) || !n) return IFR_EINVAL;
+  if (!s || (cap > 0 && !out) || !n) return fail(IFR_EINVAL, "sched_events: null argument");
   int32_t k = 0;
   while (k < cap && !s->events.empty()) {
     out[k++] = s->events.front();
@@ -528,17 +579,17 @@ int ifr_sched_events(ifr_sched* s, ifr_sched_event* out, int32_t cap, int32_t* n
 }
 
 int ifr_sched_release(ifr_sched* s, int64_t id) {
-  if (!s) return IFR_EINVAL;
+  if (!s) return fail(IFR_EINVAL, "sched_release: scheduler is null");
   auto it = s->pool.find(id);
-  if (it == s->pool.end()) return IFR_EINVAL;
-  if (!it->second->finished) return IFR_ESTATE;
+  if (it == s->pool.end()) return fail(IFR_EINVAL, "sched_release: no request %lld", (long long)id);
+  if (!it->second->finished) return fail(IFR_ESTATE, "sched_release: request %lld not finished", (long long)id);
   s->pool.erase(it);
   return IFR_OK;
 }
 
 int ifr_sched_info(ifr_sched* s, int32_t* live, int32_t* prefill, int32_t* pending,
                    int32_t* kv_capacity) {
-  if (!s) return IFR_EINVAL;
+  if (!s) return fail(IFR_EINVAL, "sched_info: scheduler is null");
   if (live) *live = (int32_t)s->live.size();
   if (prefill) *prefill = (int32_t)s->prefill_q.size();
   if (pending) *pending = (int32_t)s->pending.size();
@@ -547,7 +598,7 @@ int ifr_sched_info(ifr_sched* s, int32_t* live, int32_t* prefill, int32_t* pendi
 }
 
 int ifr_sched_last_rows(ifr_sched* s, ifr_row* out, int32_t cap, int32_t* n) {
-  if (!s) return IFR_EINVAL;
+  if (!s) return fail(IFR_EINVAL, "sched_last_rows: scheduler is null");
   const int k = std::min<int>(cap, (int)s->last_rows.size());
   for (int i = 0; i < k && out; ++i) out[i] = s->last_rows[(size_t)i];
   if (n) *n = (int32_t)s->last_rows.size();

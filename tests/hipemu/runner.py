@@ -337,6 +337,62 @@ def attention_ragged(heads=(16, 8)):
 
 
 @scenario
+def noalloc_limits():
+    """ifr_attention_noalloc at its row limit (512 rows) with ~3100 of its
+    4096 attention units (a 32-token KV split makes many short units), twice
+    (large, then small), against ifr_attention bit for bit: ASan bounds the
+    whole scratch array, and a region of it overlapping another would change
+    the results.  Then the two refusals: 513 rows, and more than 4096 units."""
+    import intfer_amd as ia
+    cfg = ia.default_cfg(layers=1, vocab=512, hidden=256, n_heads=4, n_kv=2, inter=256)
+    model = ia.SynthModel(cfg, seed=6)
+    dev = ia.Device(0)
+    L = ia.lib()
+    eng = ia.Engine(dev, model, max_seqs=20, max_seq_tokens=2048, pool_tokens=20 * 2048, max_rows=600,
+                    attn_split=32)
+    rng = np.random.default_rng(44)
+    nkv, hd, nq = cfg.n_kv, cfg.head_dim, cfg.n_heads
+    seqs = []
+    for n in [1024] + [64] * 16 + [2048]:
+        s = eng.seq_open()
+        eng.load_kv(s, rng.standard_normal((1, n, nkv, hd), dtype=np.float32),
+                    rng.standard_normal((1, n, nkv, hd), dtype=np.float32))
+        seqs.append(s)
+
+    def noalloc(rows, q):
+        arr = ia.rows_array(rows)
+        M = len(arr)
+        qd = dev.upload(np.ascontiguousarray(q, dtype=np.float16))
+        od = dev.alloc(M * nq * hd * 4)
+        try:
+            rc = L.ifr_attention_noalloc(dev.ctx, 0, arr, M, qd.p, od.p)
+            return rc, (dev.download(od, np.float32, (M, nq * hd)) if rc == 0 else None)
+        finally:
+            qd.free()
+            od.free()
+
+    big = [(seqs[0], 528 + p, 0, 1, 1) for p in range(496)] + [(seqs[1 + i], 63, 0, 0, 1) for i in range(16)]
+    small = [(seqs[0], 1000 + p, 0, 1, 1) for p in range(20)] + [(seqs[1 + i], 63, 0, 0, 1) for i in range(3)]
+    for name, rows in (("512 rows", big), ("23 rows", small)):
+        q = rng.standard_normal((len(rows), nq, hd), dtype=np.float32).astype(np.float16)
+        rc, got = noalloc(rows, q)
+        assert rc == 0, L.ifr_last_error()
+        ref = eng.attention(0, rows, q)
+        assert np.array_equal(got.view(np.uint32), ref.view(np.uint32)), name
+        say(f"noalloc {name}: bit-identical to ifr_attention")
+    over = big + [(seqs[-1], 0, 0, 1, 1)]
+    rc, _ = noalloc(over, np.zeros((len(over), nq, hd), np.float16))
+    assert rc == ia.IFR_EINVAL and b"no-allocation limit" in L.ifr_last_error()
+    many = [(seqs[-1], 1536 + p, 0, 1, 1) for p in range(512)]  # 64 q-blocks x 2 heads x 49..64 splits
+    rc, _ = noalloc(many, np.zeros((512, nq, hd), np.float16))
+    assert rc == ia.IFR_EINVAL and b"attention units" in L.ifr_last_error()
+    say("noalloc refusals: 513 rows, > 4096 units")
+    del eng
+    dev.close()
+    model.close()
+
+
+@scenario
 def forward_gqa5():
     """A layer of the 27B-class shape family at small width: 40 q / 8 kv
     heads (GQA group 5), hidden 1280 (non-power-of-two Hadamard), an FFN of

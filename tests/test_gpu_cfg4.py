@@ -1,5 +1,5 @@
 """cfg4 serve load on the full 28-layer 0.8B-class INT2 engine (the load
-bench.py times): C in {32, 64} requests with prompts U[64, 2048], max_new 64,
+bench.py times): C in {4, 8, 32, 64} requests with prompts U[64, 2048], max_new 64,
 greedy, chunk budget 512, round-robin prefill, live cap 64.
 
   * every request finishes with max_new + 1 generated tokens (the prefill's
@@ -54,7 +54,7 @@ def _run(eng, prompts):
     return res, iters, dt
 
 
-@pytest.mark.parametrize("conc", [32, 64])
+@pytest.mark.parametrize("conc", [4, 8, 32, 64])
 def test_cfg4_load_finishes_and_solo_equals_loaded(engine, conc):
     cfg, eng = engine
     prompts = wl.cfg4_requests(conc, seed=4, vocab=cfg.vocab)

@@ -7,6 +7,8 @@ main.cpp:7625-7640, :7697-7698), against the CPU oracle's restatement.
     bit for bit, through the whole 2-layer forward and greedy steps: the
     per-token quantization of x / 2 has the codes of x and half the scale;
   * the fused QKV epilogue and the separate q/k pass give the same bits;
+  * with attn_gate_off (attn_output_gate = false) the packed model equals
+    the ungated one of the same seed, bit for bit;
   * a gated one-layer model matches the oracle's tokens and logits within
     the one-layer bound (the gate's device expf may move an int8 code of the
     O-projection input by one), and the full 28-layer cfg1 iteration stays
@@ -35,8 +37,9 @@ def _zero_gate_pair(layers):
     return gated, plain
 
 
-def _run(dev, model, prompt, steps, separate_qk=0):
-    eng = ia.Engine(dev, model, max_seqs=4, max_seq_tokens=1024, max_rows=256, separate_qk=separate_qk)
+def _run(dev, model, prompt, steps, separate_qk=0, kv_int8=0):
+    eng = ia.Engine(dev, model, max_seqs=4, max_seq_tokens=1024, max_rows=256, separate_qk=separate_qk,
+                    kv_int8=kv_int8)
     try:
         s = eng.seq_open()
         n = len(prompt)
@@ -63,6 +66,27 @@ def test_zero_gate_equals_halved_o_projection(dev):
             assert np.array_equal(x.view(np.uint32), y.view(np.uint32))
     finally:
         gated.close()
+        plain.close()
+
+
+@pytest.mark.parametrize("kv_int8", [0, 1])
+def test_gate_off_equals_the_ungated_model(dev, kv_int8):
+    """attn_gate_off (attn_output_gate = false, main.cpp:250, :7697) on a
+    packed q_proj: the q rows come out of the [q, gate] layout and the gate
+    is not applied, so the device forward equals the ungated model of the
+    same seed (whose q rows are the same), bit for bit."""
+    cfg_off = ia.default_cfg(layers=2, attn_gate=1, attn_gate_off=1)
+    off = ia.SynthModel(cfg_off, seed=13, bits=2)
+    plain = ia.SynthModel(ia.default_cfg(layers=2), seed=13, bits=2)
+    try:
+        prompt = np.random.default_rng(33).integers(0, 151936, size=200).tolist()
+        announce(f"gate off vs ungated, kv_int8={kv_int8}")
+        a = _run(dev, off, prompt, 4, kv_int8=kv_int8)
+        b = _run(dev, plain, prompt, 4, kv_int8=kv_int8)
+        for x, y in zip(a, b):
+            assert np.array_equal(x.view(np.uint32), y.view(np.uint32))
+    finally:
+        off.close()
         plain.close()
 
 

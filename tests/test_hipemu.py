@@ -50,6 +50,10 @@ def test_gqa_group5_shapes_in_bounds(emu_lib):
     assert runner.run_scenarios(["attention_ragged_g5", "forward_gqa5"], timeout=900) == 0
 
 
+def test_noalloc_attention_at_its_limits_in_bounds(emu_lib):
+    assert runner.run_scenarios(["noalloc_limits"], timeout=1200) == 0
+
+
 def test_prefix_copy_and_cache_in_bounds(emu_lib):
     assert runner.run_scenarios(["prefix_copy"], timeout=900) == 0
 

@@ -219,7 +219,9 @@ def test_roundtrip_reproduces_synthetic_model(bits, gate):
     assert f.counts() == (2 + 2 * 11, 4, 2) and f.model_id() == "rt"
     h = f.host_model(small_cfg())  # the gate is read from the file
     assert h.cfg.rotate == 1 and h.cfg.group_size == 128 and not h.ptr.contents.lm_head
-    assert h.cfg.attn_gate == gate
+    assert h.cfg.attn_gate == gate and h.cfg.attn_gate_off == 0
+    # the caller's attn_output_gate = false survives the load (main.cpp:250)
+    assert f.host_model(small_cfg(attn_gate_off=1)).cfg.attn_gate_off == 1
     H, V = cfg.hidden, cfg.vocab
     for l in range(cfg.layers):
         A, B = m.layer(l), h.ptr.contents.layers[l]

@@ -239,6 +239,62 @@ def test_spec_verify_rows_keep_stream_and_accept():
     assert ver, "no verify rows were scheduled"
 
 
+def test_spec_adapt_reproduces_fixed_width_rounds():
+    """SpecAdapt (main.cpp:11454-11511) picks the width maximising
+    w * accept_ema / (w + 1) over 1..cap.  Without producer scores that
+    ratio grows with w for any accept rate in [0.05, 0.95], so every round
+    drafts up to the cap whatever the EMA has seen: a spec_adapt run issues
+    exactly the forwards of the fixed-width run with spec_k = cap, and with
+    spec_k = 0 the cap is 8 (main.cpp:11512-11514)."""
+    base = list(range(3, 23))
+    ps = [base * 3 + base[:4], base[5:] * 2, prompts_of(1, 9)[0]]
+    plain, _ = run(ps, 24, chunk_m=32, live_cap=8)
+    fixed3, lf = run(ps, 24, chunk_m=32, live_cap=8, spec_k=3)
+    adapt3, la = run(ps, 24, chunk_m=32, live_cap=8, spec_k=3, spec_adapt=1)
+    assert adapt3 == fixed3 == plain
+    assert la.forwards == lf.forwards
+    fixed8, l8 = run(ps, 24, chunk_m=32, live_cap=8, spec_k=8)
+    adapt8, la8 = run(ps, 24, chunk_m=32, live_cap=8, spec_k=0, spec_adapt=1)
+    assert adapt8 == plain
+    assert la8.forwards == l8.forwards
+    widths = []
+    for f in la8.forwards:
+        for sq in {r[0] for r in f if r[3] == ia.ROW_VERIFY}:
+            widths.append(sum(1 for r in f if r[0] == sq) - 1)
+    assert widths and max(widths) == 8
+
+
+class DecliningLM(MockLM):
+    """Declines (IFR_EDECLINE, nothing done) any forward that mixes decode
+    and prefill rows, as a backend whose joint batch is too large would."""
+
+    def _fwd(self, user, rows, M, best):
+        kinds = {rows[i].kind for i in range(M)}
+        if ia.ROW_PREFILL in kinds and len(kinds) > 1:
+            self.declined = getattr(self, "declined", 0) + 1
+            return ia.IFR_EDECLINE
+        return super()._fwd(user, rows, M, best)
+
+
+def test_declined_joint_forward_runs_the_split_path():
+    """serve_iteration (main.cpp:9247-9256): a joint forward that declines
+    has changed nothing, and the same iteration runs the split path (the
+    chunk, then the decode rows), so the streams are unchanged."""
+    ps = prompts_of(7, 2)
+    ref, _ = run(ps, 11, chunk_m=24, live_cap=8)
+    lm = DecliningLM()
+    sch = ia.Scheduler(backend=lm.table, chunk_m=24, live_cap=8)
+    ids = [sch.submit(p, 11) for p in ps]
+    for _ in range(5000):
+        if sch.step() == 0 and all(sch.result(i)[1] for i in ids):
+            break
+    out = [sch.result(i)[0] for i in ids]
+    sch.close()
+    assert out == ref
+    assert getattr(lm, "declined", 0) > 0
+    assert all(len({r[3] for r in f}) == 1 for f in lm.forwards)
+
+
 def expected_sampled(prompt, max_new, seed, T, k, p):
     """A sampling request's stream: the prompt's last row scores the argmax
     (main.cpp:8522-8523), then every decode token is the oracle's sample()
@@ -304,6 +360,7 @@ def test_sampling_needs_a_logits_forward():
         with pytest.raises(ia.IfrError) as e:
             sch.submit([1, 2, 3], 4, temperature=0.9)
         assert e.value.code == ia.IFR_EDECLINE
+        assert "forward_logits" in str(e.value)  # the library's own message, not a stale one
         sch.submit([1, 2, 3], 4)  # greedy is still accepted
     finally:
         sch.close()

@@ -71,3 +71,26 @@ def test_noalloc_attention_matches_ifr_attention(dev, kv_int8):
         del eng
     finally:
         model.close()
+
+
+def test_noalloc_refuses_more_units_than_its_scratch(dev):
+    """A batch within the row limit whose attention units exceed the 4096 the
+    scratch holds: 512 rows of one sequence at positions 1536..2047 are 64
+    q-blocks x 8 kv heads x 13..16 KV splits of 128 tokens (7424 units).
+    Refused with IFR_EINVAL and a message, before any kernel runs."""
+    cfg = ia.default_cfg(layers=1, vocab=1024)
+    model = ia.SynthModel(cfg, seed=5)
+    try:
+        eng = ia.Engine(dev, model, max_seqs=2, max_seq_tokens=2048, pool_tokens=2 * 2048, max_rows=512,
+                        attn_split=128)
+        rng = np.random.default_rng(9)
+        s = eng.seq_open()
+        eng.load_kv(s, rng.standard_normal((1, 2048, cfg.n_kv, cfg.head_dim), dtype=np.float32),
+                    rng.standard_normal((1, 2048, cfg.n_kv, cfg.head_dim), dtype=np.float32))
+        rows = [(s, 1536 + p, 0, 1, 1) for p in range(512)]
+        announce("no-alloc attention: refusal of 7424 units in 512 rows")
+        rc, _ = _noalloc(dev, eng, rows, np.zeros((512, cfg.n_heads, cfg.head_dim), np.float16))
+        assert rc == ia.IFR_EINVAL and b"attention units" in ia.lib().ifr_last_error()
+        del eng
+    finally:
+        model.close()
