@@ -289,6 +289,10 @@ struct Engine {
   ifr_model_cfg c;
   int mode = 0;     // 0 a8, 1 f32
   int kv_int8 = 0;
+  // attention evaluation order: 0 the reference host loop (main.cpp:
+  // 7657-7701); > 0 the split decomposition with this many KV tokens per
+  // split (attn_row_split), a second faithful fp32 order of the same sum
+  int attn_split = 0;
   std::vector<Unpacked> lin;           // 7 per layer (a8)
   std::vector<std::vector<float>> wf;  // 7 per layer (f32)
   std::vector<int8_t> lm_q;
@@ -326,6 +330,72 @@ void kv_int8_round(float* x, int hd) {
     int q = (int)(v >= 0 ? v + 0.5f : v - 0.5f);
     q = std::min(127, std::max(-127, q));
     x[d] = (float)q * s;
+  }
+}
+
+// Attention of one row in a second fp32 evaluation order, the decomposition
+// the device runs: the keys [0, pos] in splits of `split` tokens; inside a
+// split, pages of 32 tokens with a running (max, sum, O) in the base-2
+// domain -- scores x = (q . k) * log2(e)/sqrt(hd), alpha = 2^(m_old - m_new)
+// rescales sum and O when the max moves, p = 2^(x - m); then the splits are
+// merged in ascending order against the largest split max, O / L.  The same
+// real number as the reference loop (main.cpp:7657-7701), summed in another
+// order: the spread between the two orders is the floor of what any fp32
+// attention can promise.  k, v: token-major rows of nkv * hd.
+void attn_row_split(const float* q, const float* k, const float* v, int pos, int nq, int nkv, int hd,
+                    int split, float* out) {
+  const int G = nq / nkv, kvN = nkv * hd, nt = pos + 1, ns = (nt + split - 1) / split;
+  const float sl2 = 1.4426950408889634f / std::sqrt((float)hd);
+  std::vector<float> ms(ns), ls(ns), os((size_t)ns * hd), x(32);
+  for (int h = 0; h < nq; ++h) {
+    const int kvh = h / G;
+    const float* qh = q + (size_t)h * hd;
+    for (int s = 0; s < ns; ++s) {
+      const int lo = s * split, hi = std::min(nt, lo + split);
+      float m_run = -INFINITY, l_run = 0.0f;
+      float* o = &os[(size_t)s * hd];
+      for (int d = 0; d < hd; ++d) o[d] = 0.0f;
+      for (int p0 = lo; p0 < hi; p0 += 32) {
+        const int pe = std::min(hi, p0 + 32);
+        float mt = -INFINITY;
+        for (int t = p0; t < pe; ++t) {
+          const float* kt = k + (size_t)t * kvN + kvh * hd;
+          float dot = 0.0f;
+          for (int d = 0; d < hd; ++d) dot = std::fma(qh[d], kt[d], dot);
+          x[t - p0] = dot * sl2;
+          mt = std::max(mt, x[t - p0]);
+        }
+        const float m_new = std::max(m_run, mt);
+        const float alpha = std::exp2(m_run - m_new);
+        float rs = 0.0f;
+        for (int t = p0; t < pe; ++t) {
+          x[t - p0] = std::exp2(x[t - p0] - m_new);
+          rs += x[t - p0];
+        }
+        l_run = l_run * alpha + rs;
+        if (alpha != 1.0f)
+          for (int d = 0; d < hd; ++d) o[d] *= alpha;
+        for (int t = p0; t < pe; ++t) {
+          const float* vt = v + (size_t)t * kvN + kvh * hd;
+          for (int d = 0; d < hd; ++d) o[d] = std::fma(x[t - p0], vt[d], o[d]);
+        }
+        m_run = m_new;
+      }
+      ms[s] = m_run;
+      ls[s] = l_run;
+    }
+    float mx = -INFINITY;
+    for (int s = 0; s < ns; ++s) mx = std::max(mx, ms[s]);
+    float L = 0.0f;
+    float* oh = out + (size_t)h * hd;
+    for (int d = 0; d < hd; ++d) oh[d] = 0.0f;
+    for (int s = 0; s < ns; ++s) {
+      const float f = std::exp2(ms[s] - mx);
+      L += f * ls[s];
+      for (int d = 0; d < hd; ++d) oh[d] += f * os[(size_t)s * hd + d];
+    }
+    const float invL = 1.0f / L;
+    for (int d = 0; d < hd; ++d) oh[d] *= invL;
   }
 }
 
@@ -422,11 +492,20 @@ int forward(Engine& e, const ifr_row* rows, int M, int32_t* best, float* logits_
       std::memcpy(&s.k[l][(size_t)pos * kvN], kr, kvN * sizeof(float));
       std::memcpy(&s.v[l][(size_t)pos * kvN], vr, kvN * sizeof(float));
     }
-    // host attention, reference loop order (main.cpp:7657-7701)
+    // host attention, reference loop order (main.cpp:7657-7701), or the
+    // split order (attn_row_split)
 #pragma omp parallel for schedule(dynamic) if (e.mode == 0)
     for (int m = 0; m < M; ++m) {
       const int pos = rows[m].pos;
       const Seq& s = e.seqs[rows[m].seq];
+      if (e.attn_split > 0) {
+        attn_row_split(&qb[(size_t)m * qN], s.k[l].data(), s.v[l].data(), pos, nq, nkv, hd, e.attn_split,
+                       &attn[(size_t)m * qN]);
+        if (c.attn_gate && !c.attn_gate_off)
+          for (int i = 0; i < qN; ++i)
+            attn[(size_t)m * qN + i] *= 1.0f / (1.0f + std::exp(-gate[(size_t)m * qN + i]));
+        continue;
+      }
       std::vector<float> gs((size_t)Gq * (pos + 1));
       float* at = &attn[(size_t)m * qN];
       const float* qr = &qb[(size_t)m * qN];
@@ -464,7 +543,7 @@ int forward(Engine& e, const ifr_row* rows, int M, int32_t* best, float* logits_
         }
       }
       // output gate (main.cpp:7697-7698; sigmoidf of main.cpp:294)
-      if (c.attn_gate)
+      if (c.attn_gate && !c.attn_gate_off)
         for (int i = 0; i < qN; ++i) at[i] *= 1.0f / (1.0f + std::exp(-gate[(size_t)m * qN + i]));
     }
     // o-proj, rot_left, residual (main.cpp:7702-7727)
@@ -766,6 +845,20 @@ void or_attention_row(const float* q, const float* k, const float* v, int pos, i
 }
 
 void or_kv_int8_round(float* x, int hd) { kv_int8_round(x, hd); }
+// n consecutive vectors of hd (a whole cache at once)
+void or_kv_int8_round_rows(float* x, long n, int hd) {
+  for (long i = 0; i < n; ++i) kv_int8_round(x + i * hd, hd);
+}
+void or_attention_row_split(const float* q, const float* k, const float* v, int pos, int nq, int nkv, int hd,
+                            int split, float* out) {
+  attn_row_split(q, k, v, pos, nq, nkv, hd, split, out);
+}
+// the attention order of an engine's forward (0: reference loop; > 0: split)
+int or_engine_set_attn_split(void* p, int split) {
+  if (split < 0 || split % 32) return IFR_EINVAL;
+  static_cast<Engine*>(p)->attn_split = split;
+  return IFR_OK;
+}
 
 // ---- sampling: the reference's sample() (main.cpp:8674-8764, default path;
 // the INTFER_SAMPLE_TOPK_DIRECT variant :8695-8724 is opt-in) over the

@@ -52,6 +52,9 @@ def oracle() -> C.CDLL:
             "or_rope": (None, [P, C.c_int, C.c_int, f32]),
             "or_attention_row": (None, [P, P, P, C.c_int, C.c_int, C.c_int, C.c_int, P]),
             "or_kv_int8_round": (None, [P, C.c_int]),
+            "or_kv_int8_round_rows": (None, [P, C.c_long, C.c_int]),
+            "or_attention_row_split": (None, [P, P, P, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int, P]),
+            "or_engine_set_attn_split": (C.c_int, [P, C.c_int]),
             "or_engine_create": (P, [P, C.c_int, C.c_int, C.c_int]),
             "or_engine_destroy": (None, [P]),
             "or_seq_open": (C.c_int, [P]),
@@ -167,12 +170,16 @@ def qgemm_ts(a: np.ndarray, lin):
 class OracleEngine:
     """The oracle forward (mode 0 = device contract a8, 1 = reference f32 path)."""
 
-    def __init__(self, model, kv_int8=0, mode=0, max_seqs=8):
+    def __init__(self, model, kv_int8=0, mode=0, max_seqs=8, attn_split=0):
+        """attn_split > 0: attention in the split order (or_attention_row_split)
+        instead of the reference loop order."""
         self.cfg = model.cfg
         self.model = model
         self.h = oracle().or_engine_create(model.ptr, kv_int8, mode, max_seqs)
         if not self.h:
             raise RuntimeError("or_engine_create failed")
+        if attn_split:
+            assert oracle().or_engine_set_attn_split(self.h, attn_split) == 0
 
     def seq_open(self) -> int:
         return oracle().or_seq_open(self.h)

@@ -6,25 +6,37 @@ against the oracle except attention (fp32-accurate, not bit-identical), so:
   * a 1-layer model gives the same tokens and logits within 2e-3 sigma (most
     rows bit-identical; a rare int8 activation-code flip moves the rest);
   * the full 28-layer model drifts by such code flips, amplified layer by
-    layer: logits must stay within rms <= RMS_TOL * sigma, max <= MAX_TOL *
-    sigma and corr >= CORR_MIN of the oracle's (sigma = the oracle row's
-    logit std), bounds set just above the spread measured between the device
-    and the oracle on this workload;
+    layer.  The bounds come from the noise floor of the contract, measured on
+    the CPU alone (tests/floor/make_floor.py -> parity_floor_cfg1.json): the
+    oracle's own forward run with two faithful fp32 attention orders (the
+    reference's host loop and the device's 256-token split decomposition)
+    on this workload.  Whatever separates those two is what no fp32
+    attention can promise, so the device is held to K_FLOOR = 1.5 times the
+    floor (one more sample of the same process): per logit row rms and max
+    |d| / sigma and 1 - corr (sigma = the oracle row's std), the mean rms over
+    all compared rows, and the tie margin below;
   * greedy decode runs 64 steps free-running, each side feeding its own
     argmax (the reference's token KATs, scripts/gates/test_cpu_parity.sh:
     53-63).  A sequence's streams must stay identical until a step where the
-    two argmaxes differ, and every such divergence must be a documented tie:
-    the oracle's margin between its token and the device's token is below
-    TIE_TOL * sigma.  A divergence with a larger margin fails the test.  The
+    two argmaxes differ, and every such divergence must be a near-tie: the
+    oracle's margin between its token and the device's token below K_FLOOR
+    times the largest margin at which the two oracle orders diverge.  The
     same 64 steps then run teacher-forced (both sides fed the oracle's
     token), so every step compares the same distribution: each disagreement
-    there must be a tie by the same rule, and the agreement rate is reported.
+    there must be a tie by the same rule, and the agreement rate is reported;
+  * the random-init model's logits are nearly flat (median top-2 margin 0.15
+    sigma, so divergences within a few steps are expected of any fp32
+    order).  Its large-margin variant (workloads.successor_model: the same
+    layers, embedding N(0, 1) and an untied lm_head of permuted embedding
+    rows, top-2 margins 2.3 - 5.1 sigma against a floor of at most 0.9 sigma)
+    must give identical free-running 64-step streams on every sequence.
   Measured figures are printed, and written as JSON to $IFR_PARITY_OUT when
   that directory is set.
 """
 import ctypes as C
 import json
 import os
+from pathlib import Path
 
 import numpy as np
 import pytest
@@ -36,15 +48,26 @@ from tests.conftest import announce
 
 pytestmark = pytest.mark.gpu
 
-# measured on this workload (fp16 / int8 KV): logit rms 0.175 / 0.200 sigma
-# at worst, max |dlogit| 0.92 / 0.94 sigma, corr >= 0.985 / 0.980
-RMS_TOL = 0.22
-CORR_MIN = 0.975
-MAX_TOL = 1.0
-# a divergence of the greedy streams is a tie when the oracle's margin
-# between its token and the device's is below this many sigma (measured
-# margins at divergences: at most 0.50 sigma)
-TIE_TOL = 0.6
+# The noise floor of the cfg1 contract (two faithful fp32 attention orders of
+# the oracle against each other, CPU only; tests/floor/make_floor.py) and the
+# factor the device may exceed it by.
+FLOOR = json.loads((Path(__file__).resolve().parent / "floor" / "parity_floor_cfg1.json").read_text())
+K_FLOOR = 1.5
+
+
+def floor_bounds(kv_int8):
+    f = FLOOR[f"kv{kv_int8}"]
+    return {"rms": K_FLOOR * f["rms_sigma_max"], "max": K_FLOOR * f["max_sigma_max"],
+            "corr": 1.0 - K_FLOOR * (1.0 - f["corr_min"]), "rms_mean": K_FLOOR * f["rms_sigma_mean"],
+            "tie": K_FLOOR * f["divergence_margin_max"]}
+
+
+# per-row bounds of every model-level comparison in this file and the tests
+# that share _check_logits: the looser of the two KV formats' floors
+_B = [floor_bounds(0), floor_bounds(1)]
+RMS_TOL = max(b["rms"] for b in _B)
+MAX_TOL = max(b["max"] for b in _B)
+CORR_MIN = min(b["corr"] for b in _B)
 
 
 @pytest.fixture(scope="module")
@@ -82,7 +105,8 @@ def _setup(dev, model, kv_int8, intfer=None):
     return w, eng, ora, dec_e, dec_o, pe, pq
 
 
-def _check_logits(lg, lo, what, stats=None):
+def _check_logits(lg, lo, what, stats=None, bounds=None):
+    rt, mt, cm = (RMS_TOL, MAX_TOL, CORR_MIN) if bounds is None else (bounds["rms"], bounds["max"], bounds["corr"])
     for r in range(lg.shape[0]):
         sd = float(lo[r].std())
         d = lg[r].astype(np.float64) - lo[r]
@@ -91,9 +115,9 @@ def _check_logits(lg, lo, what, stats=None):
         dmax = float(np.abs(d).max())
         if stats is not None:
             stats.append(rms / sd)
-        assert rms <= RMS_TOL * sd and corr >= CORR_MIN and dmax <= MAX_TOL * sd, (
-            f"{what} row {r}: rms {rms:.4g} (tol {RMS_TOL * sd:.4g}), corr {corr:.6f}, "
-            f"max {dmax:.4g}")
+        assert rms <= rt * sd and corr >= cm and dmax <= mt * sd, (
+            f"{what} row {r}: rms {rms:.4g} (tol {rt * sd:.4g}), corr {corr:.6f} (min {cm:.6f}), "
+            f"max {dmax:.4g} (tol {mt * sd:.4g})")
 
 
 def test_one_layer_bit_exact(dev):
@@ -191,6 +215,7 @@ def _tie(lg, lo, t_e, t_o):
 
 @pytest.mark.parametrize("kv_int8", [0, 1])
 def test_cfg1_mixed_iteration_and_greedy64(dev, model, kv_int8):
+    fb = floor_bounds(kv_int8)
     w, eng, ora, dec_e, dec_o, pe, pq = _setup(dev, model, kv_int8)
     rows_e = wl.cfg1_rows(w, dec_e, pe)
     rows_o = wl.cfg1_rows(w, dec_o, pq)
@@ -200,8 +225,8 @@ def test_cfg1_mixed_iteration_and_greedy64(dev, model, kv_int8):
     want = [i for i, r in enumerate(rows_e) if r[4]]
     assert len(want) == 5
     stats = []
-    _check_logits(lg, lo, "cfg1", stats)
-    rec = {"kv_int8": kv_int8, "cfg1_tokens_equal": int(sum(be[i] == bo[i] for i in want)),
+    _check_logits(lg, lo, "cfg1", stats, fb)
+    rec = {"kv_int8": kv_int8, "bounds": fb, "cfg1_tokens_equal": int(sum(be[i] == bo[i] for i in want)),
            "cfg1_row_err": [_row_err(lg[j], lo[j]) for j in range(5)], "ties": []}
     for j, i in enumerate(want):
         if be[i] != bo[i]:
@@ -224,7 +249,7 @@ def test_cfg1_mixed_iteration_and_greedy64(dev, model, kv_int8):
             if not synced[j]:
                 continue
             errs.append(_row_err(l_e[j], l_o[j]))
-            _check_logits(l_e[j:j + 1], l_o[j:j + 1], f"free step {step} seq {j}", stats)
+            _check_logits(l_e[j:j + 1], l_o[j:j + 1], f"free step {step} seq {j}", stats, fb)
             if b_e[j] != b_o[j]:
                 rec["ties"].append({"phase": "free", "step": step, "seq": j,
                                     **_tie(l_e[j], l_o[j], b_e[j], b_o[j])})
@@ -243,7 +268,7 @@ def test_cfg1_mixed_iteration_and_greedy64(dev, model, kv_int8):
         announce(f"cfg1 teacher-forced step {step} kv_int8={kv_int8}")
         b_e, l_e = eng.forward([(s, p, t, 0, 1) for s, p, t in zip(seq_e, pos, tok)], logits=True)
         b_o, l_o = ora.forward([(s, p, t, 0, 1) for s, p, t in zip(seq_o, pos, tok)], logits=True)
-        _check_logits(l_e, l_o, f"teacher-forced step {step}", stats)
+        _check_logits(l_e, l_o, f"teacher-forced step {step}", stats, fb)
         for j in range(5):
             errs.append(_row_err(l_e[j], l_o[j]))
             if b_e[j] == b_o[j]:
@@ -270,11 +295,53 @@ def test_cfg1_mixed_iteration_and_greedy64(dev, model, kv_int8):
         os.makedirs(out, exist_ok=True)
         with open(os.path.join(out, f"parity_cfg1_kv{kv_int8}.json"), "w") as f:
             json.dump(rec, f, indent=1)
-    # every divergence, free-running or forced, is a documented near-tie
+    # every divergence, free-running or forced, is a near-tie by the floor
     for t in rec["ties"]:
-        assert 0 <= t["oracle_margin"] < TIE_TOL, t
+        assert 0 <= t["oracle_margin"] < fb["tie"], t
+    # and on average the device sits at the floor, not just under its worst row
+    assert rec["rms_sigma_mean"] <= fb["rms_mean"], (rec["rms_sigma_mean"], fb["rms_mean"])
     # a non-degenerate stream: the model does not just repeat a few tokens
     assert len(set(np.array(stream).reshape(-1).tolist())) > 20
+
+
+@pytest.mark.parametrize("kv_int8", [0, 1])
+def test_cfg1_large_margin_variant_streams_identical(dev, kv_int8):
+    """The cfg1 workload on the large-margin variant of the same 28-layer
+    model (workloads.successor_model, embedding N(0, 1)): the cfg1 iteration's
+    five scored rows and 64 free-running greedy steps per sequence give the
+    same tokens on the device and the oracle, every step, with the logits
+    inside the floor bounds.  The smallest top-2 margin seen is reported."""
+    fb = floor_bounds(kv_int8)
+    m = ia.SynthModel(ia.default_cfg(), seed=11, bits=2)
+    try:
+        wl.successor_model(m, 1.0)
+        w, eng, ora, dec_e, dec_o, pe, pq = _setup(dev, m, kv_int8)
+        announce(f"large-margin cfg1 kv_int8={kv_int8}: iteration")
+        be, lg = eng.forward(wl.cfg1_rows(w, dec_e, pe), logits=True)
+        bo, lo = ora.forward(wl.cfg1_rows(w, dec_o, pq), logits=True)
+        want = [i for i, r in enumerate(wl.cfg1_rows(w, dec_e, pe)) if r[4]]
+        _check_logits(lg, lo, "large-margin cfg1", None, fb)
+        assert [int(be[i]) for i in want] == [int(bo[i]) for i in want]
+        seq_e, seq_o = dec_e + [pe], dec_o + [pq]
+        pos = [n + 1 for n in w.contexts] + [len(w.pre_tokens)]
+        tok = [int(be[i]) for i in want]
+        margins, streams = [], [list(tok)]
+        for step in range(64):
+            announce(f"large-margin cfg1 kv_int8={kv_int8}: free-running step {step}")
+            b_e, l_e = eng.forward([(s, p, t, 0, 1) for s, p, t in zip(seq_e, pos, tok)], logits=True)
+            b_o, l_o = ora.forward([(s, p, t, 0, 1) for s, p, t in zip(seq_o, pos, tok)], logits=True)
+            _check_logits(l_e, l_o, f"large-margin step {step}", None, fb)
+            assert list(b_e) == list(b_o), f"step {step}: device {list(b_e)} oracle {list(b_o)}"
+            srt = np.sort(l_o, axis=1)
+            margins += ((srt[:, -1] - srt[:, -2]) / l_o.std(axis=1)).tolist()
+            tok = [int(x) for x in b_e]
+            streams.append(tok)
+            pos = [p + 1 for p in pos]
+        print(f"[large-margin cfg1 kv_int8={kv_int8}] 64 free-running steps identical on all 5 sequences; "
+              f"top-2 margin min {min(margins):.3f} sigma, median {float(np.median(margins)):.3f}")
+        assert len(set(np.array(streams).reshape(-1).tolist())) > 20  # not a repeated token
+    finally:
+        m.close()
 
 
 def _lanes(eng):

@@ -24,6 +24,8 @@ Each oracle function is checked against something other than itself:
   or_lmhead_quant        numpy float32 closed form of main.cpp:1745-1761
   or_lmhead / or_argmax  float64 logits; first-max-wins on planted ties
   or_attention_row       float64 softmax attention
+  or_attention_row_split float64 softmax attention (page / split boundaries,
+                         a moving running max); within last ulps of the loop
   or_rope                float64 cos/sin of the float32 angle
   forward (a8 / f32)     chunk invariance (M=1 == M=8 rows), f32 ~ a8 agreement
   forward (f32), whole   a float64 numpy restatement of the layer (norms,
@@ -308,6 +310,39 @@ def test_attention_row_matches_float64(O):
     assert np.allclose(out.reshape(nq, hd), ref, atol=2e-5)
 
 
+@pytest.mark.parametrize("nq,nkv,pos,split", [(16, 8, 77, 256), (16, 8, 700, 256), (40, 8, 1000, 256),
+                                              (16, 8, 1000, 32), (16, 8, 31, 32), (8, 8, 256, 256)])
+def test_attention_row_split_order_matches_float64(O, nq, nkv, pos, split):
+    """The split-order attention (the device's decomposition: 32-token pages
+    with a running base-2 max inside each KV split, splits merged in order)
+    is the same softmax attention as float64 -- across page and split
+    boundaries, at a split and a page exactly full -- and differs from the
+    reference loop order only in the last ulps.  Keys drawn with a growing
+    trend make later pages move the running max, so a dropped rescale of the
+    sum or of O, or a split weight taken from the wrong max, fails here."""
+    rng = np.random.default_rng(pos + split)
+    hd, G = 128, nq // nkv
+    q = rng.normal(0, 1, size=nq * hd).astype(np.float32)
+    k = (rng.normal(0, 1, size=(pos + 1, nkv * hd)) +
+         np.linspace(0, 0.3, pos + 1)[:, None] * q.reshape(nq, hd)[::G].reshape(-1)[None, :]).astype(np.float32)
+    v = rng.normal(0, 1, size=(pos + 1, nkv * hd)).astype(np.float32)
+    out = np.empty(nq * hd, np.float32)
+    loop = np.empty(nq * hd, np.float32)
+    O.or_attention_row_split(ptr(q), ptr(k), ptr(v), pos, nq, nkv, hd, split, ptr(out))
+    O.or_attention_row(ptr(q), ptr(k), ptr(v), pos, nq, nkv, hd, ptr(loop))
+    qd = q.astype(np.float64).reshape(nq, hd)
+    kd = k.astype(np.float64).reshape(pos + 1, nkv, hd)
+    vd = v.astype(np.float64).reshape(pos + 1, nkv, hd)
+    ref = np.empty((nq, hd))
+    for h in range(nq):
+        s = kd[:, h // G] @ qd[h] / np.sqrt(hd)
+        p = np.exp(s - s.max())
+        p /= p.sum()
+        ref[h] = p @ vd[:, h // G]
+    assert np.allclose(out.reshape(nq, hd), ref, atol=2e-5)
+    assert np.abs(out - loop).max() < 4e-6
+
+
 def test_rope_matches_float64_of_f32_angle(O):
     rng = np.random.default_rng(12)
     hd, theta = 128, 1e6
@@ -537,6 +572,25 @@ def test_zero_gate_is_half_the_attention_output(mode):
     s = e.seq_open()
     _, lg = e.forward([(s, p, t, 1, 1) for p, t in enumerate(toks)], logits=True)
     assert not np.array_equal(lg, out[1])
+
+
+@pytest.mark.parametrize("mode", [0, 1])
+def test_gate_off_reads_the_packed_q_and_skips_the_sigmoid(mode):
+    """attn_output_gate = false with a packed q_proj (main.cpp:250, :7697):
+    the q rows are taken from the [q, gate] layout and the gate is dropped.
+    The synthetic gated model's q rows are the ungated model's of the same
+    seed (the gate rows come from their own stream), so the forward equals
+    the ungated model's bit for bit; with the gate applied it does not."""
+    toks = np.random.default_rng(26).integers(0, 512, size=9).tolist()
+    out = []
+    for kw in ({"attn_gate": 1, "attn_gate_off": 1}, {}, {"attn_gate": 1}):
+        e = po.OracleEngine(ia.SynthModel(tiny_cfg(**kw), seed=26), mode=mode)
+        s = e.seq_open()
+        _, lg = e.forward([(s, p, t, 1, 1) for p, t in enumerate(toks)], logits=True)
+        out.append(lg)
+        e.close()
+    assert np.array_equal(out[0].view(np.uint32), out[1].view(np.uint32))
+    assert not np.array_equal(out[2], out[1])
 
 
 # ---- FP16-activation dequant GEMM (the reference's default GPU linear) ----------------------------
