@@ -15,6 +15,9 @@ Extra objects on the JSON line:
   serve_roofline achieved decode tok/s vs the per-iteration roofline
                 t_roof(i) = max(HBM bytes / 8 TB/s, GEMM int8 ops / 5 POP/s +
                 attention flops / 2.5 PFLOP/s)
+  peaks         measured device peaks (a 2 GiB read stream, int8 and fp16
+                MFMA loops); every roofline object also carries frac_measured,
+                its achieved rate over the measured peak of the same unit
   cpu_baseline  the reference CPU path (oracle f32 mode: CpuBackend FP32
                 dequant GEMM, host attention, serial tied lm_head), timed on a
                 bounded sample of the same workload
@@ -74,6 +77,8 @@ def parse():
                     help="comma-separated KV tokens per attention unit for --attn-sweep (0: default)")
     ap.add_argument("--copy-calib", action="store_true",
                     help="run only 8 device copies of 1 GiB (HBM traffic counter calibration)")
+    ap.add_argument("--peaks", action="store_true",
+                    help="measure only the device peaks (1 GiB read stream, int8 and fp16 MFMA loops)")
     ap.add_argument("--cfg5", action="store_true",
                     help="run only the cfg5 27B-class mixed iteration (M ~ 2160) and print its JSON line")
     ap.add_argument("--cpu-full", action="store_true",
@@ -132,8 +137,10 @@ def pct(xs, p):
     return s[f] + (s[c] - s[f]) * (k - f)
 
 
-def serve_roofline(cfg, weight_bytes, lm_bytes, iters_rows, kv_elem):
-    """Sum of per-iteration roofline times and decode tokens (decode rows)."""
+def serve_roofline(cfg, weight_bytes, lm_bytes, iters_rows, kv_elem, bw=None, i8=None, f16=None):
+    """Sum of per-iteration roofline times and decode tokens (decode rows);
+    the nominal peaks unless measured ones are given."""
+    bw, i8, f16 = bw or HBM_PEAK, i8 or INT8_PEAK, f16 or FP16_PEAK
     H, L, nq, nkv, hd = cfg.hidden, cfg.layers, cfg.n_heads, cfg.n_kv, cfg.head_dim
     F, V = cfg.inter, cfg.vocab
     macs_tok = L * (H * (nq * hd + 2 * nkv * hd) + nq * hd * H + H * 2 * F + F * H)
@@ -153,7 +160,7 @@ def serve_roofline(cfg, weight_bytes, lm_bytes, iters_rows, kv_elem):
         B = weight_bytes + (lm_bytes if want else 0) + sum(seq_len.values()) * kv_tok
         ops = 2.0 * M * macs_tok + 2.0 * want * V * H
         fl = sum(4.0 * nq * hd * (r[1] + 1) * L for r in rows)
-        t_roof += max(B / HBM_PEAK, ops / INT8_PEAK + fl / FP16_PEAK)
+        t_roof += max(B / bw, ops / i8 + fl / f16)
     return t_roof, dec
 
 
@@ -650,6 +657,39 @@ def bind_host_cpus():
             "omp_threads": threads, "cores": min(threads, len(allowed))}
 
 
+def measure_peaks(ia, dev):
+    """Measured denominators next to the nominal ones: a streaming read of a
+    2 GiB buffer (8x the 256 MB Infinity Cache; each 16-byte word read once
+    per launch, 10 launches), and back-to-back independent int8 / fp16 MFMAs
+    in two waves per SIMD (ifr_peak_read / ifr_peak_mfma, HIP events)."""
+    import ctypes as C
+    L = ia.lib()
+    n = 2 << 30
+    buf = dev.zeros(n)
+    gbps, i8, f16 = C.c_double(), C.c_double(), C.c_double()
+    ia.check(L.ifr_peak_read(dev.ctx, buf.p, C.c_size_t(n), 10, C.byref(gbps)), "ifr_peak_read")
+    buf.free()
+    ia.check(L.ifr_peak_mfma(dev.ctx, 0, 4000, 5, C.byref(i8)), "ifr_peak_mfma int8")
+    ia.check(L.ifr_peak_mfma(dev.ctx, 1, 4000, 5, C.byref(f16)), "ifr_peak_mfma fp16")
+    return {"hbm_read_GBps": round(gbps.value, 1), "int8_TOPS": round(i8.value, 1),
+            "fp16_TFLOPs": round(f16.value, 1),
+            "nominal": {"hbm_GBps": HBM_PEAK / 1e9, "int8_TOPS": INT8_PEAK / 1e12, "fp16_TFLOPs": FP16_PEAK / 1e12},
+            "method": "read: 2 GiB buffer, nontemporal 16-byte loads, 10 launches; MFMA: 8 independent "
+                      "accumulators per wave, 2 waves per SIMD, 4000 rounds, 5 launches (HIP events)"}
+
+
+def with_measured(r, peaks):
+    """Add frac_measured (achieved / the measured peak of the same unit) to a roofline dict."""
+    if not peaks or not r or r.get("achieved") is None:
+        return r
+    if r.get("unit") == "GB/s":
+        r["frac_measured"] = round(r["achieved"] / peaks["hbm_read_GBps"], 4)
+    elif r.get("unit") == "TFLOP/s":
+        meas = peaks["int8_TOPS"] if r.get("peak") == INT8_PEAK / 1e12 else peaks["fp16_TFLOPs"]
+        r["frac_measured"] = round(r["achieved"] / meas, 4)
+    return r
+
+
 def cpu_baseline(ia, model, cfg):
     """Reference CPU path on a bounded sample with the load's per-output-token
     mix: 4 decode rows at the load's mean context (1088) + one 66-row prefill
@@ -917,6 +957,11 @@ def main():
                           "bytes_written_per_copy": n, "GBps": round(2 * 8 * n / ms / 1e6, 1)}))
         dev.close()
         return 0
+    if a.peaks:
+        dev = ia.Device(0)
+        print(json.dumps({"metric": "device peaks (measured)", **measure_peaks(ia, dev)}))
+        dev.close()
+        return 0
     if a.cfg5:
         return cfg5_bench(ia, a)
     if a.cpu_full:
@@ -1042,6 +1087,17 @@ def main():
                                  "frac": round(value / roof_tok_s, 4),
                                  "decode_rows": dec, "iterations": len(rec)}
         log(f"timing pass: {dt:.3f} s; dominant {dom} {stats[dom][0]:.1f} ms; roofline tok/s {roof_tok_s:.0f}")
+        # the same fractions against the peaks measured on this device
+        peaks = measure_peaks(ia, dev)
+        out["peaks"] = peaks
+        with_measured(out["roofline"], peaks)
+        with_measured(out["quant_gemm"], peaks)
+        for v in out["kernels"].values():
+            with_measured(v, peaks)
+        t_meas, _ = serve_roofline(cfg, wbytes, lm_bytes, rec, kv_elem,
+                                   bw=peaks["hbm_read_GBps"] * 1e9, i8=peaks["int8_TOPS"] * 1e12,
+                                   f16=peaks["fp16_TFLOPs"] * 1e12)
+        out["serve_roofline"]["frac_measured"] = round(value / (C * max_new / t_meas), 4)
     if not a.no_packed:
         # the same load with the chunk budget filled from several queued
         # prompts (pack_prefill; the reference fills it from the head only):

@@ -144,6 +144,17 @@ void* ifr_ctx_stream(ifr_ctx* ctx);
 int ifr_timer_begin(ifr_ctx* ctx);
 int ifr_timer_end(ifr_ctx* ctx, double* ms);
 
+/* No reference counterpart: measured peaks of the device, the denominators
+ * reported next to the nominal ones.  ifr_peak_read streams `bytes` (at
+ * least 1 GiB, above the 256 MB Infinity Cache; a multiple of 16) from buf_d
+ * once per launch, `reps` launches timed with HIP events on the context
+ * stream, and returns the read bandwidth in GB/s.  ifr_peak_mfma runs
+ * back-to-back independent MFMAs in two waves per SIMD, `iters` rounds of 8
+ * per wave: dtype 0 v_mfma_i32_16x16x64_i8 (int8 ops), 1
+ * v_mfma_f32_16x16x32_f16 (fp16 flops); returns TOP/s (TFLOP/s). */
+int ifr_peak_read(ifr_ctx* ctx, const void* buf_d, size_t bytes, int32_t reps, double* gbps);
+int ifr_peak_mfma(ifr_ctx* ctx, int32_t dtype, int32_t iters, int32_t reps, double* tops);
+
 /* Device buffers for tests and benches (no torch in the boundary). */
 int ifr_malloc(ifr_ctx* ctx, size_t bytes, void** dptr);
 int ifr_free(ifr_ctx* ctx, void* dptr);
@@ -314,6 +325,55 @@ int ifr_seq_copy_prefix(ifr_ctx* ctx, int32_t dst, int32_t src, int32_t len);
  * the forward stores them (fp16 round, or int8 with an fp16 scale per
  * (token, kv_head)).  Used for the configs' seeded cached contexts. */
 int ifr_seq_load_kv(ifr_ctx* ctx, int32_t slot, int32_t len, const float* k, const float* v);
+
+/* ------------------------------------------------------------------------
+ * Per-linear seam over the loaded model: the reference's LinearBackend
+ * (main.cpp:455-566), for a caller that keeps its own forward (step_batch)
+ * and hands the device one linear at a time.  Host fp32 rows in, host fp32
+ * rows out, as the reference's GPU backend returns them (half_to_float of
+ * the device's fp16 outputs, dashq.cpp:111).  The linear runs the forward's
+ * integer contract: per-token int8 quantization of each input row
+ * (half-away, s = max|x| / 127, dashq.cpp:221-336), int32 T, the fp32 group
+ * fold, fp16 output (ifr_quant_gemm).  Inputs are taken as the caller
+ * passes them: the SpinQuant rotation of a site is the caller's (rot_for,
+ * main.cpp:436-445; ifr_linear_rot says which applies).  Rows are
+ * independent, so any M gives each row the bits it has alone.
+ * ---------------------------------------------------------------------- */
+enum {
+  IFR_LIN_Q = 0, IFR_LIN_K = 1, IFR_LIN_V = 2, IFR_LIN_O = 3,
+  IFR_LIN_GATE = 4, IFR_LIN_UP = 5, IFR_LIN_DOWN = 6
+};
+/* The reference's tensor names ("model.language_model.layers.<l>.
+ * self_attn.q_proj.weight", ...; main.cpp:4225-4270) to (layer, IFR_LIN_*).
+ * IFR_EINVAL for a name that is not one of the loaded model's linears. */
+int ifr_linear_lookup(ifr_ctx* ctx, const char* tensor_name, int32_t* layer, int32_t* which);
+/* Shape (N rows, K columns) of a linear; Q of a gated model is the packed
+ * [q, gate] projection of 2 * n_heads * head_dim rows, as the file holds it. */
+int ifr_linear_shape(ifr_ctx* ctx, int32_t layer, int32_t which, int32_t* N, int32_t* K);
+/* LinearBackend::rot_for (main.cpp:436-445): 0 no rotation, 1 the right
+ * site (FWHT of the input: q, k, v, gate, up), 2 the left site (FWHT of the
+ * output: o, down); the rotation is the canonical Sylvester Hadamard the
+ * loader accepts (spinquant.cpp:586-604). */
+int ifr_linear_rot(ifr_ctx* ctx, int32_t which, int32_t* site);
+/* LinearBackend::run_linear_batch (main.cpp:474-488): Y[M][N] = W X for host
+ * X[M][K]. */
+int ifr_linear_batch(ifr_ctx* ctx, int32_t layer, int32_t which, const float* X, float* Y, int32_t M);
+/* LinearBackend::run_linear_wave_batch (main.cpp:514-527): independent
+ * linears over M rows each (no item's Y may alias another's X or Y), one
+ * device round trip for all of them; each Y equals its ifr_linear_batch. */
+typedef struct ifr_linear_item {
+  int32_t layer, which;
+  const float* X;  /* [M][K] */
+  float* Y;        /* [M][N] */
+} ifr_linear_item;
+int ifr_linear_wave_batch(ifr_ctx* ctx, const ifr_linear_item* items, int32_t n, int32_t M);
+/* LinearBackend::run_mlp_fused (main.cpp:528-540): md[M][hidden] =
+ * W_down (silu(W_gate rin) * (W_up rin)) on the device, for host rin[M][hidden]
+ * (the normed, right-rotated MLP input); the left rotation of md stays the
+ * caller's.  silu(g) * u is formed from the fp16 gate and up outputs and
+ * rounded to fp16 (silumul_to_half, quant_gemm.cpp:4209), then quantized
+ * per token for the down projection, as the forward does. */
+int ifr_mlp_fused(ifr_ctx* ctx, int32_t layer, const float* rin, float* md, int32_t M);
 
 enum { IFR_ROW_DECODE = 0, IFR_ROW_PREFILL = 1, IFR_ROW_VERIFY = 2 };
 

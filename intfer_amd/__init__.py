@@ -15,7 +15,7 @@ import numpy as np
 
 from . import _abi
 from ._abi import (KVCfg, Linear, ModelCfg, Row, SchedBackend, SchedCfg, ROW_DECODE, ROW_PREFILL,
-                   ROW_VERIFY, IFR_OK, IFR_EDECLINE, IFR_EINVAL, IFR_ENOMEM, IFR_EDEVICE, IFR_ESTATE,
+                   ROW_VERIFY, LIN_Q, LIN_K, LIN_V, LIN_O, LIN_GATE, LIN_UP, LIN_DOWN, IFR_OK, IFR_EDECLINE, IFR_EINVAL, IFR_ENOMEM, IFR_EDEVICE, IFR_ESTATE,
                    IfrError, check, lib)
 
 __all__ = ["Device", "Engine", "Scheduler", "Rng", "sample", "SynthModel", "HostModelHandle", "IntferFile", "default_cfg", "make_linear", "rows_array",
@@ -380,6 +380,53 @@ class Engine:
         check(lib().ifr_attention(self.dev.ctx, layer, arr, M, q.ctypes.data_as(C.c_void_p),
                                   out.ctypes.data_as(_abi.pf32)), "ifr_attention")
         return out
+
+    # ---- the per-linear seam (LinearBackend, main.cpp:455-566) ----
+    def linear_lookup(self, name: str):
+        """(layer, IFR_LIN_*) of a reference tensor name."""
+        l, w = C.c_int32(), C.c_int32()
+        check(lib().ifr_linear_lookup(self.dev.ctx, name.encode(), C.byref(l), C.byref(w)), "ifr_linear_lookup")
+        return l.value, w.value
+
+    def linear_shape(self, layer: int, which: int):
+        n, k = C.c_int32(), C.c_int32()
+        check(lib().ifr_linear_shape(self.dev.ctx, layer, which, C.byref(n), C.byref(k)), "ifr_linear_shape")
+        return n.value, k.value
+
+    def linear_rot(self, which: int) -> int:
+        s = C.c_int32()
+        check(lib().ifr_linear_rot(self.dev.ctx, which, C.byref(s)), "ifr_linear_rot")
+        return s.value
+
+    def linear_batch(self, layer: int, which: int, X: np.ndarray) -> np.ndarray:
+        """run_linear_batch: fp32 [M][N] = W X over host fp32 rows [M][K]."""
+        X = np.ascontiguousarray(X, dtype=np.float32)
+        N, K = self.linear_shape(layer, which)
+        assert X.ndim == 2 and X.shape[1] == K
+        Y = np.empty((X.shape[0], N), np.float32)
+        check(lib().ifr_linear_batch(self.dev.ctx, layer, which, X.ctypes.data_as(_abi.pf32),
+                                     Y.ctypes.data_as(_abi.pf32), X.shape[0]), "ifr_linear_batch")
+        return Y
+
+    def linear_wave_batch(self, items, M: int):
+        """run_linear_wave_batch over [(layer, which, X)]; returns the Ys."""
+        keep, arr = [], (_abi.LinearItem * max(1, len(items)))()
+        for i, (l, w, X) in enumerate(items):
+            X = np.ascontiguousarray(X, dtype=np.float32)
+            N, _ = self.linear_shape(l, w)
+            Y = np.empty((M, N), np.float32)
+            keep.append((X, Y))
+            arr[i] = _abi.LinearItem(l, w, X.ctypes.data_as(_abi.pf32), Y.ctypes.data_as(_abi.pf32))
+        check(lib().ifr_linear_wave_batch(self.dev.ctx, arr, len(items), M), "ifr_linear_wave_batch")
+        return [y for _, y in keep]
+
+    def mlp_fused(self, layer: int, rin: np.ndarray) -> np.ndarray:
+        """run_mlp_fused: md [M][hidden] = W_down(silu(W_gate rin) * (W_up rin))."""
+        rin = np.ascontiguousarray(rin, dtype=np.float32)
+        md = np.empty((rin.shape[0], self.cfg.hidden), np.float32)
+        check(lib().ifr_mlp_fused(self.dev.ctx, layer, rin.ctypes.data_as(_abi.pf32), md.ctypes.data_as(_abi.pf32),
+                                  rin.shape[0]), "ifr_mlp_fused")
+        return md
 
     def set_timing(self, on: bool):
         check(lib().ifr_set_timing(self.dev.ctx, 1 if on else 0), "ifr_set_timing")

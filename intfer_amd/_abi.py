@@ -16,6 +16,7 @@ HEADER = HERE.parent / "include" / "intfer_amd.h"
 
 IFR_OK, IFR_EDECLINE, IFR_EINVAL, IFR_ENOMEM, IFR_EDEVICE, IFR_ESTATE = 0, -1, -2, -3, -4, -5
 ROW_DECODE, ROW_PREFILL, ROW_VERIFY = 0, 1, 2
+LIN_Q, LIN_K, LIN_V, LIN_O, LIN_GATE, LIN_UP, LIN_DOWN = range(7)
 
 
 class ModelCfg(C.Structure):
@@ -73,6 +74,11 @@ class KVCfg(C.Structure):
 class Row(C.Structure):
     _fields_ = [("seq", C.c_int32), ("pos", C.c_int32), ("token", C.c_int32),
                 ("kind", C.c_int32), ("want", C.c_int32)]
+
+
+class LinearItem(C.Structure):
+    _fields_ = [("layer", C.c_int32), ("which", C.c_int32), ("X", C.POINTER(C.c_float)),
+                ("Y", C.POINTER(C.c_float))]
 
 
 class SchedCfg(C.Structure):
@@ -174,6 +180,14 @@ _PROTOS = {
     "ifr_forward": (C.c_int, [P, C.POINTER(Row), i32, pi32, pf32]),
     "ifr_attention": (C.c_int, [P, i32, C.POINTER(Row), i32, P, pf32]),
     "ifr_attention_noalloc": (C.c_int, [P, i32, C.POINTER(Row), i32, P, P]),
+    "ifr_peak_read": (C.c_int, [P, P, sz, i32, C.POINTER(C.c_double)]),
+    "ifr_peak_mfma": (C.c_int, [P, i32, i32, i32, C.POINTER(C.c_double)]),
+    "ifr_linear_lookup": (C.c_int, [P, C.c_char_p, C.POINTER(i32), C.POINTER(i32)]),
+    "ifr_linear_shape": (C.c_int, [P, i32, i32, C.POINTER(i32), C.POINTER(i32)]),
+    "ifr_linear_rot": (C.c_int, [P, i32, C.POINTER(i32)]),
+    "ifr_linear_batch": (C.c_int, [P, i32, i32, pf32, pf32, i32]),
+    "ifr_linear_wave_batch": (C.c_int, [P, C.POINTER(LinearItem), i32, i32]),
+    "ifr_mlp_fused": (C.c_int, [P, i32, pf32, pf32, i32]),
     "ifr_set_timing": (C.c_int, [P, i32]),
     "ifr_get_timing": (C.c_int, [P, C.c_char_p, C.POINTER(C.c_double), C.POINTER(i64),
                                  C.POINTER(C.c_double), C.POINTER(C.c_double)]),

@@ -30,7 +30,7 @@ SOURCES = [("qgemm.hip", [], "qgemm"),
            ("engine.cpp", [], "engine"), ("sched.cpp", [], "sched"), ("synth.cpp", [], "synth"),
            ("intfer_file.cpp", [], "intfer_file"), ("serve.cpp", [], "serve"),
            ("sample.cpp", [], "sample"), ("qgemm_f16.hip", [], "qgemm_f16"),
-           ("qgemm_ga.hip", [], "qgemm_ga")]
+           ("qgemm_ga.hip", [], "qgemm_ga"), ("peak.hip", [], "peak")]
 SERVE_BIN = HERE / "intfer_serve"  # the --serve command line (serve_main.cpp)
 
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
@@ -44,8 +44,11 @@ COMMON = [
 
 # MFMA results of the GEMMs feed VALU work at once (the per-group fold), and
 # attention rescales its O accumulators between MFMAs, so both keep MFMA
-# results in VGPRs instead of round-tripping through AGPRs.
-EXTRA = {"qgemm.hip": ["-mllvm", "--amdgpu-mfma-vgpr-form"], "attn.hip": ["-mllvm", "--amdgpu-mfma-vgpr-form"]}
+# results in VGPRs instead of round-tripping through AGPRs; the peak
+# microbenchmark too (its accumulators otherwise shuffle between AGPRs and
+# VGPRs every round, which serializes the MFMA pipe).
+EXTRA = {"qgemm.hip": ["-mllvm", "--amdgpu-mfma-vgpr-form"], "attn.hip": ["-mllvm", "--amdgpu-mfma-vgpr-form"],
+         "peak.hip": ["-mllvm", "--amdgpu-mfma-vgpr-form"]}
 
 
 def _compile(item) -> Path:

@@ -12,6 +12,7 @@
 #include <cmath>
 #include <cstdarg>
 #include <cstdio>
+#include <cstdlib>
 #include <cstring>
 #include <string>
 #include <vector>
@@ -185,6 +186,15 @@ struct ifr_ctx {
   int last_split = 0, last_units = 0;
   int qb = 8;  // q-block tokens per attention unit: 16 MFMA columns / GQA group
   uint8_t* scratch = nullptr;  // this device's copy of `scratch` (resolved at ifr_ctx_create)
+  // per-linear seam workspaces (ifr_linear_batch & co.), allocated at first
+  // use for max_rows rows and freed with the model
+  float* sx = nullptr;        // fp32 [maxM][Kmax] input rows
+  int8_t* saq = nullptr;      // A tiles
+  float* sas = nullptr;       // [maxM] row scales
+  float* sgs = nullptr;       // [maxM][Kmax / 128] group code sums
+  uint16_t* sy = nullptr;     // fp16 [maxM][Nmax] output
+  uint16_t* smg = nullptr;    // fp16 [maxM][inter] SwiGLU output (ifr_mlp_fused)
+  std::vector<uint16_t> hy;   // host copy of one chunk's fp16 output
 
   void* dalloc(size_t bytes) {
     void* p = nullptr;
@@ -366,6 +376,10 @@ void release_model(ifr_ctx* c) {
     L.st = st;
   }
   c->layers.clear();
+  c->sx = nullptr;
+  c->saq = nullptr;
+  c->sas = c->sgs = nullptr;
+  c->sy = c->smg = nullptr;
   c->kpool.clear();
   c->vpool.clear();
   c->kscale.clear();
@@ -1596,6 +1610,221 @@ int ifr_attention_noalloc(ifr_ctx* c, int32_t layer, const ifr_row* rows, int32_
   HIPCHK(ifrk::launch_combine(cb, c->st));
   // the rows copy read the caller's host array; return once out_d is written
   HIPCHK(hipStreamSynchronize(c->st));
+  return IFR_OK;
+}
+
+}  // extern "C"
+
+namespace {
+
+// Widest input (K) and output (N) of any linear of the loaded model.
+void seam_dims(const ifr_ctx* c, int* Kmax, int* Nmax) {
+  const ifr_model_cfg& cf = c->cfg;
+  const int qN = cf.n_heads * cf.head_dim, qrows = (cf.attn_gate ? 2 : 1) * qN, kvN = cf.n_kv * cf.head_dim;
+  *Kmax = std::max(std::max(cf.hidden, qN), cf.inter);
+  *Nmax = std::max(std::max(qrows + 2 * kvN, 2 * cf.inter), cf.hidden);
+}
+
+int seam_alloc(ifr_ctx* c) {
+  if (c->sx) return IFR_OK;
+  int Kmax = 0, Nmax = 0;
+  seam_dims(c, &Kmax, &Nmax);
+  const size_t Mx = (size_t)c->maxM;
+  int r = 0;
+  if ((r = walloc(c, &c->sx, Mx * Kmax)) || (r = walloc(c, &c->saq, ifrk::atile_bytes((int)Mx, Kmax))) ||
+      (r = walloc(c, &c->sas, Mx)) || (r = walloc(c, &c->sgs, Mx * (Kmax / 128))) ||
+      (r = walloc(c, &c->sy, Mx * Nmax)) || (r = walloc(c, &c->smg, Mx * c->cfg.inter))) {
+    c->sx = nullptr;
+    return r;
+  }
+  return IFR_OK;
+}
+
+// The device linear of (layer, which) as the GEMM runs it.  Q, K and V of a
+// fused QKV projection are its tile ranges (tiles are contiguous in the
+// fragment-major layout); gate and up of an interleaved pair are the pair
+// run as a plain GEMM (tiles gate 0, up 0, gate 1, ...), *deint = 1 (gate)
+// or 2 (up) picking its tiles out of that output.
+int seam_view(ifr_ctx* c, int layer, int which, DLin& v, int* deint) {
+  if (!c->loaded) return fail(IFR_ESTATE, "no model loaded");
+  if (layer < 0 || layer >= c->cfg.layers) return fail(IFR_EINVAL, "layer %d", layer);
+  const ifr_model_cfg& cf = c->cfg;
+  const int qrows = (cf.attn_gate ? 2 : 1) * cf.n_heads * cf.head_dim, kvN = cf.n_kv * cf.head_dim;
+  const Layer& ly = c->layers[layer];
+  *deint = 0;
+  switch (which) {
+    case IFR_LIN_Q:
+    case IFR_LIN_K:
+    case IFR_LIN_V: {
+      if (ly.nqkv == 3) {
+        v = ly.qkv[which];
+        return IFR_OK;
+      }
+      const int off = which == IFR_LIN_Q ? 0 : which == IFR_LIN_K ? qrows : qrows + kvN;
+      v = ly.qkv[0];
+      const size_t t0 = (size_t)off / 16;
+      v.codes += t0 * v.nsteps * 64 * (v.bits / 2);
+      v.sz += t0 * v.ng * 16;
+      v.N = which == IFR_LIN_Q ? qrows : kvN;
+      return IFR_OK;
+    }
+    case IFR_LIN_O: v = ly.o; return IFR_OK;
+    case IFR_LIN_DOWN: v = ly.down; return IFR_OK;
+    case IFR_LIN_GATE:
+    case IFR_LIN_UP:
+      if (ly.ngu == 2) {
+        v = ly.gu[which - IFR_LIN_GATE];
+      } else {
+        v = ly.gu[0];
+        v.pair = 0;
+        *deint = 1 + (which - IFR_LIN_GATE);
+      }
+      return IFR_OK;
+    default: return fail(IFR_EINVAL, "linear id %d", which);
+  }
+}
+
+// Enqueue one linear over m rows already in c->sx: per-token quantization,
+// the GEMM into c->sy, and the fp16 rows back into c->hy.
+int seam_enqueue(ifr_ctx* c, const DLin& v, int m) {
+  HIPCHK(ifrk::launch_quant_plain(c->sx, nullptr, m, v.K, c->saq, c->sas, c->sgs, c->st));
+  ifrk::QGemmArgs a{c->saq, c->sas, c->sgs, c->sy, nullptr, m, v.N};
+  HIPCHK(ifrk::launch_qgemm(v, a, c->st));
+  return IFR_OK;
+}
+
+// fp16 rows [m][v.N] of the chunk into fp32 Y (de-interleaving a pair's tiles)
+void seam_unpack(const ifr_ctx* c, const DLin& v, int deint, int m, float* Y) {
+  const int Nout = deint ? v.N / 2 : v.N;
+  for (int r = 0; r < m; ++r) {
+    const uint16_t* src = c->hy.data() + (size_t)r * v.N;
+    float* dst = Y + (size_t)r * Nout;
+    if (!deint) {
+      for (int n = 0; n < Nout; ++n) dst[n] = ifr::h2f(src[n]);
+    } else {
+      for (int n = 0; n < Nout; ++n) dst[n] = ifr::h2f(src[32 * (n / 16) + 16 * (deint - 1) + (n % 16)]);
+    }
+  }
+}
+
+// One linear over M host rows, in chunks of max_rows.
+int seam_linear(ifr_ctx* c, int layer, int which, const float* X, float* Y, int M) {
+  DLin v;
+  int deint = 0;
+  if (int r = seam_view(c, layer, which, v, &deint)) return r;
+  if (int r = seam_alloc(c)) return r;
+  const int Nout = deint ? v.N / 2 : v.N;
+  c->hy.resize((size_t)c->maxM * v.N);
+  for (int r0 = 0; r0 < M; r0 += c->maxM) {
+    const int m = std::min(c->maxM, M - r0);
+    HIPCHK(hipMemcpyAsync(c->sx, X + (size_t)r0 * v.K, (size_t)m * v.K * sizeof(float), hipMemcpyHostToDevice, c->st));
+    if (int r = seam_enqueue(c, v, m)) return r;
+    HIPCHK(hipMemcpyAsync(c->hy.data(), c->sy, (size_t)m * v.N * 2, hipMemcpyDeviceToHost, c->st));
+    HIPCHK(hipStreamSynchronize(c->st));
+    seam_unpack(c, v, deint, m, Y + (size_t)r0 * Nout);
+  }
+  return IFR_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int ifr_linear_lookup(ifr_ctx* c, const char* name, int32_t* layer, int32_t* which) {
+  if (!c || !name || !layer || !which) return fail(IFR_EINVAL, "null arg");
+  if (!c->loaded) return fail(IFR_ESTATE, "no model loaded");
+  static const char* const kSuffix[7] = {"self_attn.q_proj.weight", "self_attn.k_proj.weight",
+                                         "self_attn.v_proj.weight", "self_attn.o_proj.weight",
+                                         "mlp.gate_proj.weight",    "mlp.up_proj.weight",
+                                         "mlp.down_proj.weight"};
+  const std::string n(name), pre = "model.language_model.layers.";
+  if (n.compare(0, pre.size(), pre) != 0) return fail(IFR_EINVAL, "not a layer linear: %s", name);
+  size_t i = pre.size(), j = i;
+  while (j < n.size() && n[j] >= '0' && n[j] <= '9') ++j;
+  if (j == i || j - i > 6 || j >= n.size() || n[j] != '.') return fail(IFR_EINVAL, "no layer index in %s", name);
+  const int l = std::atoi(n.substr(i, j - i).c_str());
+  if (l >= c->cfg.layers) return fail(IFR_EINVAL, "layer %d of %d in %s", l, c->cfg.layers, name);
+  for (int w = 0; w < 7; ++w)
+    if (n.compare(j + 1, std::string::npos, kSuffix[w]) == 0) {
+      *layer = l;
+      *which = w;
+      return IFR_OK;
+    }
+  return fail(IFR_EINVAL, "not a linear of the model: %s", name);
+}
+
+int ifr_linear_shape(ifr_ctx* c, int32_t layer, int32_t which, int32_t* N, int32_t* K) {
+  if (!c || !N || !K) return fail(IFR_EINVAL, "null arg");
+  DLin v;
+  int deint = 0;
+  if (int r = seam_view(c, layer, which, v, &deint)) return r;
+  *N = deint ? v.N / 2 : v.N;
+  *K = v.K;
+  return IFR_OK;
+}
+
+int ifr_linear_rot(ifr_ctx* c, int32_t which, int32_t* site) {
+  if (!c || !site) return fail(IFR_EINVAL, "null arg");
+  if (!c->loaded) return fail(IFR_ESTATE, "no model loaded");
+  if (which < IFR_LIN_Q || which > IFR_LIN_DOWN) return fail(IFR_EINVAL, "linear id %d", which);
+  *site = !c->cfg.rotate ? 0 : (which == IFR_LIN_O || which == IFR_LIN_DOWN) ? 2 : 1;
+  return IFR_OK;
+}
+
+int ifr_linear_batch(ifr_ctx* c, int32_t layer, int32_t which, const float* X, float* Y, int32_t M) {
+  if (!c || !X || !Y || M < 0) return fail(IFR_EINVAL, "null arg or M < 0");
+  if (M == 0) return IFR_OK;
+  HIPCHK(hipSetDevice(c->device));
+  return seam_linear(c, layer, which, X, Y, M);
+}
+
+int ifr_linear_wave_batch(ifr_ctx* c, const ifr_linear_item* items, int32_t n, int32_t M) {
+  if (!c || (n > 0 && !items) || n < 0 || M < 0) return fail(IFR_EINVAL, "null arg");
+  HIPCHK(hipSetDevice(c->device));
+  // items are independent: each one's rows run through the shared staging
+  // in turn; the results equal ifr_linear_batch item by item
+  for (int i = 0; i < n; ++i) {
+    if (!items[i].X || !items[i].Y) return fail(IFR_EINVAL, "item %d: null buffer", i);
+    if (M == 0) continue;
+    if (int r = seam_linear(c, items[i].layer, items[i].which, items[i].X, items[i].Y, M)) return r;
+  }
+  return IFR_OK;
+}
+
+int ifr_mlp_fused(ifr_ctx* c, int32_t layer, const float* rin, float* md, int32_t M) {
+  if (!c || !rin || !md || M < 0) return fail(IFR_EINVAL, "null arg or M < 0");
+  if (!c->loaded) return fail(IFR_ESTATE, "no model loaded");
+  if (layer < 0 || layer >= c->cfg.layers) return fail(IFR_EINVAL, "layer %d", layer);
+  if (M == 0) return IFR_OK;
+  HIPCHK(hipSetDevice(c->device));
+  if (int r = seam_alloc(c)) return r;
+  const ifr_model_cfg& cf = c->cfg;
+  const int H = cf.hidden, F = cf.inter;
+  const Layer& ly = c->layers[layer];
+  c->hy.resize((size_t)c->maxM * H);
+  for (int r0 = 0; r0 < M; r0 += c->maxM) {
+    const int m = std::min(c->maxM, M - r0);
+    HIPCHK(hipMemcpyAsync(c->sx, rin + (size_t)r0 * H, (size_t)m * H * sizeof(float), hipMemcpyHostToDevice, c->st));
+    HIPCHK(ifrk::launch_quant_plain(c->sx, nullptr, m, H, c->saq, c->sas, c->sgs, c->st));
+    // gate/up with the SwiGLU epilogue (or two GEMMs and the SwiGLU pass),
+    // then the down projection's per-token quantization: the forward's steps
+    if (ly.ngu == 1) {
+      ifrk::QGemmArgs a{c->saq, c->sas, c->sgs, c->smg, nullptr, m, F};
+      HIPCHK(ifrk::launch_qgemm(ly.gu[0], a, c->st));
+    } else {
+      for (int j = 0; j < 2; ++j) {
+        ifrk::QGemmArgs a{c->saq, c->sas, c->sgs, c->sy + j * F, nullptr, m, 2 * F};
+        HIPCHK(ifrk::launch_qgemm(ly.gu[j], a, c->st));
+      }
+      HIPCHK(ifrk::launch_swiglu(c->sy, m, F, c->smg, c->st));
+    }
+    HIPCHK(ifrk::launch_quant_plain(nullptr, c->smg, m, F, c->saq, c->sas, c->sgs, c->st));
+    ifrk::QGemmArgs a{c->saq, c->sas, c->sgs, c->sy, nullptr, m, H};
+    HIPCHK(ifrk::launch_qgemm(ly.down, a, c->st));
+    HIPCHK(hipMemcpyAsync(c->hy.data(), c->sy, (size_t)m * H * 2, hipMemcpyDeviceToHost, c->st));
+    HIPCHK(hipStreamSynchronize(c->st));
+    for (size_t i = 0; i < (size_t)m * H; ++i) md[(size_t)r0 * H + i] = ifr::h2f(c->hy[i]);
+  }
   return IFR_OK;
 }
 

@@ -339,6 +339,13 @@ def test_cfg1_large_margin_variant_streams_identical(dev, kv_int8):
             pos = [p + 1 for p in pos]
         print(f"[large-margin cfg1 kv_int8={kv_int8}] 64 free-running steps identical on all 5 sequences; "
               f"top-2 margin min {min(margins):.3f} sigma, median {float(np.median(margins)):.3f}")
+        out = os.environ.get("IFR_PARITY_OUT")
+        if out:
+            os.makedirs(out, exist_ok=True)
+            with open(os.path.join(out, f"parity_cfg1_margin_kv{kv_int8}.json"), "w") as f:
+                json.dump({"kv_int8": kv_int8, "steps_identical": 64, "sequences": 5,
+                           "top2_margin_min": min(margins), "top2_margin_median": float(np.median(margins)),
+                           "distinct_tokens": len(set(np.array(streams).reshape(-1).tolist()))}, f, indent=1)
         assert len(set(np.array(streams).reshape(-1).tolist())) > 20  # not a repeated token
     finally:
         m.close()
