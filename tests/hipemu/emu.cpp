@@ -452,6 +452,11 @@ hipError_t hipGetDevice(int* d) {
   *d = 0;
   return hipSuccess;
 }
+hipError_t hipDeviceGetAttribute(int* v, hipDeviceAttribute_t a, int d) {
+  if (d != 0 || a != hipDeviceAttributeMultiprocessorCount) return hipErrorInvalidValue;
+  *v = 256;
+  return hipSuccess;
+}
 hipError_t hipGetDeviceProperties(hipDeviceProp_t* p, int) {
   std::memset(p, 0, sizeof *p);
   std::snprintf(p->name, sizeof p->name, "hipemu");

@@ -247,6 +247,8 @@ hipError_t hipGetDeviceCount(int* n);
 hipError_t hipSetDevice(int d);
 hipError_t hipGetDevice(int* d);
 hipError_t hipGetDeviceProperties(hipDeviceProp_t* p, int d);
+enum hipDeviceAttribute_t { hipDeviceAttributeMultiprocessorCount };
+hipError_t hipDeviceGetAttribute(int* v, hipDeviceAttribute_t a, int d);
 hipError_t hipMalloc(void** p, size_t n);
 template <typename T>
 inline hipError_t hipMalloc(T** p, size_t n) { return hipMalloc(reinterpret_cast<void**>(p), n); }
