@@ -846,100 +846,197 @@ __global__ __launch_bounds__(256) void qk_rope_kv_kernel(QKArgs a, KVLayout kv) 
 }
 
 // ---- ragged batch packing ------------------------------------------------------
-// Block-wide exclusive scan of v[0..n) in LDS (in place); returns the total.
-// Each thread scans a contiguous chunk; chunk totals are scanned with wave
-// shuffles and one LDS pass over the wave totals.
-__device__ int block_exscan(int* v, int n, int* tmp) {
-  const int T = blockDim.x, lane = threadIdx.x & 63, w = threadIdx.x >> 6, nw = T >> 6;
-  const int per = (n + T - 1) / T;
-  const int b = threadIdx.x * per, e = min(n, b + per);
-  int s = 0;
-  for (int i = b; i < e; ++i) s += v[i];
-  int incl = s;
-#pragma unroll
-  for (int o = 1; o < 64; o <<= 1) {
-    const int y = __shfl_up(incl, o, 64);
-    if (lane >= o) incl += y;
-  }
-  if (lane == 63) tmp[w] = incl;
-  __syncthreads();
-  if (w == 0) {  // the wave totals (nw <= 64), scanned by the first wave
-    const int t = lane < nw ? tmp[lane] : 0;
-    int x = t;
-#pragma unroll
-    for (int o = 1; o < 64; o <<= 1) {
-      const int y = __shfl_up(x, o, 64);
-      if (lane >= o) x += y;
-    }
-    if (lane < nw) tmp[lane] = x - t;
-    if (lane == 63) tmp[nw] = x;
-  }
-  __syncthreads();
-  int run = tmp[w] + incl - s;
-  for (int i = b; i < e; ++i) { const int t = v[i]; v[i] = run; run += t; }
-  const int total = tmp[nw];
-  __syncthreads();
-  return total;
+// Inclusive prefix sum over the 64 lanes: Hillis-Steele inside each 16-lane
+// row with DPP row_shr (lanes shifted in from outside the row read 0), then
+// the three lower rows' totals added from scalars.  No LDS crossbar.
+__device__ __forceinline__ int wave_incl_scan(int x) {
+  x += ifrd::dpp_i<0x111>(x);  // row_shr:1
+  x += ifrd::dpp_i<0x112>(x);  // row_shr:2
+  x += ifrd::dpp_i<0x114>(x);  // row_shr:4
+  x += ifrd::dpp_i<0x118>(x);  // row_shr:8
+  const int r0 = __builtin_amdgcn_readlane(x, 15), r1 = __builtin_amdgcn_readlane(x, 31),
+            r2 = __builtin_amdgcn_readlane(x, 47);
+  const int lane = threadIdx.x & 63;
+  return x + (lane >= 16 ? r0 : 0) + (lane >= 32 ? r1 : 0) + (lane >= 48 ? r2 : 0);
 }
 
-__global__ __launch_bounds__(1024) void pack_kernel(const int32_t* rows, int M, int nkv, int qb,
-                                                    int split, PackOut o) {
+// Block-wide exclusive scans of NA arrays v[a][0..n) in LDS, one pass;
+// returns the totals.  Each thread takes a contiguous chunk of elements and
+// gets their values from f(i, x) (x[a] = element i of array a; f runs in the
+// thread that owns i, before any barrier), sums them, the chunk sums are
+// scanned per wave, and every wave then scans the 16 wave totals itself (one
+// LDS exchange, two barriers).  On return v[a][i] holds the prefix before i,
+// and v[a][n] the total where total_at_n.  tmp holds NA (blockDim / 64) ints.
+// E: int, or uint16_t for arrays whose prefixes stay below 65536.
+template <int NA>
+struct ScanTotals {
+  int t[NA];
+};
+template <int NA, typename E, typename F>
+__device__ ScanTotals<NA> block_exscan_f(E* const (&v)[NA], int n, bool total_at_n, int* tmp, F f) {
+  const int T = blockDim.x, lane = threadIdx.x & 63, nw = T >> 6;
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int per = (n + T - 1) / T;
+  const int b = threadIdx.x * per, e = min(n, b + per);
+  int s[NA], incl[NA];
+#pragma unroll
+  for (int a = 0; a < NA; ++a) s[a] = 0;
+  for (int i = b; i < e; ++i) {
+    int x[NA];
+    f(i, x);
+#pragma unroll
+    for (int a = 0; a < NA; ++a) {
+      v[a][i] = (E)x[a];
+      s[a] += x[a];
+    }
+  }
+#pragma unroll
+  for (int a = 0; a < NA; ++a) {
+    incl[a] = wave_incl_scan(s[a]);
+    if (lane == 63) tmp[a * nw + w] = incl[a];
+  }
+  __syncthreads();
+  ScanTotals<NA> tot;
+#pragma unroll
+  for (int a = 0; a < NA; ++a) {
+    const int ws = wave_incl_scan(lane < nw ? tmp[a * nw + lane] : 0);
+    const int before = w > 0 ? __builtin_amdgcn_readlane(ws, w - 1) : 0;
+    tot.t[a] = __builtin_amdgcn_readlane(ws, nw - 1);
+    int run = before + incl[a] - s[a];
+    for (int i = b; i < e; ++i) {  // this thread's own elements: no barrier needed
+      const int x = v[a][i];
+      v[a][i] = (E)run;
+      run += x;
+    }
+    if (total_at_n && threadIdx.x == 0) v[a][n] = (E)tot.t[a];
+  }
+  __syncthreads();
+  return tot;
+}
+
+// The group of q-block t: the last g < ngroups with nblk[g] <= t.
+__device__ __forceinline__ int pack_group_of(const uint16_t* nblk, int ngroups, int t) {
+  int lo = 0, hi = ngroups - 1;
+  while (lo < hi) {
+    const int mid = (lo + hi + 1) >> 1;
+    if (nblk[mid] <= t) lo = mid; else hi = mid - 1;
+  }
+  return lo;
+}
+
+// kPackGroups workgroups of kPackThreads.  Each builds the whole set of maps
+// in its own LDS (the batch is at most 6144 rows), and the workgroups share
+// the writes: workgroup g stores the per-row outputs of the rows its wave g
+// holds, and every kPackGroups-th (q-block, kv head) pair's units and
+// dispatch slots.  Row m = threadIdx.x + k kPackThreads is read from global
+// memory once, into registers (k < kPackRowsPerThread); every later phase
+// works from those registers and six LDS arrays, and every loop runs over
+// rows, groups or q-blocks in parallel (no thread walks a group's q-blocks
+// or quads).  Ten barriers in all.  LDS arrays, one map per phase (the
+// three index maps, all <= 6144, in 16 bits: 159.9 KB at M = 6144):
+//   fs, fw  group-start / want flags of row m (scanned: starts / wants before
+//           m), then the per-q-block dispatch-slot counts (scanned)
+//   gpos    first KV position of group g
+//   gseq    sequence of group g
+//   ucnt    first unit of q-block b
+//   g0      first row of group g (M at ngroups)         16 bits
+//   nblk    first q-block of group g (nb at ngroups)    16 bits
+//   bgrp    group of q-block b                          16 bits
+constexpr int kPackThreads = 1024, kPackRowsPerThread = 6, kPackMaxRows = kPackThreads * kPackRowsPerThread;
+constexpr int kPackGroups = 16;
+static_assert(kPackMaxRows < 65536, "the 16-bit index maps hold row, group and q-block indices");
+
+__global__ __launch_bounds__(kPackThreads) void pack_kernel(const int32_t* rows, int M, int nkv, int qb,
+                                                            int split, PackOut o) {
   extern __shared__ int sm[];
-  int* flag = sm;              // [M]   group start -> group index
-  int* grp_start = sm + M;     // [M+1] row offset of group g
-  int* nblk = sm + 2 * M + 1;  // [M+1] q-blocks per group -> block base
-  int* ucnt = sm + 3 * M + 2;  // [M]   units per q-block -> unit base
-  int* wnt = sm + 4 * M + 2;   // [M]   want flags -> want slot
-  int* bgrp = sm + 5 * M + 2;  // [M]   group of each q-block
-  int* tmp = sm + 6 * M + 2;   // [blockDim/64 + 1]
-  for (int m = threadIdx.x; m < M; m += blockDim.x) {
-    const int32_t* r = rows + 5 * m;
-    flag[m] = (m == 0 || rows[5 * (m - 1)] != r[0]) ? 1 : 0;
-    grp_start[m] = flag[m];
-    wnt[m] = r[4] ? 1 : 0;
-    o.row_seq[m] = r[0];
-    o.row_pos[m] = r[1];
-    o.row_kind[m] = r[3];
-    if (o.row_tok) o.row_tok[m] = r[2];
-  }
-  __syncthreads();
-  const int ngroups = block_exscan(grp_start, M, tmp);  // grp_start[m] = #starts before m
-  for (int m = threadIdx.x; m < M; m += blockDim.x) {
-    const int g = grp_start[m] + flag[m] - 1;
-    o.row_grp[m] = g;
-    flag[m] = g;
-  }
-  __syncthreads();
-  for (int m = threadIdx.x; m < M; m += blockDim.x)
-    if (m == 0 || flag[m] != flag[m - 1]) grp_start[flag[m]] = m;
-  if (threadIdx.x == 0) grp_start[ngroups] = M;
-  __syncthreads();
-  for (int g = threadIdx.x; g <= ngroups; g += blockDim.x) o.cu_seqlens[g] = grp_start[g];
-  for (int g = threadIdx.x; g < ngroups; g += blockDim.x) {
-    const int len = grp_start[g + 1] - grp_start[g];
-    nblk[g] = (len + qb - 1) / qb;
-  }
-  __syncthreads();
-  const int nb = block_exscan(nblk, ngroups, tmp);  // nblk[g] = first block of group g
-  if (threadIdx.x == 0) nblk[ngroups] = nb;
-  __syncthreads();
-  for (int g = threadIdx.x; g < ngroups; g += blockDim.x) {
-    const int r0 = grp_start[g], len = grp_start[g + 1] - r0;
-    const int pos0 = rows[5 * r0 + 1];
-    for (int b = 0; b < nblk[g + 1] - nblk[g]; ++b) {
-      const int kvhi = pos0 + min((b + 1) * qb, len);
-      ucnt[nblk[g] + b] = nkv * ((kvhi + split - 1) / split);
-      bgrp[nblk[g] + b] = g;
+  int* fs = sm;                  // [M]
+  int* fw = sm + M;              // [M]
+  int* gpos = sm + 2 * M;        // [M]
+  int* gseq = sm + 3 * M;        // [M]
+  int* ucnt = sm + 4 * M;        // [M]
+  int* tmp = sm + 5 * M;         // [2 kPackThreads / 64]
+  uint16_t* g0 = reinterpret_cast<uint16_t*>(tmp + 2 * kPackThreads / 64);  // [M + 1]
+  uint16_t* nblk = g0 + M + 1;   // [M + 1]
+  uint16_t* bgrp = nblk + M + 1; // [M]
+  constexpr int R = kPackRowsPerThread;
+  // this workgroup's share of the writes: pairs t0, t0 + tstep, ... (64
+  // consecutive pairs per wave: a store instruction costs about the same
+  // whether 4 or 64 of its lanes are active); the rows of wave wg
+  const int wg = blockIdx.x, t0 = wg + kPackGroups * threadIdx.x, tstep = kPackGroups * kPackThreads;
+  const bool rows_out = (int)(threadIdx.x >> 6) == wg;
+  // KV splits of a q-block of group g ending at its block b (q-block rows up to (b + 1) qb)
+  auto nsplit = [&](int g, int b) {
+    return (gpos[g] + min((b + 1) * qb, g0[g + 1] - g0[g]) + split - 1) / split;
+  };
+  int seq_r[R], pos_r[R], g_r[R];
+  bool start_r[R], want_r[R];
+#pragma unroll
+  for (int k = 0; k < R; ++k) {
+    const int m = threadIdx.x + k * kPackThreads;
+    start_r[k] = want_r[k] = false;
+    seq_r[k] = pos_r[k] = g_r[k] = 0;
+    if (m < M) {
+      const int32_t* r = rows + 5 * m;
+      const int seq = r[0], pos = r[1], tok = r[2], kind = r[3], want = r[4];
+      const bool st = m == 0 || rows[5 * (m - 1)] != seq;
+      seq_r[k] = seq;
+      pos_r[k] = pos;
+      start_r[k] = st;
+      want_r[k] = want != 0;
+      fs[m] = st ? 1 : 0;
+      fw[m] = want ? 1 : 0;
+      if (rows_out) {
+        o.row_seq[m] = seq;
+        o.row_pos[m] = pos;
+        o.row_kind[m] = kind;
+        if (o.row_tok) o.row_tok[m] = tok;
+      }
     }
   }
   __syncthreads();
-  block_exscan(ucnt, nb, tmp);  // ucnt[b] = first unit of block b
+  int* const sflags[2] = {fs, fw};
+  const int ngroups = block_exscan_f<2, int>(sflags, M, false, tmp, [&](int i, int (&x)[2]) {
+    x[0] = fs[i];
+    x[1] = fw[i];
+  }).t[0];
+  // each row: its group and the wanted-row list; group starts: first row,
+  // position and sequence of each group
+#pragma unroll
+  for (int k = 0; k < R; ++k) {
+    const int m = threadIdx.x + k * kPackThreads;
+    if (m < M) {
+      const int g = fs[m] + (start_r[k] ? 1 : 0) - 1;
+      g_r[k] = g;
+      if (rows_out) {
+        o.row_grp[m] = g;
+        if (want_r[k]) o.want_rows[fw[m]] = m;
+      }
+      if (start_r[k]) {
+        g0[g] = (uint16_t)m;
+        gpos[g] = pos_r[k];
+        gseq[g] = seq_r[k];
+      }
+    }
+  }
+  if (threadIdx.x == 0) g0[ngroups] = (uint16_t)M;
+  __syncthreads();
+  if (wg == 0)
+    for (int g = threadIdx.x; g <= ngroups; g += kPackThreads) o.cu_seqlens[g] = g0[g];
+  uint16_t* const sblk[1] = {nblk};
+  const int nb = block_exscan_f<1, uint16_t>(sblk, ngroups, true, tmp, [&](int g, int (&x)[1]) {
+    x[0] = (g0[g + 1] - g0[g] + qb - 1) / qb;  // q-blocks of group g
+  }).t[0];
+  int* const sunits[1] = {ucnt};
+  block_exscan_f<1, int>(sunits, nb, false, tmp, [&](int t, int (&x)[1]) {
+    const int g = pack_group_of(nblk, ngroups, t);
+    bgrp[t] = (uint16_t)g;
+    x[0] = nkv * nsplit(g, t - nblk[g]);  // units of q-block t
+  });
   // one thread per (q-block, kv head): that head's units of the q-block
-  for (int t = threadIdx.x; t < nb * nkv; t += blockDim.x) {
+  for (int t = t0; t < nb * nkv; t += tstep) {
     const int gb = t / nkv, kvh = t - gb * nkv;
     const int g = bgrp[gb], b = gb - nblk[g];
-    const int r0 = grp_start[g], len = grp_start[g + 1] - r0;
-    const int pos0 = rows[5 * r0 + 1], seq = rows[5 * r0];
+    const int r0 = g0[g], len = g0[g + 1] - r0, pos0 = gpos[g], seq = gseq[g];
     const int qn = min(qb, len - b * qb);
     const int kvhi = pos0 + b * qb + qn;
     const int ns = (kvhi + split - 1) / split;
@@ -957,81 +1054,47 @@ __global__ __launch_bounds__(1024) void pack_kernel(const int32_t* rows, int M, 
       o.units[base + kvh * ns + s] = u;
     }
   }
-  // one thread per row: its combine map (q-block gb = its group's first
-  // block + (m - r0) / qb)
-  for (int m = threadIdx.x; m < M; m += blockDim.x) {
-    const int g = flag[m];  // the row's group
-    const int r0 = grp_start[g], len = grp_start[g + 1] - r0;
-    const int b = (m - r0) / qb, gb = nblk[g] + b;
-    const int pos0 = rows[5 * r0 + 1];
-    const int qn = min(qb, len - b * qb);
-    o.comb_base[m] = ucnt[gb];
-    o.comb_nsplit[m] = (pos0 + b * qb + qn + split - 1) / split;
-    o.comb_tok[m] = m - r0 - b * qb;
-  }
-  __syncthreads();
-  // ---- dispatch order (see attn_slot_count): per-group slot counts of the
-  // chunked region (flag[]) and of the dense region (bgrp[]), both free now
-  for (int g = threadIdx.x; g < ngroups; g += blockDim.x) {
-    const int nbg = nblk[g + 1] - nblk[g];
-    const int len = grp_start[g + 1] - grp_start[g];
-    const int pos0 = rows[5 * grp_start[g] + 1];
-    int cs = 0, ss = 0;
-    if (nbg == 1) {
-      ss = nkv * ((pos0 + len + split - 1) / split);
-    } else {
-      for (int j = 0; 4 * j < nbg; ++j) {
-        const int bl = min(4 * j + 3, nbg - 1);
-        cs += 4 * nkv * ((pos0 + min((bl + 1) * qb, len) + split - 1) / split);
-      }
+  // each row's combine map (q-block gb = its group's first block + (m - r0) / qb)
+#pragma unroll
+  for (int k = 0; k < R; ++k) {
+    const int m = threadIdx.x + k * kPackThreads;
+    if (m < M && rows_out) {
+      const int g = g_r[k], r0 = g0[g], len = g0[g + 1] - r0, pos0 = gpos[g];
+      const int b = (m - r0) / qb, gb = nblk[g] + b;
+      const int qn = min(qb, len - b * qb);
+      o.comb_base[m] = ucnt[gb];
+      o.comb_nsplit[m] = (pos0 + b * qb + qn + split - 1) / split;
+      o.comb_tok[m] = m - r0 - b * qb;
     }
-    flag[g] = cs;
-    bgrp[g] = ss;
   }
-  __syncthreads();
-  const int CS = block_exscan(flag, ngroups, tmp);
-  __syncthreads();
-  block_exscan(bgrp, ngroups, tmp);
-  __syncthreads();
+  // ---- dispatch order (see attn_slot_count), counts per q-block in q-block
+  // order.  Chunked region (fs): a group of several q-blocks is cut into
+  // quads of 4 consecutive q-blocks, each quad taking 4 nkv slots per KV
+  // split of its last q-block, counted at that q-block.  Dense region after
+  // it (fw): groups of one q-block, their units packed in unit order.
+  int* const sslots[2] = {fs, fw};
+  const int CS = block_exscan_f<2, int>(sslots, nb, false, tmp, [&](int t, int (&x)[2]) {
+    const int g = bgrp[t], nbg = nblk[g + 1] - nblk[g], b = t - nblk[g];
+    x[0] = (nbg > 1 && ((b & 3) == 3 || b == nbg - 1)) ? 4 * nkv * nsplit(g, b) : 0;
+    x[1] = nbg == 1 ? nkv * nsplit(g, 0) : 0;
+  }).t[0];
   // one thread per (q-block, kv head): that head's slots of the q-block
-  for (int t = threadIdx.x; t < nb * nkv; t += blockDim.x) {
+  for (int t = t0; t < nb * nkv; t += tstep) {
     const int gb = t / nkv, kvh = t - gb * nkv;
-    int g = 0;  // group of q-block gb (nblk[] holds first blocks, ascending)
-    {
-      int lo = 0, hi = ngroups - 1;
-      while (lo < hi) {
-        const int mid = (lo + hi + 1) >> 1;
-        if (nblk[mid] <= gb) lo = mid; else hi = mid - 1;
-      }
-      g = lo;
-    }
-    const int nbg = nblk[g + 1] - nblk[g], b = gb - nblk[g];
-    const int len = grp_start[g + 1] - grp_start[g];
-    const int pos0 = rows[5 * grp_start[g] + 1];
-    const int ns = (pos0 + min((b + 1) * qb, len) + split - 1) / split;
-    const int base = ucnt[gb];
+    const int g = bgrp[gb], nbg = nblk[g + 1] - nblk[g], b = gb - nblk[g];
+    const int ns = nsplit(g, b), base = ucnt[gb];
     if (nbg == 1) {
-      for (int s = 0; s < ns; ++s) o.order[CS + bgrp[g] + kvh * ns + s] = base + kvh * ns + s;
+      for (int s = 0; s < ns; ++s) o.order[CS + fw[gb] + kvh * ns + s] = base + kvh * ns + s;
       continue;
     }
-    const int j = b >> 2, q = b & 3;
-    int off = flag[g];
-    for (int jj = 0; jj < j; ++jj) {
-      const int bl = min(4 * jj + 3, nbg - 1);
-      off += 4 * nkv * ((pos0 + min((bl + 1) * qb, len) + split - 1) / split);
-    }
-    const int bl = min(4 * j + 3, nbg - 1);
-    const int nsm = (pos0 + min((bl + 1) * qb, len) + split - 1) / split;
+    const int q = b & 3, bl = min((b | 3), nbg - 1);  // the quad's last q-block
+    const int off = fs[nblk[g] + bl], nsm = nsplit(g, bl);
     for (int s = 0; s < nsm; ++s) o.order[off + (kvh * nsm + s) * 4 + q] = s < ns ? base + kvh * ns + s : -1;
-    // slots of absent q-blocks in a short last chunk
+    // slots of absent q-blocks in a short last quad
     if (b == nbg - 1)
       for (int qq = q + 1; qq < 4; ++qq)
         for (int s = 0; s < nsm; ++s) o.order[off + (kvh * nsm + s) * 4 + qq] = -1;
   }
-  __syncthreads();
-  const int nwant = block_exscan(wnt, M, tmp);
-  for (int m = threadIdx.x; m < M; m += blockDim.x)  // row m is wanted if the scan steps at m
-    if ((m + 1 < M ? wnt[m + 1] : nwant) > wnt[m]) o.want_rows[wnt[m]] = m;
 }
 
 }  // namespace
@@ -1189,8 +1252,8 @@ hipError_t launch_qk_rope_kv(const QKArgs& a, const KVLayout& kv, hipStream_t st
 hipError_t launch_pack(const int32_t* rows, int M, int nkv, int qb, int split, const PackOut& o,
                        hipStream_t st) {
   if (M <= 0) return hipSuccess;
-  if (M > 6144 || qb <= 0 || split <= 0 || nkv <= 0) return hipErrorInvalidValue;
-  const size_t lds = (size_t)(6 * M + 2 + 16 + 1) * sizeof(int);
+  if (M > kPackMaxRows || qb <= 0 || split <= 0 || nkv <= 0) return hipErrorInvalidValue;
+  const size_t lds = (size_t)(5 * M + 2 * kPackThreads / 64) * sizeof(int) + (size_t)(3 * M + 2) * sizeof(uint16_t);
   static bool attr = false;
   if (!attr) {
     hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(pack_kernel),
@@ -1198,7 +1261,7 @@ hipError_t launch_pack(const int32_t* rows, int M, int nkv, int qb, int split, c
     if (e != hipSuccess) return e;
     attr = true;
   }
-  hipLaunchKernelGGL(pack_kernel, dim3(1), dim3(1024), lds, st, rows, M, nkv, qb, split, o);
+  hipLaunchKernelGGL(pack_kernel, dim3(kPackGroups), dim3(kPackThreads), lds, st, rows, M, nkv, qb, split, o);
   return hipGetLastError();
 }
 

@@ -290,12 +290,12 @@ def test_act_quant_bitexact(dev, K, norm, rot, rnd, ga):
     assert np.array_equal(gg, g)
 
 
-def _attn_engine(dev, kv_int8, lens, chunks, dense_attention=0, model=None):
+def _attn_engine(dev, kv_int8, lens, chunks, dense_attention=0, model=None, max_rows=1200):
     cfg = ia.default_cfg(layers=1, vocab=1024)
     model = model or ia.SynthModel(cfg, seed=5)
     total = sum(lens) + sum(o + n for o, n in chunks)
     eng = ia.Engine(dev, model, max_seqs=len(lens) + len(chunks) + 1, max_seq_tokens=8192,
-                    pool_tokens=total + 64 * (len(lens) + 4), kv_int8=kv_int8, max_rows=1200,
+                    pool_tokens=total + 64 * (len(lens) + 4), kv_int8=kv_int8, max_rows=max_rows,
                     dense_attention=dense_attention)
     return cfg, model, eng
 
@@ -386,7 +386,10 @@ def test_attention_cfg3(dev, kv_int8):
 # (sequence lengths, rows as (sequence index, position, kind, want)):
 # decode, verify and a 3-q-block chunk in one quad; then several quads of a
 # chunk whose q-blocks span 3-4 KV splits, and a chunk that crosses a split
-# boundary inside a quad (q-blocks of one quad with different split counts)
+# boundary inside a quad (q-blocks of one quad with different split counts);
+# then a cfg5-sized batch (a 2048-row chunk at offset 1000, decode, a verify
+# group, a 700-row chunk from offset 0: M = 2754, so the pack kernel's
+# threads hold up to three rows each)
 PACK_CASES = [
     ([300, 40, 1000, 20],
      [(0, 299, 0, 1), (1, 30, 2, 1), (1, 31, 2, 1), (1, 32, 2, 1), (2, 999, 0, 0)] +
@@ -394,6 +397,9 @@ PACK_CASES = [
     ([513, 900, 64, 280],
      [(0, 512, 0, 1)] + [(1, 700 + p, 1, int(p == 199)) for p in range(200)] + [(2, 63, 0, 1)] +
      [(3, 240 + p, 1, int(p == 39)) for p in range(40)]),
+    ([3100, 50, 2600, 700],
+     [(0, 1000 + p, 1, int(p == 2047)) for p in range(2048)] + [(1, 49, 0, 1)] +
+     [(2, 2590 + p, 2, 1) for p in range(5)] + [(3, p, 1, int(p == 699)) for p in range(700)]),
 ]
 
 
@@ -401,7 +407,7 @@ PACK_CASES = [
 def test_pack_maps_match_restatement(dev, case):
     from oracle import pack as pk
     lens, spec = PACK_CASES[case]
-    cfg, model, eng = _attn_engine(dev, 0, lens, [])
+    cfg, model, eng = _attn_engine(dev, 0, lens, [], max_rows=max(1200, len(spec)))
     rng = np.random.default_rng(9)
     seqs = []
     for n in lens:
