@@ -61,6 +61,9 @@ def parse():
                     help="skip the secondary pack_prefill measurement of the same load")
     ap.add_argument("--gemm-sweep", action="store_true",
                     help="run only the cache-cold cfg2 GEMM sweep and print its JSON line")
+    ap.add_argument("--gemm-mall", action="store_true",
+                    help="--gemm-variants with 100 MB of weight copies (MALL-resident, as in the serve load)")
+    ap.add_argument("--gemm-ms", default="128,256,576,1024", help="M values of --gemm-variants")
     ap.add_argument("--gemm-variants", action="store_true",
                     help="time every quant-GEMM launch shape on the 0.8B shapes and print a JSON line")
     ap.add_argument("--gemm-decode", action="store_true",
@@ -489,10 +492,13 @@ def f16_gemm(ia, dev, Ms=(1, 16, 576), reps=3, kind="f16"):
     return res
 
 
-def gemm_variants(ia, dev, Ms=(128, 256, 576, 1024), bits=2, reps=3, shapes=SHAPES_08B):
+def gemm_variants(ia, dev, Ms=(128, 256, 576, 1024), bits=2, reps=3, shapes=SHAPES_08B, rotate_bytes=320e6):
     """Every launch shape of the quant GEMM on the four projection shapes
     (gate_up as the interleaved SwiGLU pair the forward runs), cache-cold as
-    in gemm_sweep; one line per (shape, M, variant)."""
+    in gemm_sweep (rotate_bytes of distinct weight copies, above the 256 MB
+    MALL); one line per (shape, M, variant).  With rotate_bytes = 100e6 the
+    copies stay in the MALL but not in L2, as the 0.8B model's weights do in
+    the serve load (28 layers x 4.4 MB, each touched once per iteration)."""
     import ctypes as C
     L = ia.lib()
     rng = np.random.default_rng(0)
@@ -502,7 +508,7 @@ def gemm_variants(ia, dev, Ms=(128, 256, 576, 1024), bits=2, reps=3, shapes=SHAP
     for name, K, N, pair in shapes:
         lins = [ia.make_linear(N, K, bits, rng) for _ in range(2 if pair else 1)]
         wb = sum(l.N * K * bits // 8 + l.N * (K // 128) * 4 for l in lins)
-        R = int(np.ceil(320e6 / wb))
+        R = int(np.ceil(rotate_bytes / wb))
         dls = []
         for _ in range(R):
             d = C.c_void_p()
@@ -999,7 +1005,8 @@ def main():
     if a.gemm_variants or a.gemm_variants_27b or a.gemm_decode_27b or a.gemm_decode:
         dev = ia.Device(0)
         if a.gemm_variants:
-            res = gemm_variants(ia, dev)
+            res = gemm_variants(ia, dev, Ms=tuple(int(m) for m in a.gemm_ms.split(",")),
+                                rotate_bytes=100e6 if a.gemm_mall else 320e6)
         elif a.gemm_decode:
             res = gemm_variants(ia, dev, Ms=(1, 8, 16), shapes=SHAPES_08B, reps=3)
         elif a.gemm_variants_27b:

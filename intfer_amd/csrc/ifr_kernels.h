@@ -61,7 +61,7 @@ struct QGemmArgs {
 hipError_t launch_qgemm(const DLin& w, const QGemmArgs& a, hipStream_t st);
 // One launch shape of the table (0..kQGemmVariants-1); all give identical
 // bits.  Returns hipErrorInvalidValue where a shape does not apply.
-constexpr int kQGemmVariants = 16;
+constexpr int kQGemmVariants = 21;
 hipError_t launch_qgemm_variant(const DLin& w, const QGemmArgs& a, int variant, hipStream_t st);
 
 // FP16-activation dequant GEMM (qgemm_f16.hip): out = fp16(sum_k a * w) with

@@ -436,6 +436,119 @@ __device__ __forceinline__ void qk_epilogue(const KParams& p, float* lds, const 
   }
 }
 
+// One K group's fold of a wave's WM x WN accumulators, from the fold
+// operands staged in LDS (S_l [ng][BM], Z_l [ng][BN]): the general
+// three-operation fold, or the codebook fold (FF: S_l holds Y and Z_l the
+// scale / 2); DUMP writes the true int32 T of every valid output.
+template <int BITS, int WM, int WN, int MW, bool FF, bool DUMP>
+__device__ __forceinline__ void fold_group(const KParams& p, const float* S_l, const uint32_t* Z_l,
+                                           const v4i (&T)[WM][WN], v4f (&acc)[WM][WN], int g, int wm, int wn,
+                                           int lane, int row0, int tile0, const int (&tl)[WN]) {
+  constexpr int BM = 16 * WM * MW, BN = 16 * WN * (4 / MW);
+  const int lrow = lane & 15, lgrp = lane >> 4;
+  v4f S[WM];
+#pragma unroll
+  for (int i = 0; i < WM; ++i)
+    S[i] = *reinterpret_cast<const v4f*>(&S_l[g * BM + 16 * WM * wm + 16 * i + 4 * lgrp]);
+#pragma unroll
+  for (int j = 0; j < WN; ++j) {
+    const uint32_t zw = Z_l[g * BN + 16 * (WN * wn + j) + lrow];
+    if constexpr (FF) {  // S holds Y, zw the scale / 2
+      const float h = __uint_as_float(zw);
+#pragma unroll
+      for (int i = 0; i < WM; ++i)
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+          acc[i][j][r] = fmaf(h, __int_as_float(T[i][j][r]) - S[i][r], acc[i][j][r]);
+      continue;
+    }
+    const float sc = ifrd::h2f((uint16_t)(zw & 0xFFFFu));
+    const float ze = ifrd::h2f((uint16_t)(zw >> 16));
+#pragma unroll
+    for (int i = 0; i < WM; ++i)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int32_t Tv = true_t<BITS>(T[i][j][r], S[i][r]);
+        const float d = fmaf(-ze, S[i][r], (float)Tv);
+        acc[i][j][r] = fmaf(sc, d, acc[i][j][r]);
+        if (DUMP && row0 + 16 * i + 4 * lgrp + r < p.M && tile0 + j < (p.N >> 4))
+          p.tdump[((size_t)(row0 + 16 * i + 4 * lgrp + r) * p.N + 16 * tl[j] + lrow) * p.ng + g] = Tv;
+      }
+  }
+}
+
+// The stores of one wave's WM x WN output tiles (EPI 0: plain, 1: the
+// SwiGLU pair), shared by the row-block kernels.  Every wave has read its
+// last LDS operand before any wave passes the barrier of the 16-byte path.
+template <int WM, int WN, int EPI, bool DUMP>
+__device__ __forceinline__ void store_tiles(const KParams& p, float* lds_f, const v4f (&acc)[WM][WN],
+                                            const float (&asr)[WM][4], int row0, int tile0, int wave,
+                                            int lane) {
+  const int lrow = lane & 15, lgrp = lane >> 4;
+  const int ntiles = p.N >> 4;
+  if (!DUMP && p.vst) {
+    // The wave's output tile (16 WM rows x TC columns of fp16) is staged in
+    // its own LDS slice and stored as 16-byte row chunks: the MFMA layout
+    // (a lane holds one column of 4 rows) would write each row in 32-byte
+    // pieces of 2-byte stores, which cost 2.5-4.6 us of a 9-12 us launch at
+    // M = 576..1024.  Same values as store_plain / store_swiglu.
+    // (The tiles reuse the fold operands' LDS, so the launch needs no more
+    // than the larger of the two: at the 27B-class shapes that keeps 3
+    // workgroups per CU instead of 2.  Every wave has read its last fold
+    // operand before any wave passes this barrier.)
+    constexpr int TR = 16 * WM, TC = EPI == 0 ? 16 * WN : 8 * WN, CPR = TC / 8, NCH = TR * CPR;
+    __syncthreads();
+    uint16_t* yt = reinterpret_cast<uint16_t*>(lds_f) + wave * TR * TC;
+#pragma unroll
+    for (int i = 0; i < WM; ++i)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int rl = 16 * i + 4 * lgrp + r;
+        if constexpr (EPI == 0) {
+#pragma unroll
+          for (int j = 0; j < WN; ++j) yt[rl * TC + 16 * j + lrow] = ifrd::f2h(asr[i][r] * acc[i][j][r]);
+        } else {
+#pragma unroll
+          for (int j = 0; j < WN; j += 2) {
+            const float g = ifrd::fp16r(asr[i][r] * acc[i][j][r]);
+            const float u = ifrd::fp16r(asr[i][r] * acc[i][j + 1][r]);
+            yt[rl * TC + 8 * j + lrow] = ifrd::f2h(silu_f(g) * u);
+          }
+        }
+      }
+    ifrd::wave_sync();
+    const int col0 = EPI == 0 ? 16 * tile0 : 8 * tile0;
+#pragma unroll
+    for (int q = 0; q < (NCH + 63) / 64; ++q) {
+      const int ch = lane + 64 * q;
+      if (NCH % 64 != 0 && ch >= NCH) break;
+      const int rr = ch / CPR, cc = (ch % CPR) * 8, row = row0 + rr;
+      const bool colv = EPI == 0 ? tile0 + cc / 16 < ntiles : tile0 + 2 * (cc / 16) + 1 < ntiles;
+      const uint4 v = *reinterpret_cast<const uint4*>(yt + rr * TC + cc);
+      if (row < p.M && colv) *reinterpret_cast<uint4*>(p.out + (size_t)row * p.ldo + col0 + cc) = v;
+    }
+    return;
+  }
+#pragma unroll
+  for (int i = 0; i < WM; ++i)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int row = row0 + 16 * i + 4 * lgrp + r;
+      if (row >= p.M) continue;
+      if constexpr (EPI == 0) {
+#pragma unroll
+        for (int j = 0; j < WN; ++j)
+          if (tile0 + j < ntiles) store_plain(p, row, 16 * (tile0 + j) + lrow, asr[i][r], acc[i][j][r]);
+      } else {
+#pragma unroll
+        for (int j = 0; j < WN; j += 2)
+          if (tile0 + j + 1 < ntiles)
+            store_swiglu(p, row, 16 * ((tile0 + j) >> 1) + lrow, asr[i][r], acc[i][j][r],
+                         acc[i][j + 1][r]);
+      }
+    }
+}
+
 // ---- larger M: a workgroup computes a BM x BN block, its 4 waves arranged
 // MW x (4/MW); each wave owns WM x WN 16x16 tiles and folds its own
 // accumulators group by group while the next R groups are in flight.  The
@@ -550,67 +663,97 @@ __global__ __launch_bounds__(256) void qgemm_rows(KParams p) {
     qk_epilogue<BM, BN, WM, WN, MW>(p, lds_f, acc, asr, bm0, bt0, wave, lane);
     return;
   }
-  if (!DUMP && p.vst) {
-    // The wave's output tile (16 WM rows x TC columns of fp16) is staged in
-    // its own LDS slice and stored as 16-byte row chunks: the MFMA layout
-    // (a lane holds one column of 4 rows) would write each row in 32-byte
-    // pieces of 2-byte stores, which cost 2.5-4.6 us of a 9-12 us launch at
-    // M = 576..1024.  Same values as store_plain / store_swiglu.
-    // (The tiles reuse the fold operands' LDS, so the launch needs no more
-    // than the larger of the two: at the 27B-class shapes that keeps 3
-    // workgroups per CU instead of 2.  Every wave has read its last fold
-    // operand before any wave passes this barrier.)
-    constexpr int TR = 16 * WM, TC = EPI == 0 ? 16 * WN : 8 * WN, CPR = TC / 8, NCH = TR * CPR;
-    __syncthreads();
-    uint16_t* yt = reinterpret_cast<uint16_t*>(lds_f) + wave * TR * TC;
+  store_tiles<WM, WN, EPI, DUMP>(p, lds_f, acc, asr, row0, tile0, wave, lane);
+}
+
+// ---- mid M (the mixed-iteration shapes, K up to a few thousand): every
+// memory access of the K loop is issued at kernel entry, so a wave waits for
+// memory once instead of once per R groups.  The workgroup's A rows for the
+// whole K (BM x K bytes) go to LDS by the LDS DMA (global_load_lds_dwordx4:
+// one contiguous 1 KB A tile per wave instruction, no VGPRs; the waves of a
+// row block share it instead of each loading the same fragments), each
+// wave's B codes for all NG = ng groups go to registers, and the fold
+// operands are staged as in qgemm_rows.  After one wait and one barrier the
+// K loop reads A from LDS, runs the MFMAs and folds group by group in
+// ascending order, so the bits are those of every other launch shape.
+template <int BITS, int WM, int WN, int MW, int NG, int EPI, int MODE>
+__global__ __launch_bounds__(256) void qgemm_full(KParams p) {
+  constexpr bool DUMP = MODE == 1, FF = MODE == 2;
+  constexpr int NW = 4 / MW;
+  constexpr int BM = 16 * WM * MW, BN = 16 * WN * NW, NS = 2 * NG;
+  constexpr int NCHUNK = (BM / 16) * NS;  // 1 KB A tiles of the block
+  static_assert(NCHUNK % 4 == 0, "the waves share the A copies evenly");
+  extern __shared__ v4f lds_f4[];
+  float* const lds_f = reinterpret_cast<float*>(lds_f4);
+  int8_t* const A_l = reinterpret_cast<int8_t*>(lds_f4);  // [BM / 16][NS][1 KB]
+  float* const S_l = reinterpret_cast<float*>(A_l + NCHUNK * 1024);
+  uint32_t* const Z_l = reinterpret_cast<uint32_t*>(S_l + NG * BM);
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int lgrp = lane >> 4;
+  const int ntiles = p.N >> 4;
+  const int bm0 = blockIdx.y * BM, bt0 = blockIdx.x * (BN / 16);
+  const int wm = wave % MW, wn = wave / MW;
+  const int row0 = bm0 + 16 * WM * wm, tile0 = bt0 + WN * wn;
+
+  // A: chunk c = rt * NS + s is row tile rt's K step s (row tiles past the
+  // last one read the last, whose outputs are never stored)
+  const int last_rt = (p.M - 1) >> 4;
 #pragma unroll
-    for (int i = 0; i < WM; ++i)
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int rl = 16 * i + 4 * lgrp + r;
-        if constexpr (EPI == 0) {
-#pragma unroll
-          for (int j = 0; j < WN; ++j) yt[rl * TC + 16 * j + lrow] = ifrd::f2h(asr[i][r] * acc[i][j][r]);
-        } else {
-#pragma unroll
-          for (int j = 0; j < WN; j += 2) {
-            const float g = ifrd::fp16r(asr[i][r] * acc[i][j][r]);
-            const float u = ifrd::fp16r(asr[i][r] * acc[i][j + 1][r]);
-            yt[rl * TC + 8 * j + lrow] = ifrd::f2h(silu_f(g) * u);
-          }
-        }
-      }
-    ifrd::wave_sync();
-    const int col0 = EPI == 0 ? 16 * tile0 : 8 * tile0;
-#pragma unroll
-    for (int q = 0; q < (NCH + 63) / 64; ++q) {
-      const int ch = lane + 64 * q;
-      if (NCH % 64 != 0 && ch >= NCH) break;
-      const int rr = ch / CPR, cc = (ch % CPR) * 8, row = row0 + rr;
-      const bool colv = EPI == 0 ? tile0 + cc / 16 < ntiles : tile0 + 2 * (cc / 16) + 1 < ntiles;
-      const uint4 v = *reinterpret_cast<const uint4*>(yt + rr * TC + cc);
-      if (row < p.M && colv) *reinterpret_cast<uint4*>(p.out + (size_t)row * p.ldo + col0 + cc) = v;
-    }
-    return;
+  for (int q = 0; q < NCHUNK / 4; ++q) {
+    const int c = wave + 4 * q, rt = c / NS, s = c - rt * NS;
+    const int8_t* src = p.a + ((size_t)min((bm0 >> 4) + rt, last_rt) * NS + s) * 1024 + 16 * lane;
+    __builtin_amdgcn_global_load_lds(src, A_l + c * 1024, 16, 0, 0);
   }
+  int tl[WN];
+#pragma unroll
+  for (int j = 0; j < WN; ++j) tl[j] = min(tile0 + j, ntiles - 1);
+  uint32_t Bw[NG][2][WN][BITS / 2];
+#pragma unroll
+  for (int g = 0; g < NG; ++g)
+#pragma unroll
+    for (int h = 0; h < 2; ++h)
+#pragma unroll
+      for (int j = 0; j < WN; ++j)
+        load_raw<BITS>(p.codes + ((size_t)tl[j] * NS + 2 * g + h) * 64 * (BITS / 2), lane, Bw[g][h][j]);
+  stage_fold_operands<BM, BN, 12, BITS, FF>(p, bm0, bt0, S_l, Z_l);
+  float asr[WM][4];
 #pragma unroll
   for (int i = 0; i < WM; ++i)
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int row = row0 + 16 * i + 4 * lgrp + r;
-      if (row >= p.M) continue;
-      if constexpr (EPI == 0) {
+    for (int r = 0; r < 4; ++r) asr[i][r] = p.as[min(row0 + 16 * i + 4 * lgrp + r, p.M - 1)] * p.post;
+  // the LDS copies are counted by vmcnt: every wave's must land before any
+  // wave reads A
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+
+  v4i T[WM][WN];
+  v4f acc[WM][WN];
 #pragma unroll
-        for (int j = 0; j < WN; ++j)
-          if (tile0 + j < ntiles) store_plain(p, row, 16 * (tile0 + j) + lrow, asr[i][r], acc[i][j][r]);
-      } else {
+  for (int i = 0; i < WM; ++i)
 #pragma unroll
-        for (int j = 0; j < WN; j += 2)
-          if (tile0 + j + 1 < ntiles)
-            store_swiglu(p, row, 16 * ((tile0 + j) >> 1) + lrow, asr[i][r], acc[i][j][r],
-                         acc[i][j + 1][r]);
-      }
+    for (int j = 0; j < WN; ++j) acc[i][j] = (v4f){0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int g = 0; g < NG; ++g) {
+    GroupOps<BITS, WM, WN> ops;
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+#pragma unroll
+      for (int i = 0; i < WM; ++i)
+        ops.A[h][i] = *reinterpret_cast<const v4i*>(A_l + ((wm * WM + i) * NS + 2 * g + h) * 1024 + 16 * lane);
+#pragma unroll
+      for (int j = 0; j < WN; ++j)
+#pragma unroll
+        for (int q = 0; q < BITS / 2; ++q) ops.B[h][j][q] = Bw[g][h][j][q];
     }
+    mma_group<BITS, WM, WN, FF>(ops, T);
+    fold_group<BITS, WM, WN, MW, FF, DUMP>(p, S_l, Z_l, T, acc, g, wm, wn, lane, row0, tile0, tl);
+  }
+  if constexpr (EPI == 2) {
+    qk_epilogue<BM, BN, WM, WN, MW>(p, lds_f, acc, asr, bm0, bt0, wave, lane);
+    return;
+  }
+  store_tiles<WM, WN, EPI, DUMP>(p, lds_f, acc, asr, row0, tile0, wave, lane);
 }
 
 // ---- small M (decode, weight-stream bound): the 4 waves split the K groups
@@ -1028,6 +1171,67 @@ hipError_t launch_stream_ng(const KParams& p, hipStream_t st) {
   return hipErrorInvalidValue;
 }
 
+// qgemm_full: NG = ng is a template constant (the 0.8B-class depths 8, 16
+// and 24 groups), and every wave's B codes for the whole K must fit 64 VGPRs
+// (more spill, and make the compiler's AGPR-copy rewrite fail).
+template <int BITS, int WM, int WN, int MW, int NG, int EPI>
+hipError_t launch_full_ng(const KParams& p, hipStream_t st) {
+  constexpr int NW = 4 / MW;
+  constexpr int BM = 16 * WM * MW, BN = 16 * WN * NW;
+  if constexpr (NG * 2 * WN * (BITS / 2) > 64) {
+    return hipErrorInvalidValue;
+  } else {
+    size_t lds = (size_t)BM * NG * 128 + (size_t)NG * (BM + BN) * sizeof(float);
+    if constexpr (EPI == 2) {
+      if (BM != 32 || BN != 128 || p.qa.rotary != 128 || p.kv.hd != 128) return hipErrorInvalidValue;
+      lds = std::max(lds, (size_t)(BM * (BN + 4) + BM * 8) * sizeof(float));
+    } else {
+      lds = std::max(lds, (size_t)4 * 16 * WM * (EPI == 0 ? 16 * WN : 8 * WN) * sizeof(uint16_t));
+    }
+    if (lds > 160 * 1024) return hipErrorInvalidValue;
+    constexpr bool kFF = BITS != 8;
+    static bool attr_set = false;
+    if (!attr_set) {
+      hipError_t e = set_lds_limit(qgemm_full<BITS, WM, WN, MW, NG, EPI, 0>);
+      if constexpr (EPI == 0)
+        if (e == hipSuccess) e = set_lds_limit(qgemm_full<BITS, WM, WN, MW, NG, EPI, 1>);
+      if constexpr (kFF)
+        if (e == hipSuccess) e = set_lds_limit(qgemm_full<BITS, WM, WN, MW, NG, EPI, 2>);
+      if (e != hipSuccess) return e;
+      attr_set = true;
+    }
+    KParams q = p;
+    q.vst = EPI != 2 && !p.tdump && reinterpret_cast<uintptr_t>(p.out) % 16 == 0 && p.ldo % 8 == 0;
+    const dim3 grid((p.N / 16 + BN / 16 - 1) / (BN / 16), (p.M + BM - 1) / BM);
+    if constexpr (EPI == 0)
+      if (p.tdump) {
+        hipLaunchKernelGGL((qgemm_full<BITS, WM, WN, MW, NG, EPI, 1>), grid, dim3(256), lds, st, q);
+        return hipGetLastError();
+      }
+    if constexpr (kFF)
+      if (p.ff) {
+        hipLaunchKernelGGL((qgemm_full<BITS, WM, WN, MW, NG, EPI, 2>), grid, dim3(256), lds, st, q);
+        return hipGetLastError();
+      }
+    hipLaunchKernelGGL((qgemm_full<BITS, WM, WN, MW, NG, EPI, 0>), grid, dim3(256), lds, st, q);
+    return hipGetLastError();
+  }
+}
+
+template <int BITS, int WM, int WN, int MW, int EPI>
+hipError_t launch_full(const KParams& p, hipStream_t st) {
+  if constexpr (BITS == 8) {
+    return hipErrorInvalidValue;  // the codes of the whole K do not fit registers
+  } else {
+    switch (p.ng) {
+      case 8: return launch_full_ng<BITS, WM, WN, MW, 8, EPI>(p, st);
+      case 16: return launch_full_ng<BITS, WM, WN, MW, 16, EPI>(p, st);
+      case 24: return launch_full_ng<BITS, WM, WN, MW, 24, EPI>(p, st);
+      default: return hipErrorInvalidValue;
+    }
+  }
+}
+
 // R (K groups in flight per wave) is the largest power of two <= RMAX that
 // divides ng.
 template <int BITS, int WM, int WN, int MW, int RMAX, int EPI>
@@ -1054,11 +1258,14 @@ hipError_t launch_bits_qk(const KParams& p, int variant, hipStream_t st) {
     variant = (ng <= 24 && p.M <= 128) ? 0 : 5;
     if (p.K >= 4096 && p.M > 256 && (ng >= 96 || p.M >= 1024 || p.N >= 6144)) variant = -1;
     if (p.K >= 4096 && p.M <= 16) variant = -1;
+    // (the whole-K 32 x 128 block, variant 17, holds the epilogue at 234
+    // VGPRs against 126 here: slower in the serve load, 12.7 -> 13.4 us)
   }
   switch (variant) {
     case 4: return launch_rows_r<BITS, 2, 2, 1, 4, 2>(p, st);
     case 5: return launch_rows_r<BITS, 2, 2, 1, 2, 2>(p, st);
     case 12: return launch_rows_r<BITS, 2, 2, 1, 8, 2>(p, st);
+    case 17: return launch_full<BITS, 2, 2, 1, 2>(p, st);
     default: return hipErrorInvalidValue;
   }
 }
@@ -1082,6 +1289,27 @@ hipError_t launch_bits(const KParams& p, int variant, hipStream_t st) {
     if (p.K >= 4096 && p.M > 256) {
       if (p.ng >= 96) variant = 3;
       else if (p.M >= 1024 || p.N >= 6144) variant = 6;
+    }
+    // The mixed-iteration shapes (K of 8, 16 or 24 groups, 128 < M <= 1024;
+    // bench.py --gemm-variants --gemm-mall, weights MALL-resident as in the
+    // serve load): the whole-K blocks with A in LDS, 16 x 128 up to M = 384
+    // and 32 x 128 above for the wide projections, 16 x 64 for O up to
+    // M = 768 and 32 x 64 above, 16 x 64 for down up to M = 384 (deeper
+    // than that, 64 x 64 blocks of qgemm_rows).  A shape the whole-K kernel
+    // cannot hold (wider codes) keeps the choice above.
+    if ((p.ng == 8 || p.ng == 16 || p.ng == 24) && p.M > 128 && p.M <= 1024) {
+      int fv = -1;
+      if (p.ng == 24) {
+        if (narrow) fv = p.M <= 384 ? 16 : 3;
+      } else if (p.ng == 16 && narrow) {
+        fv = p.M <= 768 ? 16 : 19;
+      } else {
+        fv = p.M <= 384 ? 18 : 17;
+      }
+      if (fv >= 0) {
+        const hipError_t e = launch_bits<BITS, EPI>(p, fv, st);
+        if (e != hipErrorInvalidValue) return e;
+      }
     }
     // Decode rows on those shapes (bench.py --gemm-decode-27b, M = 1, 8, 16):
     // the weight stream, two tiles per workgroup for the plain projections
@@ -1118,6 +1346,12 @@ hipError_t launch_bits(const KParams& p, int variant, hipStream_t st) {
     case 13: return launch_stream_ng<BITS, WNs, 16, EPI>(p, st);  // decode stream, 16 waves
     case 14: return launch_stream_ng<BITS, WNs, 8, EPI>(p, st);   // decode stream, 8 waves
     case 15: return launch_stream_ng<BITS, 2 * WNs, 16, EPI>(p, st);  // 2 tiles, 16 waves
+    // A in LDS and every load issued at entry (K of 8, 16 or 24 groups)
+    case 16: return launch_full<BITS, 1, WNs, 1, EPI>(p, st);         // 16 x 64 block
+    case 17: return launch_full<BITS, 2, 2, 1, EPI>(p, st);           // 32 x 128 block
+    case 18: return launch_full<BITS, 1, 2, 1, EPI>(p, st);           // 16 x 128 block
+    case 19: return launch_full<BITS, 2, WNs, 1, EPI>(p, st);         // 32 x 64 block
+    case 20: return launch_full<BITS, 1, WNs, 2, EPI>(p, st);         // 32 x 32 block
     default: return hipErrorInvalidValue;
   }
 }

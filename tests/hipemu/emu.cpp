@@ -343,6 +343,16 @@ int launch_raw(KernelBody body, void* args, dim3 g, dim3 b, size_t shmem) {
 
 // ---- builtins ------------------------------------------------------------------------
 
+void emu_global_load_lds(const void* g, void* l, unsigned size, int offset, int aux) {
+  if (offset != 0 || aux != 0 || (size != 1 && size != 2 && size != 4 && size != 12 && size != 16))
+    emu::fail("global_load_lds: offset, aux or size not emulated");
+  const uint64_t live = emu::live_mask_of_current_wave();
+  const unsigned char* s = emu::wave_exchange(&l, sizeof(void*), emu::kOpFirst);
+  for (int k = 0; k < 64; ++k)
+    if (((live >> k) & 1) && emu::lane_value<void*>(s, k) != l) emu::fail("global_load_lds: LDS address not wave-uniform");
+  std::memcpy(static_cast<unsigned char*>(l) + (size_t)emu::cur()->lane * size, g, size);
+}
+
 int emu_readfirstlane(int v) {
   const uint64_t live = emu::live_mask_of_current_wave();
   const unsigned char* s = emu::wave_exchange(&v, 4, emu::kOpFirst);

@@ -221,6 +221,13 @@ inline unsigned emu_perm(unsigned s0, unsigned s1, unsigned sel) {
 #define __builtin_amdgcn_wave_barrier() ::emu::wave_barrier()
 #define __builtin_amdgcn_fence(...) ((void)0)
 #define __builtin_amdgcn_s_barrier() __syncthreads()
+// LDS DMA (global_load_lds_dword*): lane l's `size` bytes from its own
+// global address land at the wave-uniform LDS address + l * size (checked
+// uniform); the immediate offset is not used by the library.  The wait for
+// the copies (s_waitcnt) is a no-op: the copy is complete on return.
+void emu_global_load_lds(const void* g, void* l, unsigned size, int offset, int aux);
+#define __builtin_amdgcn_global_load_lds(...) emu_global_load_lds(__VA_ARGS__)
+#define __builtin_amdgcn_s_waitcnt(x) ((void)(x))
 // plain loads on the host (x86 non-temporal vector loads demand alignment)
 #define __builtin_nontemporal_load(p) (*(p))
 

@@ -102,7 +102,16 @@ def gemm_stream():
     _gemm_shapes((2, 4), ((32, 5120), (16, 17408)), Ms=(1, 5, 16), pair_check=True)
 
 
-def _gemm_shapes(bits_list, shapes, Ms=(1, 17, 70), pair_check=False):
+@scenario
+def gemm_full():
+    """The whole-K row-block shapes (A in LDS by the LDS DMA, every load at
+    entry) at K of 8, 16 and 24 groups, ragged M across 16- and 32-row
+    blocks, INT2 and INT4, plain and SwiGLU pair."""
+    _gemm_shapes((2, 4), ((64, 1024), (128, 2048), (64, 3072)), Ms=(1, 17, 40, 70), pair_check=True,
+                 variants=range(16, 21))
+
+
+def _gemm_shapes(bits_list, shapes, Ms=(1, 17, 70), pair_check=False, variants=None):
     import intfer_amd as ia
     from oracle import pyoracle as po
     L = ia.lib()
@@ -128,11 +137,13 @@ def _gemm_shapes(bits_list, shapes, Ms=(1, 17, 70), pair_check=False):
                 od = dev.alloc(M * N * 2)
                 ref = po.qgemm(q, sc[:, 0], lin)
                 pair_ref = None
-                for v in range(nv):
+                ran = 0
+                for v in (range(nv) if variants is None else variants):
                     rc = L.ifr_quant_gemm_variant(dev.ctx, dl, qd.p, sd.p, gd.p, M, od.p, v)
                     if rc == ia.IFR_EDECLINE:
                         continue
                     ia.check(rc, f"variant {v}")
+                    ran += 1
                     out = dev.download(od, np.uint16, (M, N))
                     assert np.array_equal(out, ref), f"bits {bits} N {N} K {K} M {M} variant {v} {zmode}"
                     rc = L.ifr_quant_gemm_variant(dev.ctx, dp, qd.p, sd.p, gd.p, M, od.p, v)
@@ -145,7 +156,9 @@ def _gemm_shapes(bits_list, shapes, Ms=(1, 17, 70), pair_check=False):
                             assert np.array_equal(po_, pair_ref), f"pair variant {v} N {N} K {K} M {M}"
                 for b in (qd, sd, gd, od):
                     b.free()
-                say(f"gemm bits={bits} N={N} K={K} M={M} zeros={zmode} ok")
+                # (a restricted variant list may hold no shape for wide codes)
+                assert ran > 0 or variants is not None, f"no launch shape ran: bits {bits} N {N} K {K} M {M}"
+                say(f"gemm bits={bits} N={N} K={K} M={M} zeros={zmode} ok ({ran} shapes)")
             L.ifr_linear_free(dev.ctx, dl)
             L.ifr_linear_free(dev.ctx, dp)
     dev.close()
