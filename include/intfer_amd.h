@@ -418,9 +418,10 @@ int ifr_attention(ifr_ctx* ctx, int32_t layer, const ifr_row* rows, int32_t M,
  * 8192, and at most 4096 attention units (one per q-block of 16 / GQA-group
  * tokens, kv head and 256-token KV split); beyond them it returns IFR_EINVAL
  * with a message and does nothing.  Results are bit-identical to
- * ifr_attention's.  Every call on one GPU shares that array: calls that
- * overlap on one GPU (other threads or contexts) race.  Returns after out_d
- * is written. */
+ * ifr_attention's.  Every call on one GPU shares that array, so calls on one
+ * GPU from other threads or contexts of the process wait for each other (a
+ * per-device lock held from the first launch until out_d is written); each
+ * process has its own array.  Returns after out_d is written. */
 int ifr_attention_noalloc(ifr_ctx* ctx, int32_t layer, const ifr_row* rows, int32_t M,
                           const uint16_t* q_d, float* out_d);
 

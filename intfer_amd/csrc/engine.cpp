@@ -14,6 +14,7 @@
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
+#include <mutex>
 #include <string>
 #include <vector>
 
@@ -142,6 +143,11 @@ struct Lane {
 // process ends.  Host code uses the address hipGetSymbolAddress gives for the
 // current device (ifr_ctx::scratch), never this name.
 static __device__ __align__(256) uint8_t scratch[kNaScratchBytes];
+// Calls of ifr_attention_noalloc on one GPU share that GPU's array; each call
+// holds its device's lock from its first launch until its results are back,
+// so calls from different threads or contexts run one after the other.
+constexpr int kNaLockDevices = 64;
+std::mutex g_na_lock[kNaLockDevices];
 
 struct ifr_dlinear {
   DLin d;
@@ -1577,6 +1583,7 @@ int ifr_attention_noalloc(ifr_ctx* c, int32_t layer, const ifr_row* rows, int32_
   if (nunits > kNaUnits || nslots > 4L * kNaUnits)
     return fail(IFR_EINVAL, "%ld attention units (%ld slots) > %d (no-allocation limit)", nunits, nslots, kNaUnits);
   HIPCHK(hipSetDevice(c->device));
+  std::lock_guard<std::mutex> hold(g_na_lock[c->device % kNaLockDevices]);
   uint8_t* S = c->scratch;
   int32_t* rows_d = reinterpret_cast<int32_t*>(S + kNaRowsOff);
   auto map = [&](int i) { return reinterpret_cast<int32_t*>(S + kNaMapsOff + (size_t)i * kNaMapLen); };

@@ -94,3 +94,54 @@ def test_noalloc_refuses_more_units_than_its_scratch(dev):
         del eng
     finally:
         model.close()
+
+
+def test_noalloc_calls_from_two_contexts_wait_for_each_other():
+    """Two contexts on the one GPU, each with its own engine, call
+    ifr_attention_noalloc from two threads at once, 12 times each with
+    different batches: every result equals its own context's ifr_attention,
+    bit for bit (the calls share the GPU's scratch array and are serialized
+    by the library's per-device lock)."""
+    import threading
+    cfg = ia.default_cfg(layers=1, vocab=1024)
+    model = ia.SynthModel(cfg, seed=9)
+    devs = [ia.Device(0), ia.Device(0)]
+    try:
+        jobs = []
+        for di, d in enumerate(devs):
+            rng = np.random.default_rng(500 + di)
+            eng = ia.Engine(d, model, max_seqs=8, max_seq_tokens=2048, pool_tokens=8 * 2048, max_rows=512)
+            seqs = []
+            for n in (300 + 200 * di, 900, 1500 - 100 * di, 700):
+                s = eng.seq_open()
+                k = rng.standard_normal((1, n, cfg.n_kv, cfg.head_dim), dtype=np.float32)
+                v = rng.standard_normal((1, n, cfg.n_kv, cfg.head_dim), dtype=np.float32)
+                eng.load_kv(s, k, v)
+                seqs.append((s, n))
+            cases = []
+            for it in range(12):
+                rows = [(s, n - 1 - it, 0, 0, 1) for s, n in seqs[:3]]
+                rows += [(seqs[3][0], 500 + p, 0, 1, 1) for p in range(40 + 10 * it)]
+                q = rng.standard_normal((len(rows), cfg.n_heads, cfg.head_dim), dtype=np.float32).astype(np.float16)
+                cases.append((rows, q, eng.attention(0, rows, q)))
+            jobs.append((d, eng, cases))
+        errors = []
+
+        def run(d, eng, cases):
+            for i, (rows, q, ref) in enumerate(cases):
+                rc, got = _noalloc(d, eng, rows, q)
+                if rc != ia.IFR_OK or not np.array_equal(got.view(np.uint32), ref.view(np.uint32)):
+                    errors.append((d, i, rc))
+
+        announce("no-alloc attention: two contexts, two threads, 12 calls each")
+        th = [threading.Thread(target=run, args=j) for j in jobs]
+        for t in th:
+            t.start()
+        for t in th:
+            t.join()
+        assert not errors, errors
+        del jobs
+    finally:
+        for d in devs:
+            d.close()
+        model.close()
