@@ -436,15 +436,16 @@ __device__ __forceinline__ void qk_epilogue(const KParams& p, float* lds, const 
   }
 }
 
-// One K group's fold of a wave's WM x WN accumulators, from the fold
-// operands staged in LDS (S_l [ng][BM], Z_l [ng][BN]): the general
-// three-operation fold, or the codebook fold (FF: S_l holds Y and Z_l the
-// scale / 2); DUMP writes the true int32 T of every valid output.
+// One K group's fold of a wave's WM x WN accumulators: S from the fold
+// operand staged in LDS (S_l [ng][BM]), the packed fp16 scale | zero << 16
+// of the lane's column of tile j in zr[j]: the general three-operation fold,
+// or the codebook fold (FF: S_l holds Y, the scale is halved here); DUMP
+// writes the true int32 T of every valid output.
 template <int BITS, int WM, int WN, int MW, bool FF, bool DUMP>
-__device__ __forceinline__ void fold_group(const KParams& p, const float* S_l, const uint32_t* Z_l,
+__device__ __forceinline__ void fold_group(const KParams& p, const float* S_l, const uint32_t (&zr)[WN],
                                            const v4i (&T)[WM][WN], v4f (&acc)[WM][WN], int g, int wm, int wn,
                                            int lane, int row0, int tile0, const int (&tl)[WN]) {
-  constexpr int BM = 16 * WM * MW, BN = 16 * WN * (4 / MW);
+  constexpr int BM = 16 * WM * MW;
   const int lrow = lane & 15, lgrp = lane >> 4;
   v4f S[WM];
 #pragma unroll
@@ -452,9 +453,9 @@ __device__ __forceinline__ void fold_group(const KParams& p, const float* S_l, c
     S[i] = *reinterpret_cast<const v4f*>(&S_l[g * BM + 16 * WM * wm + 16 * i + 4 * lgrp]);
 #pragma unroll
   for (int j = 0; j < WN; ++j) {
-    const uint32_t zw = Z_l[g * BN + 16 * (WN * wn + j) + lrow];
-    if constexpr (FF) {  // S holds Y, zw the scale / 2
-      const float h = __uint_as_float(zw);
+    const uint32_t zw = zr[j];
+    if constexpr (FF) {  // S holds Y; h = scale / 2 (exact)
+      const float h = 0.5f * ifrd::h2f((uint16_t)(zw & 0xFFFFu));
 #pragma unroll
       for (int i = 0; i < WM; ++i)
 #pragma unroll
@@ -675,7 +676,10 @@ __global__ __launch_bounds__(256) void qgemm_rows(KParams p) {
 // wave's B codes for all NG = ng groups go to registers, and the fold
 // operands are staged as in qgemm_rows.  After one wait and one barrier the
 // K loop reads A from LDS, runs the MFMAs and folds group by group in
-// ascending order, so the bits are those of every other launch shape.
+// ascending order, so the bits are those of every other launch shape.  The
+// scale | zero pairs of the wave's own columns are loaded into registers
+// with the codes (NG x WN of them) instead of LDS, which keeps the 16-row
+// block of the 24-group down projection at 3 workgroups per CU.
 template <int BITS, int WM, int WN, int MW, int NG, int EPI, int MODE>
 __global__ __launch_bounds__(256) void qgemm_full(KParams p) {
   constexpr bool DUMP = MODE == 1, FF = MODE == 2;
@@ -686,11 +690,10 @@ __global__ __launch_bounds__(256) void qgemm_full(KParams p) {
   extern __shared__ v4f lds_f4[];
   float* const lds_f = reinterpret_cast<float*>(lds_f4);
   int8_t* const A_l = reinterpret_cast<int8_t*>(lds_f4);  // [BM / 16][NS][1 KB]
-  float* const S_l = reinterpret_cast<float*>(A_l + NCHUNK * 1024);
-  uint32_t* const Z_l = reinterpret_cast<uint32_t*>(S_l + NG * BM);
+  float* const S_l = reinterpret_cast<float*>(A_l + NCHUNK * 1024);  // [NG][BM]
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int lgrp = lane >> 4;
+  const int lrow = lane & 15, lgrp = lane >> 4;
   const int ntiles = p.N >> 4;
   const int bm0 = blockIdx.y * BM, bt0 = blockIdx.x * (BN / 16);
   const int wm = wave % MW, wn = wave / MW;
@@ -716,7 +719,28 @@ __global__ __launch_bounds__(256) void qgemm_full(KParams p) {
 #pragma unroll
       for (int j = 0; j < WN; ++j)
         load_raw<BITS>(p.codes + ((size_t)tl[j] * NS + 2 * g + h) * 64 * (BITS / 2), lane, Bw[g][h][j]);
-  stage_fold_operands<BM, BN, 12, BITS, FF>(p, bm0, bt0, S_l, Z_l);
+  uint32_t zr[NG][WN];
+#pragma unroll
+  for (int g = 0; g < NG; ++g)
+#pragma unroll
+    for (int j = 0; j < WN; ++j) zr[g][j] = p.sz[((size_t)tl[j] * NG + g) * 16 + lrow];
+  {
+    // S (FF: Y = 1.5 * 2^23 + C * S) of the block's rows, [NG][BM]; rows
+    // past M read row M - 1 (their outputs are never stored)
+    constexpr float C = (float)((1 << BITS) - 1);
+    constexpr int NQ = (NG * BM + 255) / 256;
+    float sv[NQ];
+#pragma unroll
+    for (int q = 0; q < NQ; ++q) {
+      const int t = threadIdx.x + 256 * q;
+      if (t < NG * BM) sv[q] = p.gs[(size_t)min(bm0 + t % BM, p.M - 1) * NG + t / BM];
+    }
+#pragma unroll
+    for (int q = 0; q < NQ; ++q) {
+      const int t = threadIdx.x + 256 * q;
+      if (t < NG * BM) S_l[t] = FF ? kFoldBiasF + C * sv[q] : sv[q];
+    }
+  }
   float asr[WM][4];
 #pragma unroll
   for (int i = 0; i < WM; ++i)
@@ -747,7 +771,7 @@ __global__ __launch_bounds__(256) void qgemm_full(KParams p) {
         for (int q = 0; q < BITS / 2; ++q) ops.B[h][j][q] = Bw[g][h][j][q];
     }
     mma_group<BITS, WM, WN, FF>(ops, T);
-    fold_group<BITS, WM, WN, MW, FF, DUMP>(p, S_l, Z_l, T, acc, g, wm, wn, lane, row0, tile0, tl);
+    fold_group<BITS, WM, WN, MW, FF, DUMP>(p, S_l, zr[g], T, acc, g, wm, wn, lane, row0, tile0, tl);
   }
   if constexpr (EPI == 2) {
     qk_epilogue<BM, BN, WM, WN, MW>(p, lds_f, acc, asr, bm0, bt0, wave, lane);
@@ -1173,7 +1197,10 @@ hipError_t launch_stream_ng(const KParams& p, hipStream_t st) {
 
 // qgemm_full: NG = ng is a template constant (the 0.8B-class depths 8, 16
 // and 24 groups), and every wave's B codes for the whole K must fit 64 VGPRs
-// (more spill, and make the compiler's AGPR-copy rewrite fail).
+// (more spill, and make the compiler's AGPR-copy rewrite fail).  LDS: the A
+// rows of the whole K and S, 49.5 KB for the 16-row block at 24 groups (3
+// workgroups per CU: the 576 blocks of a 576-row down projection in one
+// round).
 template <int BITS, int WM, int WN, int MW, int NG, int EPI>
 hipError_t launch_full_ng(const KParams& p, hipStream_t st) {
   constexpr int NW = 4 / MW;
@@ -1181,7 +1208,7 @@ hipError_t launch_full_ng(const KParams& p, hipStream_t st) {
   if constexpr (NG * 2 * WN * (BITS / 2) > 64) {
     return hipErrorInvalidValue;
   } else {
-    size_t lds = (size_t)BM * NG * 128 + (size_t)NG * (BM + BN) * sizeof(float);
+    size_t lds = (size_t)BM * NG * 128 + (size_t)NG * BM * sizeof(float);
     if constexpr (EPI == 2) {
       if (BM != 32 || BN != 128 || p.qa.rotary != 128 || p.kv.hd != 128) return hipErrorInvalidValue;
       lds = std::max(lds, (size_t)(BM * (BN + 4) + BM * 8) * sizeof(float));
@@ -1294,13 +1321,14 @@ hipError_t launch_bits(const KParams& p, int variant, hipStream_t st) {
     // bench.py --gemm-variants --gemm-mall, weights MALL-resident as in the
     // serve load): the whole-K blocks with A in LDS, 16 x 128 up to M = 384
     // and 32 x 128 above for the wide projections, 16 x 64 for O up to
-    // M = 768 and 32 x 64 above, 16 x 64 for down up to M = 384 (deeper
-    // than that, 64 x 64 blocks of qgemm_rows).  A shape the whole-K kernel
-    // cannot hold (wider codes) keeps the choice above.
+    // M = 768 and 32 x 64 above, 16 x 64 for down up to M = 768 (its blocks
+    // then fit one round at 3 per CU; deeper than that, 64 x 64 blocks of
+    // qgemm_rows).  A shape the whole-K kernel cannot hold (wider codes)
+    // keeps the choice above.
     if ((p.ng == 8 || p.ng == 16 || p.ng == 24) && p.M > 128 && p.M <= 1024) {
       int fv = -1;
       if (p.ng == 24) {
-        if (narrow) fv = p.M <= 384 ? 16 : 3;
+        if (narrow) fv = p.M <= 768 ? 16 : 3;
       } else if (p.ng == 16 && narrow) {
         fv = p.M <= 768 ? 16 : 19;
       } else {
