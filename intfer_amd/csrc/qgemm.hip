@@ -1311,10 +1311,10 @@ hipError_t launch_bits(const KParams& p, int variant, hipStream_t st) {
     else variant = narrow ? 4 : 5;
     // The 27B-class shapes (K >= 4096; bench.py --gemm-variants-27b, M = 512
     // and 2160): the 136-group down projection keeps its A and B tiles
-    // resident best in 64 x 64 blocks; the others gain from 32 x 256 once M
-    // or N is large.
+    // resident best in 64 x 64 blocks, 128 x 64 from M = 1024 (M = 2160:
+    // 465 -> 449 us); the others gain from 32 x 256 once M or N is large.
     if (p.K >= 4096 && p.M > 256) {
-      if (p.ng >= 96) variant = 3;
+      if (p.ng >= 96) variant = p.M >= 1024 ? 9 : 3;
       else if (p.M >= 1024 || p.N >= 6144) variant = 6;
     }
     // The mixed-iteration shapes (K of 8, 16 or 24 groups, 128 < M <= 1024;
