@@ -479,8 +479,11 @@ __device__ __forceinline__ void fold_group(const KParams& p, const float* S_l, c
 }
 
 // The stores of one wave's WM x WN output tiles (EPI 0: plain, 1: the
-// SwiGLU pair), shared by the row-block kernels.  Every wave has read its
-// last LDS operand before any wave passes the barrier of the 16-byte path.
+// SwiGLU pair) of the whole-K kernel: the same code qgemm_rows has inline
+// (called from there, the function raised the 27B gate/up launch from 168
+// to 170 VGPRs, 3 -> 2 waves per SIMD, 45.3 -> 48.1 ms per cfg5 iteration).
+// Every wave has read its last LDS operand before any wave passes the
+// barrier of the 16-byte path.
 template <int WM, int WN, int EPI, bool DUMP>
 __device__ __forceinline__ void store_tiles(const KParams& p, float* lds_f, const v4f (&acc)[WM][WN],
                                             const float (&asr)[WM][4], int row0, int tile0, int wave,
@@ -664,7 +667,67 @@ __global__ __launch_bounds__(256) void qgemm_rows(KParams p) {
     qk_epilogue<BM, BN, WM, WN, MW>(p, lds_f, acc, asr, bm0, bt0, wave, lane);
     return;
   }
-  store_tiles<WM, WN, EPI, DUMP>(p, lds_f, acc, asr, row0, tile0, wave, lane);
+  if (!DUMP && p.vst) {
+    // The wave's output tile (16 WM rows x TC columns of fp16) is staged in
+    // its own LDS slice and stored as 16-byte row chunks: the MFMA layout
+    // (a lane holds one column of 4 rows) would write each row in 32-byte
+    // pieces of 2-byte stores, which cost 2.5-4.6 us of a 9-12 us launch at
+    // M = 576..1024.  Same values as store_plain / store_swiglu.
+    // (The tiles reuse the fold operands' LDS, so the launch needs no more
+    // than the larger of the two: at the 27B-class shapes that keeps 3
+    // workgroups per CU instead of 2.  Every wave has read its last fold
+    // operand before any wave passes this barrier.)
+    constexpr int TR = 16 * WM, TC = EPI == 0 ? 16 * WN : 8 * WN, CPR = TC / 8, NCH = TR * CPR;
+    __syncthreads();
+    uint16_t* yt = reinterpret_cast<uint16_t*>(lds_f) + wave * TR * TC;
+#pragma unroll
+    for (int i = 0; i < WM; ++i)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int rl = 16 * i + 4 * lgrp + r;
+        if constexpr (EPI == 0) {
+#pragma unroll
+          for (int j = 0; j < WN; ++j) yt[rl * TC + 16 * j + lrow] = ifrd::f2h(asr[i][r] * acc[i][j][r]);
+        } else {
+#pragma unroll
+          for (int j = 0; j < WN; j += 2) {
+            const float g = ifrd::fp16r(asr[i][r] * acc[i][j][r]);
+            const float u = ifrd::fp16r(asr[i][r] * acc[i][j + 1][r]);
+            yt[rl * TC + 8 * j + lrow] = ifrd::f2h(silu_f(g) * u);
+          }
+        }
+      }
+    ifrd::wave_sync();
+    const int col0 = EPI == 0 ? 16 * tile0 : 8 * tile0;
+#pragma unroll
+    for (int q = 0; q < (NCH + 63) / 64; ++q) {
+      const int ch = lane + 64 * q;
+      if (NCH % 64 != 0 && ch >= NCH) break;
+      const int rr = ch / CPR, cc = (ch % CPR) * 8, row = row0 + rr;
+      const bool colv = EPI == 0 ? tile0 + cc / 16 < ntiles : tile0 + 2 * (cc / 16) + 1 < ntiles;
+      const uint4 v = *reinterpret_cast<const uint4*>(yt + rr * TC + cc);
+      if (row < p.M && colv) *reinterpret_cast<uint4*>(p.out + (size_t)row * p.ldo + col0 + cc) = v;
+    }
+    return;
+  }
+#pragma unroll
+  for (int i = 0; i < WM; ++i)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int row = row0 + 16 * i + 4 * lgrp + r;
+      if (row >= p.M) continue;
+      if constexpr (EPI == 0) {
+#pragma unroll
+        for (int j = 0; j < WN; ++j)
+          if (tile0 + j < ntiles) store_plain(p, row, 16 * (tile0 + j) + lrow, asr[i][r], acc[i][j][r]);
+      } else {
+#pragma unroll
+        for (int j = 0; j < WN; j += 2)
+          if (tile0 + j + 1 < ntiles)
+            store_swiglu(p, row, 16 * ((tile0 + j) >> 1) + lrow, asr[i][r], acc[i][j][r],
+                         acc[i][j + 1][r]);
+      }
+    }
 }
 
 // ---- mid M (the mixed-iteration shapes, K up to a few thousand): every
