@@ -45,6 +45,8 @@ namespace ifrk {
 namespace qg {
 
 constexpr int kG = 128;
+// groups in flight per wave in the decode weight stream's ring
+constexpr int kStreamRing = 4;
 
 struct KParams {
   const int8_t* a;
@@ -68,6 +70,8 @@ struct KParams {
   // 1: out is 16-byte aligned and ldo a multiple of 8, so qgemm_rows stores
   // its output tile as 16-byte row chunks
   int vst;
+  // qgemm_stream: the pitch (in groups) of its parked d and scale rows
+  int spitch;
   // EPI 2 (QKV projection with the q/k norm + RoPE + KV append epilogue):
   // the arguments of the separate pass (row maps, norms, RoPE tables, q
   // output, paged KV)
@@ -943,161 +947,194 @@ __global__ __launch_bounds__(256) void qgemm_splitk(KParams p) {
 
 // ---- decode on large weights (M <= 16): the weight stream.  A workgroup of
 // NWV waves owns WN column tiles over the whole K; wave w takes the K groups
-// [ng w / NWV, ng (w + 1) / NWV) (at most NGW) and issues all their loads at
-// entry, so a CU keeps NWV * NGW groups of codes in flight.  Only the row
-// quads that hold real rows are kept: A fragments of rows >= M are zero and
-// not fetched, and the int32 T parked in LDS covers ceil(M / 4) quads.  After
-// one barrier each output's groups fold in ascending order, as everywhere.
-template <int BITS, int WN, int NWV, int NGW, int EPI, bool ALDS, bool DUMP>
+// [ng w / NWV, ng (w + 1) / NWV) (at most NGW) through a ring of P groups
+// of codes: a group's slot is refilled with the group P ahead as soon as
+// its MFMAs have read it, so the fold of arrived groups overlaps the stream
+// of the rest.  The code loads are the only vector-memory instructions per
+// group: the scale | zero pairs of the wave's groups arrive at entry, four
+// groups x 16 columns per load, and reach the lanes that fold a group by a
+// lane permute; the A rows come from LDS where M <= 4 (the block fetches
+// the M rows of the whole K once, ALDS), else per group with the codes.
+// Only real rows are fetched and folded: A fragments of rows >= M are zero,
+// and a lane's row quad runs min(4, M) fold steps.  Each wave turns the T of
+// its groups into d = fma(-zero, S, T) right after the MFMAs and parks d in
+// one row per output (groups along the row, pitch p.spitch) and the group's
+// scale as fp32 in one row per column; after the last barrier each output
+// runs the dependent chain acc = fma(scale, d, acc) along its row, groups
+// ascending, four groups per 128-bit LDS read.  S and the ALDS rows, shared
+// by the waves, are staged before the one barrier ahead of the ring.
+template <int BITS, int WN, int NWV, int NGW, int P, int EPI, bool ALDS, bool DUMP>
 __global__ __launch_bounds__(64 * NWV) void qgemm_stream(KParams p) {
-  extern __shared__ v4i lds4[];  // 16-byte aligned: T parks as 128-bit stores
-  int32_t* const lds = reinterpret_cast<int32_t*>(lds4);
+  extern __shared__ v4i lds4[];  // 16-byte aligned: the rows are read 128 bits at a time
+  float* const D_l = reinterpret_cast<float*>(lds4);  // [M][BN][gp] d
   constexpr int BN = 16 * WN, NT = 64 * NWV;
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int ntiles = p.N >> 4, ng = p.ng, M = p.M;
-  const int MQ = (M + 3) >> 2;
+  const int ntiles = p.N >> 4, ng = p.ng, M = p.M, gp = p.spitch;
   const int tile0 = blockIdx.x * WN;
   const int g0 = (ng * wave) / NWV, g1 = (ng * (wave + 1)) / NWV;
   int tl[WN];
 #pragma unroll
   for (int j = 0; j < WN; ++j) tl[j] = min(tile0 + j, ntiles - 1);
-  int32_t* T_l = lds;  // [ng][WN][16 MQ lanes][4]
-  float* S_l = reinterpret_cast<float*>(lds + (size_t)ng * WN * MQ * 64);  // [ng][16]
-  uint32_t* Z_l = reinterpret_cast<uint32_t*>(S_l + 16 * ng);              // [ng][BN]
+  float* const C_l = D_l + (size_t)M * BN * gp;  // [BN][gp] fp32 scale
+  float* const S_l = C_l + (size_t)BN * gp;      // [ng][16] S of the M rows
+  int8_t* const As = reinterpret_cast<int8_t*>(S_l + 16 * ng);
+  const int lrow = lane & 15, lgrp = lane >> 4;
+  const int glast = max(g1 - 1, 0);
 
-  // The fold operands (S of the M rows, scale | zero of the WN tiles) are
-  // fetched first, each thread's share at once, so that storing them to LDS
-  // waits only for them while the code stream is still in flight.
-  constexpr int SQ = (NGW + 3) / 4, ZQ = (WN * NGW + 3) / 4;
+  // S: 16 row slots of NT / 16 threads; slot r copies row r's ng group sums.
+  constexpr int SL = NT / 16, SQ = (NGW * NWV + SL - 1) / SL;
+  const int sr = threadIdx.x / SL, sk = threadIdx.x % SL;
   float sv[SQ];
-  uint32_t zv[ZQ];
 #pragma unroll
   for (int q = 0; q < SQ; ++q) {
-    const int t = threadIdx.x + NT * q;
-    const int r = t / ng, g = t - r * ng;
-    sv[q] = t < M * ng ? p.gs[(size_t)r * ng + g] : 0.f;
+    const int g = sk + SL * q;
+    sv[q] = (sr < M && g < ng) ? p.gs[(size_t)sr * ng + g] : 0.f;
   }
-#pragma unroll
-  for (int q = 0; q < ZQ; ++q) {
-    const int t = threadIdx.x + NT * q;
-    const int c = t & 15, g = (t >> 4) % ng, jt = min((t >> 4) / ng, WN - 1);
-    zv[q] = t < WN * ng * 16 ? p.sz[((size_t)tl[jt] * ng + g) * 16 + c] : 0u;
-  }
-  // ALDS (M <= 4): the block fetches the M real rows of A once, 16-byte
-  // chunks (row, step, quarter) at As[((row * nsteps + step) * 4 + quarter) * 16],
-  // instead of every wave reading its 16-row fragments from L2.
-  constexpr bool alds = ALDS;
-  int8_t* As = reinterpret_cast<int8_t*>(Z_l + (size_t)ng * BN);
-  constexpr int AQ = ALDS ? (NGW + 1) / 2 : 1;  // chunks per thread: M * 8 ng <= 4 * NT * AQ
+  // ALDS: 16-byte chunks (row, step, quarter) at
+  // As[((row * nsteps + step) * 4 + quarter) * 16]; 4 row slots of NT / 4 threads.
+  constexpr int AL = NT / 4, AQ = ALDS ? (8 * NGW * NWV + AL - 1) / AL : 1;
+  const int ar = threadIdx.x / AL, ak = threadIdx.x % AL;
   v4i av[AQ];
   if constexpr (ALDS) {
 #pragma unroll
     for (int q = 0; q < AQ; ++q) {
-      const int ch = threadIdx.x + NT * q;
-      const int r = ch % M, sq = ch / M;  // sq = step * 4 + quarter
-      av[q] = ch < M * 4 * p.nsteps
-                  ? *reinterpret_cast<const v4i*>(p.a + 1024 * (sq >> 2) + 16 * (16 * (sq & 3) + r))
+      const int sq = ak + AL * q;  // step * 4 + quarter
+      av[q] = (ar < M && sq < 4 * p.nsteps)
+                  ? *reinterpret_cast<const v4i*>(p.a + 1024 * (sq >> 2) + 16 * (16 * (sq & 3) + ar))
                   : (v4i){0, 0, 0, 0};
     }
   }
-  // A row (lane & 15) of the single 16-row tile; rows >= M contribute zeros
-  const bool arow = (lane & 15) < M;
-  GroupOps<BITS, 1, WN> ops[NGW];
-  const int glast = max(g1 - 1, 0);
+  // scale | zero pairs: load q of tile j holds groups g0 + 4q .. + 3 (lane
+  // group lgrp) x the 16 columns (lane row).  Issued after S and the ALDS
+  // rows (L2-resident), so that staging those waits for them alone, not for
+  // these first reads of the weights.
+  constexpr int ZW = (NGW + 3) / 4;
+  uint32_t zq[WN][ZW];
 #pragma unroll
-  for (int d = 0; d < NGW; ++d) {
+  for (int q = 0; q < ZW; ++q)
+#pragma unroll
+    for (int j = 0; j < WN; ++j)
+      zq[j][q] = p.sz[((size_t)tl[j] * ng + min(g0 + 4 * q + lgrp, glast)) * 16 + lrow];
+  // the ring: group d of the wave in slot d % P.  Loads are unconditional
+  // (past the wave's last group they repeat it) so that the wait before each
+  // group covers only that group's operands.
+  const bool arow = lrow < M;
+  GroupOps<BITS, 1, WN> ring[P];
+  auto fetch = [&](int d, GroupOps<BITS, 1, WN>& o) {
     const int g = min(g0 + d, glast);
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
       const int st = 2 * g + h;
-      ops[d].A[h][0] = (arow && !alds) ? *reinterpret_cast<const v4i*>(p.a + 1024 * st + 16 * lane)
-                                        : (v4i){0, 0, 0, 0};
+      if constexpr (!ALDS)
+        o.A[h][0] = arow ? *reinterpret_cast<const v4i*>(p.a + 1024 * st + 16 * lane) : (v4i){0, 0, 0, 0};
 #pragma unroll
       for (int j = 0; j < WN; ++j)
-        load_raw<BITS>(p.codes + ((size_t)tl[j] * p.nsteps + st) * 64 * (BITS / 2), lane, ops[d].B[h][j]);
+        load_raw<BITS>(p.codes + ((size_t)tl[j] * p.nsteps + st) * 64 * (BITS / 2), lane, o.B[h][j]);
     }
-  }
+  };
+#pragma unroll
+  for (int d = 0; d < P && d < NGW; ++d) fetch(d, ring[d]);
 #pragma unroll
   for (int q = 0; q < SQ; ++q) {
-    const int t = threadIdx.x + NT * q;
-    const int r = t / ng, g = t - r * ng;
-    if (t < M * ng) S_l[g * 16 + r] = sv[q];
-  }
-#pragma unroll
-  for (int q = 0; q < ZQ; ++q) {
-    const int t = threadIdx.x + NT * q;
-    const int c = t & 15, g = (t >> 4) % ng, jt = (t >> 4) / ng;
-    if (t < WN * ng * 16) Z_l[g * BN + 16 * jt + c] = zv[q];
+    const int g = sk + SL * q;
+    if (sr < M && g < ng) S_l[g * 16 + sr] = sv[q];
   }
   if constexpr (ALDS) {
 #pragma unroll
     for (int q = 0; q < AQ; ++q) {
-      const int ch = threadIdx.x + NT * q;
-      const int r = ch % M, sq = ch / M;
-      if (ch < M * 4 * p.nsteps) *reinterpret_cast<v4i*>(As + ((size_t)r * p.nsteps * 4 + sq) * 16) = av[q];
+      const int sq = ak + AL * q;
+      if (ar < M && sq < 4 * p.nsteps) *reinterpret_cast<v4i*>(As + ((size_t)ar * p.nsteps * 4 + sq) * 16) = av[q];
     }
   }
   __syncthreads();
-  // The fold in two passes.  Each wave turns the T of its own groups into
-  // d = fma(-zero, S, T) in registers right after the MFMAs and parks d, and
-  // the group's scale as fp32 in place of the packed pair; then each output
-  // runs only the dependent chain acc = fma(scale, d, acc), groups ascending.
-  const int lrow = lane & 15, lgrp = lane >> 4;
-  v4i T[1][WN];
+  // this lane's real rows: 4 lgrp .. 4 lgrp + rq - 1; the fold steps run to
+  // the wave-uniform min(4, M)
+  const int rq = M - 4 * lgrp, rmax = min(4, M);
+  // The LDS operands of group d + 1 (ALDS rows, S, the permuted scale | zero
+  // pairs) are read while group d folds: issued after group d's MFMAs and
+  // before its stores, in program order, so they are in registers when
+  // group d + 1 starts.
+  v4i an[2];
+  v4f Sn;
+  uint32_t zn[WN];
+  auto lds_ops = [&](int d) {
+    const int g = min(g0 + d, glast);
+    if constexpr (ALDS) {
+#pragma unroll
+      for (int h = 0; h < 2; ++h)
+        an[h] = arow ? *reinterpret_cast<const v4i*>(As + (((size_t)lrow * p.nsteps + 2 * g + h) * 4 + lgrp) * 16)
+                     : (v4i){0, 0, 0, 0};
+    }
+    Sn = *reinterpret_cast<const v4f*>(&S_l[g * 16 + 4 * lgrp]);
+#pragma unroll
+    for (int j = 0; j < WN; ++j) zn[j] = (uint32_t)__shfl((int)zq[j][d >> 2], lrow + 16 * (d & 3), 64);
+  };
+  lds_ops(0);
 #pragma unroll
   for (int d = 0; d < NGW; ++d) {
-    if (g0 + d < g1) {
-      const int g = g0 + d;
-      if (ALDS && arow)
+    GroupOps<BITS, 1, WN>& o = ring[d % P];
+    const int g = g0 + d;
+    if constexpr (ALDS) {
+      o.A[0][0] = an[0];
+      o.A[1][0] = an[1];
+    }
+    const v4f S4 = Sn;
+    uint32_t zw[WN];
 #pragma unroll
-        for (int h = 0; h < 2; ++h)
-          ops[d].A[h][0] = *reinterpret_cast<const v4i*>(
-              As + (((size_t)(lane & 15) * p.nsteps + 2 * g + h) * 4 + (lane >> 4)) * 16);
-      mma_group<BITS, 1, WN>(ops[d], T);
-      uint32_t zw[WN];
-      if (lgrp < MQ) {
-        // rows 4 lgrp .. +3 (S of rows >= M is never written: their d is unused)
-        const v4f S4 = *reinterpret_cast<const v4f*>(&S_l[g * 16 + 4 * lgrp]);
+    for (int j = 0; j < WN; ++j) zw[j] = zn[j];
+    v4i T[1][WN];
+    mma_group<BITS, 1, WN>(o, T);
+    if (d + P < NGW) fetch(d + P, o);
+    if (d + 1 < NGW) lds_ops(d + 1);
+    if (g < g1) {
 #pragma unroll
-        for (int j = 0; j < WN; ++j) {
-          zw[j] = Z_l[g * BN + 16 * j + lrow];
-          const float ze = ifrd::h2f((uint16_t)(zw[j] >> 16));
-          v4i dv;
+      for (int j = 0; j < WN; ++j) {
+        if (lgrp == 0) C_l[(size_t)(16 * j + lrow) * gp + g] = ifrd::h2f((uint16_t)(zw[j] & 0xFFFFu));
+        const float ze = ifrd::h2f((uint16_t)(zw[j] >> 16));
 #pragma unroll
-          for (int r = 0; r < 4; ++r) {
+        for (int r = 0; r < 4; ++r) {
+          if (r < rmax && r < rq) {
             const int32_t Tv = true_t<BITS>(T[0][j][r], S4[r]);
-            dv[r] = __float_as_int(fmaf(-ze, S4[r], (float)Tv));
-            if (DUMP && 4 * lgrp + r < M && tile0 + j < ntiles)
+            D_l[((size_t)(4 * lgrp + r) * BN + 16 * j + lrow) * gp + g] = fmaf(-ze, S4[r], (float)Tv);
+            if (DUMP && tile0 + j < ntiles)
               p.tdump[((size_t)(4 * lgrp + r) * p.N + 16 * tl[j] + lrow) * ng + g] = Tv;
           }
-          *reinterpret_cast<v4i*>(&T_l[(((size_t)g * WN + j) * MQ * 16 + lane) * 4]) = dv;
         }
       }
-      // every lane of the wave has read the packed pairs before they are
-      // replaced by the fp32 scale
-      ifrd::wave_sync();
-      if (lgrp == 0)
-#pragma unroll
-        for (int j = 0; j < WN; ++j) Z_l[g * BN + 16 * j + lrow] = __float_as_uint(ifrd::h2f((uint16_t)(zw[j] & 0xFFFFu)));
     }
   }
   __syncthreads();
+  // outputs o = (pair jp, row, column c) over 256-slot pair blocks; slots
+  // of rows >= M idle
   constexpr int JS = (EPI == 0) ? 1 : 2;  // swiglu: one thread folds the pair
-  const int nout = M * 16 * (WN / JS);
-  for (int o = threadIdx.x; o < nout; o += NT) {
-    const int c = o & 15, row = (o >> 4) % M, jj = ((o >> 4) / M) * JS;
-    const int ln = 16 * (row >> 2) + c, r = row & 3;
+  for (int o = threadIdx.x; o < 256 * (WN / JS); o += NT) {
+    const int c = o & 15, row = (o >> 4) & 15, jj = (o >> 8) * JS;
+    if (row >= M) continue;
+    const float* d0 = D_l + ((size_t)row * BN + 16 * jj + c) * gp;
+    const float* s0 = C_l + (size_t)(16 * jj + c) * gp;
+    const float* d1 = d0 + (JS == 2 ? 16 * gp : 0);
+    const float* s1 = s0 + (JS == 2 ? 16 * gp : 0);
     float a0 = 0.f, a1 = 0.f;
-#pragma unroll 8
-    for (int g = 0; g < ng; ++g) {
-#pragma unroll
-      for (int q = 0; q < JS; ++q) {
-        const int j = jj + q;
-        const float d = __int_as_float(T_l[(((size_t)g * WN + j) * MQ * 16 + ln) * 4 + r]);
-        const float sc = __uint_as_float(Z_l[g * BN + 16 * j + c]);
-        if (q == 0) a0 = fmaf(sc, d, a0); else a1 = fmaf(sc, d, a1);
+    int g = 0;
+#pragma unroll 4
+    for (; g + 4 <= ng; g += 4) {
+      const v4f dv = *reinterpret_cast<const v4f*>(d0 + g), sc = *reinterpret_cast<const v4f*>(s0 + g);
+      a0 = fmaf(sc.x, dv.x, a0);
+      a0 = fmaf(sc.y, dv.y, a0);
+      a0 = fmaf(sc.z, dv.z, a0);
+      a0 = fmaf(sc.w, dv.w, a0);
+      if constexpr (JS == 2) {
+        const v4f dw = *reinterpret_cast<const v4f*>(d1 + g), sw = *reinterpret_cast<const v4f*>(s1 + g);
+        a1 = fmaf(sw.x, dw.x, a1);
+        a1 = fmaf(sw.y, dw.y, a1);
+        a1 = fmaf(sw.z, dw.z, a1);
+        a1 = fmaf(sw.w, dw.w, a1);
       }
+    }
+    for (; g < ng; ++g) {
+      a0 = fmaf(s0[g], d0[g], a0);
+      if constexpr (JS == 2) a1 = fmaf(s1[g], d1[g], a1);
     }
     const float as = p.as[row] * p.post;
     if constexpr (EPI == 0) {
@@ -1212,41 +1249,75 @@ hipError_t launch_splitk_ng(const KParams& p, hipStream_t st) {
 
 template <int BITS, int WN, int NWV, int NGW, int EPI>
 hipError_t launch_stream(const KParams& p, hipStream_t st) {
-  // the operand registers (8 for A and WN * BITS for B per group) must fit
-  // the 128 VGPRs of a 16-wave workgroup without spilling
-  if constexpr (NGW * (8 + WN * BITS) + (NGW + 3) / 4 + (WN * NGW + 3) / 4 > 120) {
-    return hipErrorInvalidValue;
-  } else {
-  const int MQ = (p.M + 3) / 4;
-  size_t lds = ((size_t)p.ng * WN * MQ * 64 + (size_t)p.ng * (16 + 16 * WN)) * sizeof(int32_t);
-  if (p.M > 16 || (p.ng + NWV - 1) / NWV > NGW || lds > 160 * 1024) return hipErrorInvalidValue;
-  const bool alds = p.M <= 4 && lds + (size_t)p.M * p.K <= 160 * 1024;
-  if (alds) lds += (size_t)p.M * p.K;
+  // P groups in the ring: the operand registers per group (WN * BITS for the
+  // codes, and 8 for A unless ALDS) times P, beside the staging registers
+  // (S, the scale | zero pairs, the ALDS rows), T, S and the addresses
+  // (24 + 4 WN, and 4 WN more for the SwiGLU tail, as the compiler's counts
+  // show), fit the VGPRs of a 64 * NWV-thread workgroup.
+  constexpr int kLim = NWV >= 16 ? 120 : 232;
+  constexpr int kOver = 24 + 4 * WN + (EPI == 1 ? 4 * WN : 0) + WN * ((NGW + 3) / 4) + (NGW + 3) / 4;
+  constexpr int kRing = kStreamRing < NGW ? kStreamRing : NGW;
+  constexpr int kFitF = (kLim - kOver) / (8 + WN * BITS);
+  constexpr int kFitA = (kLim - kOver - 4 * ((NGW + 1) / 2)) / (WN * BITS);
+  constexpr int PF = kRing < kFitF ? kRing : kFitF, PA = kRing < kFitA ? kRing : kFitA;
+  if (p.M > 16 || (p.ng + NWV - 1) / NWV > NGW) return hipErrorInvalidValue;
+  // LDS: d rows [M][BN] and scale rows [BN] (pitch gp), S [ng][16], the
+  // ALDS rows.  gp: a multiple of 4 (four groups per 128-bit read) that is
+  // 4 mod 8, so the rows of the 16 columns of one group start in different
+  // banks; the plain multiple of 4 where the padded rows do not fit.
+  constexpr int BN = 16 * WN;
+  auto need = [&](int gp, bool alds) {
+    return ((size_t)(p.M + 1) * BN * gp + 16 * (size_t)p.ng) * sizeof(float) + (alds ? (size_t)p.M * p.K : 0);
+  };
+  bool alds = PA >= 1 && p.M <= 4;
+  if (alds && need((p.ng + 3) & ~3, true) > 160 * 1024) alds = false;
+  if (!alds && PF < 1) return hipErrorInvalidValue;
+  int gp = ((p.ng + 3) & ~7) + 4;
+  if (need(gp, alds) > 160 * 1024) gp = (p.ng + 3) & ~3;
+  const size_t lds = need(gp, alds);
+  if (lds > 160 * 1024) return hipErrorInvalidValue;
   static bool attr_set = false;
   if (!attr_set) {
-    hipError_t e = set_lds_limit(qgemm_stream<BITS, WN, NWV, NGW, EPI, false, false>);
-    if (e == hipSuccess) e = set_lds_limit(qgemm_stream<BITS, WN, NWV, NGW, EPI, true, false>);
-    if constexpr (EPI == 0) {
-      if (e == hipSuccess) e = set_lds_limit(qgemm_stream<BITS, WN, NWV, NGW, EPI, false, true>);
-      if (e == hipSuccess) e = set_lds_limit(qgemm_stream<BITS, WN, NWV, NGW, EPI, true, true>);
+    hipError_t e = hipSuccess;
+    if constexpr (PF >= 1) {
+      e = set_lds_limit(qgemm_stream<BITS, WN, NWV, NGW, PF, EPI, false, false>);
+      if constexpr (EPI == 0)
+        if (e == hipSuccess) e = set_lds_limit(qgemm_stream<BITS, WN, NWV, NGW, PF, EPI, false, true>);
+    }
+    if constexpr (PA >= 1) {
+      if (e == hipSuccess) e = set_lds_limit(qgemm_stream<BITS, WN, NWV, NGW, PA, EPI, true, false>);
+      if constexpr (EPI == 0)
+        if (e == hipSuccess) e = set_lds_limit(qgemm_stream<BITS, WN, NWV, NGW, PA, EPI, true, true>);
     }
     if (e != hipSuccess) return e;
     attr_set = true;
   }
+  KParams q = p;
+  q.spitch = gp;
   const dim3 grid((p.N / 16 + WN - 1) / WN), block(64 * NWV);
-  if constexpr (EPI == 0)
-    if (p.tdump) {
-      if (alds) hipLaunchKernelGGL((qgemm_stream<BITS, WN, NWV, NGW, EPI, true, true>), grid, block, lds, st, p);
-      else hipLaunchKernelGGL((qgemm_stream<BITS, WN, NWV, NGW, EPI, false, true>), grid, block, lds, st, p);
-      return hipGetLastError();
+  const bool dump = EPI == 0 && p.tdump;
+  if (alds) {
+    if constexpr (PA >= 1) {
+      if (dump) {
+        if constexpr (EPI == 0) hipLaunchKernelGGL((qgemm_stream<BITS, WN, NWV, NGW, PA, EPI, true, true>), grid, block, lds, st, q);
+      } else {
+        hipLaunchKernelGGL((qgemm_stream<BITS, WN, NWV, NGW, PA, EPI, true, false>), grid, block, lds, st, q);
+      }
     }
-  if (alds) hipLaunchKernelGGL((qgemm_stream<BITS, WN, NWV, NGW, EPI, true, false>), grid, block, lds, st, p);
-  else hipLaunchKernelGGL((qgemm_stream<BITS, WN, NWV, NGW, EPI, false, false>), grid, block, lds, st, p);
-  return hipGetLastError();
+  } else {
+    if constexpr (PF >= 1) {
+      if (dump) {
+        if constexpr (EPI == 0) hipLaunchKernelGGL((qgemm_stream<BITS, WN, NWV, NGW, PF, EPI, false, true>), grid, block, lds, st, q);
+      } else {
+        hipLaunchKernelGGL((qgemm_stream<BITS, WN, NWV, NGW, PF, EPI, false, false>), grid, block, lds, st, q);
+      }
+    }
   }
+  return hipGetLastError();
 }
 
-// NGW: the smallest instantiated depth that holds ceil(ng / NWV) groups.
+// NGW: the smallest instantiated depth that holds ceil(ng / NWV) groups
+// (17: the 136-group projection over 8 waves).
 template <int BITS, int WN, int NWV, int EPI>
 hipError_t launch_stream_ng(const KParams& p, hipStream_t st) {
   const int per = (p.ng + NWV - 1) / NWV;
@@ -1255,6 +1326,7 @@ hipError_t launch_stream_ng(const KParams& p, hipStream_t st) {
   if (per <= 3) return launch_stream<BITS, WN, NWV, 3, EPI>(p, st);
   if (per <= 5) return launch_stream<BITS, WN, NWV, 5, EPI>(p, st);
   if (per <= 9) return launch_stream<BITS, WN, NWV, 9, EPI>(p, st);
+  if (per <= 17) return launch_stream<BITS, WN, NWV, 17, EPI>(p, st);
   return hipErrorInvalidValue;
 }
 
@@ -1403,18 +1475,18 @@ hipError_t launch_bits(const KParams& p, int variant, hipStream_t st) {
       }
     }
     // Decode rows on those shapes (bench.py --gemm-decode-27b, M = 1, 8, 16):
-    // the weight stream, two tiles per workgroup for the plain projections
-    // (one for the deep down projection above M = 4, where the T of two
-    // tiles no longer fits LDS) and one tile of 8 waves for the SwiGLU pair
-    // up to M = 8.
-    // A shape a stream variant cannot hold (registers or LDS for wider codes)
-    // falls back to the next one, then to the choice above.
+    // the weight stream; for the plain projections two tiles per workgroup
+    // up to M = 4, above it one tile (16 waves for the deep down projection,
+    // 8 for the others), and one tile pair of 8 waves for the SwiGLU pair up
+    // to M = 8.  A shape a stream variant cannot hold (registers or LDS for
+    // wider codes) falls back to the next one, then to the choice above.
     if (p.K >= 4096 && p.M <= 16) {
       hipError_t e = hipErrorInvalidValue;
       if (EPI == 1) {
         if (p.M <= 8) e = launch_bits<BITS, EPI>(p, 14, st);
       } else {
-        if (!(p.ng >= 96 && p.M > 4)) e = launch_bits<BITS, EPI>(p, 15, st);
+        if (p.M <= 4) e = launch_bits<BITS, EPI>(p, 15, st);
+        else if (p.ng < 96) e = launch_bits<BITS, EPI>(p, 14, st);
         if (e == hipErrorInvalidValue) e = launch_bits<BITS, EPI>(p, 13, st);
       }
       if (e != hipErrorInvalidValue) return e;
@@ -1521,7 +1593,7 @@ hipError_t launch_qgemm_qkrope(const DLin& w, const QGemmArgs& a, const QKArgs& 
       (kv.kv_int8 && (!kv.kscale || !kv.vscale)))
     return hipErrorInvalidValue;
   qg::KParams p{a.a, a.as, a.gs, w.codes, w.sz, nullptr, nullptr, a.M, w.N, w.K, w.ng, w.nsteps, w.N,
-                w.post, 0, 0, 0, w.ff, 0, qa, kv};
+                w.post, 0, 0, 0, w.ff, 0, 0, qa, kv};
   switch (w.bits) {
     case 2: return qg::launch_b2(p, 2, variant, st);
     case 4: return qg::launch_b4(p, 2, variant, st);
@@ -1536,7 +1608,7 @@ hipError_t launch_qgemm_variant(const DLin& w, const QGemmArgs& a, int variant, 
     return hipErrorInvalidValue;
   if (w.pair && (w.N % 32 != 0 || a.tdump)) return hipErrorInvalidValue;
   qg::KParams p{a.a, a.as, a.gs, w.codes, w.sz, a.out, a.tdump, a.M, w.N, w.K, w.ng, w.nsteps, a.ldo,
-                w.post, 0, 0, 0, w.ff, 0, {}, {}};
+                w.post, 0, 0, 0, w.ff, 0, 0, {}, {}};
   const int epi = w.pair ? 1 : 0;
   switch (w.bits) {
     case 2: return qg::launch_b2(p, epi, variant, st);

@@ -103,6 +103,15 @@ def gemm_stream():
 
 
 @scenario
+def gemm_stream_rows():
+    """The weight-stream shapes alone at every row count class: A staged in
+    LDS (M = 2, 3, 4), the partial last row quad (M = 6, 7) and two full
+    quads (M = 8), INT2 / INT4 / INT8."""
+    _gemm_shapes((2, 4, 8), ((32, 5120), (16, 17408)), Ms=(2, 3, 4, 6, 7, 8), pair_check=True,
+                 variants=(13, 14, 15))
+
+
+@scenario
 def gemm_full():
     """The whole-K row-block shapes (A in LDS by the LDS DMA, every load at
     entry) at K of 8, 16 and 24 groups, ragged M across 16- and 32-row

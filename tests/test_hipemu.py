@@ -39,7 +39,8 @@ def test_ragged_attention_in_bounds(emu_lib):
 
 
 def test_every_gemm_launch_shape_in_bounds(emu_lib):
-    assert runner.run_scenarios(["gemm_small", "gemm_full", "gemm_stream", "gemm_grouped", "gemm_f16", "gemm_ga"],
+    assert runner.run_scenarios(["gemm_small", "gemm_full", "gemm_stream", "gemm_stream_rows", "gemm_grouped",
+                                 "gemm_f16", "gemm_ga"],
                                 timeout=1800) == 0
 
 
