@@ -69,7 +69,8 @@ def parse():
     ap.add_argument("--gemm-decode", action="store_true",
                     help="every launch shape at decode M (1, 8, 16) on the 0.8B projections")
     ap.add_argument("--gemm-decode-27b", action="store_true",
-                    help="every launch shape at decode M (1, 8, 16) on the 27B-class projections")
+                    help="every launch shape at decode M (1, 8, 16) on the 27B-class projections, then at "
+                         "M = 1, 4 with A also row-major (ifr_quant_gemm_rows)")
     ap.add_argument("--gemm-variants-27b", action="store_true",
                     help="the same on the 27B-class (cfg5) shapes at M = 512 and 2160")
     ap.add_argument("--attn-sweep", action="store_true",
@@ -492,13 +493,16 @@ def f16_gemm(ia, dev, Ms=(1, 16, 576), reps=3, kind="f16"):
     return res
 
 
-def gemm_variants(ia, dev, Ms=(128, 256, 576, 1024), bits=2, reps=3, shapes=SHAPES_08B, rotate_bytes=320e6):
+def gemm_variants(ia, dev, Ms=(128, 256, 576, 1024), bits=2, reps=3, shapes=SHAPES_08B, rotate_bytes=320e6,
+                  rows=False):
     """Every launch shape of the quant GEMM on the four projection shapes
     (gate_up as the interleaved SwiGLU pair the forward runs), cache-cold as
     in gemm_sweep (rotate_bytes of distinct weight copies, above the 256 MB
     MALL); one line per (shape, M, variant).  With rotate_bytes = 100e6 the
     copies stay in the MALL but not in L2, as the 0.8B model's weights do in
-    the serve load (28 layers x 4.4 MB, each touched once per iteration)."""
+    the serve load (28 layers x 4.4 MB, each touched once per iteration).
+    rows: A also passed row-major (ifr_quant_gemm_rows; the weight stream
+    stages its A rows from it at M <= 4)."""
     import ctypes as C
     L = ia.lib()
     rng = np.random.default_rng(0)
@@ -518,19 +522,26 @@ def gemm_variants(ia, dev, Ms=(128, 256, 576, 1024), bits=2, reps=3, shapes=SHAP
             else:
                 ia.check(L.ifr_linear_upload(dev.ctx, C.byref(lins[0].struct), C.byref(d)), "upload")
             dls.append(d)
-        q = dev.upload(rng.integers(-127, 128, size=((Mmax + 15) // 16 * 16) * K, dtype=np.int8))
+        qrow = rng.integers(-127, 128, size=(Mmax, K), dtype=np.int8)
+        q = dev.upload(ia.atile(qrow))
+        qr = dev.upload(qrow)
         asc = dev.upload(np.full(Mmax, 1e-3, dtype=np.float32))
         gs = dev.upload(rng.integers(-2000, 2000, size=Mmax * (K // 128)).astype(np.float32))
         out = dev.alloc(Mmax * N * 2 * 2)
+
+        def gemm(d, M, v):
+            if rows:
+                return L.ifr_quant_gemm_rows(dev.ctx, d, q.p, qr.p, asc.p, gs.p, M, out.p, v)
+            return L.ifr_quant_gemm_variant(dev.ctx, d, q.p, asc.p, gs.p, M, out.p, v)
         for M in Ms:
             for v in range(nv):
-                if L.ifr_quant_gemm_variant(dev.ctx, dls[0], q.p, asc.p, gs.p, M, out.p, v) != 0:
+                if gemm(dls[0], M, v) != 0:
                     continue
                 best = None
                 for _ in range(reps + 1):
                     dev.timer_begin()
                     for d in dls:
-                        ia.check(L.ifr_quant_gemm_variant(dev.ctx, d, q.p, asc.p, gs.p, M, out.p, v), "gemm")
+                        ia.check(gemm(d, M, v), "gemm")
                     ms = dev.timer_end()
                     best = ms if best is None else min(best, ms)
                 us = best * 1e3 / R
@@ -546,7 +557,7 @@ def gemm_variants(ia, dev, Ms=(128, 256, 576, 1024), bits=2, reps=3, shapes=SHAP
                 " ".join(f"v{r['variant']}:{r['us']}" for r in row))
         for d in dls:
             L.ifr_linear_free(dev.ctx, d)
-        for b in (q, asc, gs, out):
+        for b in (q, qr, asc, gs, out):
             b.free()
     return res
 
@@ -554,7 +565,10 @@ def gemm_variants(ia, dev, Ms=(128, 256, 576, 1024), bits=2, reps=3, shapes=SHAP
 def decode_gemm_brief(ia, dev, reps=3):
     """The W2A8 decode GEMM (M = 1, the library's default launch shape),
     cache-cold as in gemm_sweep: the 0.8B gate/up pair and the 27B-class
-    gate/up pair and down projection (the largest weight streams)."""
+    gate/up pair and down projection (the largest weight streams).  us: A in
+    the A-tile layout (ifr_quant_gemm / ifr_quant_gemm_swiglu, what the
+    engine's forward passes); us_rows: A also row-major
+    (ifr_quant_gemm_rows)."""
     import ctypes as C
     L = ia.lib()
     rng = np.random.default_rng(1)
@@ -573,29 +587,37 @@ def decode_gemm_brief(ia, dev, reps=3):
             else:
                 ia.check(L.ifr_linear_upload(dev.ctx, C.byref(lins[0].struct), C.byref(d)), "upload")
             dls.append(d)
-        q = dev.upload(rng.integers(-127, 128, size=16 * K, dtype=np.int8))
+        qrow = rng.integers(-127, 128, size=(1, K), dtype=np.int8)
+        q = dev.upload(ia.atile(qrow))
+        qr = dev.upload(qrow)
         asc = dev.upload(np.full(16, 1e-3, dtype=np.float32))
         gs = dev.upload(rng.integers(-2000, 2000, size=16 * (K // 128)).astype(np.float32))
         out = dev.alloc(16 * N * 2 * 2)
-        best = None
-        for _ in range(reps + 1):
-            dev.timer_begin()
-            for d in dls:
-                if pair:
-                    ia.check(L.ifr_quant_gemm_swiglu(dev.ctx, d, q.p, asc.p, gs.p, 1, out.p), "swiglu")
-                else:
-                    ia.check(L.ifr_quant_gemm(dev.ctx, d, q.p, asc.p, gs.p, 1, out.p, None), "gemm")
-            ms = dev.timer_end()
-            best = ms if best is None else min(best, ms)
-        us = best * 1e3 / R
+
+        def timed(rows):
+            best = None
+            for _ in range(reps + 1):
+                dev.timer_begin()
+                for d in dls:
+                    if rows:
+                        ia.check(L.ifr_quant_gemm_rows(dev.ctx, d, q.p, qr.p, asc.p, gs.p, 1, out.p, -1), "rows")
+                    elif pair:
+                        ia.check(L.ifr_quant_gemm_swiglu(dev.ctx, d, q.p, asc.p, gs.p, 1, out.p), "swiglu")
+                    else:
+                        ia.check(L.ifr_quant_gemm(dev.ctx, d, q.p, asc.p, gs.p, 1, out.p, None), "gemm")
+                ms = dev.timer_end()
+                best = ms if best is None else min(best, ms)
+            return best * 1e3 / R
+        us, us_rows = timed(False), timed(True)
         byts = wb + K + 4 + N * 2
         res.append({"shape": name, "M": 1, "K": K, "N": N * len(lins), "weight_MB": round(wb / 1e6, 2),
                     "us": round(us, 2), "GBps": round(byts / us / 1e3, 1),
-                    "hbm_frac": round(byts / us / 1e3 / 8000, 4)})
-        log(f"decode GEMM {name} M=1: {us:.2f} us, {byts / us / 1e3:.0f} GB/s")
+                    "hbm_frac": round(byts / us / 1e3 / 8000, 4), "us_rows": round(us_rows, 2),
+                    "hbm_frac_rows": round(byts / us_rows / 1e3 / 8000, 4)})
+        log(f"decode GEMM {name} M=1: {us:.2f} us, {byts / us / 1e3:.0f} GB/s; A row-major {us_rows:.2f} us")
         for d in dls:
             L.ifr_linear_free(dev.ctx, d)
-        for b in (q, asc, gs, out):
+        for b in (q, qr, asc, gs, out):
             b.free()
     return res
 
@@ -1013,6 +1035,8 @@ def main():
             res = gemm_variants(ia, dev, Ms=(512, 2160), shapes=SHAPES_27B, reps=2)
         else:
             res = gemm_variants(ia, dev, Ms=(1, 8, 16), shapes=SHAPES_27B, reps=3)
+            res += [dict(r, A="rows") for r in gemm_variants(ia, dev, Ms=(1, 4), shapes=SHAPES_27B, reps=3,
+                                                               rows=True)]
         print(json.dumps({"metric": "quant-GEMM launch shapes (cache-cold)", "unit": "us", "results": res}))
         dev.close()
         return 0
@@ -1121,7 +1145,8 @@ def main():
     if not a.no_gemm:
         out["decode_gemm"] = {
             "note": "W2A8 decode GEMM at M=1, cache-cold (rotating weight copies > MALL), HIP events "
-                    "around back-to-back launches (each includes the ~2.3 us launch floor)",
+                    "around back-to-back launches (each includes the ~2.3 us launch floor); us: A-tile "
+                    "layout (the engine's path), us_rows: A also row-major (ifr_quant_gemm_rows)",
             "results": decode_gemm_brief(ia, dev)}
     if not a.no_cpu:
         log("timing the reference CPU path on a bounded sample")

@@ -238,6 +238,19 @@ int ifr_quant_gemm_variant(ifr_ctx* ctx, const ifr_dlinear* w, const int8_t* a_d
                            const float* ascale_d, const float* gsum_d, int32_t M,
                            uint16_t* out_d, int32_t variant);
 
+/* No counterpart in the reference (its activation codes have one layout):
+ * ifr_quant_gemm (plain linear) or ifr_quant_gemm_swiglu (gate/up pair) with
+ * the activation codes also given row-major, arow_d int8 [M][K] (the codes of
+ * a_d's M rows, unpadded).  The decode weight stream (M <= 4, K >= 4096)
+ * stages its A rows from arow_d, K contiguous bytes per row, where in the
+ * A-tile layout a row holds 16 of every 128 bytes it touches; every other
+ * launch shape reads a_d.  arow_d may be NULL.  variant: -1 for the size
+ * heuristic, else a launch shape as in ifr_quant_gemm_variant (IFR_EDECLINE
+ * where it does not apply).  The bits are those of ifr_quant_gemm. */
+int ifr_quant_gemm_rows(ifr_ctx* ctx, const ifr_dlinear* w, const int8_t* a_d,
+                        const int8_t* arow_d, const float* ascale_d, const float* gsum_d,
+                        int32_t M, uint16_t* out_d, int32_t variant);
+
 /* FP16-activation dequant GEMM (replaces quant_gemm_forward_usm, the
  * reference's default GPU linear, quant_gemm.cpp:359-2153):
  *   out(m,n) = fp16_rne( sum_k a(m,k) * w(n,k) ), fp32, k ascending

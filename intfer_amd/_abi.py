@@ -161,6 +161,7 @@ _PROTOS = {
     "ifr_d2d": (C.c_int, [P, P, P, C.c_size_t]),
     "ifr_timer_end": (C.c_int, [P, C.POINTER(C.c_double)]),
     "ifr_quant_gemm_variant": (C.c_int, [P, P, P, P, P, i32, P, i32]),
+    "ifr_quant_gemm_rows": (C.c_int, [P, P, P, P, P, P, i32, P, i32]),
     "ifr_quant_gemm_f16": (C.c_int, [P, P, P, i32, C.c_float, P]),
     "ifr_quant_gemm_ga": (C.c_int, [P, P, P, P, i32, i32, C.c_float, P]),
     "ifr_model_load": (C.c_int, [P, C.POINTER(HostModel), C.POINTER(KVCfg)]),

@@ -953,6 +953,20 @@ int ifr_quant_gemm_ga(ifr_ctx* c, const ifr_dlinear* w, const int8_t* a_d, const
 
 int ifr_quant_gemm_variants(void) { return ifrk::kQGemmVariants; }
 
+int ifr_quant_gemm_rows(ifr_ctx* c, const ifr_dlinear* w, const int8_t* a_d, const int8_t* arow_d,
+                        const float* ascale_d, const float* gsum_d, int32_t M, uint16_t* out_d, int32_t variant) {
+  if (!c || !w) return fail(IFR_EINVAL, "null arg");
+  if (variant < -1 || variant >= ifrk::kQGemmVariants) return fail(IFR_EINVAL, "variant %d", variant);
+  ifrk::QGemmArgs a{a_d, ascale_d, gsum_d, out_d, nullptr, M, w->d.pair ? w->d.N / 2 : w->d.N, arow_d};
+  const hipError_t e = ifrk::launch_qgemm_variant(w->d, a, variant, c->st);
+  if (e == hipErrorInvalidValue && variant >= 0) {
+    (void)hipGetLastError();
+    return fail(IFR_EDECLINE, "variant %d does not apply to M=%d N=%d K=%d", variant, M, w->d.N, w->d.K);
+  }
+  HIPCHK(e);
+  return IFR_OK;
+}
+
 int ifr_quant_gemm_variant(ifr_ctx* c, const ifr_dlinear* w, const int8_t* a_d,
                            const float* ascale_d, const float* gsum_d, int32_t M, uint16_t* out_d,
                            int32_t variant) {

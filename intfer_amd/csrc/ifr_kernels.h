@@ -57,6 +57,7 @@ struct QGemmArgs {
   int32_t* tdump;       // optional [M][N][K/128]
   int M;
   int ldo;
+  const int8_t* arow = nullptr;  // optional: the same codes row-major [M][K]
 };
 hipError_t launch_qgemm(const DLin& w, const QGemmArgs& a, hipStream_t st);
 // One launch shape of the table (0..kQGemmVariants-1); all give identical

@@ -77,6 +77,9 @@ struct KParams {
   // output, paged KV)
   QKArgs qa;
   KVLayout kv;
+  // optional: the codes of A row-major [M][K] (the weight stream stages its
+  // A rows from here when given)
+  const int8_t* arow;
 };
 
 // One compilation of this file per code width (IFR_QGEMM_BITS = 2, 4, 8)
@@ -992,17 +995,21 @@ __global__ __launch_bounds__(64 * NWV) void qgemm_stream(KParams p) {
     sv[q] = (sr < M && g < ng) ? p.gs[(size_t)sr * ng + g] : 0.f;
   }
   // ALDS: 16-byte chunks (row, step, quarter) at
-  // As[((row * nsteps + step) * 4 + quarter) * 16]; 4 row slots of NT / 4 threads.
+  // As[((row * nsteps + step) * 4 + quarter) * 16], which is the row-major
+  // [M][K] order; 4 row slots of NT / 4 threads.  From p.arow when given
+  // (contiguous), else gathered from the A tiles (16 useful bytes per 128-byte
+  // line a row touches).
   constexpr int AL = NT / 4, AQ = ALDS ? (8 * NGW * NWV + AL - 1) / AL : 1;
   const int ar = threadIdx.x / AL, ak = threadIdx.x % AL;
   v4i av[AQ];
   if constexpr (ALDS) {
+    const bool rows = p.arow != nullptr;
 #pragma unroll
     for (int q = 0; q < AQ; ++q) {
       const int sq = ak + AL * q;  // step * 4 + quarter
-      av[q] = (ar < M && sq < 4 * p.nsteps)
-                  ? *reinterpret_cast<const v4i*>(p.a + 1024 * (sq >> 2) + 16 * (16 * (sq & 3) + ar))
-                  : (v4i){0, 0, 0, 0};
+      const int8_t* src = rows ? p.arow + (size_t)ar * p.K + 16 * sq
+                               : p.a + 1024 * (sq >> 2) + 16 * (16 * (sq & 3) + ar);
+      av[q] = (ar < M && sq < 4 * p.nsteps) ? *reinterpret_cast<const v4i*>(src) : (v4i){0, 0, 0, 0};
     }
   }
   // scale | zero pairs: load q of tile j holds groups g0 + 4q .. + 3 (lane
@@ -1608,7 +1615,7 @@ hipError_t launch_qgemm_variant(const DLin& w, const QGemmArgs& a, int variant, 
     return hipErrorInvalidValue;
   if (w.pair && (w.N % 32 != 0 || a.tdump)) return hipErrorInvalidValue;
   qg::KParams p{a.a, a.as, a.gs, w.codes, w.sz, a.out, a.tdump, a.M, w.N, w.K, w.ng, w.nsteps, a.ldo,
-                w.post, 0, 0, 0, w.ff, 0, 0, {}, {}};
+                w.post, 0, 0, 0, w.ff, 0, 0, {}, {}, a.arow};
   const int epi = w.pair ? 1 : 0;
   switch (w.bits) {
     case 2: return qg::launch_b2(p, epi, variant, st);

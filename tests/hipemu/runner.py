@@ -105,10 +105,11 @@ def gemm_stream():
 @scenario
 def gemm_stream_rows():
     """The weight-stream shapes alone at every row count class: A staged in
-    LDS (M = 2, 3, 4), the partial last row quad (M = 6, 7) and two full
-    quads (M = 8), INT2 / INT4 / INT8."""
-    _gemm_shapes((2, 4, 8), ((32, 5120), (16, 17408)), Ms=(2, 3, 4, 6, 7, 8), pair_check=True,
-                 variants=(13, 14, 15))
+    LDS (M = 1 .. 4), the partial last row quad (M = 6, 7) and two full
+    quads (M = 8), INT2 / INT4 / INT8; each also with A given row-major
+    (ifr_quant_gemm_rows)."""
+    _gemm_shapes((2, 4, 8), ((32, 5120), (16, 17408)), Ms=(1, 2, 3, 4, 6, 7, 8), pair_check=True,
+                 variants=(13, 14, 15), rows=True)
 
 
 @scenario
@@ -120,7 +121,7 @@ def gemm_full():
                  variants=range(16, 21))
 
 
-def _gemm_shapes(bits_list, shapes, Ms=(1, 17, 70), pair_check=False, variants=None):
+def _gemm_shapes(bits_list, shapes, Ms=(1, 17, 70), pair_check=False, variants=None, rows=False):
     import intfer_amd as ia
     from oracle import pyoracle as po
     L = ia.lib()
@@ -163,6 +164,16 @@ def _gemm_shapes(bits_list, shapes, Ms=(1, 17, 70), pair_check=False, variants=N
                             if pair_ref is None:
                                 pair_ref = po_
                             assert np.array_equal(po_, pair_ref), f"pair variant {v} N {N} K {K} M {M}"
+                    if rows:  # A also row-major: the same bits
+                        qr = dev.upload(np.ascontiguousarray(q))
+                        ia.check(L.ifr_quant_gemm_rows(dev.ctx, dl, qd.p, qr.p, sd.p, gd.p, M, od.p, v), "rows")
+                        assert np.array_equal(dev.download(od, np.uint16, (M, N)), ref), f"rows variant {v}"
+                        rc = L.ifr_quant_gemm_rows(dev.ctx, dp, qd.p, qr.p, sd.p, gd.p, M, od.p, v)
+                        if pair_check and pair_ref is not None and rc != ia.IFR_EDECLINE:
+                            ia.check(rc, "pair rows")
+                            assert np.array_equal(dev.download(od, np.uint16, (M, N)), pair_ref), \
+                                f"pair rows variant {v}"
+                        qr.free()
                 for b in (qd, sd, gd, od):
                     b.free()
                 # (a restricted variant list may hold no shape for wide codes)

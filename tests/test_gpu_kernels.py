@@ -248,6 +248,20 @@ def test_qgemm_decode_stream_large_k_bitexact(dev, bits):
                         if pair_ref is None:
                             pair_ref = po_
                         assert np.array_equal(po_, pair_ref), f"pair variant {v} N={N} K={K} M={M}"
+                # A also given row-major (ifr_quant_gemm_rows: the stream
+                # stages its A rows from it at M <= 4): the same bits
+                qr = dev.upload(np.ascontiguousarray(q))
+                for v in (13, 14, 15, -1):
+                    announce(f"qgemm rows variant {v} bits={bits} N={N} K={K} M={M}")
+                    for lin_d, want in ((dl, ref), (dp, pair_ref)):
+                        rc = L.ifr_quant_gemm_rows(dev.ctx, lin_d, qd.p, qr.p, sd.p, gd.p, M, od.p, v)
+                        if rc == ia.IFR_EDECLINE:
+                            continue
+                        ia.check(rc, f"rows variant {v}")
+                        if want is not None:
+                            assert np.array_equal(dev.download(od, np.uint16, (M, N)), want), \
+                                f"rows variant {v} N={N} K={K} M={M} pair={lin_d is dp}"
+                qr.free()
                 # the heuristic's own choice (a stream shape, or its fallback
                 # where one cannot hold the codes) gives the same bits
                 ia.check(L.ifr_quant_gemm(dev.ctx, dl, qd.p, sd.p, gd.p, M, od.p, None), "default")
