@@ -964,8 +964,9 @@ __global__ __launch_bounds__(256) void qgemm_splitk(KParams p) {
 // one row per output (groups along the row, pitch p.spitch) and the group's
 // scale as fp32 in one row per column; after the last barrier each output
 // runs the dependent chain acc = fma(scale, d, acc) along its row, groups
-// ascending, four groups per 128-bit LDS read.  S and the ALDS rows, shared
-// by the waves, are staged before the one barrier ahead of the ring.
+// ascending, four groups per 128-bit LDS read.  Each wave stages S and the
+// ALDS rows of its own groups in its own LDS region, so no workgroup barrier
+// precedes the ring.
 template <int BITS, int WN, int NWV, int NGW, int P, int EPI, bool ALDS, bool DUMP>
 __global__ __launch_bounds__(64 * NWV) void qgemm_stream(KParams p) {
   extern __shared__ v4i lds4[];  // 16-byte aligned: the rows are read 128 bits at a time
@@ -980,36 +981,37 @@ __global__ __launch_bounds__(64 * NWV) void qgemm_stream(KParams p) {
 #pragma unroll
   for (int j = 0; j < WN; ++j) tl[j] = min(tile0 + j, ntiles - 1);
   float* const C_l = D_l + (size_t)M * BN * gp;  // [BN][gp] fp32 scale
-  float* const S_l = C_l + (size_t)BN * gp;      // [ng][16] S of the M rows
-  int8_t* const As = reinterpret_cast<int8_t*>(S_l + 16 * ng);
+  // each wave's own operands: S of its groups [NGW][16] and, ALDS, its A
+  // rows [M][8 NGW chunks of 16 bytes] (the chunks (step, quarter) of its
+  // groups, in row-major order)
+  float* const S_w = C_l + (size_t)BN * gp + (size_t)wave * 16 * NGW;
+  int8_t* const As_w = reinterpret_cast<int8_t*>(C_l + (size_t)BN * gp + (size_t)NWV * 16 * NGW) +
+                       (size_t)wave * M * 128 * NGW;
   const int lrow = lane & 15, lgrp = lane >> 4;
-  const int glast = max(g1 - 1, 0);
+  const int glast = max(g1 - 1, 0), ngw = g1 - g0;
 
-  // S: 16 row slots of NT / 16 threads; slot r copies row r's ng group sums.
-  constexpr int SL = NT / 16, SQ = (NGW * NWV + SL - 1) / SL;
-  const int sr = threadIdx.x / SL, sk = threadIdx.x % SL;
+  // S: item t = (group gi = t / 16, row r = t % 16)
+  constexpr int SQ = (16 * NGW + 63) / 64;
   float sv[SQ];
 #pragma unroll
   for (int q = 0; q < SQ; ++q) {
-    const int g = sk + SL * q;
-    sv[q] = (sr < M && g < ng) ? p.gs[(size_t)sr * ng + g] : 0.f;
+    const int t = lane + 64 * q, gi = t >> 4, r = t & 15;
+    sv[q] = (r < M && gi < ngw) ? p.gs[(size_t)r * ng + g0 + gi] : 0.f;
   }
-  // ALDS: 16-byte chunks (row, step, quarter) at
-  // As[((row * nsteps + step) * 4 + quarter) * 16], which is the row-major
-  // [M][K] order; 4 row slots of NT / 4 threads.  From p.arow when given
-  // (contiguous), else gathered from the A tiles (16 useful bytes per 128-byte
-  // line a row touches).
-  constexpr int AL = NT / 4, AQ = ALDS ? (8 * NGW * NWV + AL - 1) / AL : 1;
-  const int ar = threadIdx.x / AL, ak = threadIdx.x % AL;
+  // ALDS: item t = (row r, chunk c = 4 step + quarter of the wave's steps),
+  // from p.arow when given (contiguous), else gathered from the A tiles (16
+  // useful bytes per 128-byte line a row touches)
+  constexpr int CW = 8 * NGW, AQ = ALDS ? (4 * CW + 63) / 64 : 1;
   v4i av[AQ];
   if constexpr (ALDS) {
     const bool rows = p.arow != nullptr;
 #pragma unroll
     for (int q = 0; q < AQ; ++q) {
-      const int sq = ak + AL * q;  // step * 4 + quarter
-      const int8_t* src = rows ? p.arow + (size_t)ar * p.K + 16 * sq
-                               : p.a + 1024 * (sq >> 2) + 16 * (16 * (sq & 3) + ar);
-      av[q] = (ar < M && sq < 4 * p.nsteps) ? *reinterpret_cast<const v4i*>(src) : (v4i){0, 0, 0, 0};
+      const int t = lane + 64 * q, r = t / CW, c = t % CW;
+      const int st = 2 * g0 + (c >> 2), qu = c & 3;
+      const int8_t* src = rows ? p.arow + (size_t)r * p.K + 64 * st + 16 * qu
+                               : p.a + 1024 * st + 16 * (16 * qu + r);
+      av[q] = (r < M && (c >> 3) < ngw) ? *reinterpret_cast<const v4i*>(src) : (v4i){0, 0, 0, 0};
     }
   }
   // scale | zero pairs: load q of tile j holds groups g0 + 4q .. + 3 (lane
@@ -1044,17 +1046,18 @@ __global__ __launch_bounds__(64 * NWV) void qgemm_stream(KParams p) {
   for (int d = 0; d < P && d < NGW; ++d) fetch(d, ring[d]);
 #pragma unroll
   for (int q = 0; q < SQ; ++q) {
-    const int g = sk + SL * q;
-    if (sr < M && g < ng) S_l[g * 16 + sr] = sv[q];
+    const int t = lane + 64 * q;
+    if (t < 16 * NGW) S_w[t] = sv[q];
   }
   if constexpr (ALDS) {
 #pragma unroll
     for (int q = 0; q < AQ; ++q) {
-      const int sq = ak + AL * q;
-      if (ar < M && sq < 4 * p.nsteps) *reinterpret_cast<v4i*>(As + ((size_t)ar * p.nsteps * 4 + sq) * 16) = av[q];
+      const int t = lane + 64 * q, r = t / CW, c = t % CW;
+      if (r < M) *reinterpret_cast<v4i*>(As_w + ((size_t)r * CW + c) * 16) = av[q];
     }
   }
-  __syncthreads();
+  // the wave's own LDS regions: no workgroup barrier before the ring
+  ifrd::wave_sync();
   // this lane's real rows: 4 lgrp .. 4 lgrp + rq - 1; the fold steps run to
   // the wave-uniform min(4, M)
   const int rq = M - 4 * lgrp, rmax = min(4, M);
@@ -1066,14 +1069,13 @@ __global__ __launch_bounds__(64 * NWV) void qgemm_stream(KParams p) {
   v4f Sn;
   uint32_t zn[WN];
   auto lds_ops = [&](int d) {
-    const int g = min(g0 + d, glast);
     if constexpr (ALDS) {
 #pragma unroll
       for (int h = 0; h < 2; ++h)
-        an[h] = arow ? *reinterpret_cast<const v4i*>(As + (((size_t)lrow * p.nsteps + 2 * g + h) * 4 + lgrp) * 16)
+        an[h] = arow ? *reinterpret_cast<const v4i*>(As_w + ((size_t)lrow * CW + (2 * d + h) * 4 + lgrp) * 16)
                      : (v4i){0, 0, 0, 0};
     }
-    Sn = *reinterpret_cast<const v4f*>(&S_l[g * 16 + 4 * lgrp]);
+    Sn = *reinterpret_cast<const v4f*>(&S_w[d * 16 + 4 * lgrp]);
 #pragma unroll
     for (int j = 0; j < WN; ++j) zn[j] = (uint32_t)__shfl((int)zq[j][d >> 2], lrow + 16 * (d & 3), 64);
   };
@@ -1268,13 +1270,15 @@ hipError_t launch_stream(const KParams& p, hipStream_t st) {
   constexpr int kFitA = (kLim - kOver - 4 * ((NGW + 1) / 2)) / (WN * BITS);
   constexpr int PF = kRing < kFitF ? kRing : kFitF, PA = kRing < kFitA ? kRing : kFitA;
   if (p.M > 16 || (p.ng + NWV - 1) / NWV > NGW) return hipErrorInvalidValue;
-  // LDS: d rows [M][BN] and scale rows [BN] (pitch gp), S [ng][16], the
-  // ALDS rows.  gp: a multiple of 4 (four groups per 128-bit read) that is
-  // 4 mod 8, so the rows of the 16 columns of one group start in different
-  // banks; the plain multiple of 4 where the padded rows do not fit.
+  // LDS: d rows [M][BN] and scale rows [BN] (pitch gp), then per wave S
+  // [NGW][16] and the ALDS rows [M][NGW x 128 bytes].  gp: a multiple of 4
+  // (four groups per 128-bit read) that is 4 mod 8, so the rows of the 16
+  // columns of one group start in different banks; the plain multiple of 4
+  // where the padded rows do not fit.
   constexpr int BN = 16 * WN;
   auto need = [&](int gp, bool alds) {
-    return ((size_t)(p.M + 1) * BN * gp + 16 * (size_t)p.ng) * sizeof(float) + (alds ? (size_t)p.M * p.K : 0);
+    return ((size_t)(p.M + 1) * BN * gp + (size_t)NWV * 16 * NGW) * sizeof(float) +
+           (alds ? (size_t)NWV * p.M * 128 * NGW : 0);
   };
   bool alds = PA >= 1 && p.M <= 4;
   if (alds && need((p.ng + 3) & ~3, true) > 160 * 1024) alds = false;
