@@ -154,69 +154,80 @@ __global__ __launch_bounds__(256) void row_quant_kernel(RowQuantArgs a) {
             a.gsum ? a.gsum + (size_t)m * (K / 128) : nullptr, red, codes);
 }
 
-// ---- fast path: K = 1024 rows, 4 contiguous elements per thread --------------
+// ---- fast path: K = 1024 rows, 8 waves per row, 2 contiguous elements per thread
 //
-// FWHT stages in the reference order (half = 1, 2, ..., 512): half 1-2 inside a
-// thread, half 4-128 across lanes of a wave (partner lane ^ half/4), half
-// 256-512 through one LDS exchange.  Every output is formed by the same adds
-// on the same operands as the sequential loop, so the result is bit-identical.
+// FWHT stages in the reference order (half = 1, 2, ..., 512): half 1 inside a
+// thread, half 2-64 across lanes of a wave (partner lane ^ half/2), half
+// 128-512 through one LDS exchange across the eight waves.  Every output is
+// formed by the same adds on the same operands as the sequential loop, so the
+// result is bit-identical.
 template <int M>
 __device__ __forceinline__ float bfly_lane(float x) {
   const float o = ifrd::lane_xor<M>(x);
   return (threadIdx.x & M) ? (o - x) : (x + o);
 }
 
-__device__ void fwht1024(float (&v)[4], float* xs) {
-  float a, b;
-  a = v[0]; b = v[1]; v[0] = a + b; v[1] = a - b;
-  a = v[2]; b = v[3]; v[2] = a + b; v[3] = a - b;
-  a = v[0]; b = v[2]; v[0] = a + b; v[2] = a - b;
-  a = v[1]; b = v[3]; v[1] = a + b; v[3] = a - b;
-#pragma unroll
-  for (int e = 0; e < 4; ++e) v[e] = bfly_lane<1>(v[e]);
-#pragma unroll
-  for (int e = 0; e < 4; ++e) v[e] = bfly_lane<2>(v[e]);
-#pragma unroll
-  for (int e = 0; e < 4; ++e) v[e] = bfly_lane<4>(v[e]);
-#pragma unroll
-  for (int e = 0; e < 4; ++e) v[e] = bfly_lane<8>(v[e]);
-#pragma unroll
-  for (int e = 0; e < 4; ++e) v[e] = bfly_lane<16>(v[e]);
-#pragma unroll
-  for (int e = 0; e < 4; ++e) v[e] = bfly_lane<32>(v[e]);
-  __syncthreads();
-#pragma unroll
-  for (int e = 0; e < 4; ++e) xs[4 * threadIdx.x + e] = v[e];
-  __syncthreads();
-  const int q = threadIdx.x >> 6;  // quarter of the 1024 elements
-  const float inv = 1.0f / sqrtf(1024.0f);
-  // element (4 t + e) & 255 of each quarter: one 16-byte read per quarter
-  float aq[4][4];
-#pragma unroll
-  for (int k = 0; k < 4; ++k) {
-    const float4 x = *reinterpret_cast<const float4*>(xs + ((4 * threadIdx.x) & 255) + 256 * k);
-    aq[k][0] = x.x; aq[k][1] = x.y; aq[k][2] = x.z; aq[k][3] = x.w;
+__device__ void fwht1024(float (&v)[2], float* xs) {
+  {
+    const float a = v[0], b = v[1];
+    v[0] = a + b;
+    v[1] = a - b;
   }
 #pragma unroll
-  for (int e = 0; e < 4; ++e) {
-    const float a0 = aq[0][e], a1 = aq[1][e], a2 = aq[2][e], a3 = aq[3][e];
-    const float b0 = a0 + a1, b1 = a0 - a1, b2 = a2 + a3, b3 = a2 - a3;
-    const float c = q == 0 ? b0 + b2 : q == 1 ? b1 + b3 : q == 2 ? b0 - b2 : b1 - b3;
+  for (int e = 0; e < 2; ++e) v[e] = bfly_lane<1>(v[e]);
+#pragma unroll
+  for (int e = 0; e < 2; ++e) v[e] = bfly_lane<2>(v[e]);
+#pragma unroll
+  for (int e = 0; e < 2; ++e) v[e] = bfly_lane<4>(v[e]);
+#pragma unroll
+  for (int e = 0; e < 2; ++e) v[e] = bfly_lane<8>(v[e]);
+#pragma unroll
+  for (int e = 0; e < 2; ++e) v[e] = bfly_lane<16>(v[e]);
+#pragma unroll
+  for (int e = 0; e < 2; ++e) v[e] = bfly_lane<32>(v[e]);
+  __syncthreads();
+  *reinterpret_cast<float2*>(xs + 2 * threadIdx.x) = make_float2(v[0], v[1]);
+  __syncthreads();
+  // element 2 t + e sits in 128-block kb = wave; the last three stages combine
+  // the eight blocks' values at the same offset: (a_k = x_k +- x_k^1), then
+  // (b = a_k +- a_k^2), then (c = b_k +- b_k^4), each with the reference's
+  // operand order, for the one output kb
+  const int kb = threadIdx.x >> 6;
+  const float inv = 1.0f / sqrtf(1024.0f);
+#pragma unroll
+  for (int e = 0; e < 2; ++e) {
+    const int off = (2 * threadIdx.x + e) & 127;
+    float x[8];
+#pragma unroll
+    for (int k = 0; k < 8; ++k) x[k] = xs[off + 128 * k];
+    // the four stage-128 pairs feeding output kb: pairs (b4 + 2 j2 + {0,1}) for
+    // j2 in {0,1} and b4 in {0,4}; keep a_k with k = 2 q + (kb & 1)
+    float a[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const float lo = x[2 * q], hi = x[2 * q + 1];
+      a[q] = (kb & 1) ? lo - hi : lo + hi;
+    }
+    // stage 256: b over (a_q, a_q+1) within each half: b_k with (k & 2) = kb & 2
+    const float b0 = (kb & 2) ? a[0] - a[1] : a[0] + a[1];
+    const float b1 = (kb & 2) ? a[2] - a[3] : a[2] + a[3];
+    // stage 512
+    const float c = (kb & 4) ? b0 - b1 : b0 + b1;
     v[e] = c * inv;
   }
 }
 
-// RMSNorm factor of the 1024 values held 4 per thread, reference order: eight
+// RMSNorm factor of the 1024 values held 2 per thread, reference order: eight
 // sequential fused chains over x[j + 8n], folded (j, j+4) then two horizontal
 // adds.  The row is stored chain-major (chain j = i % 8 holds x[j + 8n] at
 // 132 j + n; the stride 132 keeps the stores on distinct banks), so each
-// chain reads its 128 values 4 at a time, in batches that overlap.
+// chain reads its 128 values 4 at a time.
 constexpr int kRms1024Lds = 8 * 132;  // floats of xs the chain-major copy uses
-__device__ float rms1024(const float (&v)[4], float* xs, float* red, float eps) {
+__device__ float rms1024(const float (&v)[2], float* xs, float* red, float eps) {
   __syncthreads();
 #pragma unroll
-  for (int e = 0; e < 4; ++e) {
-    const int i = 4 * threadIdx.x + e;
+  for (int e = 0; e < 2; ++e) {
+    const int i = 2 * threadIdx.x + e;
     xs[(i & 7) * 132 + (i >> 3)] = v[e];
   }
   __syncthreads();
@@ -244,73 +255,71 @@ __device__ float rms1024(const float (&v)[4], float* xs, float* red, float eps) 
   return 1.0f / sqrtf(tot / 1024.0f + eps);
 }
 
-__global__ __launch_bounds__(256) void row_quant1024_kernel(RowQuantArgs a) {
+__global__ __launch_bounds__(512) void row_quant1024_kernel(RowQuantArgs a) {
   __shared__ __attribute__((aligned(16))) float xs[kRms1024Lds];  // fwht1024 uses the first 1024
   __shared__ float red[16];
   const int m = blockIdx.x, t = threadIdx.x, lane = t & 63;
   const int src = a.rowmap ? a.rowmap[m] : m;
-  float v[4];
+  float v[2];
   if (a.src == SRC_X) {
-    const float4 x4 = *reinterpret_cast<const float4*>(a.x + (size_t)src * 1024 + 4 * t);
-    v[0] = x4.x; v[1] = x4.y; v[2] = x4.z; v[3] = x4.w;
+    const float2 x2 = *reinterpret_cast<const float2*>(a.x + (size_t)src * 1024 + 2 * t);
+    v[0] = x2.x; v[1] = x2.y;
   } else if (a.src == SRC_EMBED) {
-    const float4 x4 = *reinterpret_cast<const float4*>(a.embed + (size_t)a.tokens[src] * 1024 + 4 * t);
-    v[0] = x4.x; v[1] = x4.y; v[2] = x4.z; v[3] = x4.w;
-    *reinterpret_cast<float4*>(a.resid + (size_t)src * 1024 + 4 * t) = x4;
+    const float2 x2 = *reinterpret_cast<const float2*>(a.embed + (size_t)a.tokens[src] * 1024 + 2 * t);
+    v[0] = x2.x; v[1] = x2.y;
+    *reinterpret_cast<float2*>(a.resid + (size_t)src * 1024 + 2 * t) = x2;
   } else {
     // both loads issued together: the residual does not wait behind the
     // rotation's barriers
-    const uint2 y2 = *reinterpret_cast<const uint2*>(a.y + (size_t)src * 1024 + 4 * t);
-    float4* rp = reinterpret_cast<float4*>(a.resid + (size_t)src * 1024 + 4 * t);
-    float4 r4 = *rp;
-    v[0] = ifrd::h2f((uint16_t)(y2.x & 0xFFFF));
-    v[1] = ifrd::h2f((uint16_t)(y2.x >> 16));
-    v[2] = ifrd::h2f((uint16_t)(y2.y & 0xFFFF));
-    v[3] = ifrd::h2f((uint16_t)(y2.y >> 16));
+    const uint32_t y2 = *reinterpret_cast<const uint32_t*>(a.y + (size_t)src * 1024 + 2 * t);
+    float2* rp = reinterpret_cast<float2*>(a.resid + (size_t)src * 1024 + 2 * t);
+    float2 r2 = *rp;
+    v[0] = ifrd::h2f((uint16_t)(y2 & 0xFFFF));
+    v[1] = ifrd::h2f((uint16_t)(y2 >> 16));
     if (a.rot_y) fwht1024(v, xs);
-    r4.x = r4.x + v[0]; r4.y = r4.y + v[1]; r4.z = r4.z + v[2]; r4.w = r4.w + v[3];
-    *rp = r4;
-    v[0] = r4.x; v[1] = r4.y; v[2] = r4.z; v[3] = r4.w;
+    r2.x = r2.x + v[0]; r2.y = r2.y + v[1];
+    *rp = r2;
+    v[0] = r2.x; v[1] = r2.y;
   }
   if (a.norm_w) {
     const float f = rms1024(v, xs, red, a.eps);
-    const float4 w4 = *reinterpret_cast<const float4*>(a.norm_w + 4 * t);
-    v[0] = (v[0] * f) * (1.0f + w4.x);
-    v[1] = (v[1] * f) * (1.0f + w4.y);
-    v[2] = (v[2] * f) * (1.0f + w4.z);
-    v[3] = (v[3] * f) * (1.0f + w4.w);
+    const float2 w2 = *reinterpret_cast<const float2*>(a.norm_w + 2 * t);
+    v[0] = (v[0] * f) * (1.0f + w2.x);
+    v[1] = (v[1] * f) * (1.0f + w2.y);
   }
   if (a.rotate) fwht1024(v, xs);
-  int c[4];
+  int c[2];
   if (a.ga == 0) {
-    float mx = fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3])));
+    float mx = fmaxf(fabsf(v[0]), fabsf(v[1]));
     mx = ifrd::wave_max(mx);
     __syncthreads();
     if (lane == 0) red[8 + (t >> 6)] = mx;
     __syncthreads();
-    mx = fmaxf(1e-6f, fmaxf(fmaxf(red[8], red[9]), fmaxf(red[10], red[11])));
+    mx = fmaxf(fmaxf(fmaxf(red[8], red[9]), fmaxf(red[10], red[11])),
+               fmaxf(fmaxf(red[12], red[13]), fmaxf(red[14], red[15])));
+    mx = fmaxf(1e-6f, mx);
     const float s = mx / 127.0f;
     const float inv = 1.0f / s;
     if (t == 0) a.qscale[m] = s;
 #pragma unroll
-    for (int e = 0; e < 4; ++e)
+    for (int e = 0; e < 2; ++e)
       c[e] = a.round == 0 ? ifrd::quant_half_away(v[e], inv) : ifrd::quant_rne(v[e], inv);
-  } else {  // 64-wide slices = 16 lanes
-    float mx = fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3])));
-    mx = fmaxf(1e-6f, ifrd::row16_max(mx));
+  } else {  // 64-wide slices = 32 lanes
+    float mx = fmaxf(fabsf(v[0]), fabsf(v[1]));
+    mx = ifrd::row16_max(mx);
+    mx = fmaxf(1e-6f, fmaxf(mx, ifrd::lane_xor<16>(mx)));
     const float s = mx / 127.0f;
     const float inv = 1.0f / s;
-    if ((lane & 15) == 0) a.qscale[(size_t)m * 16 + (t >> 4)] = s;
+    if ((lane & 31) == 0) a.qscale[(size_t)m * 16 + (t >> 5)] = s;
 #pragma unroll
-    for (int e = 0; e < 4; ++e)
+    for (int e = 0; e < 2; ++e)
       c[e] = a.round == 0 ? ifrd::quant_half_away(v[e], inv) : ifrd::quant_rne(v[e], inv);
   }
-  const uint32_t packed = (uint32_t)(c[0] & 0xFF) | ((uint32_t)(c[1] & 0xFF) << 8) |
-                          ((uint32_t)(c[2] & 0xFF) << 16) | ((uint32_t)(c[3] & 0xFF) << 24);
-  *reinterpret_cast<uint32_t*>(a.q + atile_off(m, 4 * t, 1024)) = packed;
-  if (a.gsum) {  // 128-wide groups = 32 lanes (integer sums: order-free)
-    const int S = ifrd::half_sum_int(c[0] + c[1] + c[2] + c[3]);
-    if ((lane & 31) == 0) a.gsum[(size_t)m * 8 + (t >> 5)] = (float)S;
+  const uint16_t packed = (uint16_t)((uint32_t)(c[0] & 0xFF) | ((uint32_t)(c[1] & 0xFF) << 8));
+  *reinterpret_cast<uint16_t*>(a.q + atile_off(m, 2 * t, 1024)) = packed;
+  if (a.gsum) {  // 128-wide groups = one wave (integer sums: order-free)
+    const int S = ifrd::wave_sum_int(c[0] + c[1]);
+    if (lane == 0) a.gsum[(size_t)m * 8 + (t >> 6)] = (float)S;
   }
 }
 
@@ -1180,7 +1189,7 @@ hipError_t launch_row_quant(const RowQuantArgs& a, hipStream_t st) {
   if (a.src == SRC_EMBED && (!a.embed || !a.tokens || !a.resid)) return hipErrorInvalidValue;
   if (a.src == SRC_RESID && (!a.y || !a.resid)) return hipErrorInvalidValue;
   if (a.K == 1024 && (a.ga == 0 || a.ga == 64)) {
-    hipLaunchKernelGGL(row_quant1024_kernel, dim3(a.M), dim3(256), 0, st, a);
+    hipLaunchKernelGGL(row_quant1024_kernel, dim3(a.M), dim3(512), 0, st, a);
     return hipGetLastError();
   }
   {

@@ -70,6 +70,7 @@ struct __attribute__((aligned(16))) int4 { int x, y, z, w; };
 inline uint2 make_uint2(unsigned a, unsigned b) { return uint2{a, b}; }
 inline uint4 make_uint4(unsigned a, unsigned b, unsigned c, unsigned d) { return uint4{a, b, c, d}; }
 inline float4 make_float4(float a, float b, float c, float d) { return float4{a, b, c, d}; }
+inline float2 make_float2(float a, float b) { return float2{a, b}; }
 
 inline int min(int a, int b) { return a < b ? a : b; }
 inline int max(int a, int b) { return a > b ? a : b; }
