@@ -730,16 +730,73 @@ def intfer_load():
     model.close()
 
 
-def run_scenarios(names, timeout=3600) -> int:
-    """Run scenarios in a child process with the ASan runtime preloaded."""
+def _child_env() -> dict:
     from tests.hipemu import build as eb
     env = dict(os.environ)
     pre = env.get("LD_PRELOAD", "")
     env["LD_PRELOAD"] = eb.asan_runtime() + (":" + pre if pre else "")
     env["IFR_EMU_CHILD"] = "1"
     env["ASAN_OPTIONS"] = "detect_leaks=0:halt_on_error=1:abort_on_error=1:detect_stack_use_after_return=0"
-    r = subprocess.run([sys.executable, str(HERE / "runner.py"), *names], env=env, timeout=timeout)
+    return env
+
+
+def run_scenarios(names, timeout=3600) -> int:
+    """Run scenarios in a child process with the ASan runtime preloaded."""
+    r = subprocess.run([sys.executable, str(HERE / "runner.py"), *names], env=_child_env(), timeout=timeout)
     return r.returncode
+
+
+class ScenarioPool:
+    """Every scenario in a child process of its own, at most `jobs` at once,
+    started in the given order as soon as a slot frees up; result() waits for
+    the named ones.  close() kills the children it started (by their own
+    process ids) that are still running."""
+
+    def __init__(self, names, jobs):
+        import threading
+        self._env = _child_env()
+        self._todo = list(names)
+        self._jobs = max(1, jobs)
+        self._procs = {}
+        self._rc = {}
+        self._cv = threading.Condition()
+        self._closed = False
+        self._thread = threading.Thread(target=self._loop, daemon=True)
+        self._thread.start()
+
+    def _loop(self):
+        while True:
+            with self._cv:
+                for n, p in list(self._procs.items()):
+                    if p.poll() is not None:
+                        self._rc[n] = p.returncode
+                        del self._procs[n]
+                        self._cv.notify_all()
+                if self._closed or (not self._todo and not self._procs):
+                    return
+                while self._todo and len(self._procs) < self._jobs:
+                    n = self._todo.pop(0)
+                    self._procs[n] = subprocess.Popen([sys.executable, str(HERE / "runner.py"), n], env=self._env)
+            time.sleep(0.2)
+
+    def result(self, names, timeout=3600) -> int:
+        end = time.time() + timeout
+        with self._cv:
+            while not all(n in self._rc for n in names):
+                left = end - time.time()
+                if left <= 0:
+                    raise TimeoutError(f"scenarios {names} still running after {timeout} s")
+                self._cv.wait(min(left, 1.0))
+            return next((self._rc[n] for n in names if self._rc[n] != 0), 0)
+
+    def close(self):
+        with self._cv:
+            self._closed = True
+            for p in self._procs.values():
+                p.kill()
+            for p in self._procs.values():
+                p.wait()
+        self._thread.join()
 
 
 if __name__ == "__main__":
